@@ -1,0 +1,150 @@
+/*
+ * turingserve_hip.h -- C ABI of the MI355X (gfx950) per-step hot path of TuringServe.
+ *
+ * One shared library, libturingserve_hip.so, exports these entry points. They replace the
+ * Triton kernels behind the reference's op namespace (turingserve/ops/__init__.py:22-35):
+ *
+ *   ts_kv_write            <- ops/triton_kv_write.py:28-35   (twin ops/reference.py:50-57)
+ *   ts_decode_attention    <- ops/triton_ops.py:35-57 (_decode) and
+ *                             ops/triton_decode_attention.py:169-200 (v1 / v2 / v3 launchers)
+ *   ts_prefill_attention   <- ops/triton_prefill_attention.py:66-79
+ *   ts_paged_attention     <- ops/triton_ops.py:60-71        (twin ops/reference.py:94-111)
+ *   ts_w8a16_gemm          <- ops/triton_w8a16.py:38-51 and ops/triton_ops.py:74-91
+ *                             (twin ops/reference.py:45-47 + quant/int8.py:15-16)
+ *
+ * Conventions shared by every entry point
+ *  - Plain pointers to device memory; the caller owns every buffer. The library never
+ *    allocates or frees device memory; scratch space comes in through `workspace`.
+ *  - Activations, K/V caches and outputs are IEEE fp16 (the reference's serving dtype).
+ *    Strides are in elements, not bytes.
+ *  - `stream` is a hipStream_t passed as void*; every launch is stream-ordered and no entry
+ *    point synchronises with the host, so all of them can be captured into a hipGraph.
+ *  - Return value: TS_OK (0) or a negative status. On error nothing has been launched and
+ *    ts_last_error() returns a message (thread-local) naming the offending argument.
+ *  - Paged KV cache of one layer: k_cache / v_cache are [num_blocks, num_kv_heads, 16, head_dim]
+ *    contiguous (the per-layer views kv_cache[l, 0] / kv_cache[l, 1] of the reference's
+ *    [L, 2, num_blocks, KVH, 16, D] tensor, engine/builder.py:76-80). Block 0 is the null block.
+ *  - Memory safety instead of undefined behaviour: slot ids outside [0, num_blocks*16) are
+ *    skipped like -1, block ids outside [0, num_blocks) read block 0, and a sequence whose
+ *    seq_len exceeds 16 * max_blocks_per_seq attends only to the blocks its table holds.
+ */
+#ifndef TURINGSERVE_HIP_H
+#define TURINGSERVE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TS_OK 0
+#define TS_ERR_INVALID_ARG (-1)   /* null pointer, negative size, bad stride, bad alignment */
+#define TS_ERR_UNSUPPORTED (-2)   /* a shape the kernels are not built for (e.g. head_dim 96) */
+#define TS_ERR_WORKSPACE (-3)     /* workspace missing or smaller than *_workspace_bytes() */
+#define TS_ERR_LAUNCH (-4)        /* the HIP runtime refused a launch */
+#define TS_ERR_DEVICE (-5)        /* device query failed */
+
+/* Decode kernel versions (ops/triton_decode_attention.py:1-10). */
+#define TS_DECODE_AUTO 0          /* the split policy of ops/triton_ops.py:44-57, retuned for 256 CUs */
+#define TS_DECODE_V1 1            /* one wavefront per (sequence, query head), VALU only */
+#define TS_DECODE_V2 2            /* one workgroup per (sequence, KV head), GQA group on MFMA */
+#define TS_DECODE_V3 3            /* v2 split over context partitions + reduction of the partials */
+
+/* Library version string, e.g. "turingserve_hip 0.1.0 gfx950". */
+const char* ts_version(void);
+
+/* Message of the last failing call on this host thread ("" if none). */
+const char* ts_last_error(void);
+
+/* Number of compute units of `device` (the reference's num_sms, utils/gpu.py:19-24). */
+int ts_device_cu_count(int device, int* cu_count);
+
+/*
+ * kv_write: for every token t with s = slot_mapping[t] >= 0,
+ *   k_cache[s / 16, h, s % 16, :] = k[t, h, :] and v_cache[...] = v[t, h, :]  for all h.
+ * Bit-exact copy. k and v may be strided views of the fused qkv activation
+ * (stride over tokens k_stride_t, over heads k_stride_h, unit stride over head_dim).
+ * Replaces ops/triton_kv_write.py:28-35 (twin ops/reference.py:50-57).
+ */
+int ts_kv_write(const void* k, const void* v,
+                int64_t k_stride_t, int64_t k_stride_h,
+                int64_t v_stride_t, int64_t v_stride_h,
+                void* k_cache, void* v_cache, int64_t num_blocks,
+                const int64_t* slot_mapping, int64_t num_tokens,
+                int32_t num_kv_heads, int32_t head_dim, void* stream);
+
+/*
+ * Decode attention over the first num_seqs rows of the flat batch (one query token each,
+ * q row s belongs to sequence s). out[s, h*D:(h+1)*D] = softmax(q_s,h . K^T * scale) . V over
+ * the seq_lens[s] cached tokens of sequence s; rows with seq_len 0 are written as zeros.
+ * version: TS_DECODE_*. partition: tokens per split for v3 (multiple of 16; 0 = default).
+ * max_seq_len: a host-side upper bound of seq_lens (inside graphs: max_model_len); it fixes
+ * the split count of v3 exactly as ops/triton_ops.py:50-51 does.
+ * Workspace: ts_decode_workspace_bytes() bytes, 256-byte aligned (0 bytes for v1 / v2).
+ * Replaces ops/triton_ops.py:35-57 and ops/triton_decode_attention.py:169-200.
+ */
+size_t ts_decode_workspace_bytes(int32_t version, int32_t num_seqs, int32_t num_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t max_seq_len,
+                                 int32_t partition, int32_t cu_count);
+int ts_decode_attention(int32_t version,
+                        const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                        void* out, int64_t out_stride_t,
+                        const void* k_cache, const void* v_cache, int64_t num_blocks,
+                        const int32_t* block_tables, int64_t bt_stride, int32_t max_blocks_per_seq,
+                        const int32_t* seq_lens, int32_t num_seqs,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                        float scale, int32_t max_seq_len, int32_t partition,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Chunked-prefill attention for sequences num_decode .. num_seqs-1 of the flat batch.
+ * Query row i of sequence b (rows query_start_loc[b] .. query_start_loc[b+1]-1) sits at
+ * absolute position prefix + i, prefix = seq_lens[b] - q_len; it attends to keys
+ * j <= prefix + i (bottom-right causal mask) read through block_tables[b].
+ * num_tokens bounds every q / out row the kernel touches.
+ * Replaces ops/triton_prefill_attention.py:66-79.
+ */
+int ts_prefill_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                         void* out, int64_t out_stride_t, int64_t num_tokens,
+                         const void* k_cache, const void* v_cache, int64_t num_blocks,
+                         const int32_t* block_tables, int64_t bt_stride, int32_t max_blocks_per_seq,
+                         const int32_t* seq_lens, const int32_t* query_start_loc,
+                         int32_t num_seqs, int32_t num_decode, int32_t max_query_len,
+                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                         float scale, void* stream);
+
+/*
+ * paged_attention: decode kernel on rows [0, num_decode), prefill kernel on the remaining
+ * sequences; one call per layer. Workspace as ts_decode_workspace_bytes(TS_DECODE_AUTO, ...).
+ * Replaces ops/triton_ops.py:60-71.
+ */
+int ts_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                       void* out, int64_t out_stride_t, int64_t num_tokens,
+                       const void* k_cache, const void* v_cache, int64_t num_blocks,
+                       const int32_t* block_tables, int64_t bt_stride, int32_t max_blocks_per_seq,
+                       const int32_t* seq_lens, const int32_t* query_start_loc,
+                       int32_t num_seqs, int32_t num_decode, int32_t max_query_len,
+                       int32_t max_seq_len,
+                       int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
+                       float scale, int32_t decode_version, int32_t partition,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * W8A16 GEMM: y[M, N] = x[M, K] . (wq[N, K] * scale[N])^T (+ bias[N]), fp32 accumulation,
+ * the per-output-channel scale applied once after the int8 x fp16 contraction
+ * (ops/triton_w8a16.py:11-35). x, y fp16 row-major with leading dimensions ldx, ldy;
+ * wq int8 row-major [N, K]; scale fp32 (scale_is_fp16 = 0, quant/int8.py:8-12) or fp16
+ * (scale_is_fp16 = 1); bias fp16 or NULL.
+ * Workspace: ts_w8a16_workspace_bytes() bytes (split-K partials for small M).
+ */
+size_t ts_w8a16_workspace_bytes(int32_t M, int32_t N, int32_t K, int32_t cu_count);
+int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const void* scale,
+                  int32_t scale_is_fp16, const void* bias, void* y, int64_t ldy,
+                  int32_t M, int32_t N, int32_t K,
+                  void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* TURINGSERVE_HIP_H */

@@ -1,0 +1,298 @@
+"""The gfx950 kernels against the oracle on identical seeded inputs (needs an MI355X).
+
+Shapes and criteria follow the reference's kernel tests (tests/kernels/test_kernels.py:15-169):
+kv_write bit-exact; attention within atol = rtol = 1e-2 of the fp32 twin arithmetic and, as the
+hot-path goal states, max |err| <= 1e-2 and mean |err| <= 1e-3; padding rows exactly 0;
+W8A16 relative Frobenius error < 1e-3. Inputs are drawn on the host and copied to the GPU, so the
+oracle sees the same bytes.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged as OP
+from oracle import quant as OQ
+from turingserve_amd import hip_ops as K
+from turingserve_amd import reference_ops as R
+from turingserve_amd import synth
+from turingserve_amd.metadata import AttentionMetadata
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+HEADS = [(4, 2, 16), (14, 2, 64), (12, 2, 128), (8, 8, 64)]
+ATOL = RTOL = 1e-2        # tests/kernels/test_kernels.py:117,132
+MAX_ABS, MEAN_ABS = 1e-2, 1e-3
+
+
+def assert_attn(out: torch.Tensor, ref: np.ndarray, what: str = "") -> None:
+    o = out.float().cpu().numpy().astype(np.float64)
+    r = np.asarray(ref, dtype=np.float64)
+    err = np.abs(o - r)
+    assert np.isfinite(o).all(), f"{what}: non-finite output"
+    bad = err > ATOL + RTOL * np.abs(r)
+    assert not bad.any(), f"{what}: {bad.sum()} elements outside atol=rtol=1e-2, max err {err.max()}"
+    assert err.max() <= MAX_ABS, f"{what}: max abs err {err.max()}"
+    assert err.mean() <= MEAN_ABS, f"{what}: mean abs err {err.mean()}"
+
+
+def make_paged(seq_lens, H, KVH, D, q_lens=None, seed=0):
+    """Shuffled block ids with block 0 reserved, N(0, 1) caches and queries
+    (tests/kernels/test_kernels.py:78-95), drawn on the host."""
+    g = torch.Generator().manual_seed(seed)
+    B = len(seq_lens)
+    q_lens = q_lens or [1] * B
+    nbs = [-(-s // 16) for s in seq_lens]
+    total = sum(nbs) + 1
+    perm = torch.randperm(total - 1, generator=g) + 1
+    kc = torch.randn(total, KVH, 16, D, generator=g).half()
+    vc = torch.randn(total, KVH, 16, D, generator=g).half()
+    bt = torch.zeros(B, max(1, max(nbs)), dtype=torch.int32)
+    off = 0
+    for b, nb in enumerate(nbs):
+        bt[b, :nb] = perm[off:off + nb].int()
+        off += nb
+    qsl = torch.tensor([0] + np.cumsum(q_lens).tolist(), dtype=torch.int32)
+    q = torch.randn(sum(q_lens), H, D, generator=g).half()
+    return q, kc, vc, qsl, torch.tensor(seq_lens, dtype=torch.int32), bt
+
+
+def meta_of(qsl, sl, bt, num_decode, q_lens, T, device=DEV):
+    return AttentionMetadata(qsl.to(device), sl.to(device), bt.to(device),
+                             torch.zeros(T, dtype=torch.int64, device=device), num_decode,
+                             max(q_lens), int(sl.max()))
+
+
+def oracle_attn(q, kc, vc, qsl, sl, bt, scale):
+    return OP.paged_attention(q.numpy(), kc.numpy(), vc.numpy(), qsl.numpy(), sl.numpy(),
+                              bt.numpy(), scale)
+
+
+# ------------------------------------------------------------------------------------------
+# kv_write: bit-exact (tests/kernels/test_kernels.py:61-75)
+# ------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("T", [1, 17, 300])
+def test_kv_write_exact(T):
+    g = torch.Generator().manual_seed(T)
+    KVH, D, NB = 2, 64, 64
+    k = torch.randn(T, KVH, D, generator=g).half()
+    v = torch.randn(T, KVH, D, generator=g).half()
+    slots = torch.randperm(NB * 16, generator=g)[:T].long()
+    slots[::5] = -1
+    kc = torch.randn(NB, KVH, 16, D, generator=g).half()
+    vc = torch.randn_like(kc)
+    kc1, vc1 = kc.cuda(), vc.cuda()
+    K.kv_write(k.cuda(), v.cuda(), kc1, vc1, slots.cuda())
+    kc2, vc2 = kc.cuda(), vc.cuda()
+    R.kv_write(k.cuda(), v.cuda(), kc2, vc2, slots.cuda())
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    kn, vn = kc.numpy().copy(), vc.numpy().copy()
+    OP.kv_write(k.numpy(), v.numpy(), kn, vn, slots.numpy())
+    assert np.array_equal(kc1.cpu().numpy(), kn) and np.array_equal(vc1.cpu().numpy(), vn)
+
+
+@pytest.mark.parametrize("H,KVH,D", HEADS)
+def test_kv_write_strided_qkv(H, KVH, D):
+    """k / v as strided views of the fused qkv activation, as the model passes them."""
+    st = synth.make_step(H, KVH, D, 96, [(40, 1), (7, 1), (0, 33), (16, 70)], seed=3)
+    _, k, v = st.views()
+    kc, vc = st.k_cache.cuda(), st.v_cache.cuda()
+    qkv = st.qkv.cuda()
+    _, kd, vd = st.views(qkv)
+    K.kv_write(kd, vd, kc, vc, st.slot_mapping.cuda())
+    kn, vn = st.k_cache.numpy().copy(), st.v_cache.numpy().copy()
+    OP.kv_write(k.numpy(), v.numpy(), kn, vn, st.slot_mapping.numpy())
+    assert np.array_equal(kc.cpu().numpy(), kn) and np.array_equal(vc.cpu().numpy(), vn)
+
+
+def test_kv_write_skips_out_of_range_slots():
+    """Slots outside [0, NB*16) are skipped like -1 instead of writing out of bounds."""
+    KVH, D, NB = 2, 64, 4
+    k = torch.randn(3, KVH, D).half().cuda()
+    kc = torch.zeros(NB, KVH, 16, D, dtype=torch.float16, device=DEV)
+    vc = torch.zeros_like(kc)
+    K.kv_write(k, k, kc, vc, torch.tensor([NB * 16, -1, 5], dtype=torch.int64, device=DEV))
+    assert torch.equal(kc[0, :, 5], k[2]) and int((kc != 0).sum()) == KVH * D
+
+
+# ------------------------------------------------------------------------------------------
+# decode (tests/kernels/test_kernels.py:103-118)
+# ------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("H,KVH,D", HEADS)
+@pytest.mark.parametrize("S", [1, 3, 64])
+@pytest.mark.parametrize("version", ["v1", "v2", "v3", None])
+def test_decode_versions(H, KVH, D, S, version):
+    lens = [[1, 2, 15, 16, 17, 100, 1000, 4096][(i * 3) % 8] for i in range(S)] + [0]
+    q, kc, vc, qsl, sl, bt = make_paged(lens, H, KVH, D)
+    n = len(lens)
+    q = q[:n]
+    meta = meta_of(qsl, sl, bt, n, [1] * n, n)
+    out = torch.full((n, H * D), float("nan"), device=DEV, dtype=torch.float16)
+    K._decode(q.cuda(), out, kc.cuda(), vc.cuda(), meta, D ** -0.5, version)
+    assert_attn(out, oracle_attn(q, kc, vc, qsl, sl, bt, D ** -0.5), f"decode {version}")
+    assert (out[-1] == 0).all()                                   # padding row (seq_len 0)
+
+
+@pytest.mark.parametrize("partition", [16, 64, 512])
+def test_decode_v3_partitions(partition):
+    H, KVH, D = 12, 2, 128
+    lens = [4096, 1, 17, 513, 1024, 2500, 0, 16]
+    q, kc, vc, qsl, sl, bt = make_paged(lens, H, KVH, D, seed=7)
+    n = len(lens)
+    out = torch.empty(n, H * D, device=DEV, dtype=torch.float16)
+    splits = -(-max(lens) // partition)
+    K.decode_attention_v3(q.cuda(), out, kc.cuda(), vc.cuda(), bt.cuda(), sl.cuda(), D ** -0.5, n,
+                          splits, partition)
+    assert_attn(out, oracle_attn(q, kc, vc, qsl, sl, bt, D ** -0.5), f"v3 partition {partition}")
+    assert (out[6] == 0).all()
+
+
+def test_decode_stale_nan_beyond_seq_len():
+    """Cache slots past seq_len in the last block may hold anything (a reused block); NaN there
+    must not reach the output (the twin slices [:seq_len], ops/reference.py:108-109)."""
+    H, KVH, D = 12, 2, 128
+    lens = [17, 100, 1000]
+    q, kc, vc, qsl, sl, bt = make_paged(lens, H, KVH, D, seed=11)
+    ref = oracle_attn(q, kc, vc, qsl, sl, bt, D ** -0.5)
+    for b, L in enumerate(lens):
+        blk = int(bt[b, (L - 1) // 16])
+        kc[blk, :, L % 16:] = float("nan")
+        vc[blk, :, L % 16:] = float("nan")
+    meta = meta_of(qsl, sl, bt, 3, [1] * 3, 3)
+    for version in ("v1", "v2", "v3"):
+        out = torch.empty(3, H * D, device=DEV, dtype=torch.float16)
+        K._decode(q.cuda(), out, kc.cuda(), vc.cuda(), meta, D ** -0.5, version)
+        assert_attn(out, ref, f"stale NaN {version}")
+
+
+# ------------------------------------------------------------------------------------------
+# prefill (tests/kernels/test_kernels.py:121-132)
+# ------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("H,KVH,D", HEADS)
+@pytest.mark.parametrize("q_len,prefix", [(1, 0), (15, 16), (16, 37), (17, 1000), (300, 0),
+                                          (2048, 16)])
+@pytest.mark.parametrize("P", [1, 3])
+def test_prefill(H, KVH, D, q_len, prefix, P):
+    q_lens = [q_len] * P
+    q, kc, vc, qsl, sl, bt = make_paged([prefix + q_len] * P, H, KVH, D, q_lens)
+    meta = meta_of(qsl, sl, bt, 0, q_lens, q.shape[0])
+    out = K.paged_attention(q.cuda(), kc.cuda(), vc.cuda(), meta, D ** -0.5)
+    assert_attn(out, oracle_attn(q, kc, vc, qsl, sl, bt, D ** -0.5), "prefill")
+
+
+def test_mixed_batch_ragged():
+    """Decodes and several ragged prefill chunks in one flat batch, one paged_attention call."""
+    H, KVH, D = 14, 2, 64
+    seq = [33, 1, 700, 16, 90, 301, 64]
+    ql = [1, 1, 1, 1, 90, 5, 64]
+    q, kc, vc, qsl, sl, bt = make_paged(seq, H, KVH, D, ql, seed=5)
+    meta = meta_of(qsl, sl, bt, 4, ql, q.shape[0])
+    out = K.paged_attention(q.cuda(), kc.cuda(), vc.cuda(), meta, D ** -0.5)
+    assert_attn(out, oracle_attn(q, kc, vc, qsl, sl, bt, D ** -0.5), "mixed")
+
+
+# ------------------------------------------------------------------------------------------
+# GQA-correct needles (the reference's needle test skips every G > 1 case,
+# tests/kernels/test_kernels.py:135-154): each query head of a group gets its own needle.
+# ------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("H,KVH,D", HEADS[:3])
+@pytest.mark.parametrize("mode", ["decode", "prefill"])
+def test_needle_gqa(H, KVH, D, mode):
+    L = 100
+    q_len = 1 if mode == "decode" else 9
+    q, kc, vc, qsl, sl, bt = make_paged([L], H, KVH, D, [q_len], seed=2)
+    G = H // KVH
+    q.zero_()
+    last = q_len - 1
+    positions = [0, 14, 15, 16, 17, 31, 32, 61, 77, 90]
+    want = torch.zeros(H, D, dtype=torch.float16)
+    for h in range(H):
+        kvh, r = h // G, h % G
+        q[last, h, r] = 8.0                        # orthogonal queries within a group
+        pos = positions[r % len(positions)]
+        blk = int(bt[0, pos // 16])
+        kc[blk, kvh, pos % 16] = 0.0
+        kc[blk, kvh, pos % 16, r] = 100.0          # score 800 vs |score| << 100 elsewhere
+        want[h] = vc[blk, kvh, pos % 16]
+    meta = meta_of(qsl, sl, bt, 1 if mode == "decode" else 0, [q_len], q_len)
+    out = K.paged_attention(q.cuda(), kc.cuda(), vc.cuda(), meta, 1.0)
+    got = out[last].view(H, D).float().cpu()
+    torch.testing.assert_close(got, want.float(), atol=1e-2, rtol=1e-2)
+
+
+# ------------------------------------------------------------------------------------------
+# the configs' ragged step through the product twins and through the kernels
+# ------------------------------------------------------------------------------------------
+def test_config1_step_matches_twins_and_oracle():
+    st = synth.config1(seed=0)
+    dev_qkv = st.qkv.cuda()
+    q, k, v = st.views(dev_qkv)
+    meta = st.meta(DEV)
+    kc1, vc1 = st.k_cache.cuda(), st.v_cache.cuda()
+    K.kv_write(k, v, kc1, vc1, meta.slot_mapping)
+    out = K.paged_attention(q, kc1, vc1, meta, 1 / 8)
+    kc2, vc2 = st.k_cache.cuda(), st.v_cache.cuda()
+    R.kv_write(k, v, kc2, vc2, meta.slot_mapping)
+    twin = R.paged_attention(q, kc2, vc2, meta, 1 / 8)
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    qn, kn, vn = (x.numpy() for x in st.views())
+    kcn, vcn = st.k_cache.numpy().copy(), st.v_cache.numpy().copy()
+    OP.kv_write(kn, vn, kcn, vcn, st.slot_mapping.numpy())
+    ref = OP.paged_attention(qn, kcn, vcn, st.query_start_loc.numpy(), st.seq_lens.numpy(),
+                             st.block_tables.numpy(), 1 / 8)
+    assert_attn(out, ref, "config1 vs oracle")
+    assert_attn(out, twin.float().cpu().numpy(), "config1 vs twin")
+
+
+# ------------------------------------------------------------------------------------------
+# W8A16 (tests/kernels/test_kernels.py:157-169)
+# ------------------------------------------------------------------------------------------
+@pytest.mark.parametrize("M", [1, 7, 16, 64, 300, 2048])
+@pytest.mark.parametrize("N,Kd", [(1152, 896), (896, 896), (9728, 896), (896, 4864),
+                                  (2048, 1536), (1536, 1536), (17920, 1536), (1536, 8960)])
+def test_w8a16(M, N, Kd):
+    g = torch.Generator().manual_seed(M * 7 + N)
+    w = torch.randn(N, Kd, generator=g) * 0.05
+    wq, sc = OQ.quantize(w.numpy())
+    x = torch.randn(M, Kd, generator=g).half()
+    y = K.w8a16_linear(x.cuda(), torch.from_numpy(wq).cuda(), torch.from_numpy(sc).cuda(), None)
+    ref = OQ.w8a16(x.numpy(), wq, sc, None, np.float64)
+    yn = y.float().cpu().numpy()
+    assert np.linalg.norm(yn - ref) / np.linalg.norm(ref) < 1e-3
+
+
+@pytest.mark.parametrize("M", synth.W8A16_M)
+@pytest.mark.parametrize("N,Kd", synth.QWEN15_LINEAR_SHAPES)
+def test_w8a16_config4(M, N, Kd):
+    """The benchmark's W8A16 inputs: W uniform int8, fp16 scales in [0.002, 0.02]. Besides the
+    reference's relative-Frobenius bound, the error against the exact product rounded to fp16 is
+    held to 1 fp16 ulp of the output magnitude (the scale-free reading of the 1e-2 / 1e-3
+    absolute bounds for outputs whose RMS is ~35-85)."""
+    x, wq, sc = synth.w8a16_problem(M, N, Kd, seed=1)
+    bias = (torch.randn(N, generator=torch.Generator().manual_seed(2)) * 0.5).half()
+    y = K.w8a16_linear(x.cuda(), wq.cuda(), sc.cuda(), bias.cuda()).float().cpu().numpy()
+    ref = OQ.w8a16(x.numpy(), wq.numpy(), sc.numpy().astype(np.float64), bias.numpy(), np.float64)
+    assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < 1e-3
+    rms = float(np.sqrt((ref ** 2).mean()))
+    ulp = np.spacing(np.abs(ref).astype(np.float16)).astype(np.float64)
+    # 1 ulp, plus fp32 accumulation noise for outputs near zero
+    assert (np.abs(y - ref.astype(np.float16).astype(np.float64)) <= ulp + 1e-4 * rms).all()
+    err = np.abs(y - ref) / rms
+    assert err.max() <= 1e-2 and err.mean() <= 1e-3
+
+
+def test_w8a16_bias_and_linear_routing():
+    from turingserve_amd.quant import LinearWeight
+
+    g = torch.Generator().manual_seed(3)
+    w = torch.randn(2048, 1536, generator=g) * 0.05
+    wq, sc = OQ.quantize(w.numpy())
+    b = (torch.randn(2048, generator=g) * 0.1).half()
+    for M in (3, 560):
+        x = torch.randn(M, 1536, generator=g).half()
+        lw = LinearWeight(torch.from_numpy(wq).cuda(), b.cuda(), torch.from_numpy(sc).cuda())
+        y = K.linear(x.cuda(), lw).float().cpu().numpy()
+        ref = OQ.w8a16(x.numpy(), wq, sc, b.numpy(), np.float64)
+        assert np.linalg.norm(y - ref) / np.linalg.norm(ref) < 1e-3

@@ -1,0 +1,105 @@
+"""The C-ABI library on the CPU: it loads, exports every entry point include/turingserve_hip.h
+declares, and its host-side argument checks and size functions answer without touching a GPU."""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from turingserve_amd import _native as N
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "turingserve_hip.h")
+
+
+def declared_functions() -> list[str]:
+    text = open(HEADER, encoding="utf-8").read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ts_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    names = declared_functions()
+    assert len(names) >= 10
+    lib = N.lib()
+    for name in names:
+        assert hasattr(lib, name), f"{name} declared but not exported"
+        assert name in N.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(N.SIGNATURES) == set(names)
+
+
+def test_version_and_empty_error():
+    assert N.version().startswith("turingserve_hip") and "gfx950" in N.version()
+
+
+def test_invalid_arguments_return_status_and_message():
+    lib = N.lib()
+    st = lib.ts_kv_write(None, None, 0, 0, 0, 0, None, None, 1, None, 4, 2, 64, None)
+    assert st == N.TS_ERR_INVALID_ARG and "null pointer" in N.last_error()
+    st = lib.ts_decode_attention(9, None, 0, 0, None, 0, None, None, 1, None, 1, 1, None, 1, 2, 1,
+                                 64, 1.0, 16, 0, None, 0, None)
+    assert st == N.TS_ERR_INVALID_ARG and "unknown version" in N.last_error()
+    p = ctypes.c_void_p(256)            # never dereferenced: the call fails validation first
+    st = lib.ts_decode_attention(2, p, 96, 96, p, 96, p, p, 4, p, 1, 1, p, 1, 2, 1, 96, 1.0,
+                                 16, 0, None, 0, None)
+    assert st == N.TS_ERR_UNSUPPORTED and "head_dim 96" in N.last_error()
+    st = lib.ts_w8a16_gemm(p, 12, p, p, 0, None, p, 8, 3, 8, 12, None, 0, None)
+    assert st == N.TS_ERR_UNSUPPORTED and "multiple of 8" in N.last_error()
+    with pytest.raises(ValueError, match="multiple of 8"):
+        N.check(st, "w8a16")
+
+
+def test_zero_size_calls_are_no_ops():
+    lib = N.lib()
+    assert lib.ts_kv_write(None, None, 0, 0, 0, 0, None, None, 0, None, 0, 2, 64, None) == N.TS_OK
+    assert lib.ts_decode_attention(0, None, 0, 0, None, 0, None, None, 0, None, 0, 0, None, 0, 12,
+                                   2, 128, 1.0, 0, 0, None, 0, None) == N.TS_OK
+    assert lib.ts_w8a16_gemm(None, 0, None, None, 0, None, None, 0, 0, 16, 16, None, 0,
+                             None) == N.TS_OK
+
+
+def test_workspace_sizes():
+    lib = N.lib()
+    # v3 partials for 64 sequences x 12 heads x 16 splits (4096 / 256) x (128 + 2) fp32
+    n = 64 * 12 * 16
+    want = ((n * 128 * 4 + 255) // 256 * 256) + 2 * ((n * 4 + 255) // 256 * 256)
+    assert lib.ts_decode_workspace_bytes(3, 64, 12, 2, 128, 4096, 256, 256) == want
+    assert lib.ts_decode_workspace_bytes(2, 64, 12, 2, 128, 4096, 0, 256) == 0
+    assert lib.ts_decode_workspace_bytes(1, 64, 12, 2, 128, 4096, 0, 256) == 0
+    # the automatic policy splits 64 x 2 (seq, KV head) units < 2 x 256 CUs at 4096 tokens ...
+    assert lib.ts_decode_workspace_bytes(0, 64, 12, 2, 128, 4096, 256, 256) == want
+    # ... but not short contexts or a batch that fills the device
+    assert lib.ts_decode_workspace_bytes(0, 64, 12, 2, 128, 1024, 256, 256) == 0
+    assert lib.ts_decode_workspace_bytes(0, 256, 12, 2, 128, 4096, 256, 256) == 0
+    # W8A16: the large-M path needs none; small M splits K into fp32 partials
+    assert lib.ts_w8a16_workspace_bytes(2048, 17920, 1536, 256) == 0
+    ws = lib.ts_w8a16_workspace_bytes(1, 1536, 8960, 256)
+    assert ws > 0 and ws % (1536 * 4) == 0
+
+
+def test_python_wrappers_reject_cpu_tensors():
+    from turingserve_amd import hip_ops as K
+
+    kc = torch.zeros(4, 2, 16, 64, dtype=torch.float16)
+    k = torch.zeros(3, 2, 64, dtype=torch.float16)
+    with pytest.raises(ValueError, match="GPU"):
+        K.kv_write(k, k, kc, kc.clone(), torch.zeros(3, dtype=torch.int64))
+
+
+def test_get_ops_namespaces():
+    from turingserve_amd import get_ops
+
+    ref = get_ops("reference")
+    hip = get_ops("hip")
+    assert ref.name == "reference" and hip.name == "hip"
+    assert get_ops("triton").name == "hip"
+    for op in ("kv_write", "paged_attention", "linear", "rmsnorm", "rope_", "silu_mul"):
+        assert callable(getattr(hip, op))
+    assert hip.kv_write.__module__ == "turingserve_amd.hip_ops"
+    assert ref.kv_write.__module__ == "turingserve_amd.reference_ops"
+    with pytest.raises(ValueError):
+        get_ops("cuda")

@@ -1,0 +1,87 @@
+// Shared device and host helpers of the gfx950 hot-path kernels.
+//
+// MFMA operand layouts used throughout (CDNA3/CDNA4 matrix cores, 64-lane wavefront).
+// Lane l is split into c = l % 16 and g = l / 16.
+//   v_mfma_f32_16x16x16_f16  A[16][16] x B[16][16]: lane holds A[c][4g .. 4g+3] and
+//                            B[4g .. 4g+3][c]; result lane holds D[4g + r][c], r = 0..3.
+//   v_mfma_f32_16x16x32_f16  A[16][32] x B[32][16]: lane holds A[c][8g .. 8g+7] and
+//                            B[8g .. 8g+7][c]; result as above.
+// The contraction index k may be permuted freely as long as A and B use the same
+// permutation; the kernels use that freedom so that every operand is a contiguous
+// 8- or 16-byte load of the natural memory layout.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/turingserve_hip.h"
+
+namespace ts {
+
+typedef _Float16 half_t;
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef int int4_t __attribute__((ext_vector_type(4)));
+typedef int int2_t __attribute__((ext_vector_type(2)));
+
+constexpr int kBlockSize = 16;    // tokens per KV block (config.py:74-75)
+constexpr int kWave = 64;         // CDNA wavefront width
+
+__device__ __forceinline__ float4_t mfma16x16x16(half4_t a, half4_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ half4_t lo4(half8_t v) { return {v[0], v[1], v[2], v[3]}; }
+__device__ __forceinline__ half4_t hi4(half8_t v) { return {v[4], v[5], v[6], v[7]}; }
+
+__device__ __forceinline__ half4_t to_half4(float4_t v) {
+  return {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+}
+
+// Base-2 exponential on the hardware transcendental unit (v_exp_f32).
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+
+// Max / sum over the four 16-lane rows of a wavefront (lanes c, c+16, c+32, c+48).
+__device__ __forceinline__ float rows_max(float v) {
+  v = fmaxf(v, shfl_xor(v, 16));
+  return fmaxf(v, shfl_xor(v, 32));
+}
+__device__ __forceinline__ float rows_sum(float v) {
+  v += shfl_xor(v, 16);
+  return v + shfl_xor(v, 32);
+}
+
+__device__ __forceinline__ int clamp_block(int blk, int64_t num_blocks) {
+  return (blk >= 0 && (int64_t)blk < num_blocks) ? blk : 0;
+}
+
+// 16-byte vector load / store through the vector memory path.
+template <typename T>
+__device__ __forceinline__ T ld(const void* p) { return *reinterpret_cast<const T*>(p); }
+template <typename T>
+__device__ __forceinline__ void st(void* p, T v) { *reinterpret_cast<T*>(p) = v; }
+
+}  // namespace ts
+
+// ---------------------------------------------------------------------------------------------
+// Host side: error reporting shared by every entry point (defined in capi.hip).
+// ---------------------------------------------------------------------------------------------
+namespace ts {
+int set_error(int status, const char* fmt, ...);
+int check_launch(const char* what);
+int device_cu_count(int* out);
+inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+}  // namespace ts
+
+#define TS_REQUIRE(cond, status, ...)                 \
+  do {                                                \
+    if (!(cond)) return ::ts::set_error((status), __VA_ARGS__); \
+  } while (0)

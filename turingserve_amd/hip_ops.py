@@ -1,0 +1,245 @@
+"""The ``hip`` op namespace: the reference's op signatures on the gfx950 kernels.
+
+Mirrors ops/triton_ops.py (dispatch, decode-version selection, linear routing),
+ops/triton_kv_write.py:28-35, ops/triton_decode_attention.py:169-200,
+ops/triton_prefill_attention.py:66-79 and ops/triton_w8a16.py:38-51. Every op turns its tensors
+into pointers and strides, allocates outputs and scratch from the torch caching allocator (so the
+calls can be captured into a hipGraph) and launches on torch's current stream. A shape the
+kernels do not support raises ValueError; nothing falls back to another implementation.
+
+Triton tuning knobs the reference's launch helpers accept (block_n, num_warps, num_stages,
+block_m) are accepted and ignored: the HIP kernels fix their own tile shapes.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+from turingserve_amd import _native as N
+from turingserve_amd.quant import LinearWeight
+
+__all__ = ["kv_write", "paged_attention", "linear", "lm_head_int8", "w8a16_linear",
+           "decode_attention_v1", "decode_attention_v2", "decode_attention_v3",
+           "prefill_attention"]
+
+DEFAULT_PARTITION = 256          # v3 tokens per split when the caller names none
+
+
+def _ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _check_gpu(*ts: torch.Tensor) -> None:
+    for t in ts:
+        _require(t.is_cuda, "hip backend: every tensor must live on the GPU")
+
+
+def _check_cache(k_cache: torch.Tensor, v_cache: torch.Tensor) -> tuple[int, int, int]:
+    _require(k_cache.dim() == 4 and k_cache.shape[2] == 16 and k_cache.shape == v_cache.shape,
+             f"caches must be [num_blocks, KVH, 16, D], got {tuple(k_cache.shape)}")
+    _require(k_cache.is_contiguous() and v_cache.is_contiguous(), "caches must be contiguous")
+    _require(k_cache.dtype == torch.float16 and v_cache.dtype == torch.float16,
+             "hip backend: the KV cache must be fp16")
+    NB, KVH, _, D = k_cache.shape
+    return NB, KVH, D
+
+
+def _i32(t: torch.Tensor) -> torch.Tensor:
+    return t if (t.dtype == torch.int32 and t.is_contiguous()) else t.to(torch.int32).contiguous()
+
+
+def _workspace(nbytes: int, device) -> torch.Tensor | None:
+    return None if nbytes == 0 else torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+# ------------------------------------------------------------------------------------------
+# kv_write (ops/triton_kv_write.py:28-35)
+# ------------------------------------------------------------------------------------------
+def kv_write(k: torch.Tensor, v: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+             slot_mapping: torch.Tensor) -> None:
+    """k, v: [T, KVH, D] (strided views of qkv allowed); caches [NB, KVH, 16, D]."""
+    T, KVH, D = k.shape
+    if T == 0:
+        return
+    _check_gpu(k, v, k_cache, v_cache, slot_mapping)
+    NB, ckvh, cd = _check_cache(k_cache, v_cache)
+    _require(v.shape == k.shape and ckvh == KVH and cd == D, "kv_write: shape mismatch")
+    _require(k.dtype == torch.float16 and v.dtype == torch.float16, "kv_write: k, v must be fp16")
+    _require(k.stride(2) == 1 and v.stride(2) == 1, "kv_write: head_dim must be unit-stride")
+    _require(slot_mapping.shape[0] >= T, "kv_write: slot_mapping shorter than k")
+    slots = slot_mapping if (slot_mapping.dtype == torch.int64 and slot_mapping.is_contiguous()) \
+        else slot_mapping.to(torch.int64).contiguous()
+    N.check(N.lib().ts_kv_write(_ptr(k), _ptr(v), k.stride(0), k.stride(1), v.stride(0),
+                                v.stride(1), _ptr(k_cache), _ptr(v_cache), NB, _ptr(slots), T,
+                                KVH, D, _stream(k)), "kv_write")
+
+
+# ------------------------------------------------------------------------------------------
+# decode (ops/triton_ops.py:35-57, ops/triton_decode_attention.py:169-200)
+# ------------------------------------------------------------------------------------------
+def _decode_call(version: int, q, out, k_cache, v_cache, block_tables, seq_lens, scale: float,
+                 S: int, max_seq_len: int, partition: int) -> None:
+    if S == 0:
+        return
+    _check_gpu(q, out, k_cache, v_cache, block_tables, seq_lens)
+    NB, KVH, D = _check_cache(k_cache, v_cache)
+    _, H, qd = q.shape
+    _require(qd == D and q.stride(2) == 1 and q.dtype == torch.float16,
+             "decode: q must be fp16 [T, H, D] with unit stride over D")
+    _require(out.stride(1) == 1 and out.dtype == torch.float16, "decode: out must be fp16 rows")
+    bt = _i32(block_tables)
+    sl = _i32(seq_lens)
+    dev = q.device
+    cus = N.cu_count(dev.index or 0)
+    ws_bytes = N.lib().ts_decode_workspace_bytes(version, S, H, KVH, D, max_seq_len, partition, cus)
+    ws = _workspace(ws_bytes, dev)
+    N.check(N.lib().ts_decode_attention(
+        version, _ptr(q), q.stride(0), q.stride(1), _ptr(out), out.stride(0), _ptr(k_cache),
+        _ptr(v_cache), NB, _ptr(bt), bt.stride(0), bt.shape[1], _ptr(sl), S, H, KVH, D,
+        float(scale), int(max_seq_len), int(partition), _ptr(ws), ws_bytes, _stream(q)),
+        "decode_attention")
+
+
+def decode_attention_v1(q, out, k_cache, v_cache, block_tables, seq_lens, scale, S: int):
+    """One wavefront per (sequence, query head) (ops/triton_decode_attention.py:169-174)."""
+    _decode_call(1, q, out, k_cache, v_cache, block_tables, seq_lens, scale, S, 0, 0)
+
+
+def decode_attention_v2(q, out, k_cache, v_cache, block_tables, seq_lens, scale, S: int,
+                        block_n: int = 32, num_warps: int = 4):
+    """One workgroup per (sequence, KV head) (ops/triton_decode_attention.py:177-184)."""
+    _decode_call(2, q, out, k_cache, v_cache, block_tables, seq_lens, scale, S, 0, 0)
+
+
+def decode_attention_v3(q, out, k_cache, v_cache, block_tables, seq_lens, scale, S: int,
+                        num_splits: int, partition: int = 512, block_n: int = 32,
+                        num_warps: int = 4):
+    """Split-K over `num_splits` partitions of `partition` tokens + merge
+    (ops/triton_decode_attention.py:187-200)."""
+    _decode_call(3, q, out, k_cache, v_cache, block_tables, seq_lens, scale, S,
+                 num_splits * partition, partition)
+
+
+def _decode(q, out, k_cache, v_cache, meta, scale, version: str | None = None):
+    """Decode rows [0, num_decode) of the batch (ops/triton_ops.py:35-57). version None lets the
+    library apply the split rule (split when S * KVH < 2 * CUs and max_seq_len > 1024)."""
+    _require(version in N.DECODE_VERSIONS, f"unknown decode version {version!r}")
+    S = meta.num_decode
+    code = N.DECODE_VERSIONS[version]
+    part = DEFAULT_PARTITION if code in (0, 3) else 0
+    _decode_call(code, q, out, k_cache, v_cache, meta.block_tables, meta.seq_lens, scale, S,
+                 meta.max_seq_len, part)
+
+
+# ------------------------------------------------------------------------------------------
+# prefill (ops/triton_prefill_attention.py:66-79)
+# ------------------------------------------------------------------------------------------
+def prefill_attention(q, out, k_cache, v_cache, meta, scale, block_m: int = 64,
+                      block_n: int = 64, num_warps: int = 4, num_stages: int = 2):
+    """Sequences num_decode .. B-1 of the batch; q [T, H, D] flat, out [T, H*D]."""
+    B = meta.seq_lens.shape[0]
+    if B <= meta.num_decode:
+        return
+    _check_gpu(q, out, k_cache, v_cache)
+    NB, KVH, D = _check_cache(k_cache, v_cache)
+    T, H, qd = q.shape
+    _require(qd == D and q.stride(2) == 1 and q.dtype == torch.float16,
+             "prefill: q must be fp16 [T, H, D] with unit stride over D")
+    bt, sl, qsl = _i32(meta.block_tables), _i32(meta.seq_lens), _i32(meta.query_start_loc)
+    N.check(N.lib().ts_prefill_attention(
+        _ptr(q), q.stride(0), q.stride(1), _ptr(out), out.stride(0), T, _ptr(k_cache),
+        _ptr(v_cache), NB, _ptr(bt), bt.stride(0), bt.shape[1], _ptr(sl), _ptr(qsl), B,
+        meta.num_decode, int(meta.max_query_len), H, KVH, D, float(scale), _stream(q)),
+        "prefill_attention")
+
+
+# ------------------------------------------------------------------------------------------
+# paged_attention (ops/triton_ops.py:60-71)
+# ------------------------------------------------------------------------------------------
+def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, meta,
+                    scale: float, decode_version: str | None = None,
+                    partition: int = DEFAULT_PARTITION) -> torch.Tensor:
+    """q [T, H, D] -> [T, H*D]: decode kernel on rows [0, num_decode), prefill kernel on the
+    remaining sequences, one library call."""
+    T, H, D = q.shape
+    out = torch.empty(T, H * D, dtype=q.dtype, device=q.device)
+    if T == 0:
+        return out
+    _check_gpu(q, k_cache, v_cache)
+    NB, KVH, cd = _check_cache(k_cache, v_cache)
+    _require(cd == D and q.stride(2) == 1 and q.dtype == torch.float16,
+             "paged_attention: q must be fp16 [T, H, D] with unit stride over D")
+    _require(decode_version in N.DECODE_VERSIONS, f"unknown decode version {decode_version!r}")
+    bt, sl, qsl = _i32(meta.block_tables), _i32(meta.seq_lens), _i32(meta.query_start_loc)
+    B = sl.shape[0]
+    S = meta.num_decode
+    code = N.DECODE_VERSIONS[decode_version]
+    ws_bytes = 0
+    if S > 0:
+        cus = N.cu_count(q.device.index or 0)
+        ws_bytes = N.lib().ts_decode_workspace_bytes(code, S, H, KVH, D, meta.max_seq_len,
+                                                     partition, cus)
+    ws = _workspace(ws_bytes, q.device)
+    N.check(N.lib().ts_paged_attention(
+        _ptr(q), q.stride(0), q.stride(1), _ptr(out), out.stride(0), T, _ptr(k_cache),
+        _ptr(v_cache), NB, _ptr(bt), bt.stride(0), bt.shape[1], _ptr(sl), _ptr(qsl), B, S,
+        int(meta.max_query_len), int(meta.max_seq_len), H, KVH, D, float(scale), code,
+        int(partition), _ptr(ws), ws_bytes, _stream(q)), "paged_attention")
+    return out
+
+
+# ------------------------------------------------------------------------------------------
+# W8A16 (ops/triton_w8a16.py:38-51, ops/triton_ops.py:74-91)
+# ------------------------------------------------------------------------------------------
+def w8a16_linear(x: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor,
+                 bias: torch.Tensor | None, cfg=None) -> torch.Tensor:
+    """y = x . (wq * scale)^T + bias, x fp16 [M, K], wq int8 [N, K], scale fp32 or fp16 [N]."""
+    x = x.contiguous()
+    M, K = x.shape
+    Nn, Kw = wq.shape
+    _require(Kw == K, f"w8a16: x has K={K}, weight has K={Kw}")
+    _require(x.dtype == torch.float16, "w8a16: activations must be fp16")
+    _require(wq.dtype == torch.int8 and wq.is_contiguous(), "w8a16: weight must be int8 row-major")
+    _require(scale.dtype in (torch.float32, torch.float16) and scale.numel() == Nn,
+             "w8a16: scale must be fp32 or fp16 [N]")
+    y = torch.empty(M, Nn, dtype=x.dtype, device=x.device)
+    if M == 0:
+        return y
+    _check_gpu(x, wq, scale)
+    sc = scale.contiguous()
+    b = None
+    if bias is not None:
+        _require(bias.numel() == Nn, "w8a16: bias must be [N]")
+        b = bias.to(torch.float16).contiguous()
+    cus = N.cu_count(x.device.index or 0)
+    ws_bytes = N.lib().ts_w8a16_workspace_bytes(M, Nn, K, cus)
+    ws = _workspace(ws_bytes, x.device)
+    N.check(N.lib().ts_w8a16_gemm(_ptr(x), x.stride(0), _ptr(wq), _ptr(sc),
+                                  1 if sc.dtype == torch.float16 else 0, _ptr(b), _ptr(y),
+                                  y.stride(0), M, Nn, K, _ptr(ws), ws_bytes, _stream(x)),
+            "w8a16_gemm")
+    return y
+
+
+def linear(x: torch.Tensor, lw: LinearWeight) -> torch.Tensor:
+    """fp16 weights stay on the vendor BLAS (F.linear, as ops/triton_ops.py:75-76 keeps cuBLAS);
+    int8 weights take the W8A16 kernel at every M (the library picks its small-M streaming or
+    MFMA tile path), replacing the reference's dequantise + cuBLAS route for M > 256."""
+    if not lw.quantized:
+        return F.linear(x, lw.w, lw.b)
+    return w8a16_linear(x, lw.w, lw.scale, lw.b)
+
+
+def lm_head_int8(h: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """int8 tied lm head (ops/triton_ops.py:88-91)."""
+    return w8a16_linear(h, wq, scale, None)

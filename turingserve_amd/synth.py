@@ -1,0 +1,157 @@
+"""Seeded synthetic ragged batches for the hot-path configurations.
+
+All data is drawn on the host with ``torch.Generator().manual_seed(seed)`` so the CPU twins and the
+GPU kernels see identical bytes. Conventions of the reference's engine are kept: block 0 is the
+null block and is never handed out (kv/block_allocator.py:3-4,21), block tables are a random
+permutation of the free blocks, decodes come first in the flat batch
+(scheduler/scheduler.py:126-130) and each step writes the new K/V rows before attending
+(model/qwen2.py:87-90). The new q/k/v rows are views of one fused qkv activation
+[T, (H + 2 KVH) D], the layout the model hands to kv_write and paged_attention
+(model/qwen2.py:24-33).
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import torch
+
+from turingserve_amd.metadata import AttentionMetadata
+
+BLOCK = 16
+
+
+@dataclass
+class PagedStep:
+    """One layer's step: qkv rows of the flat batch, the paged caches and the metadata."""
+
+    H: int
+    KVH: int
+    D: int
+    qkv: torch.Tensor            # [T, (H + 2 KVH) D] fp16
+    k_cache: torch.Tensor        # [NB, KVH, 16, D] fp16 (state before kv_write)
+    v_cache: torch.Tensor
+    query_start_loc: torch.Tensor
+    seq_lens: torch.Tensor
+    block_tables: torch.Tensor
+    slot_mapping: torch.Tensor
+    num_decode: int
+    max_query_len: int
+    max_seq_len: int
+
+    @property
+    def T(self) -> int:
+        return self.qkv.shape[0]
+
+    def views(self, qkv: torch.Tensor | None = None):
+        """q [T, H, D], k [T, KVH, D], v [T, KVH, D] as strided views of qkv."""
+        x = self.qkv if qkv is None else qkv
+        T, H, KVH, D = x.shape[0], self.H, self.KVH, self.D
+        q = x[:, : H * D].view(T, H, D)
+        k = x[:, H * D:(H + KVH) * D].view(T, KVH, D)
+        v = x[:, (H + KVH) * D:].view(T, KVH, D)
+        return q, k, v
+
+    def meta(self, device) -> AttentionMetadata:
+        return AttentionMetadata(
+            query_start_loc=self.query_start_loc.to(device), seq_lens=self.seq_lens.to(device),
+            block_tables=self.block_tables.to(device), slot_mapping=self.slot_mapping.to(device),
+            num_decode=self.num_decode, max_query_len=self.max_query_len,
+            max_seq_len=self.max_seq_len)
+
+    def kv_bytes_read(self) -> int:
+        """K and V bytes one attention pass must read: sum of seq_lens x KVH x D x 2 x 2."""
+        return int(self.seq_lens.sum()) * self.KVH * self.D * 2 * 2
+
+
+def make_step(H: int, KVH: int, D: int, num_blocks: int, items: list[tuple[int, int]],
+              seed: int = 0, std: float = 0.5, gen: torch.Generator | None = None) -> PagedStep:
+    """items: (cached_tokens, new_tokens) per sequence, decodes (new_tokens == 1) first.
+    The whole cache is filled with std * N(0, 1); the new rows are written by kv_write."""
+    g = gen or torch.Generator().manual_seed(seed)
+    need = [-(-(c + n) // BLOCK) for c, n in items]
+    if sum(need) > num_blocks - 1:
+        raise ValueError(f"{sum(need)} blocks needed, cache has {num_blocks - 1} free")
+    perm = (torch.randperm(num_blocks - 1, generator=g) + 1).to(torch.int32)
+    width = max(1, max(need))
+    bt = torch.zeros(len(items), width, dtype=torch.int32)
+    off = 0
+    slots, qsl, sl = [], [0], []
+    for b, ((c, n), nb) in enumerate(zip(items, need)):
+        table = perm[off:off + nb]
+        bt[b, :nb] = table
+        off += nb
+        pos = torch.arange(c, c + n, dtype=torch.int64)
+        slots.append(table.long()[pos // BLOCK] * BLOCK + pos % BLOCK)
+        qsl.append(qsl[-1] + n)
+        sl.append(c + n)
+    T = qsl[-1]
+    kc = (torch.randn(num_blocks, KVH, BLOCK, D, generator=g) * std).half()
+    vc = (torch.randn(num_blocks, KVH, BLOCK, D, generator=g) * std).half()
+    qkv = (torch.randn(T, (H + 2 * KVH) * D, generator=g) * std).half()
+    num_decode = 0
+    for c, n in items:
+        if n == 1:
+            num_decode += 1
+        else:
+            break
+    return PagedStep(H, KVH, D, qkv, kc, vc, torch.tensor(qsl, dtype=torch.int32),
+                     torch.tensor(sl, dtype=torch.int32), bt, torch.cat(slots),
+                     num_decode, max(n for _, n in items), max(sl))
+
+
+def config1(seed: int = 0) -> PagedStep:
+    """Ragged CPU-twin step: 14/2 heads, D 64, 512 blocks; 8 decodes with contexts U[16, 512]
+    plus one 256-token prefill chunk on a 128-token cached prefix."""
+    g = torch.Generator().manual_seed(seed)
+    ctx = torch.randint(16, 513, (8,), generator=g).tolist()
+    items = [(c - 1, 1) for c in ctx] + [(128, 256)]
+    return make_step(14, 2, 64, 512, items, gen=g)
+
+
+def log_uniform_ints(n: int, lo: int, hi: int, g: torch.Generator) -> list[int]:
+    u = torch.rand(n, generator=g, dtype=torch.float64)
+    return [int(round(math.exp(math.log(lo) + float(x) * (math.log(hi) - math.log(lo))))) for x in u]
+
+
+def config2(seed: int = 0, num_seqs: int = 64, num_blocks: int = 16384) -> PagedStep:
+    """Pure decode at the Qwen2.5-1.5B attention shape: 12/2 heads, D 128, 16384 blocks, 64
+    sequences with contexts log-uniform in [128, 4096], one new token each."""
+    g = torch.Generator().manual_seed(seed)
+    ctx = log_uniform_ints(num_seqs, 128, 4096, g)
+    return make_step(12, 2, 128, num_blocks, [(c - 1, 1) for c in ctx], gen=g)
+
+
+def config3_chunks(prompt: int = 8000, chunk: int = 2048) -> list[tuple[int, int]]:
+    """(prefix, q_len) of the cold chunked prefill: 2048 x 3 + 1856 for an 8000-token prompt."""
+    out, p = [], 0
+    while p < prompt:
+        n = min(chunk, prompt - p)
+        out.append((p, n))
+        p += n
+    return out
+
+
+def config3(chunk_index: int, seed: int = 0, prompt: int = 8000, chunk: int = 2048) -> PagedStep:
+    """One chunk of the cold 8000-token prefill at the 1.5B attention shape (12/2, D 128):
+    the chunk's K/V are written, then it attends causally over all cached blocks so far.
+    (The cache outside this prompt's prefix is random, standing in for earlier chunks.)"""
+    prefix, n = config3_chunks(prompt, chunk)[chunk_index]
+    nb = -(-prompt // BLOCK) + 1
+    return make_step(12, 2, 128, nb + 16, [(prefix, n)], seed=seed)
+
+
+QWEN15_LINEAR_SHAPES = [(2048, 1536), (1536, 1536), (17920, 1536), (1536, 8960)]
+W8A16_M = [1, 16, 64, 256, 2048]
+
+
+def w8a16_problem(M: int, N: int, K: int, seed: int = 0, scale_fp16: bool = True):
+    """X fp16 ~ N(0, 1) [M, K]; W int8 ~ U{-127..127} [N, K]; per-channel scales U[0.002, 0.02]
+    (fp16 by default), symmetric, no bias."""
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g).half()
+    wq = torch.randint(-127, 128, (N, K), generator=g, dtype=torch.int32).to(torch.int8)
+    scale = torch.rand(N, generator=g) * 0.018 + 0.002
+    scale = scale.half() if scale_fp16 else scale.float()
+    return x, wq, scale
