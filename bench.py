@@ -1,0 +1,329 @@
+"""Benchmark of the per-step hot path on one MI355X.
+
+    python bench.py [--gpus 1] [--steps 400] [--warmup 40]
+
+Headline workload (the configuration the metric is quoted on): pure-decode paged attention at the
+Qwen2.5-1.5B attention shape -- 12 query / 2 KV heads, head_dim 128, block 16, 64 sequences with
+contexts log-uniform in [128, 4096], 16384 cache blocks, fp16. One *step* is one layer's work:
+kv_write of the 64 new K/V rows, then decode attention over every cached token. Steps rotate over
+8 layer caches (2 GiB in total, far above the 256 MB Infinity Cache) so each step reads its KV
+from HBM, and every step is a hipGraph replay (pure-decode steps are graph-captured, as the
+reference's CudaGraphRunner does). Inputs are resident in HBM before timing starts.
+
+value = algorithmic bytes of one step / wall time of one step, in GB/s. The roofline entry prices
+the decode-attention graph alone (timed with HIP events on the stream it runs on) against the
+8 TB/s HBM peak. The CPU baseline is the oracle's numpy restatement of the same step
+(ops/reference.py semantics) on the host cores. Secondary results for the other configurations go
+under "extra".
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import re
+import statistics
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+MFMA_FP16_PEAK_TFLOPS = 2500.0
+ROOT = os.path.dirname(os.path.abspath(__file__))
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--layers", type=int, default=8, help="layer caches rotated over")
+    ap.add_argument("--partition", type=int, default=0, help="v3 split size (0 = library policy)")
+    ap.add_argument("--decode-version", default="auto", choices=["auto", "v1", "v2", "v3"])
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-extra", action="store_true", help="headline workload only")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+# ------------------------------------------------------------------------------------------
+# algorithmic work
+# ------------------------------------------------------------------------------------------
+def decode_step_bytes(st) -> dict:
+    """Bytes one decode step must move: every cached K/V row once, q in, out written, the new
+    K/V rows read and written by kv_write, block-table entries, seq_lens and slots."""
+    S, H, KVH, D = st.num_decode, st.H, st.KVH, st.D
+    seq = st.seq_lens.tolist()
+    kv = sum(seq) * KVH * D * 2 * 2
+    q_out = 2 * S * H * D * 2
+    tables = sum(-(-L // 16) for L in seq) * 4 + S * 4
+    kvw = 2 * (S * KVH * D * 2 * 2) + S * 8
+    return {"attention": kv + q_out + tables, "kv_write": kvw, "step": kv + q_out + tables + kvw}
+
+
+def prefill_flops(H: int, D: int, prefix: int, q_len: int) -> float:
+    """Causal-exact FLOPs: 4 H D per visible (query, key) pair, row i sees prefix + i + 1 keys."""
+    pairs = q_len * prefix + q_len * (q_len + 1) // 2
+    return 4.0 * H * D * pairs
+
+
+def traffic_from_profiles(name: str):
+    """HBM bytes per launch measured with rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, scaled by the
+    copy-kernel calibration), committed under profiles/; None when not measured."""
+    path = os.path.join(ROOT, "profiles", f"{name}.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(path, encoding="utf-8").read())
+    return float(m.group(1)) if m else None
+
+
+# ------------------------------------------------------------------------------------------
+# headline: config 2
+# ------------------------------------------------------------------------------------------
+def bench_decode(args, torch, K, synth):
+    dev = torch.device("cuda", 0)
+    st = synth.config2(seed=0)
+    L = args.layers
+    NB, KVH, D, H = st.k_cache.shape[0], st.KVH, st.D, st.H
+    kv = torch.empty(L, 2, NB, KVH, 16, D, dtype=torch.float16, device=dev)
+    kc0, vc0 = st.k_cache.to(dev), st.v_cache.to(dev)
+    for l in range(L):
+        kv[l, 0].copy_(kc0)
+        kv[l, 1].copy_(vc0)
+    del kc0, vc0
+    qkv = st.qkv.to(dev)
+    q, k, v = st.views(qkv)
+    meta = st.meta(dev)
+    meta.in_graph = True
+    scale = D ** -0.5
+    version = None if args.decode_version == "auto" else args.decode_version
+    outs = [None] * L
+
+    def kv_step(l):
+        K.kv_write(k, v, kv[l, 0], kv[l, 1], meta.slot_mapping)
+
+    def attn_step(l):
+        outs[l] = K.paged_attention(q, kv[l, 0], kv[l, 1], meta, scale, decode_version=version,
+                                    partition=args.partition or K.DEFAULT_PARTITION)
+
+    for l in range(L):                      # eager warm-up (library, workspace, allocator)
+        kv_step(l)
+        attn_step(l)
+    torch.cuda.synchronize()
+    # One replay = L steps (every layer's kv_write + attention), the way a model's layer stack
+    # sits in one graph; a second graph holds the L attention calls alone for the kernel timing.
+    pool = torch.cuda.graph_pool_handle()
+    g_step = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_step, pool=pool):
+        for l in range(L):
+            kv_step(l)
+            attn_step(l)
+    step_outs = list(outs)
+    g_attn = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_attn, pool=pool):
+        for l in range(L):
+            attn_step(l)
+    torch.cuda.synchronize()
+    for _ in range(max(1, args.warmup // L)):
+        g_step.replay()
+    replays = max(1, -(-args.steps // L))
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(replays)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(replays):
+        ev[i][0].record()
+        g_step.replay()
+        ev[i][1].record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    step_ev_ms = statistics.fmean(a.elapsed_time(b) for a, b in ev) / L
+    a_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+            for _ in range(replays)]
+    for i in range(replays):
+        a_ev[i][0].record()
+        g_attn.replay()
+        a_ev[i][1].record()
+    torch.cuda.synchronize()
+    attn_ms = [a.elapsed_time(b) / L for a, b in a_ev]
+    # graph == eager: the last layer's output of the step graph against an eager call
+    ref_out = K.paged_attention(q, kv[L - 1, 0], kv[L - 1, 1], meta, scale,
+                                decode_version=version,
+                                partition=args.partition or K.DEFAULT_PARTITION)
+    same = bool(torch.equal(ref_out, step_outs[L - 1]))
+    steps_timed = replays * L
+    b = decode_step_bytes(st)
+    step_s = (t1 - t0) / steps_timed
+    res = {
+        "step_s": step_s, "steps": steps_timed, "bytes": b, "step_ev_ms": step_ev_ms,
+        "attn_ms_mean": statistics.fmean(attn_ms), "attn_ms_median": statistics.median(attn_ms),
+        "graph_equals_eager": same, "mean_ctx": float(st.seq_lens.float().mean()),
+    }
+    del kv, g_step, g_attn
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return st, res
+
+
+def cpu_baseline(st, seconds: float):
+    """The oracle (numpy restatement of the reference twins) on the host: kv_write + paged
+    attention of the same step, repeated for about `seconds`."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+
+    from oracle import paged as OP
+
+    cores = max(1, min(16, os.cpu_count() or 1))
+    q, k, v = (x.numpy() for x in st.views())
+    kc, vc = st.k_cache.numpy().copy(), st.v_cache.numpy().copy()
+    qsl, sl, bt, sm = (st.query_start_loc.numpy(), st.seq_lens.numpy(), st.block_tables.numpy(),
+                       st.slot_mapping.numpy())
+    times = []
+    with threadpool_limits(limits=cores):
+        t_end = time.perf_counter() + seconds
+        while True:
+            t0 = time.perf_counter()
+            OP.kv_write(k, v, kc, vc, sm)
+            out = OP.paged_attention(q, kc, vc, qsl, sl, bt, st.D ** -0.5, np.float32)
+            out.astype(np.float16)
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() >= t_end:
+                break
+    return statistics.median(times), cores, len(times)
+
+
+# ------------------------------------------------------------------------------------------
+# secondary configurations
+# ------------------------------------------------------------------------------------------
+def time_graph(torch, fn, reps: int, inner: int = 1):
+    """Capture `inner` back-to-back calls in one hipGraph, replay `reps` times, return the mean
+    per-call milliseconds from HIP events."""
+    fn()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(inner):
+            fn()
+    for _ in range(3):
+        g.replay()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    s.record()
+    for _ in range(reps):
+        g.replay()
+    e.record()
+    torch.cuda.synchronize()
+    return s.elapsed_time(e) / (reps * inner)
+
+
+def bench_prefill(torch, K, synth):
+    dev = torch.device("cuda", 0)
+    rows = []
+    tot_flop, tot_ms = 0.0, 0.0
+    for ci, (prefix, n) in enumerate(synth.config3_chunks()):
+        st = synth.config3(ci, seed=0)
+        kc, vc = st.k_cache.to(dev), st.v_cache.to(dev)
+        qkv = st.qkv.to(dev)
+        q, k, v = st.views(qkv)
+        meta = st.meta(dev)
+        K.kv_write(k, v, kc, vc, meta.slot_mapping)
+        ms = time_graph(torch, lambda: K.paged_attention(q, kc, vc, meta, st.D ** -0.5), reps=10)
+        fl = prefill_flops(st.H, st.D, prefix, n)
+        rows.append({"prefix": prefix, "q_len": n, "ms": round(ms, 4),
+                     "tflops": round(fl / ms / 1e9, 2)})
+        tot_flop += fl
+        tot_ms += ms
+    tf = tot_flop / tot_ms / 1e9
+    return {"chunks": rows, "total_ms": round(tot_ms, 3), "gflop": round(tot_flop / 1e9, 2),
+            "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4)}
+
+
+def bench_w8a16(torch, K, synth):
+    dev = torch.device("cuda", 0)
+    rows = []
+    for (Nn, Kd) in synth.QWEN15_LINEAR_SHAPES:
+        x_all, wq, sc = synth.w8a16_problem(max(synth.W8A16_M), Nn, Kd, seed=0)
+        wq, sc = wq.to(dev), sc.to(dev)
+        for M in synth.W8A16_M:
+            x = x_all[:M].to(dev)
+            inner = 20 if M <= 64 else 5
+            ms = time_graph(torch, lambda: K.w8a16_linear(x, wq, sc, None), reps=10, inner=inner)
+            byts = Nn * Kd + 2 * Nn + 2 * M * Kd + 2 * M * Nn
+            flop = 2.0 * M * Nn * Kd
+            t_hbm = byts / (HBM_PEAK_GBS * 1e9)
+            t_mfma = flop / (MFMA_FP16_PEAK_TFLOPS * 1e12)
+            rows.append({"M": M, "N": Nn, "K": Kd, "us": round(ms * 1e3, 2),
+                         "GBps": round(byts / ms / 1e6, 1), "TFLOPs": round(flop / ms / 1e9, 2),
+                         "bound": "hbm" if t_hbm >= t_mfma else "mfma",
+                         "roofline_frac": round(max(t_hbm, t_mfma) / (ms / 1e3), 4)})
+    return rows
+
+
+def main() -> int:
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the hot path has no multi-GPU form; see the sharding notes)", file=sys.stderr)
+        return 2
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        return 2
+    sys.path.insert(0, ROOT)
+    from turingserve_amd import _native, hip_ops as K, synth
+
+    _native.lib()
+    log(f"device: {torch.cuda.get_device_name(0)}  library: {_native.version()}")
+    log("headline: config 2 decode step (kv_write + paged decode attention)")
+    st, r = bench_decode(args, torch, K, synth)
+    b = r["bytes"]
+    value = b["step"] / r["step_s"] / 1e9
+    attn_s = r["attn_ms_mean"] / 1e3
+    achieved = b["attention"] / attn_s / 1e9
+    log(f"step {r['step_s'] * 1e6:.2f} us (events {r['step_ev_ms'] * 1e3:.2f} us)  attention "
+        f"{r['attn_ms_mean'] * 1e3:.2f} us ({achieved:.0f} GB/s)  graph==eager {r['graph_equals_eager']}")
+    traffic = traffic_from_profiles("decode_c2_traffic")
+    out = {
+        "metric": "paged-attn HBM GB/s (% of peak) + mixed-step tokens/s @ Qwen2.5-1.5B shape",
+        "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": r["steps"],
+        "warmup": args.warmup, "ms_per_step": round(r["step_s"] * 1e3, 5),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1)*0.5 KV cache, log-uniform contexts, shuffled blocks)",
+        "config": {"workload": "config2: pure-decode paged attention + kv_write, Qwen2.5-1.5B "
+                               "attention shape (H 12, KVH 2, D 128, block 16)",
+                   "num_seqs": st.num_decode, "mean_context": round(r["mean_ctx"], 1),
+                   "max_context": st.max_seq_len, "num_blocks": st.k_cache.shape[0],
+                   "layers_rotated": args.layers, "hipgraph": True,
+                   "bytes_per_step": b["step"], "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "decode attention (paged_attention, decode rows)",
+                     "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "algorithmic_bytes": b["attention"],
+                     "avg_duration_us": round(r["attn_ms_mean"] * 1e3, 3)},
+        "graph_equals_eager": r["graph_equals_eager"],
+    }
+    if not args.no_cpu:
+        log(f"cpu baseline: oracle step on the host for ~{args.cpu_seconds:.0f} s")
+        t_cpu, cores, n = cpu_baseline(st, args.cpu_seconds)
+        out["cpu_baseline"] = {"value": round(b["step"] / t_cpu / 1e9, 3), "unit": "GB/s",
+                               "cores": cores, "kind": "port",
+                               "sample": f"config2 full step (64 sequences), numpy oracle, "
+                                         f"median of {n} runs, {t_cpu * 1e3:.1f} ms/step"}
+    if not args.no_extra:
+        log("extra: config 3 chunked prefill")
+        extra = {"prefill_config3": bench_prefill(torch, K, synth)}
+        log("extra: config 4 W8A16")
+        extra["w8a16_config4"] = bench_w8a16(torch, K, synth)
+        out["extra"] = extra
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

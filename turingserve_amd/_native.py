@@ -14,7 +14,9 @@ import os
 
 import torch  # noqa: F401  (loads the HIP runtime before the library)
 
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "lib", "libturingserve_hip.so")
+# TS_HIP_LIB selects another build of the same library (e.g. to compare kernel variants).
+LIB_PATH = os.environ.get("TS_HIP_LIB") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), "lib", "libturingserve_hip.so")
 
 TS_OK = 0
 TS_ERR_INVALID_ARG = -1

@@ -6,20 +6,21 @@
 //  v2  one workgroup per (sequence, KV head, group of <= 16 query heads): the whole GQA group
 //      shares each 16-token K/V block, which is read from HBM exactly once per KV head.
 //  v3  v2 split over context partitions of `partition` tokens ("flash-decoding"): partials
-//      (m, l, acc) in fp32 go to the workspace and a second kernel merges them.
+//      (m, l, acc) in fp32 go to the workspace and a merge kernel combines them (sequences
+//      that fit one split are finished by the first kernel).
 //
-// Inner loop of v2/v3 (one wavefront, one 16-token block; lane l = 16 g + c):
+// Inner loop of v2/v3 (one wavefront, a pair of 16-token blocks; lane l = 16 g + c):
 //   S^T[16 tok][16 heads] = K[16 tok][D] . Q^T[D][16 heads]       v_mfma_f32_16x16x32_f16
 //   K lane (c, g) loads K[tok c][32kk + 8g .. +7]: 16-byte loads, 64 contiguous bytes per token
 //   per instruction; Q^T uses the same dim permutation, so no shuffles are needed.
 //   The result leaves lane (c, g) holding tokens 4g..4g+3 of head c: every per-head softmax
 //   statistic (running max m, sum l, rescale alpha) lives in lane column c.
-//   V is transposed in registers by one v_mfma_f32_16x16x16_f16 against the identity (exact:
-//   one non-zero product per output), which turns V[tok][dim] rows into the token-packed A
-//   operand of O^T[D][16 heads] += V^T . P^T (v_mfma_f32_16x16x16_f16, P rounded to fp16
-//   exactly like ops/triton_decode_attention.py:91).
-//   Afterwards lane (c, g) owns dims 32kk + 8g .. +7 of head c: 16-byte stores.
-// The waves of a workgroup take interleaved blocks and merge their (m, l, acc) in LDS.
+//   V rows are loaded coalesced (lane (c, g): tokens 4g..4g+3, dims 8c..8c+7 at D = 128) and
+//   tile t of O^T takes dims {8i + t}, so each lane's token-packed operand is two byte
+//   permutes of what it loaded: O^T[D][16 heads] += V^T . P^T runs on v_mfma_f32_16x16x32_f16
+//   over both blocks of the pair with no transpose; P is rounded to fp16 first, exactly like
+//   ops/triton_decode_attention.py:91. Afterwards lane (c, g) owns dims 32g .. 32g+31 of head c.
+// The waves of a workgroup take consecutive blocks and merge their (m, l, acc) in LDS.
 #include <math.h>
 
 #include "common.h"
@@ -98,18 +99,21 @@ __global__ void __launch_bounds__(64) decode_v1_kernel(
 }
 
 // ------------------------------------------------------------------------------------------
-// v2 / v3 partial kernel (ops/triton_decode_attention.py:60-141)
+// v2 / v3 (ops/triton_decode_attention.py:60-163)
 // ------------------------------------------------------------------------------------------
 template <int D>
 struct DecodeRegs {
-  // D >= 32: KK 16-byte pieces per lane; D == 16: one 8-byte piece.
+  // D >= 32: KK 16-byte pieces of K per lane; D == 16: one 8-byte piece.
   static constexpr int KK = D >= 32 ? D / 32 : 1;
-  static constexpr int TILES = D / 16;           // 16-dim output tiles of O^T
+  // V: each lane holds VW consecutive dims of 4 tokens; O^T is split into VW tiles of 16 dims.
+  static constexpr int VW = D / 16;
+  static constexpr int TILES = VW;
 };
 
+// K rows in their natural layout: lane (c, g) gets K[tok c][32kk + 8g .. +7] (16-byte loads).
 template <int D>
-__device__ __forceinline__ void load_kv_block(const half_t* __restrict__ base, int c, int g,
-                                              half8_t (&x)[DecodeRegs<D>::KK]) {
+__device__ __forceinline__ void load_k_block(const half_t* __restrict__ base, int c, int g,
+                                             half8_t (&x)[DecodeRegs<D>::KK]) {
   if constexpr (D >= 32) {
 #pragma unroll
     for (int kk = 0; kk < DecodeRegs<D>::KK; ++kk) x[kk] = ld<half8_t>(base + c * D + 32 * kk + 8 * g);
@@ -119,49 +123,86 @@ __device__ __forceinline__ void load_kv_block(const half_t* __restrict__ base, i
   }
 }
 
-template <int D, int NW>
+// V rows in their natural layout: lane (c, g) loads V[tok 4g + r][VW c .. VW c + VW-1] for
+// r = 0..3 (16 lanes cover one whole token row, so every load is fully coalesced). Tile q of
+// O^T then uses dims {VW i + q : i = 0..15}: its token-packed A operand for lane (c, g) is
+// {x[0][q], x[1][q], x[2][q], x[3][q]}, two byte permutes and no transpose product.
+template <int D>
+__device__ __forceinline__ void load_v_rows(const half_t* __restrict__ base, int c, int g,
+                                            half_t (&x)[4][DecodeRegs<D>::VW]) {
+  constexpr int VW = DecodeRegs<D>::VW;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const half_t* p = base + (4 * g + r) * D + VW * c;
+    if constexpr (VW % 8 == 0) {
+#pragma unroll
+      for (int u = 0; u < VW / 8; ++u) {
+        const half8_t v = ld<half8_t>(p + 8 * u);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[r][8 * u + e] = v[e];
+      }
+    } else if constexpr (VW == 4) {
+      const half4_t v = ld<half4_t>(p);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) x[r][e] = v[e];
+    } else if constexpr (VW == 2) {
+      const half2_t v = ld<half2_t>(p);
+      x[r][0] = v[0];
+      x[r][1] = v[1];
+    } else {
+      x[r][0] = p[0];
+    }
+  }
+}
+
+// Tokens 4g .. 4g+3 of a V^T operand at or past seq_len are zeroed: a reused block may hold
+// anything there, and 0 * NaN would reach the output.
+__device__ __forceinline__ half4_t mask_tokens(half4_t v, int tok0, int seq_len) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) v[r] = (tok0 + r < seq_len) ? v[r] : (half_t)0.f;
+  return v;
+}
+
+// One workgroup = NW wavefronts = one (sequence, split, KV head, head group). A wavefront owns
+// BPW consecutive 16-token blocks per round and issues all their loads before computing; the
+// block-table entries, seq_len and q are requested together at the start. Blocks are consumed
+// in pairs: two independent S^T chains, one online-softmax update per 32 tokens, and the P.V
+// product as v_mfma_f32_16x16x32_f16 over the 32 tokens of the pair. A sequence with one active
+// split writes its output here; otherwise the split's (m, l, acc) go to the workspace for
+// decode_merge_kernel.
+template <int D, int NW, int BPW>
 __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
     const half_t* __restrict__ q, int64_t q_st, int64_t q_sh, half_t* __restrict__ out,
     int64_t o_st, const half_t* __restrict__ kc, const half_t* __restrict__ vc, int64_t NB,
     const int* __restrict__ bt, int64_t bt_st, int max_blocks, const int* __restrict__ seq_lens,
     int H, int KVH, int G, int HG, float scale_log2, int part_blocks, int num_splits,
     float* __restrict__ ws_acc, float* __restrict__ ws_m, float* __restrict__ ws_l) {
+  static_assert(BPW % 2 == 0, "blocks are consumed in pairs");
   constexpr int KK = DecodeRegs<D>::KK;
+  constexpr int VW = DecodeRegs<D>::VW;
   constexpr int TILES = DecodeRegs<D>::TILES;
   constexpr int OROW = D + 4;                    // padded LDS row (floats) against bank conflicts
   __shared__ float s_o[NW][16][OROW];
   __shared__ float s_m[NW][16];
   __shared__ float s_l[NW][16];
 
-  const int split = blockIdx.x, s = blockIdx.y;
+  const int s = blockIdx.x, split = blockIdx.y;
   const int kvh = blockIdx.z / HG, hg = blockIdx.z % HG;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int c = lane & 15, g = lane >> 4;
   const int hq = hg * 16 + c;                    // query head within the GQA group
   const bool head_ok = hq < G;
   const int nh = (G - hg * 16) < 16 ? (G - hg * 16) : 16;   // real heads in this group
-
-  int seq_len = seq_lens[s];
-  seq_len = seq_len < 0 ? 0 : (seq_len > max_blocks * kBlockSize ? max_blocks * kBlockSize : seq_len);
-  const int nblk = (seq_len + kBlockSize - 1) / kBlockSize;
-  // A seq_len beyond the caller's max_seq_len is truncated to the launched splits, as the fixed
-  // split grid of ops/triton_ops.py:50-51 does; it never indexes past the workspace.
-  int n_active = (nblk + part_blocks - 1) / part_blocks;
-  n_active = n_active < num_splits ? n_active : num_splits;
-  if (seq_len == 0) {                            // padding row: zeros (ops/reference.py:99,104-105)
-    if (split == 0) {
-      for (int e = tid; e < nh * D; e += NW * 64) {
-        const int hh = e / D, d = e % D;
-        out[(int64_t)s * o_st + (int64_t)(kvh * G + hg * 16 + hh) * D + d] = (half_t)0.f;
-      }
-    }
-    return;
-  }
+  const int head0 = kvh * G + hg * 16;           // first query head of this group
   const int blk_lo = split * part_blocks;
-  if (blk_lo >= nblk) return;                    // idle split of a short sequence
-  const int blk_hi = (blk_lo + part_blocks) < nblk ? (blk_lo + part_blocks) : nblk;
+  const int* btrow = bt + (int64_t)s * bt_st;
 
-  // Q^T operand: lane (c, g) holds Q[head c][32kk + 8g .. +7] (zeros for padding heads).
+  // Requests that do not depend on seq_len go out first, together.
+  int seq_len = seq_lens[s];
+  int r0 = blk_lo + w * BPW;
+  int btv[BPW];
+#pragma unroll
+  for (int j = 0; j < BPW; ++j) btv[j] = btrow[(r0 + j) < max_blocks ? (r0 + j) : (max_blocks - 1)];
   half8_t qf[KK];
   {
     const half_t* qp = q + (int64_t)s * q_st + (int64_t)(kvh * G + hq) * q_sh;
@@ -175,100 +216,130 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
       }
     }
   }
-  // Identity B operand for the register transpose: B[4g + r][c] = (4g + r == c).
-  const half4_t ident = {(half_t)(4 * g + 0 == c ? 1.f : 0.f), (half_t)(4 * g + 1 == c ? 1.f : 0.f),
-                         (half_t)(4 * g + 2 == c ? 1.f : 0.f), (half_t)(4 * g + 3 == c ? 1.f : 0.f)};
 
+  seq_len = seq_len < 0 ? 0 : (seq_len > max_blocks * kBlockSize ? max_blocks * kBlockSize : seq_len);
+  const int nblk = (seq_len + kBlockSize - 1) / kBlockSize;
+  // A seq_len beyond the caller's max_seq_len is truncated to the launched splits, as the fixed
+  // split grid of ops/triton_ops.py:50-51 does; it never indexes past the workspace.
+  int n_active = (nblk + part_blocks - 1) / part_blocks;
+  n_active = n_active < num_splits ? n_active : num_splits;
+  // With split partials, every split slot that carries no partial (idle split, a sequence that
+  // fits one split, seq_len 0) is marked m = -inf so the merge needs no seq_len.
+  const bool idle = seq_len == 0 || blk_lo >= nblk;
+  if ((idle || n_active == 1) && num_splits > 1 && tid < nh)
+    ws_m[((int64_t)s * H + head0 + tid) * num_splits + split] = -INFINITY;
+  if (seq_len == 0) {                            // padding row: zeros (ops/reference.py:99,104-105)
+    if (split == 0) {
+      for (int e = tid; e < nh * D; e += NW * 64)
+        out[(int64_t)s * o_st + (int64_t)(head0 + e / D) * D + e % D] = (half_t)0.f;
+    }
+    return;
+  }
+  if (idle) return;                              // idle split of a short sequence
+  const int blk_hi = (blk_lo + part_blocks) < nblk ? (blk_lo + part_blocks) : nblk;
+  // Tokens this split may use: a pair's second block can lie past the split (or be a repeat of
+  // its last block) while its tokens are still below seq_len.
+  const int tok_hi = blk_hi * kBlockSize < seq_len ? blk_hi * kBlockSize : seq_len;
+
+  const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
   float4_t o[TILES];
 #pragma unroll
-  for (int t = 0; t < TILES; ++t) o[t] = {0.f, 0.f, 0.f, 0.f};
+  for (int t = 0; t < TILES; ++t) o[t] = zero4;
   float m = -INFINITY, l = 0.f;
 
-  const int* btrow = bt + (int64_t)s * bt_st;
   const int64_t head_off = (int64_t)kvh * kBlockSize * D;
   const int64_t blk_stride = (int64_t)KVH * kBlockSize * D;
-  half8_t kf[KK], vf[KK], kn[KK], vn[KK];
-  // V rows past seq_len are zeroed so stale cache contents never reach P.V (0 * NaN).
-  const half8_t hz = {0, 0, 0, 0, 0, 0, 0, 0};
-  int i = blk_lo + w;
-  if (i < blk_hi) {
-    const int64_t off = clamp_block(btrow[i], NB) * blk_stride + head_off;
-    load_kv_block<D>(kc + off, c, g, kf);
-    load_kv_block<D>(vc + off, c, g, vf);
-    if (i * kBlockSize + c >= seq_len) {
+  for (; r0 < blk_hi; r0 += NW * BPW) {
+    // Blocks past blk_hi repeat the last valid block (a cache hit, no extra HBM read), so the
+    // loads below carry no branches; the repeated data is masked out of the softmax.
+    int phys[BPW];
 #pragma unroll
-      for (int kk = 0; kk < KK; ++kk) vf[kk] = hz;
+    for (int j = 0; j < BPW; ++j) {
+      int id = btv[j];
+#pragma unroll
+      for (int i = 0; i < BPW; ++i)
+        if (r0 + j >= blk_hi && r0 + i == blk_hi - 1) id = btv[i];
+      phys[j] = clamp_block(id, NB);
     }
-  }
-  for (; i < blk_hi; i += NW) {
-    const int inext = i + NW;
-    if (inext < blk_hi) {                        // prefetch the next block of this wave
-      const int64_t off = clamp_block(btrow[inext], NB) * blk_stride + head_off;
-      load_kv_block<D>(kc + off, c, g, kn);
-      load_kv_block<D>(vc + off, c, g, vn);
-      if (inext * kBlockSize + c >= seq_len) {
+    half8_t kf[BPW][KK];
+    half_t vr[BPW][4][VW];
 #pragma unroll
-        for (int kk = 0; kk < KK; ++kk) vn[kk] = hz;
+    for (int j = 0; j < BPW; ++j) {
+      const int64_t off = phys[j] * blk_stride + head_off;
+      load_k_block<D>(kc + off, c, g, kf[j]);
+      load_v_rows<D>(vc + off, c, g, vr[j]);
+    }
+    const int r_next = r0 + NW * BPW;
+    if (r_next < blk_hi) {                       // next round's table entries, early
+#pragma unroll
+      for (int j = 0; j < BPW; ++j)
+        btv[j] = btrow[(r_next + j) < max_blocks ? (r_next + j) : (max_blocks - 1)];
+    }
+#pragma unroll
+    for (int pr = 0; pr < BPW / 2; ++pr) {
+      const int ja = 2 * pr, jb = 2 * pr + 1;
+      const int ba = r0 + ja, bb = r0 + jb;
+      if (ba >= blk_hi) break;
+      // S^T = K . Q^T for both blocks: two independent MFMA chains
+      float4_t sa = zero4, sb = zero4;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        if constexpr (D >= 32) {
+          sa = mfma16x16x32(kf[ja][kk], qf[kk], sa);
+          sb = mfma16x16x32(kf[jb][kk], qf[kk], sb);
+        } else {
+          sa = mfma16x16x16(lo4(kf[ja][kk]), lo4(qf[kk]), sa);
+          sb = mfma16x16x16(lo4(kf[jb][kk]), lo4(qf[kk]), sb);
+        }
       }
-    }
-    // S^T = K . Q^T
-    float4_t st4 = {0.f, 0.f, 0.f, 0.f};
+      const int ta = ba * kBlockSize + 4 * g, tb = bb * kBlockSize + 4 * g;
+      float sca[4], scb[4];
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      if constexpr (D >= 32) st4 = mfma16x16x32(kf[kk], qf[kk], st4);
-      else st4 = mfma16x16x16(lo4(kf[kk]), lo4(qf[kk]), st4);
-    }
-    const int tok0 = i * kBlockSize + 4 * g;
-    float sc[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) sc[r] = (tok0 + r < seq_len) ? st4[r] * scale_log2 : -INFINITY;
-    const float bmax = rows_max(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])));
-    const float m_new = fmaxf(m, bmax);          // finite: token 0 of every block is valid
-    const float alpha = fast_exp2(m - m_new);
-    float p[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) p[r] = fast_exp2(sc[r] - m_new);
-    l = l * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    m = m_new;
-    const half4_t pb = {(half_t)p[0], (half_t)p[1], (half_t)p[2], (half_t)p[3]};
-#pragma unroll
-    for (int t = 0; t < TILES; ++t) o[t] *= alpha;
-    // O^T += V^T . P^T, V transposed through the identity product.
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      const float4_t zero = {0.f, 0.f, 0.f, 0.f};
-      const half4_t va = to_half4(mfma16x16x16(lo4(vf[kk]), ident, zero));
-      o[2 * kk] = mfma16x16x16(va, pb, o[2 * kk]);
-      if constexpr (D >= 32) {
-        const half4_t vb = to_half4(mfma16x16x16(hi4(vf[kk]), ident, zero));
-        o[2 * kk + 1] = mfma16x16x16(vb, pb, o[2 * kk + 1]);
+      for (int r = 0; r < 4; ++r) {
+        sca[r] = (ta + r < tok_hi) ? sa[r] * scale_log2 : -INFINITY;
+        scb[r] = (tb + r < tok_hi) ? sb[r] * scale_log2 : -INFINITY;
       }
-    }
+      const float bmax = rows_max(fmaxf(fmaxf(fmaxf(sca[0], sca[1]), fmaxf(sca[2], sca[3])),
+                                        fmaxf(fmaxf(scb[0], scb[1]), fmaxf(scb[2], scb[3]))));
+      const float m_new = fmaxf(m, bmax);        // finite: token 0 of block ba is valid
+      const float alpha = fast_exp2(m - m_new);
+      float pa[4], pb[4];
 #pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      kf[kk] = kn[kk];
-      vf[kk] = vn[kk];
+      for (int r = 0; r < 4; ++r) {
+        pa[r] = fast_exp2(sca[r] - m_new);
+        pb[r] = fast_exp2(scb[r] - m_new);
+      }
+      l = l * alpha + (((pa[0] + pa[1]) + (pa[2] + pa[3])) + ((pb[0] + pb[1]) + (pb[2] + pb[3])));
+      m = m_new;
+      const half8_t p8 = {(half_t)pa[0], (half_t)pa[1], (half_t)pa[2], (half_t)pa[3],
+                          (half_t)pb[0], (half_t)pb[1], (half_t)pb[2], (half_t)pb[3]};
+      const bool tail_a = (ba + 1) * kBlockSize > tok_hi;
+      const bool tail_b = (bb + 1) * kBlockSize > tok_hi;
+#pragma unroll
+      for (int t = 0; t < TILES; ++t) {
+        o[t] *= alpha;
+        half4_t va = {vr[ja][0][t], vr[ja][1][t], vr[ja][2][t], vr[ja][3][t]};
+        half4_t vb = {vr[jb][0][t], vr[jb][1][t], vr[jb][2][t], vr[jb][3][t]};
+        if (tail_a) va = mask_tokens(va, ta, tok_hi);
+        if (tail_b) vb = mask_tokens(vb, tb, tok_hi);
+        const half8_t v8 = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
+        o[t] = mfma16x16x32(v8, p8, o[t]);        // lane (c, g): dims VW (4g + r) + t of head c
+      }
     }
   }
   l = rows_sum(l);
 
-  // Merge the NW waves of this workgroup.
+  // Merge the NW wavefronts of this workgroup in LDS.
   if (g == 0) {
     s_m[w][c] = m;
     s_l[w][c] = l;
   }
 #pragma unroll
-  for (int kk = 0; kk < KK; ++kk) {
-    if constexpr (D >= 32) {
-      float* dst = &s_o[w][c][32 * kk + 8 * g];
-      st<float4_t>(dst, o[2 * kk]);
-      st<float4_t>(dst + 4, o[2 * kk + 1]);
-    } else {
-      st<float4_t>(&s_o[w][c][4 * g], o[0]);
-    }
-  }
+  for (int t = 0; t < TILES; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s_o[w][c][VW * (4 * g + r) + t] = o[t][r];
   __syncthreads();
-  const bool final_out = n_active == 1;
+  const bool single = n_active == 1;
   for (int e = tid; e < nh * D; e += NW * 64) {
     const int hh = e / D, d = e % D;
     float M = -INFINITY;
@@ -277,15 +348,14 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
     float L = 0.f, O = 0.f;
 #pragma unroll
     for (int ww = 0; ww < NW; ++ww) {
-      const float wt = fast_exp2(s_m[ww][hh] - M);    // idle wave: m = -inf -> 0
+      const float wt = fast_exp2(s_m[ww][hh] - M);    // idle wavefront: m = -inf -> 0
       L += wt * s_l[ww][hh];
       O += wt * s_o[ww][hh][d];
     }
-    const int head = kvh * G + hg * 16 + hh;
-    if (final_out) {
-      out[(int64_t)s * o_st + (int64_t)head * D + d] = (half_t)(O / L);
+    if (single) {
+      out[(int64_t)s * o_st + (int64_t)(head0 + hh) * D + d] = (half_t)(O / L);
     } else {
-      const int64_t pidx = ((int64_t)s * H + head) * num_splits + split;
+      const int64_t pidx = ((int64_t)s * H + head0 + hh) * num_splits + split;
       ws_acc[pidx * D + d] = O;
       if (d == 0) {
         ws_m[pidx] = M;
@@ -296,39 +366,115 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
 }
 
 // Merge of the split partials (ops/triton_decode_attention.py:144-163): M = max m_j,
-// w_j = 2^(m_j - M), out = sum w_j acc_j / sum w_j l_j. Sequences with a single active split
-// were finished by the partial kernel.
+// w_j = 2^(m_j - M), out = sum w_j acc_j / sum w_j l_j. One workgroup per (sequence, KV head,
+// head group), two dependent memory steps: every (head, split) statistic is loaded at once
+// (slots without a partial hold m = -inf, so seq_len is not needed), then the partials of the
+// active splits (a compact list, identical for all heads) are read without branches. A group
+// whose slots are all -inf was finished by the first kernel.
 template <int D>
-__global__ void __launch_bounds__(D < 64 ? 64 : D) decode_reduce_kernel(
+__global__ void __launch_bounds__(256) decode_merge_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_m,
-    const float* __restrict__ ws_l, half_t* __restrict__ out, int64_t o_st,
-    const int* __restrict__ seq_lens, int max_blocks, int H, int part_blocks, int num_splits) {
-  const int s = blockIdx.x, h = blockIdx.y;
-  int seq_len = seq_lens[s];
-  seq_len = seq_len < 0 ? 0 : (seq_len > max_blocks * kBlockSize ? max_blocks * kBlockSize : seq_len);
-  const int nblk = (seq_len + kBlockSize - 1) / kBlockSize;
-  int n_active = (nblk + part_blocks - 1) / part_blocks;
-  n_active = n_active < num_splits ? n_active : num_splits;
-  if (n_active <= 1) return;
-  const int64_t base = ((int64_t)s * H + h) * num_splits;
-  float M = -INFINITY;
-  for (int j = 0; j < n_active; ++j) M = fmaxf(M, ws_m[base + j]);
-  for (int d = threadIdx.x; d < D; d += blockDim.x) {
-    float L = 0.f, O = 0.f;
-    for (int j = 0; j < n_active; ++j) {
-      const float wt = fast_exp2(ws_m[base + j] - M);
-      L += wt * ws_l[base + j];
-      O += wt * ws_acc[(base + j) * D + d];
+    const float* __restrict__ ws_l, half_t* __restrict__ out, int64_t o_st, int H, int G, int HG,
+    int num_splits) {
+  constexpr int kMaxSplits = 256;               // the launcher caps num_splits
+  __shared__ float s_w[16][kMaxSplits];
+  __shared__ float s_l[16][kMaxSplits];
+  __shared__ float s_inv[16];
+  __shared__ int s_act[kMaxSplits];             // splits that carry a partial (same for all heads)
+  __shared__ int s_nact;
+  const int s = blockIdx.x, kvh = blockIdx.y / HG, hg = blockIdx.y % HG;
+  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int nh = (G - hg * 16) < 16 ? (G - hg * 16) : 16;
+  const int head0 = kvh * G + hg * 16;
+  const int64_t base0 = ((int64_t)s * H + head0) * num_splits;
+  for (int e = tid; e < nh * num_splits; e += 256) {
+    const int hh = e / num_splits, j = e % num_splits;
+    s_w[hh][j] = ws_m[base0 + (int64_t)hh * num_splits + j];
+    s_l[hh][j] = ws_l[base0 + (int64_t)hh * num_splits + j];
+  }
+  __syncthreads();
+  if (w == 0) {                                 // compact list of active splits (ballot + popcount)
+    int n = 0;
+    for (int j0 = 0; j0 < num_splits; j0 += 64) {
+      const int j = j0 + lane;
+      const bool act = j < num_splits && s_w[0][j] != -INFINITY;
+      const uint64_t mask = __ballot(act);
+      if (act) s_act[n + __popcll(mask & ((1ull << lane) - 1))] = j;
+      n += __popcll(mask);
     }
-    out[(int64_t)s * o_st + (int64_t)h * D + d] = (half_t)(O / L);
+    if (lane == 0) s_nact = n;
+  }
+  for (int hh = w; hh < nh; hh += 4) {
+    float M = -INFINITY;
+    for (int j = lane; j < num_splits; j += 64) M = fmaxf(M, s_w[hh][j]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
+    float L = 0.f;
+    for (int j = lane; j < num_splits; j += 64) {
+      const float m = s_w[hh][j];
+      const float wt = m == -INFINITY ? 0.f : fast_exp2(m - M);
+      s_w[hh][j] = wt;
+      L += m == -INFINITY ? 0.f : wt * s_l[hh][j];   // a slot without a partial holds garbage l
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) L += shfl_xor(L, off);
+    if (lane == 0) s_inv[hh] = M == -INFINITY ? 0.f : 1.f / L;
+  }
+  __syncthreads();
+  const int nact = s_nact;
+  if (nact == 0) return;                        // finished (or zeroed) by the first kernel
+  // Each thread owns up to EPT outputs; for every chunk of CH active splits all EPT x CH loads
+  // are issued before any is consumed (indices past nact repeat the last split with weight 0).
+  constexpr int EPT = 4, CH = 16;
+  for (int e0 = tid; e0 < nh * D; e0 += 256 * EPT) {
+    float O[EPT];
+    const float* accp[EPT];
+    int hh_[EPT];
+    bool ok[EPT];
+#pragma unroll
+    for (int q = 0; q < EPT; ++q) {
+      const int e = e0 + 256 * q;
+      ok[q] = e < nh * D;
+      const int ee = ok[q] ? e : 0;
+      hh_[q] = ee / D;
+      accp[q] = ws_acc + (base0 + (int64_t)hh_[q] * num_splits) * D + ee % D;
+      O[q] = 0.f;
+    }
+    for (int t0 = 0; t0 < nact; t0 += CH) {
+      float v[EPT][CH];
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const int j = s_act[(t0 + u) < nact ? (t0 + u) : (nact - 1)];
+#pragma unroll
+        for (int q = 0; q < EPT; ++q) v[q][u] = accp[q][(int64_t)j * D];
+      }
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const int j = s_act[(t0 + u) < nact ? (t0 + u) : (nact - 1)];
+#pragma unroll
+        for (int q = 0; q < EPT; ++q) O[q] += (t0 + u < nact) ? s_w[hh_[q]][j] * v[q][u] : 0.f;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < EPT; ++q) {
+      const int e = e0 + 256 * q;
+      if (ok[q]) out[(int64_t)s * o_st + (int64_t)(head0 + hh_[q]) * D + e % D] = (half_t)(O[q] * s_inv[hh_[q]]);
+    }
   }
 }
 
 // ------------------------------------------------------------------------------------------
 // Host side
 // ------------------------------------------------------------------------------------------
-constexpr int kDecodeWaves = 4;
-constexpr int kDefaultPartition = 256;     // tokens per v3 split (multiple of 16 * kDecodeWaves)
+#ifndef TS_DECODE_WAVES
+#define TS_DECODE_WAVES 4
+#endif
+#ifndef TS_DECODE_BLOCKS_PER_WAVE
+#define TS_DECODE_BLOCKS_PER_WAVE 4
+#endif
+constexpr int kDecodeWaves = TS_DECODE_WAVES;               // wavefronts per workgroup
+constexpr int kBlocksPerWave = TS_DECODE_BLOCKS_PER_WAVE;   // blocks loaded up front per round
+constexpr int kDefaultPartition = kDecodeWaves * kBlocksPerWave * kBlockSize;   // 256 tokens
 
 struct SplitPlan {
   int version;        // 1, 2 or 3 after resolving AUTO
@@ -353,6 +499,10 @@ static SplitPlan plan_decode(int version, int S, int H, int KVH, int max_seq_len
     p.part_blocks = part / kBlockSize;
     const int max_blk = (max_seq_len + kBlockSize - 1) / kBlockSize;
     p.num_splits = (max_blk + p.part_blocks - 1) / p.part_blocks;   // ops/triton_ops.py:50-51
+    if (p.num_splits > 256) {                    // the merge keeps <= 256 split weights in LDS
+      p.part_blocks = (max_blk + 255) / 256;
+      p.num_splits = (max_blk + p.part_blocks - 1) / p.part_blocks;
+    }
     if (p.num_splits < 1) p.num_splits = 1;
   }
   return p;
@@ -360,10 +510,20 @@ static SplitPlan plan_decode(int version, int S, int H, int KVH, int max_seq_len
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-static size_t workspace_for(const SplitPlan& p, int S, int H, int D) {
-  if (p.version != TS_DECODE_V3 || p.num_splits <= 1) return 0;
+struct WsLayout {
+  size_t acc, m, l, total;
+};
+
+// [acc: S * H * splits * D fp32][m: S * H * splits][l: S * H * splits]
+static WsLayout ws_layout(const SplitPlan& p, int S, int H, int D) {
+  WsLayout w{0, 0, 0, 0};
+  if (p.version != TS_DECODE_V3 || p.num_splits <= 1) return w;
   const size_t n = (size_t)S * H * p.num_splits;
-  return align256(n * D * sizeof(float)) + 2 * align256(n * sizeof(float));
+  w.acc = 0;
+  w.m = align256(n * D * sizeof(float));
+  w.l = w.m + align256(n * sizeof(float));
+  w.total = w.l + align256(n * sizeof(float));
+  return w;
 }
 
 template <int D>
@@ -381,18 +541,19 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
   const int HG = (G + 15) / 16;
   float *ws_acc = nullptr, *ws_m = nullptr, *ws_l = nullptr;
   if (p.num_splits > 1) {
-    const size_t n = (size_t)S * H * p.num_splits;
+    const WsLayout w = ws_layout(p, S, H, D);
     char* b = static_cast<char*>(ws);
-    ws_acc = reinterpret_cast<float*>(b);
-    ws_m = reinterpret_cast<float*>(b + align256(n * D * sizeof(float)));
-    ws_l = reinterpret_cast<float*>(b + align256(n * D * sizeof(float)) + align256(n * sizeof(float)));
+    ws_acc = reinterpret_cast<float*>(b + w.acc);
+    ws_m = reinterpret_cast<float*>(b + w.m);
+    ws_l = reinterpret_cast<float*>(b + w.l);
   }
-  decode_mfma_kernel<D, kDecodeWaves><<<dim3(p.num_splits, S, KVH * HG), kDecodeWaves * 64, 0, st>>>(
-      q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, H, KVH, G, HG, scale_log2,
-      p.part_blocks, p.num_splits, ws_acc, ws_m, ws_l);
+  decode_mfma_kernel<D, kDecodeWaves, kBlocksPerWave>
+      <<<dim3(S, p.num_splits, KVH * HG), kDecodeWaves * 64, 0, st>>>(
+          q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, H, KVH, G, HG,
+          scale_log2, p.part_blocks, p.num_splits, ws_acc, ws_m, ws_l);
   if (p.num_splits > 1) {
-    decode_reduce_kernel<D><<<dim3(S, H), D < 64 ? 64 : D, 0, st>>>(
-        ws_acc, ws_m, ws_l, out, o_st, sl, max_blocks, H, p.part_blocks, p.num_splits);
+    decode_merge_kernel<D><<<dim3(S, KVH * HG), 256, 0, st>>>(ws_acc, ws_m, ws_l, out, o_st, H,
+                                                              G, HG, p.num_splits);
   }
 }
 
@@ -411,7 +572,7 @@ extern "C" size_t ts_decode_workspace_bytes(int32_t version, int32_t num_seqs, i
   if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
   const SplitPlan p = plan_decode(version, num_seqs, num_heads, num_kv_heads, max_seq_len,
                                   partition, cu_count > 0 ? cu_count : 256);
-  return workspace_for(p, num_seqs, num_heads, head_dim);
+  return ws_layout(p, num_seqs, num_heads, head_dim).total;
 }
 
 extern "C" int ts_decode_attention(int32_t version, const void* q, int64_t q_stride_t,
@@ -448,7 +609,7 @@ extern "C" int ts_decode_attention(int32_t version, const void* q, int64_t q_str
   if (st != TS_OK) return st;
   const SplitPlan p = plan_decode(version, num_seqs, num_heads, num_kv_heads, max_seq_len,
                                   partition, cus);
-  const size_t need = workspace_for(p, num_seqs, num_heads, head_dim);
+  const size_t need = ws_layout(p, num_seqs, num_heads, head_dim).total;
   TS_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 256)),
              TS_ERR_WORKSPACE, "decode_attention: workspace of %zu bytes (256-aligned) needed, got %zu",
              need, workspace_bytes);
