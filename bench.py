@@ -264,6 +264,73 @@ def bench_w8a16(torch, K, synth):
     return rows
 
 
+def bench_mixed(torch, synth, reps: int = 5):
+    """Config 5: one mixed forward step of a random-init Qwen2 at the Qwen2.5-1.5B dimensions
+    (28 layers, W8A16 linears, tied fp16 lm head) over 48 decodes with contexts log-uniform in
+    [256, 4096] plus one 512-token prefill chunk; tokens/s = 560 / step time. The chunk belongs to
+    a prompt whose already-cached prefix is drawn lognormal with median 200 tokens (the
+    configuration's prompt-length distribution). Timed eagerly (the serving path for mixed steps)
+    and as a hipGraph replay (GPU time alone)."""
+    import random as _r
+
+    from turingserve_amd import get_ops
+    from turingserve_amd.metadata import BatchItem, InputBuilder, SeqState
+    from turingserve_amd.qwen2 import QWEN25_15B, Qwen2Model, random_weights
+
+    dev = torch.device("cuda", 0)
+    cfg = QWEN25_15B
+    g = torch.Generator().manual_seed(0)
+    ctx = synth.log_uniform_ints(48, 256, 4096, g)
+    prefix = int(min(3000, round(float(torch.empty(1).log_normal_(math.log(200), 0.8, generator=g)))))
+    w = random_weights(cfg, dev, quantization="int8", init_std=0.02, seed=0)
+    model = Qwen2Model(cfg, w, get_ops("hip"), dev, max_model_len=8192)
+    nb = sum(-(-c // 16) for c in ctx) + -(-(prefix + 512) // 16) + 8
+    kv = model.new_kv_cache(nb)
+    kv.normal_(0.0, 0.5)
+    rng = _r.Random(0)
+    free = list(range(1, nb))
+    rng.shuffle(free)
+    items = []
+    for c in ctx:
+        s = SeqState([rng.randrange(cfg.vocab_size) for _ in range(c)])
+        s.block_table = [free.pop() for _ in range(-(-c // 16))]
+        items.append(BatchItem(s, c - 1, [s.token_ids[-1]], "last"))
+    s = SeqState([rng.randrange(cfg.vocab_size) for _ in range(prefix + 512)])
+    s.block_table = [free.pop() for _ in range(-(-(prefix + 512) // 16))]
+    items.append(BatchItem(s, prefix, s.token_ids[prefix:], "last"))
+    inp = InputBuilder(1024, 64, 512, dev).build(items)
+    T = inp.input_ids.shape[0]
+
+    def step():
+        hidden = model.forward(inp.input_ids, inp.positions, inp.meta, kv)
+        return model.compute_logits(hidden, inp.sample_indices)
+
+    logits = step()
+    torch.cuda.synchronize()
+    finite = bool(torch.isfinite(logits).all())
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        step()
+    torch.cuda.synchronize()
+    eager_s = (time.perf_counter() - t0) / reps
+    g_ = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_):
+        step()
+    g_.replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        g_.replay()
+    torch.cuda.synchronize()
+    graph_s = (time.perf_counter() - t0) / reps
+    del model, w, kv, g_
+    torch.cuda.empty_cache()
+    return {"tokens_per_step": T, "num_decode": 48, "prefill_chunk": 512, "chunk_prefix": prefix,
+            "eager_ms": round(eager_s * 1e3, 3), "graph_ms": round(graph_s * 1e3, 3),
+            "eager_tokens_per_s": round(T / eager_s, 1), "graph_tokens_per_s": round(T / graph_s, 1),
+            "logits_finite": finite}
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -320,6 +387,8 @@ def main() -> int:
         extra = {"prefill_config3": bench_prefill(torch, K, synth)}
         log("extra: config 4 W8A16")
         extra["w8a16_config4"] = bench_w8a16(torch, K, synth)
+        log("extra: config 5 mixed step")
+        extra["mixed_config5"] = bench_mixed(torch, synth)
         out["extra"] = extra
     print(json.dumps(out), flush=True)
     return 0
