@@ -44,6 +44,11 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["decode", "prefill", "w8a16", "mixed"], default=None,
+                    help="run one workload alone (for profiling); prints its result as JSON")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="copy a 256 MiB buffer 8 times (the known-size kernel that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters) and exit")
     return ap.parse_args()
 
 
@@ -345,7 +350,24 @@ def main() -> int:
     sys.path.insert(0, ROOT)
     from turingserve_amd import _native, hip_ops as K, synth
 
+    if args.copy_calibration:
+        a = torch.empty(256 * 2 ** 20, dtype=torch.uint8, device="cuda")
+        b = torch.empty_like(a)
+        for _ in range(8):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_bytes_read_per_launch": a.numel(),
+                          "copy_bytes_written_per_launch": a.numel(), "launches": 8}))
+        return 0
     _native.lib()
+    if args.only in ("prefill", "w8a16", "mixed"):
+        fn = {"prefill": lambda: bench_prefill(torch, K, synth),
+              "w8a16": lambda: bench_w8a16(torch, K, synth),
+              "mixed": lambda: bench_mixed(torch, synth)}[args.only]
+        print(json.dumps({args.only: fn()}), flush=True)
+        return 0
+    if args.only == "decode":
+        args.no_extra = args.no_cpu = True
     log(f"device: {torch.cuda.get_device_name(0)}  library: {_native.version()}")
     log("headline: config 2 decode step (kv_write + paged decode attention)")
     st, r = bench_decode(args, torch, K, synth)
