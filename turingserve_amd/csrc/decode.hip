@@ -24,6 +24,7 @@
 #include <math.h>
 
 #include "common.h"
+#include "paged_kv.h"
 
 namespace ts {
 
@@ -101,68 +102,6 @@ __global__ void __launch_bounds__(64) decode_v1_kernel(
 // ------------------------------------------------------------------------------------------
 // v2 / v3 (ops/triton_decode_attention.py:60-163)
 // ------------------------------------------------------------------------------------------
-template <int D>
-struct DecodeRegs {
-  // D >= 32: KK 16-byte pieces of K per lane; D == 16: one 8-byte piece.
-  static constexpr int KK = D >= 32 ? D / 32 : 1;
-  // V: each lane holds VW consecutive dims of 4 tokens; O^T is split into VW tiles of 16 dims.
-  static constexpr int VW = D / 16;
-  static constexpr int TILES = VW;
-};
-
-// K rows in their natural layout: lane (c, g) gets K[tok c][32kk + 8g .. +7] (16-byte loads).
-template <int D>
-__device__ __forceinline__ void load_k_block(const half_t* __restrict__ base, int c, int g,
-                                             half8_t (&x)[DecodeRegs<D>::KK]) {
-  if constexpr (D >= 32) {
-#pragma unroll
-    for (int kk = 0; kk < DecodeRegs<D>::KK; ++kk) x[kk] = ld<half8_t>(base + c * D + 32 * kk + 8 * g);
-  } else {
-    const half4_t t = ld<half4_t>(base + c * D + 4 * g);
-    x[0] = {t[0], t[1], t[2], t[3], 0, 0, 0, 0};
-  }
-}
-
-// V rows in their natural layout: lane (c, g) loads V[tok 4g + r][VW c .. VW c + VW-1] for
-// r = 0..3 (16 lanes cover one whole token row, so every load is fully coalesced). Tile q of
-// O^T then uses dims {VW i + q : i = 0..15}: its token-packed A operand for lane (c, g) is
-// {x[0][q], x[1][q], x[2][q], x[3][q]}, two byte permutes and no transpose product.
-template <int D>
-__device__ __forceinline__ void load_v_rows(const half_t* __restrict__ base, int c, int g,
-                                            half_t (&x)[4][DecodeRegs<D>::VW]) {
-  constexpr int VW = DecodeRegs<D>::VW;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const half_t* p = base + (4 * g + r) * D + VW * c;
-    if constexpr (VW % 8 == 0) {
-#pragma unroll
-      for (int u = 0; u < VW / 8; ++u) {
-        const half8_t v = ld<half8_t>(p + 8 * u);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[r][8 * u + e] = v[e];
-      }
-    } else if constexpr (VW == 4) {
-      const half4_t v = ld<half4_t>(p);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) x[r][e] = v[e];
-    } else if constexpr (VW == 2) {
-      const half2_t v = ld<half2_t>(p);
-      x[r][0] = v[0];
-      x[r][1] = v[1];
-    } else {
-      x[r][0] = p[0];
-    }
-  }
-}
-
-// Tokens 4g .. 4g+3 of a V^T operand at or past seq_len are zeroed: a reused block may hold
-// anything there, and 0 * NaN would reach the output.
-__device__ __forceinline__ half4_t mask_tokens(half4_t v, int tok0, int seq_len) {
-#pragma unroll
-  for (int r = 0; r < 4; ++r) v[r] = (tok0 + r < seq_len) ? v[r] : (half_t)0.f;
-  return v;
-}
-
 // One workgroup = NW wavefronts = one (sequence, split, KV head, head group). A wavefront owns
 // BPW consecutive 16-token blocks per round and issues all their loads before computing; the
 // block-table entries, seq_len and q are requested together at the start. Blocks are consumed
@@ -178,9 +117,9 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
     int H, int KVH, int G, int HG, float scale_log2, int part_blocks, int num_splits,
     float* __restrict__ ws_acc, float* __restrict__ ws_m, float* __restrict__ ws_l) {
   static_assert(BPW % 2 == 0, "blocks are consumed in pairs");
-  constexpr int KK = DecodeRegs<D>::KK;
-  constexpr int VW = DecodeRegs<D>::VW;
-  constexpr int TILES = DecodeRegs<D>::TILES;
+  constexpr int KK = KvRegs<D>::KK;
+  constexpr int VW = KvRegs<D>::VW;
+  constexpr int TILES = KvRegs<D>::TILES;
   constexpr int OROW = D + 4;                    // padded LDS row (floats) against bank conflicts
   __shared__ float s_o[NW][16][OROW];
   __shared__ float s_m[NW][16];
@@ -262,7 +201,7 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
       phys[j] = clamp_block(id, NB);
     }
     half8_t kf[BPW][KK];
-    half_t vr[BPW][4][VW];
+    typename HalfVec<VW>::type vr[BPW][4];
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
       const int64_t off = phys[j] * blk_stride + head_off;
@@ -293,16 +232,28 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
         }
       }
       const int ta = ba * kBlockSize + 4 * g, tb = bb * kBlockSize + 4 * g;
+      const bool interior = (bb + 1) * kBlockSize <= tok_hi;   // every token of the pair valid
       float sca[4], scb[4];
+      if (interior) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        sca[r] = (ta + r < tok_hi) ? sa[r] * scale_log2 : -INFINITY;
-        scb[r] = (tb + r < tok_hi) ? sb[r] * scale_log2 : -INFINITY;
+        for (int r = 0; r < 4; ++r) {
+          sca[r] = sa[r] * scale_log2;
+          scb[r] = sb[r] * scale_log2;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          sca[r] = (ta + r < tok_hi) ? sa[r] * scale_log2 : -INFINITY;
+          scb[r] = (tb + r < tok_hi) ? sb[r] * scale_log2 : -INFINITY;
+        }
       }
       const float bmax = rows_max(fmaxf(fmaxf(fmaxf(sca[0], sca[1]), fmaxf(sca[2], sca[3])),
                                         fmaxf(fmaxf(scb[0], scb[1]), fmaxf(scb[2], scb[3]))));
       const float m_new = fmaxf(m, bmax);        // finite: token 0 of block ba is valid
       const float alpha = fast_exp2(m - m_new);
+      // O is rescaled only when some head's running max moved (alpha == 1 exactly otherwise),
+      // which after the first blocks is rare: the accumulators then stay in the MFMA registers.
+      const bool rescale = __ballot(m_new != m) != 0;
       float pa[4], pb[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
@@ -315,9 +266,12 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
                           (half_t)pb[0], (half_t)pb[1], (half_t)pb[2], (half_t)pb[3]};
       const bool tail_a = (ba + 1) * kBlockSize > tok_hi;
       const bool tail_b = (bb + 1) * kBlockSize > tok_hi;
+      if (rescale) {
+#pragma unroll
+        for (int t = 0; t < TILES; ++t) o[t] *= alpha;
+      }
 #pragma unroll
       for (int t = 0; t < TILES; ++t) {
-        o[t] *= alpha;
         half4_t va = {vr[ja][0][t], vr[ja][1][t], vr[ja][2][t], vr[ja][3][t]};
         half4_t vb = {vr[jb][0][t], vr[jb][1][t], vr[jb][2][t], vr[jb][3][t]};
         if (tail_a) va = mask_tokens(va, ta, tok_hi);

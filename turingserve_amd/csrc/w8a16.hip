@@ -13,8 +13,9 @@
 //    a K range; lane (c, g) reads 16 contiguous weight bytes per 64-wide K step (64 bytes per
 //    row and instruction). The K dimension is split over workgroups until the device is full;
 //    fp32 partials are merged (and scaled) by a second kernel.
-//  * large M: LDS-tiled MFMA GEMM, 128 x 128 output tile per workgroup of four wavefronts
-//    (2 x 2, 64 x 64 each), K step 64, int8 tile kept as int8 in LDS and widened on read.
+//  * larger M: double-buffered LDS-tiled MFMA GEMM (128x128, 128x64 or 64x64 tiles chosen so
+//    the grid covers the CUs, split-K when even the smallest tile does not), K step 64, int8
+//    tile kept as int8 in LDS and widened on read.
 #include "common.h"
 
 namespace ts {
@@ -50,12 +51,15 @@ __device__ __forceinline__ float load_scale(const void* scale, int scale_is_fp16
 constexpr int kSmWaves = 4;        // wavefronts per workgroup = 4 x 16 output channels
 constexpr int kSmKStep = 64;       // K per step: lane (c, g) covers k + 16g .. k + 16g + 15
 
-template <int MT>   // number of 16-row m tiles (M <= 16 * MT)
+// U K steps are loaded before any is multiplied, so each wavefront keeps U x (1 KiB of weights
+// + MT x 2 KiB of activations) in flight instead of waiting one round trip per step.
+template <int MT, bool WIDE>   // MT 16-row m tiles (M <= 16 MT); WIDE: 16-byte weight loads
 __global__ void __launch_bounds__(kSmWaves * 64) w8a16_small_kernel(
     const half_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ wq,
     const void* __restrict__ scale, int scale_is_fp16, const half_t* __restrict__ bias,
     half_t* __restrict__ y, int64_t ldy, int M, int N, int K, int k_per_split,
     float* __restrict__ part) {
+  constexpr int U = MT <= 2 ? 4 : 2;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int c = lane & 15, g = lane >> 4;
   const int n0 = (blockIdx.x * kSmWaves + w) * 16;
@@ -79,20 +83,37 @@ __global__ void __launch_bounds__(kSmWaves * 64) w8a16_small_kernel(
   for (int mt = 0; mt < MT; ++mt) acc[mt] = {0.f, 0.f, 0.f, 0.f};
 
   const half8_t hz = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int k = kb; k < ke; k += kSmKStep) {
-    // Two 8-element chunks per lane; K % 8 == 0, so a chunk is entirely inside or outside.
-    const int ka = k + 16 * g, kb2 = ka + 8;
-    const bool a_ok = ka < ke, b_ok = kb2 < ke;
-    int2_t wa = {0, 0}, wb = {0, 0};
-    if (n_ok && a_ok) wa = ld<int2_t>(wrow + ka);
-    if (n_ok && b_ok) wb = ld<int2_t>(wrow + kb2);
-    const half8_t fa = i8x8_to_half8(wa), fb = i8x8_to_half8(wb);
+  for (int k = kb; k < ke; k += U * kSmKStep) {
+    int2_t wa[U], wb[U];
+    half8_t xa[U][MT], xb[U][MT];
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const half8_t xa = (m_ok[mt] && a_ok) ? ld<half8_t>(xrow[mt] + ka) : hz;
-      const half8_t xb = (m_ok[mt] && b_ok) ? ld<half8_t>(xrow[mt] + kb2) : hz;
-      acc[mt] = mfma16x16x32(fa, xa, acc[mt]);
-      acc[mt] = mfma16x16x32(fb, xb, acc[mt]);
+    for (int u = 0; u < U; ++u) {
+      // lane (c, g): K columns ka .. ka+15 in two 8-element chunks; K % 8 == 0, so a chunk is
+      // entirely inside or outside [kb, ke) (WIDE: K % 16 == 0 and the pair goes together).
+      const int ka = k + u * kSmKStep + 16 * g, kb2 = ka + 8;
+      const bool a_ok = ka < ke, b_ok = kb2 < ke;
+      if constexpr (WIDE) {
+        const int4_t v = (n_ok && a_ok) ? ld<int4_t>(wrow + ka) : int4_t{0, 0, 0, 0};
+        wa[u] = {v[0], v[1]};
+        wb[u] = {v[2], v[3]};
+      } else {
+        wa[u] = (n_ok && a_ok) ? ld<int2_t>(wrow + ka) : int2_t{0, 0};
+        wb[u] = (n_ok && b_ok) ? ld<int2_t>(wrow + kb2) : int2_t{0, 0};
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        xa[u][mt] = (m_ok[mt] && a_ok) ? ld<half8_t>(xrow[mt] + ka) : hz;
+        xb[u][mt] = (m_ok[mt] && b_ok) ? ld<half8_t>(xrow[mt] + kb2) : hz;
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const half8_t fa = i8x8_to_half8(wa[u]), fb = i8x8_to_half8(wb[u]);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc[mt] = mfma16x16x32(fa, xa[u][mt], acc[mt]);
+        acc[mt] = mfma16x16x32(fb, xb[u][mt], acc[mt]);
+      }
     }
   }
   // lane (c, g) holds Y[m = 16 mt + c][n0 + 4g + r]
@@ -153,79 +174,126 @@ __global__ void __launch_bounds__(256) w8a16_reduce_kernel(
 }
 
 // ------------------------------------------------------------------------------------------
-// Large M: LDS-tiled MFMA GEMM.
+// Larger M: LDS-tiled MFMA GEMM, double-buffered.
 // ------------------------------------------------------------------------------------------
-constexpr int kLgBN = 128;     // output channels per workgroup
-constexpr int kLgBM = 128;     // activation rows per workgroup
-constexpr int kLgBK = 64;
-constexpr int kLgWP = kLgBK + 16;   // padded int8 row (bytes)
-constexpr int kLgXP = kLgBK + 8;    // padded fp16 row (halfs)
+// Workgroup = 4 wavefronts (2 x 2) on a BN (output channels) x BM (activation rows) tile, K step
+// 64. The int8 tile stays int8 in LDS (half the bytes) and is widened when it is read into the A
+// operand. Tile kt + 1 is fetched into registers while tile kt is multiplied out of LDS, then
+// stored into the other LDS buffer: one barrier per K step and the global latency hidden behind
+// the MFMAs. With split-K (gridDim.z > 1) each workgroup covers k_per_split columns of K and
+// writes fp32 partials for w8a16_reduce_kernel.
+constexpr int kTileBK = 64;
 
-__global__ void __launch_bounds__(256) w8a16_large_kernel(
+template <int BN, int BM>
+__global__ void __launch_bounds__(256) w8a16_tile_kernel(
     const half_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ wq,
     const void* __restrict__ scale, int scale_is_fp16, const half_t* __restrict__ bias,
-    half_t* __restrict__ y, int64_t ldy, int M, int N, int K) {
-  __shared__ int8_t s_w[kLgBN][kLgWP];
-  __shared__ half_t s_x[kLgBM][kLgXP];
+    half_t* __restrict__ y, int64_t ldy, int M, int N, int K, int k_per_split,
+    float* __restrict__ part) {
+  constexpr int BK = kTileBK;
+  constexpr int WP = BK + 16;                 // padded int8 row (bytes)
+  constexpr int XP = BK + 8;                  // padded fp16 row (halfs)
+  constexpr int TN = BN / 32, TM = BM / 32;   // 16 x 16 MFMA tiles per wavefront
+  constexpr int WCH = BN * BK / 8;            // 8-byte chunks of the W tile (K % 8 == 0)
+  constexpr int XCH = BM * BK / 8;            // 16-byte chunks of the X tile
+  constexpr int WPT = WCH / 256, XPT = XCH / 256;
+  static_assert(WPT * 256 == WCH && XPT * 256 == XCH, "tile must split evenly over 256 threads");
+  __shared__ int8_t s_w[2][BN][WP];
+  __shared__ half_t s_x[2][BM][XP];
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int c = lane & 15, g = lane >> 4;
-  const int wn = w >> 1, wm = w & 1;                 // 2 x 2 wavefronts, 64 x 64 each
-  const int n_base = blockIdx.x * kLgBN, m_base = blockIdx.y * kLgBM;
+  const int wn = w >> 1, wm = w & 1;
+  const int n_base = blockIdx.x * BN, m_base = blockIdx.y * BM;
+  const int kb = blockIdx.z * k_per_split;
+  const int ke = (kb + k_per_split < K) ? kb + k_per_split : K;
+  const int nk = (ke - kb + BK - 1) / BK;
 
-  float4_t acc[4][4];
+  int2_t wreg[WPT];
+  half8_t xreg[XPT];
+  auto gload = [&](int kt) {
+    const int k0 = kb + kt * BK;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) acc[i][j] = {0.f, 0.f, 0.f, 0.f};
-
-  for (int k0 = 0; k0 < K; k0 += kLgBK) {
-    // W tile: 128 rows x 64 bytes = 512 chunks of 16 bytes (K % 8 == 0: 8-byte granules).
-    for (int u = tid; u < kLgBN * (kLgBK / 8); u += 256) {
-      const int r = u / (kLgBK / 8), cc = u % (kLgBK / 8);
+    for (int i = 0; i < WPT; ++i) {
+      const int u = tid + 256 * i, r = u / (BK / 8), cc = u % (BK / 8);
       const int n = n_base + r, k = k0 + 8 * cc;
-      int2_t v = {0, 0};
-      if (n < N && k < K) v = ld<int2_t>(wq + (int64_t)n * K + k);
-      st<int2_t>(&s_w[r][8 * cc], v);
+      wreg[i] = (n < N && k < ke) ? ld<int2_t>(wq + (int64_t)n * K + k) : int2_t{0, 0};
     }
-    // X tile: 128 rows x 64 halfs = 1024 chunks of 16 bytes.
-    for (int u = tid; u < kLgBM * (kLgBK / 8); u += 256) {
-      const int r = u / (kLgBK / 8), cc = u % (kLgBK / 8);
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int u = tid + 256 * i, r = u / (BK / 8), cc = u % (BK / 8);
       const int mm = m_base + r, k = k0 + 8 * cc;
-      half8_t v = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (mm < M && k < K) v = ld<half8_t>(x + (int64_t)mm * ldx + k);
-      st<half8_t>(&s_x[r][8 * cc], v);
+      xreg[i] = (mm < M && k < ke) ? ld<half8_t>(x + (int64_t)mm * ldx + k)
+                                   : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
     }
-    __syncthreads();
+  };
+  auto lstore = [&](int buf) {
 #pragma unroll
-    for (int ks = 0; ks < kLgBK / 32; ++ks) {
-      half8_t a[4], bq[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        a[i] = i8x8_to_half8(ld<int2_t>(&s_w[wn * 64 + 16 * i + c][32 * ks + 8 * g]));
-#pragma unroll
-      for (int j = 0; j < 4; ++j) bq[j] = ld<half8_t>(&s_x[wm * 64 + 16 * j + c][32 * ks + 8 * g]);
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = mfma16x16x32(a[i], bq[j], acc[i][j]);
+    for (int i = 0; i < WPT; ++i) {
+      const int u = tid + 256 * i;
+      st<int2_t>(&s_w[buf][u / (BK / 8)][8 * (u % (BK / 8))], wreg[i]);
     }
-    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < XPT; ++i) {
+      const int u = tid + 256 * i;
+      st<half8_t>(&s_x[buf][u / (BK / 8)][8 * (u % (BK / 8))], xreg[i]);
+    }
+  };
+
+  float4_t acc[TN][TM];
+#pragma unroll
+  for (int i = 0; i < TN; ++i)
+#pragma unroll
+    for (int j = 0; j < TM; ++j) acc[i][j] = {0.f, 0.f, 0.f, 0.f};
+
+  if (nk > 0) {
+    gload(0);
+    lstore(0);
+  }
+  __syncthreads();
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) gload(kt + 1);              // in flight during the MFMAs below
+#pragma unroll
+    for (int ks = 0; ks < BK / 32; ++ks) {
+      half8_t a[TN], b[TM];
+#pragma unroll
+      for (int i = 0; i < TN; ++i)
+        a[i] = i8x8_to_half8(ld<int2_t>(&s_w[cur][wn * (BN / 2) + 16 * i + c][32 * ks + 8 * g]));
+#pragma unroll
+      for (int j = 0; j < TM; ++j) b[j] = ld<half8_t>(&s_x[cur][wm * (BM / 2) + 16 * j + c][32 * ks + 8 * g]);
+#pragma unroll
+      for (int i = 0; i < TN; ++i)
+#pragma unroll
+        for (int j = 0; j < TM; ++j) acc[i][j] = mfma16x16x32(a[i], b[j], acc[i][j]);
+    }
+    if (kt + 1 < nk) lstore(cur ^ 1);            // the other buffer was last read before the
+    __syncthreads();                             // previous barrier
   }
   // lane (c, g) of tile (i, j) holds Y[m = .. + 16 j + c][n = .. + 16 i + 4g + r]
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int nn = n_base + wn * 64 + 16 * i + 4 * g;
+  for (int i = 0; i < TN; ++i) {
+    const int nn = n_base + wn * (BN / 2) + 16 * i + 4 * g;
     float sc[4], bs[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const bool ok = nn + r < N;
-      sc[r] = ok ? load_scale(scale, scale_is_fp16, nn + r) : 0.f;
-      bs[r] = (ok && bias) ? (float)bias[nn + r] : 0.f;
+      sc[r] = (ok && !part) ? load_scale(scale, scale_is_fp16, nn + r) : 0.f;
+      bs[r] = (ok && !part && bias) ? (float)bias[nn + r] : 0.f;
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int mm = m_base + wm * 64 + 16 * j + c;
+    for (int j = 0; j < TM; ++j) {
+      const int mm = m_base + wm * (BM / 2) + 16 * j + c;
       if (mm >= M) continue;
+      if (part) {
+        float* dst = part + ((int64_t)blockIdx.z * M + mm) * N + nn;
+        if (nn + 3 < N) {
+          st<float4_t>(dst, acc[i][j]);
+        } else {
+          for (int r = 0; r < 4; ++r)
+            if (nn + r < N) dst[r] = acc[i][j][r];
+        }
+        continue;
+      }
       half_t* yp = y + (int64_t)mm * ldy + nn;
       if (nn + 3 < N) {
         const half4_t v = {(half_t)(acc[i][j][0] * sc[0] + bs[0]), (half_t)(acc[i][j][1] * sc[1] + bs[1]),
@@ -247,33 +315,61 @@ constexpr int kSmallMMax = 64;
 struct GemmPlan {
   bool small;
   int mt;          // m tiles (small path)
-  int splits;      // K splits (small path)
+  int bn, bm;      // tile shape (tile path)
+  int splits;      // K splits
   int k_per_split;
 };
 
 static GemmPlan plan_gemm(int M, int N, int K, int cus) {
-  GemmPlan p{M <= kSmallMMax, (M + 15) / 16, 1, K};
-  if (!p.small) return p;
-  // Fill the device with wavefronts (about eight per CU) by splitting K, keeping at least
-  // 256 K per split and the partial traffic (splits * M * N * 4 bytes) below 1/8 of the
-  // weight bytes.
-  const int64_t wgs = (N + 16 * kSmWaves - 1) / (16 * kSmWaves);
-  const int64_t target_wgs = 2LL * cus;
-  int splits = (int)((target_wgs + wgs - 1) / wgs);
-  const int max_by_k = K / 256 > 1 ? K / 256 : 1;
-  const int max_by_traffic = (int)((int64_t)K / (32LL * M) > 1 ? (int64_t)K / (32LL * M) : 1);
-  if (splits > max_by_k) splits = max_by_k;
-  if (splits > max_by_traffic) splits = max_by_traffic;
-  if (splits < 1) splits = 1;
-  int kps = (K + splits - 1) / splits;
-  kps = (kps + kSmKStep - 1) / kSmKStep * kSmKStep;
-  p.splits = (K + kps - 1) / kps;
-  p.k_per_split = kps;
+  GemmPlan p{M <= kSmallMMax, (M + 15) / 16, 0, 0, 1, K};
+  if (p.small) {
+    // Fill the device with wavefronts (about eight per CU) by splitting K, keeping at least
+    // 256 K per split and the partial traffic (splits * M * N * 4 bytes) below 1/8 of the
+    // weight bytes.
+    const int64_t wgs = (N + 16 * kSmWaves - 1) / (16 * kSmWaves);
+    const int64_t target_wgs = 2LL * cus;
+    int splits = (int)((target_wgs + wgs - 1) / wgs);
+    const int max_by_k = K / 256 > 1 ? K / 256 : 1;
+    const int max_by_traffic = (int)((int64_t)K / (32LL * M) > 1 ? (int64_t)K / (32LL * M) : 1);
+    if (splits > max_by_k) splits = max_by_k;
+    if (splits > max_by_traffic) splits = max_by_traffic;
+    if (splits < 1) splits = 1;
+    int kps = (K + splits - 1) / splits;
+    kps = (kps + kSmKStep - 1) / kSmKStep * kSmKStep;
+    p.splits = (K + kps - 1) / kps;
+    p.k_per_split = kps;
+    return p;
+  }
+  // Largest tile whose grid covers every CU; the smallest tile otherwise.
+  static const int tiles[3][2] = {{128, 128}, {128, 64}, {64, 64}};
+  int64_t grid = 0;
+  for (int t = 0; t < 3; ++t) {
+    p.bn = tiles[t][0];
+    p.bm = tiles[t][1];
+    grid = (int64_t)((N + p.bn - 1) / p.bn) * ((M + p.bm - 1) / p.bm);
+    if (grid >= cus) break;
+  }
+  // Still short of the CU count: split K, keeping >= 4 K steps per split and the fp32 partial
+  // traffic (splits * M * N * 4 bytes) within half the weight bytes.
+  if (grid < cus) {
+    const int nk = (K + kTileBK - 1) / kTileBK;
+    int splits = (int)((cus + grid - 1) / grid);
+    const int by_k = nk / 4 > 1 ? nk / 4 : 1;
+    const int64_t by_traffic64 = ((int64_t)N * K / 2) / ((int64_t)M * N * 4);
+    const int by_traffic = by_traffic64 > 1 ? (int)by_traffic64 : 1;
+    if (splits > by_k) splits = by_k;
+    if (splits > by_traffic) splits = by_traffic;
+    if (splits > 1) {
+      const int steps = (nk + splits - 1) / splits;
+      p.k_per_split = steps * kTileBK;
+      p.splits = (K + p.k_per_split - 1) / p.k_per_split;
+    }
+  }
   return p;
 }
 
 static size_t gemm_workspace(const GemmPlan& p, int M, int N) {
-  return (p.small && p.splits > 1) ? (size_t)p.splits * M * N * sizeof(float) : 0;
+  return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
 }
 
 }  // namespace ts
@@ -314,11 +410,15 @@ extern "C" int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const
   if (p.small) {
     float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const dim3 grid((N + 16 * kSmWaves - 1) / (16 * kSmWaves), p.splits);
+    const bool wide = K % 16 == 0 && aligned(wq, 16);
 #define TS_SM_CASE(MTV)                                                                          \
   case MTV:                                                                                      \
-    w8a16_small_kernel<MTV><<<grid, kSmWaves * 64, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16,   \
-                                                           bp, yp, ldy, M, N, K, p.k_per_split, \
-                                                           part);                               \
+    if (wide)                                                                                    \
+      w8a16_small_kernel<MTV, true><<<grid, kSmWaves * 64, 0, s>>>(                             \
+          xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part);        \
+    else                                                                                         \
+      w8a16_small_kernel<MTV, false><<<grid, kSmWaves * 64, 0, s>>>(                            \
+          xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part);        \
     break;
     switch (p.mt) {
       TS_SM_CASE(1)
@@ -334,9 +434,23 @@ extern "C" int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const
           part, p.splits, scale, scale_is_fp16, bp, yp, ldy, M, N);
     }
   } else {
-    const dim3 grid((N + kLgBN - 1) / kLgBN, (M + kLgBM - 1) / kLgBM);
-    w8a16_large_kernel<<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N,
-                                            K);
+    float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    const dim3 grid((N + p.bn - 1) / p.bn, (M + p.bm - 1) / p.bm, p.splits);
+    if (p.bn == 128 && p.bm == 128)
+      w8a16_tile_kernel<128, 128><<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy,
+                                                       M, N, K, p.k_per_split, part);
+    else if (p.bn == 128)
+      w8a16_tile_kernel<128, 64><<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy,
+                                                      M, N, K, p.k_per_split, part);
+    else
+      w8a16_tile_kernel<64, 64><<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy,
+                                                     M, N, K, p.k_per_split, part);
+    if (p.splits > 1) {
+      const int64_t total = (int64_t)M * N;
+      const int64_t want = (total + 255) / 256;
+      w8a16_reduce_kernel<<<(int)(want < 4096 ? want : 4096), 256, 0, s>>>(
+          part, p.splits, scale, scale_is_fp16, bp, yp, ldy, M, N);
+    }
   }
   return check_launch("w8a16_gemm");
 }
