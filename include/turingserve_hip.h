@@ -46,7 +46,7 @@ extern "C" {
 #define TS_ERR_DEVICE (-5)        /* device query failed */
 
 /* Decode kernel versions (ops/triton_decode_attention.py:1-10). */
-#define TS_DECODE_AUTO 0          /* the split policy of ops/triton_ops.py:44-57, retuned for 256 CUs */
+#define TS_DECODE_AUTO 0          /* split (v3) when one workgroup per (seq, KV head) leaves CUs idle */
 #define TS_DECODE_V1 1            /* one wavefront per (sequence, query head), VALU only */
 #define TS_DECODE_V2 2            /* one workgroup per (sequence, KV head), GQA group on MFMA */
 #define TS_DECODE_V3 3            /* v2 split over context partitions + reduction of the partials */
@@ -78,9 +78,13 @@ int ts_kv_write(const void* k, const void* v,
  * Decode attention over the first num_seqs rows of the flat batch (one query token each,
  * q row s belongs to sequence s). out[s, h*D:(h+1)*D] = softmax(q_s,h . K^T * scale) . V over
  * the seq_lens[s] cached tokens of sequence s; rows with seq_len 0 are written as zeros.
- * version: TS_DECODE_*. partition: tokens per split for v3 (multiple of 16; 0 = default).
- * max_seq_len: a host-side upper bound of seq_lens (inside graphs: max_model_len); it fixes
- * the split count of v3 exactly as ops/triton_ops.py:50-51 does.
+ * version: TS_DECODE_*. partition: tokens per split for v3 (multiple of 16). partition > 0
+ * gives the reference's fixed split grid: ceil(max_seq_len / partition) splits per sequence
+ * (ops/triton_ops.py:50-51), tokens past max_seq_len are not attended. partition = 0 gives the
+ * balanced schedule: the kernel numbers the splits of the whole batch densely and sizes them
+ * from the batch's total block count, so every launched workgroup gets about the same work
+ * and no split slot is idle (max_seq_len then only feeds TS_DECODE_AUTO's choice).
+ * max_seq_len: a host-side upper bound of seq_lens (inside graphs: max_model_len).
  * Workspace: ts_decode_workspace_bytes() bytes, 256-byte aligned (0 bytes for v1 / v2).
  * Replaces ops/triton_ops.py:35-57 and ops/triton_decode_attention.py:169-200.
  */

@@ -70,11 +70,18 @@ def test_workspace_sizes():
     assert lib.ts_decode_workspace_bytes(3, 64, 12, 2, 128, 4096, 256, 256) == want
     assert lib.ts_decode_workspace_bytes(2, 64, 12, 2, 128, 4096, 0, 256) == 0
     assert lib.ts_decode_workspace_bytes(1, 64, 12, 2, 128, 4096, 0, 256) == 0
-    # the automatic policy splits 64 x 2 (seq, KV head) units < 2 x 256 CUs at 4096 tokens ...
+    # balanced v3 (partition 0): nx = 256 CUs x 2 resident workgroups / 2 KV heads - 64 / 2 = 224
+    # split slots per KV head plus one per sequence, each slot holding all 12 heads
+    nb = (224 + 64) * 12
+    balanced = ((nb * 128 * 4 + 255) // 256 * 256) + 2 * ((nb * 4 + 255) // 256 * 256)
+    assert lib.ts_decode_workspace_bytes(3, 64, 12, 2, 128, 4096, 0, 256) == balanced
+    # the automatic policy splits 64 x 2 (seq, KV head) workgroups < 512 resident ones, with the
+    # fixed grid when a partition is named and the balanced schedule otherwise ...
     assert lib.ts_decode_workspace_bytes(0, 64, 12, 2, 128, 4096, 256, 256) == want
-    # ... but not short contexts or a batch that fills the device
-    assert lib.ts_decode_workspace_bytes(0, 64, 12, 2, 128, 1024, 256, 256) == 0
-    assert lib.ts_decode_workspace_bytes(0, 256, 12, 2, 128, 4096, 256, 256) == 0
+    assert lib.ts_decode_workspace_bytes(0, 64, 12, 2, 128, 1024, 0, 256) == balanced
+    # ... but not contexts of at most two minimum splits or a batch that fills the device
+    assert lib.ts_decode_workspace_bytes(0, 64, 12, 2, 128, 256, 0, 256) == 0
+    assert lib.ts_decode_workspace_bytes(0, 256, 12, 2, 128, 4096, 0, 256) == 0
     # W8A16: the large-M path needs none; small M splits K into fp32 partials
     assert lib.ts_w8a16_workspace_bytes(2048, 17920, 1536, 256) == 0
     ws = lib.ts_w8a16_workspace_bytes(1, 1536, 8960, 256)

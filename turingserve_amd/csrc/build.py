@@ -26,6 +26,10 @@ ARCH = "gfx950"
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs (gfx90a+ allows either file): with the default AGPR form the
+    # register allocator copied whole O^T accumulator sets between AGPRs around the rarely taken
+    # softmax rescale branch; the VGPR form needs no copies at the same occupancy.
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

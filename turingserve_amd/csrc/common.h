@@ -49,15 +49,19 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, kWave); }
 
+// NaN-propagating maximum (llvm.maximum, v_maximum3_f32 on gfx950). Unlike fmaxf it needs no
+// quieting of its inputs in IEEE mode, so reductions over MFMA results cost one op per value.
+__device__ __forceinline__ float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 // Max / sum over the four 16-lane rows of a wavefront (lanes c, c+16, c+32, c+48), on the VALU:
 // v_permlane16_swap(x, x) returns rows (0, 0, 2, 2) and (1, 1, 3, 3) of x, v_permlane32_swap(x, x)
 // returns (lo, lo) and (hi, hi) halves, so combining each pair is an all-reduce over 2 then 4
 // rows with no LDS round trip (gfx950 instructions).
 __device__ __forceinline__ float rows_max(float v) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  v = vmax(__uint_as_float(a[0]), __uint_as_float(a[1]));
   const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+  return vmax(__uint_as_float(b[0]), __uint_as_float(b[1]));
 }
 __device__ __forceinline__ float rows_sum(float v) {
   const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);

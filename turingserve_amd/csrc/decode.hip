@@ -23,6 +23,8 @@
 // The waves of a workgroup take consecutive blocks and merge their (m, l, acc) in LDS.
 #include <math.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "paged_kv.h"
 
@@ -102,46 +104,169 @@ __global__ void __launch_bounds__(64) decode_v1_kernel(
 // ------------------------------------------------------------------------------------------
 // v2 / v3 (ops/triton_decode_attention.py:60-163)
 // ------------------------------------------------------------------------------------------
-// One workgroup = NW wavefronts = one (sequence, split, KV head, head group). A wavefront owns
-// BPW consecutive 16-token blocks per round and issues all their loads before computing; the
-// block-table entries, seq_len and q are requested together at the start. Blocks are consumed
-// in pairs: two independent S^T chains, one online-softmax update per 32 tokens, and the P.V
-// product as v_mfma_f32_16x16x32_f16 over the 32 tokens of the pair. A sequence with one active
-// split writes its output here; otherwise the split's (m, l, acc) go to the workspace for
-// decode_merge_kernel.
-template <int D, int NW, int BPW>
+// Dense split map of v3. Sequence s has nb_s = ceil(len_s / 16) blocks (len_s clamped to
+// cap_blocks * 16) cut into n_s = ceil(nb_s / P) splits of P blocks; split j of sequence s is
+// slot C_s + j with C_s = sum_{t<s} n_t, so the launched slots carry no idle workgroups. P is
+// the caller's partition, or, when part_blocks == 0, P = max(kMinPartBlocks, ceil(TB / nx)) for
+// the batch's total TB blocks: then sum_s n_s <= nx + S and n_s <= nx whatever the lengths, and
+// every workgroup gets about the same number of blocks (the balanced schedule).
+constexpr int kMinPartBlocks = 8;
+
+struct SplitSlot {
+  int seq;     // sequence owning the slot (-1: the slot is past the batch's last split)
+  int first;   // C_s
+  int count;   // n_s
+  int part;    // P in blocks
+  int len;     // clamped seq_len
+};
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ int wave_inclusive_sum(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int t = __shfl_up(v, d, kWave);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+
+// Called by every thread of an NT-thread workgroup (S >= 1). slot >= 0: find the sequence that
+// owns `slot`; slot < 0: report sequence `seq`. s_map holds NT / 64 + 5 ints of LDS.
+template <int NT>
+__device__ SplitSlot split_lookup(const int* __restrict__ seq_lens, int S, int cap_blocks,
+                                  int part_blocks, int nx, int slot, int seq, int* s_map) {
+  constexpr int NWV = NT / kWave;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  const int cap = cap_blocks * kBlockSize;
+  auto clamp_len = [&](int len) { return len < 0 ? 0 : (len > cap ? cap : len); };
+  const int len0 = tid < S ? clamp_len(seq_lens[tid]) : 0;
+  int P = part_blocks;
+  if (P <= 0) {
+    int tb = (len0 + kBlockSize - 1) / kBlockSize;
+    for (int i = tid + NT; i < S; i += NT) tb += (clamp_len(seq_lens[i]) + kBlockSize - 1) / kBlockSize;
+    tb = wave_sum(tb);
+    if (lane == 0) s_map[w] = tb;
+    __syncthreads();
+    int total = 0;
+#pragma unroll
+    for (int k = 0; k < NWV; ++k) total += s_map[k];
+    P = (total + nx - 1) / nx;
+    P = P > kMinPartBlocks ? P : kMinPartBlocks;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    s_map[NWV] = -1;
+    s_map[NWV + 1] = 0;
+    s_map[NWV + 2] = 0;
+    s_map[NWV + 3] = 0;
+  }
+  int base = 0;
+  for (int c0 = 0; c0 < S; c0 += NT) {
+    const int i = c0 + tid;
+    const int len = c0 == 0 ? len0 : (i < S ? clamp_len(seq_lens[i]) : 0);
+    const int n = ((len + kBlockSize - 1) / kBlockSize + P - 1) / P;
+    const int incl = wave_inclusive_sum(n, lane);
+    if (lane == kWave - 1) s_map[w] = incl;
+    __syncthreads();
+    int off = base, tot = 0;
+#pragma unroll
+    for (int k = 0; k < NWV; ++k) {
+      const int v = s_map[k];
+      off += k < w ? v : 0;
+      tot += v;
+    }
+    const int excl = off + incl - n;
+    const bool hit = i < S && (slot >= 0 ? (n > 0 && slot >= excl && slot < excl + n) : i == seq);
+    if (hit) {
+      s_map[NWV] = i;
+      s_map[NWV + 1] = excl;
+      s_map[NWV + 2] = n;
+      s_map[NWV + 3] = len;
+    }
+    base += tot;
+    __syncthreads();
+  }
+  return {__builtin_amdgcn_readfirstlane(s_map[NWV]), __builtin_amdgcn_readfirstlane(s_map[NWV + 1]),
+          __builtin_amdgcn_readfirstlane(s_map[NWV + 2]), P,
+          __builtin_amdgcn_readfirstlane(s_map[NWV + 3])};
+}
+
+// One workgroup = NW wavefronts = one (split slot, KV head, head group) in v3 or one (sequence,
+// KV head, head group) in v2 (ws_acc == nullptr). The blocks of the range are consumed in pairs,
+// pair p by wavefront p % NW: two S^T chains, one online-softmax step per 32 tokens and the P.V
+// product as v_mfma_f32_16x16x32_f16 over the pair. Each wavefront keeps the next pair's loads in
+// flight while it multiplies the current one; block-table entries are wave-uniform scalar loads
+// issued a pair further ahead, so they never wait behind the K/V vector loads. The wavefronts
+// merge their (m, l, acc) in LDS; a sequence with one split writes its output here, otherwise
+// the split's partial goes to the workspace for decode_merge_kernel.
+template <int D, int NW>
 __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
     const half_t* __restrict__ q, int64_t q_st, int64_t q_sh, half_t* __restrict__ out,
     int64_t o_st, const half_t* __restrict__ kc, const half_t* __restrict__ vc, int64_t NB,
     const int* __restrict__ bt, int64_t bt_st, int max_blocks, const int* __restrict__ seq_lens,
-    int H, int KVH, int G, int HG, float scale_log2, int part_blocks, int num_splits,
+    int S, int H, int KVH, int G, int HG, float sl2, int cap_blocks, int part_blocks, int nx,
     float* __restrict__ ws_acc, float* __restrict__ ws_m, float* __restrict__ ws_l) {
-  static_assert(BPW % 2 == 0, "blocks are consumed in pairs");
   constexpr int KK = KvRegs<D>::KK;
   constexpr int VW = KvRegs<D>::VW;
   constexpr int TILES = KvRegs<D>::TILES;
   constexpr int OROW = D + 4;                    // padded LDS row (floats) against bank conflicts
+  typedef typename HalfVec<VW>::type VRow;
   __shared__ float s_o[NW][16][OROW];
   __shared__ float s_m[NW][16];
   __shared__ float s_l[NW][16];
+  __shared__ int s_map[NW + 5];
 
-  const int s = blockIdx.x, split = blockIdx.y;
   const int kvh = blockIdx.z / HG, hg = blockIdx.z % HG;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15, g = lane >> 4;
   const int hq = hg * 16 + c;                    // query head within the GQA group
   const bool head_ok = hq < G;
   const int nh = (G - hg * 16) < 16 ? (G - hg * 16) : 16;   // real heads in this group
   const int head0 = kvh * G + hg * 16;           // first query head of this group
-  const int blk_lo = split * part_blocks;
-  const int* btrow = bt + (int64_t)s * bt_st;
+  const bool split = ws_acc != nullptr;
 
-  // Requests that do not depend on seq_len go out first, together.
-  int seq_len = seq_lens[s];
-  int r0 = blk_lo + w * BPW;
-  int btv[BPW];
-#pragma unroll
-  for (int j = 0; j < BPW; ++j) btv[j] = btrow[(r0 + j) < max_blocks ? (r0 + j) : (max_blocks - 1)];
+  int s, seq_len, blk_lo, blk_hi, nsplit;
+  if (split) {
+    const SplitSlot sp = split_lookup<NW * 64>(seq_lens, S, cap_blocks, part_blocks, nx,
+                                               blockIdx.x, -1, s_map);
+    if (sp.seq < 0) return;                      // slot past the batch's last split
+    s = sp.seq;
+    seq_len = sp.len;
+    nsplit = sp.count;
+    const int nblk = (seq_len + kBlockSize - 1) / kBlockSize;
+    blk_lo = ((int)blockIdx.x - sp.first) * sp.part;
+    blk_hi = (blk_lo + sp.part) < nblk ? (blk_lo + sp.part) : nblk;
+  } else {
+    s = blockIdx.x;
+    seq_len = seq_lens[s];
+    seq_len = seq_len < 0 ? 0 : (seq_len > max_blocks * kBlockSize ? max_blocks * kBlockSize : seq_len);
+    seq_len = __builtin_amdgcn_readfirstlane(seq_len);
+    nsplit = 1;
+    blk_lo = 0;
+    blk_hi = (seq_len + kBlockSize - 1) / kBlockSize;
+    if (seq_len == 0) {                          // padding row: zeros (ops/reference.py:99,104-105)
+      for (int e = tid; e < nh * D; e += NW * 64)
+        out[(int64_t)s * o_st + (int64_t)(head0 + e / D) * D + e % D] = (half_t)0.f;
+      return;
+    }
+  }
+  // Tokens this range may use: a pair's second block can lie past the range (it then repeats
+  // the range's last block, a cache hit) while its tokens are still below seq_len.
+  const int tok_hi = blk_hi * kBlockSize < seq_len ? blk_hi * kBlockSize : seq_len;
+  const int npairs = (blk_hi - blk_lo + 1) >> 1;
+  const int* btrow = bt + (int64_t)s * bt_st;
+  auto blk_id = [&](int p, int j) {
+    int bi = blk_lo + 2 * p + j;
+    bi = bi < blk_hi ? bi : blk_hi - 1;
+    return clamp_block(btrow[bi], NB);
+  };
+
   half8_t qf[KK];
   {
     const half_t* qp = q + (int64_t)s * q_st + (int64_t)(kvh * G + hq) * q_sh;
@@ -155,31 +280,6 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
       }
     }
   }
-
-  seq_len = seq_len < 0 ? 0 : (seq_len > max_blocks * kBlockSize ? max_blocks * kBlockSize : seq_len);
-  const int nblk = (seq_len + kBlockSize - 1) / kBlockSize;
-  // A seq_len beyond the caller's max_seq_len is truncated to the launched splits, as the fixed
-  // split grid of ops/triton_ops.py:50-51 does; it never indexes past the workspace.
-  int n_active = (nblk + part_blocks - 1) / part_blocks;
-  n_active = n_active < num_splits ? n_active : num_splits;
-  // With split partials, every split slot that carries no partial (idle split, a sequence that
-  // fits one split, seq_len 0) is marked m = -inf so the merge needs no seq_len.
-  const bool idle = seq_len == 0 || blk_lo >= nblk;
-  if ((idle || n_active == 1) && num_splits > 1 && tid < nh)
-    ws_m[((int64_t)s * H + head0 + tid) * num_splits + split] = -INFINITY;
-  if (seq_len == 0) {                            // padding row: zeros (ops/reference.py:99,104-105)
-    if (split == 0) {
-      for (int e = tid; e < nh * D; e += NW * 64)
-        out[(int64_t)s * o_st + (int64_t)(head0 + e / D) * D + e % D] = (half_t)0.f;
-    }
-    return;
-  }
-  if (idle) return;                              // idle split of a short sequence
-  const int blk_hi = (blk_lo + part_blocks) < nblk ? (blk_lo + part_blocks) : nblk;
-  // Tokens this split may use: a pair's second block can lie past the split (or be a repeat of
-  // its last block) while its tokens are still below seq_len.
-  const int tok_hi = blk_hi * kBlockSize < seq_len ? blk_hi * kBlockSize : seq_len;
-
   const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
   float4_t o[TILES];
 #pragma unroll
@@ -188,98 +288,92 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
 
   const int64_t head_off = (int64_t)kvh * kBlockSize * D;
   const int64_t blk_stride = (int64_t)KVH * kBlockSize * D;
-  for (; r0 < blk_hi; r0 += NW * BPW) {
-    // Blocks past blk_hi repeat the last valid block (a cache hit, no extra HBM read), so the
-    // loads below carry no branches; the repeated data is masked out of the softmax.
-    int phys[BPW];
+  // Register budget per wavefront: K of one pair (refilled for the next pair as soon as the
+  // S^T MFMAs have consumed it) and V of two pairs (the next pair's V is requested a whole
+  // iteration before its P.V product). At D = 128 this keeps the kernel at two wavefronts per
+  // SIMD; the remaining latency is hidden by the other resident wavefronts. The refills are
+  // unconditional (past a wavefront's last pair they repeat its current pair, a cache hit) so
+  // every iteration has the same loads in flight and each wait covers exactly what it needs.
+  // Block-table entries are scalar loads issued two pairs ahead.
+  auto load_k = [&](const int (&id)[2], half8_t (&kf)[2][KK]) {
 #pragma unroll
-    for (int j = 0; j < BPW; ++j) {
-      int id = btv[j];
+    for (int j = 0; j < 2; ++j) load_k_block<D>(kc + id[j] * blk_stride + head_off, c, g, kf[j]);
+  };
+  auto load_v = [&](const int (&id)[2], VRow (&vr)[2][4]) {
 #pragma unroll
-      for (int i = 0; i < BPW; ++i)
-        if (r0 + j >= blk_hi && r0 + i == blk_hi - 1) id = btv[i];
-      phys[j] = clamp_block(id, NB);
-    }
-    half8_t kf[BPW][KK];
-    typename HalfVec<VW>::type vr[BPW][4];
+    for (int j = 0; j < 2; ++j) load_v_rows<D>(vc + id[j] * blk_stride + head_off, c, g, vr[j]);
+  };
+  auto ids_of = [&](int pp, int (&id)[2]) {
+    id[0] = blk_id(pp, 0);
+    id[1] = blk_id(pp, 1);
+  };
+  half8_t kf[2][KK];
+  VRow vA[2][4], vB[2][4];
+  int idk[2] = {0, 0}, idv[2] = {0, 0};        // next K refill / next V refill (two pairs on)
+  auto last_or = [&](int pp, int fallback) { return pp < npairs ? pp : fallback; };
+  // Pair p: S^T from kf, refill kf with pair p + NW, softmax, P.V from vr, refill vr with pair
+  // p + 2 NW.
+  auto step = [&](int p, VRow (&vr)[2][4]) {
+    int idk_next[2], idv_next[2];
+    ids_of(last_or(p + 2 * NW, last_or(p + NW, p)), idk_next);
+    ids_of(last_or(p + 3 * NW, last_or(p + 2 * NW, last_or(p + NW, p))), idv_next);
+    const int ba = blk_lo + 2 * p;
+    const int ta = ba * kBlockSize + 4 * g, tb = ta + kBlockSize;
+    float4_t sa = zero4, sb = zero4;             // S^T = K . Q^T: two independent MFMA chains
 #pragma unroll
-    for (int j = 0; j < BPW; ++j) {
-      const int64_t off = phys[j] * blk_stride + head_off;
-      load_k_block<D>(kc + off, c, g, kf[j]);
-      load_v_rows<D>(vc + off, c, g, vr[j]);
-    }
-    const int r_next = r0 + NW * BPW;
-    if (r_next < blk_hi) {                       // next round's table entries, early
-#pragma unroll
-      for (int j = 0; j < BPW; ++j)
-        btv[j] = btrow[(r_next + j) < max_blocks ? (r_next + j) : (max_blocks - 1)];
-    }
-#pragma unroll
-    for (int pr = 0; pr < BPW / 2; ++pr) {
-      const int ja = 2 * pr, jb = 2 * pr + 1;
-      const int ba = r0 + ja, bb = r0 + jb;
-      if (ba >= blk_hi) break;
-      // S^T = K . Q^T for both blocks: two independent MFMA chains
-      float4_t sa = zero4, sb = zero4;
-#pragma unroll
-      for (int kk = 0; kk < KK; ++kk) {
-        if constexpr (D >= 32) {
-          sa = mfma16x16x32(kf[ja][kk], qf[kk], sa);
-          sb = mfma16x16x32(kf[jb][kk], qf[kk], sb);
-        } else {
-          sa = mfma16x16x16(lo4(kf[ja][kk]), lo4(qf[kk]), sa);
-          sb = mfma16x16x16(lo4(kf[jb][kk]), lo4(qf[kk]), sb);
-        }
-      }
-      const int ta = ba * kBlockSize + 4 * g, tb = bb * kBlockSize + 4 * g;
-      const bool interior = (bb + 1) * kBlockSize <= tok_hi;   // every token of the pair valid
-      float sca[4], scb[4];
-      if (interior) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          sca[r] = sa[r] * scale_log2;
-          scb[r] = sb[r] * scale_log2;
-        }
+    for (int kk = 0; kk < KK; ++kk) {
+      if constexpr (D >= 32) {
+        sa = mfma16x16x32(kf[0][kk], qf[kk], sa);
+        sb = mfma16x16x32(kf[1][kk], qf[kk], sb);
       } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          sca[r] = (ta + r < tok_hi) ? sa[r] * scale_log2 : -INFINITY;
-          scb[r] = (tb + r < tok_hi) ? sb[r] * scale_log2 : -INFINITY;
-        }
-      }
-      const float bmax = rows_max(fmaxf(fmaxf(fmaxf(sca[0], sca[1]), fmaxf(sca[2], sca[3])),
-                                        fmaxf(fmaxf(scb[0], scb[1]), fmaxf(scb[2], scb[3]))));
-      const float m_new = fmaxf(m, bmax);        // finite: token 0 of block ba is valid
-      const float alpha = fast_exp2(m - m_new);
-      // O is rescaled only when some head's running max moved (alpha == 1 exactly otherwise),
-      // which after the first blocks is rare: the accumulators then stay in the MFMA registers.
-      const bool rescale = __ballot(m_new != m) != 0;
-      float pa[4], pb[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        pa[r] = fast_exp2(sca[r] - m_new);
-        pb[r] = fast_exp2(scb[r] - m_new);
-      }
-      l = l * alpha + (((pa[0] + pa[1]) + (pa[2] + pa[3])) + ((pb[0] + pb[1]) + (pb[2] + pb[3])));
-      m = m_new;
-      const half8_t p8 = {(half_t)pa[0], (half_t)pa[1], (half_t)pa[2], (half_t)pa[3],
-                          (half_t)pb[0], (half_t)pb[1], (half_t)pb[2], (half_t)pb[3]};
-      const bool tail_a = (ba + 1) * kBlockSize > tok_hi;
-      const bool tail_b = (bb + 1) * kBlockSize > tok_hi;
-      if (rescale) {
-#pragma unroll
-        for (int t = 0; t < TILES; ++t) o[t] *= alpha;
-      }
-#pragma unroll
-      for (int t = 0; t < TILES; ++t) {
-        half4_t va = {vr[ja][0][t], vr[ja][1][t], vr[ja][2][t], vr[ja][3][t]};
-        half4_t vb = {vr[jb][0][t], vr[jb][1][t], vr[jb][2][t], vr[jb][3][t]};
-        if (tail_a) va = mask_tokens(va, ta, tok_hi);
-        if (tail_b) vb = mask_tokens(vb, tb, tok_hi);
-        const half8_t v8 = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
-        o[t] = mfma16x16x32(v8, p8, o[t]);        // lane (c, g): dims VW (4g + r) + t of head c
+        sa = mfma16x16x16(lo4(kf[0][kk]), lo4(qf[kk]), sa);
+        sb = mfma16x16x16(lo4(kf[1][kk]), lo4(qf[kk]), sb);
       }
     }
+    load_k(idk, kf);
+    // Only the last pair of a range can reach past tok_hi (token 0 of block a never does), so
+    // the masked form is a separate, rarely taken path and the common one carries no selects.
+    auto finish = [&](auto masked) {
+      constexpr bool kMasked = decltype(masked)::value;
+      const bool tail_a = kMasked && (ba + 1) * kBlockSize > tok_hi;
+      if constexpr (kMasked) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          sa[r] = ta + r < tok_hi ? sa[r] : -INFINITY;
+          sb[r] = tb + r < tok_hi ? sb[r] : -INFINITY;
+        }
+      }
+      const SoftmaxStep st = softmax_pair(sa, sb, sl2, m, l);
+      // lane (c, g) of tile t: dims VW (4g + r) + t of head c
+      pv_update<TILES>(o, st, [&](int t) {
+        return vt_operand<VW>(vr[0], vr[1], t, tail_a, kMasked, ta, tb, tok_hi);
+      });
+    };
+    if ((ba + 2) * kBlockSize > tok_hi)
+      finish(std::true_type());
+    else
+      finish(std::false_type());
+    load_v(idv, vr);
+    idk[0] = idk_next[0];
+    idk[1] = idk_next[1];
+    idv[0] = idv_next[0];
+    idv[1] = idv_next[1];
+  };
+  int p = w;
+  if (p < npairs) {
+    int id0[2], id1[2];
+    ids_of(p, id0);
+    ids_of(last_or(p + NW, p), id1);
+    load_k(id0, kf);
+    load_v(id0, vA);
+    load_v(id1, vB);
+    ids_of(last_or(p + NW, p), idk);
+    ids_of(last_or(p + 2 * NW, last_or(p + NW, p)), idv);
+  }
+  for (; p < npairs; p += 2 * NW) {
+    step(p, vA);
+    if (p + NW >= npairs) break;
+    step(p + NW, vB);
   }
   l = rows_sum(l);
 
@@ -293,7 +387,6 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
 #pragma unroll
     for (int r = 0; r < 4; ++r) s_o[w][c][VW * (4 * g + r) + t] = o[t][r];
   __syncthreads();
-  const bool single = n_active == 1;
   for (int e = tid; e < nh * D; e += NW * 64) {
     const int hh = e / D, d = e % D;
     float M = -INFINITY;
@@ -306,10 +399,10 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
       L += wt * s_l[ww][hh];
       O += wt * s_o[ww][hh][d];
     }
-    if (single) {
+    if (nsplit == 1) {
       out[(int64_t)s * o_st + (int64_t)(head0 + hh) * D + d] = (half_t)(O / L);
     } else {
-      const int64_t pidx = ((int64_t)s * H + head0 + hh) * num_splits + split;
+      const int64_t pidx = (int64_t)blockIdx.x * H + head0 + hh;
       ws_acc[pidx * D + d] = O;
       if (d == 0) {
         ws_m[pidx] = M;
@@ -321,92 +414,101 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
 
 // Merge of the split partials (ops/triton_decode_attention.py:144-163): M = max m_j,
 // w_j = 2^(m_j - M), out = sum w_j acc_j / sum w_j l_j. One workgroup per (sequence, KV head,
-// head group), two dependent memory steps: every (head, split) statistic is loaded at once
-// (slots without a partial hold m = -inf, so seq_len is not needed), then the partials of the
-// active splits (a compact list, identical for all heads) are read without branches. A group
-// whose slots are all -inf was finished by the first kernel.
+// head group): it recomputes the split map, then loads every (head, split) statistic and the
+// first chunk of partials at once (two dependent memory steps in all for up to 16 splits).
+// Sequences with one split were finished by the first kernel; a sequence with none (seq_len 0)
+// gets zeros here.
+constexpr int kMaxSplits = 256;
+
 template <int D>
 __global__ void __launch_bounds__(256) decode_merge_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_m,
-    const float* __restrict__ ws_l, half_t* __restrict__ out, int64_t o_st, int H, int G, int HG,
-    int num_splits) {
-  constexpr int kMaxSplits = 256;               // the launcher caps num_splits
+    const float* __restrict__ ws_l, half_t* __restrict__ out, int64_t o_st,
+    const int* __restrict__ seq_lens, int S, int H, int G, int HG, int cap_blocks,
+    int part_blocks, int nx, int nslots) {
   __shared__ float s_w[16][kMaxSplits];
   __shared__ float s_l[16][kMaxSplits];
   __shared__ float s_inv[16];
-  __shared__ int s_act[kMaxSplits];             // splits that carry a partial (same for all heads)
-  __shared__ int s_nact;
+  __shared__ int s_map[4 + 5];
   const int s = blockIdx.x, kvh = blockIdx.y / HG, hg = blockIdx.y % HG;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int nh = (G - hg * 16) < 16 ? (G - hg * 16) : 16;
   const int head0 = kvh * G + hg * 16;
-  const int64_t base0 = ((int64_t)s * H + head0) * num_splits;
-  for (int e = tid; e < nh * num_splits; e += 256) {
-    const int hh = e / num_splits, j = e % num_splits;
-    s_w[hh][j] = ws_m[base0 + (int64_t)hh * num_splits + j];
-    s_l[hh][j] = ws_l[base0 + (int64_t)hh * num_splits + j];
+  const SplitSlot sp = split_lookup<256>(seq_lens, S, cap_blocks, part_blocks, nx, -1, s, s_map);
+  if (sp.count == 1) return;                     // written by the first kernel
+  if (sp.count == 0) {                           // padding row: zeros (ops/reference.py:99,104-105)
+    for (int e = tid; e < nh * D; e += 256)
+      out[(int64_t)s * o_st + (int64_t)(head0 + e / D) * D + e % D] = (half_t)0.f;
+    return;
   }
-  __syncthreads();
-  if (w == 0) {                                 // compact list of active splits (ballot + popcount)
-    int n = 0;
-    for (int j0 = 0; j0 < num_splits; j0 += 64) {
-      const int j = j0 + lane;
-      const bool act = j < num_splits && s_w[0][j] != -INFINITY;
-      const uint64_t mask = __ballot(act);
-      if (act) s_act[n + __popcll(mask & ((1ull << lane) - 1))] = j;
-      n += __popcll(mask);
-    }
-    if (lane == 0) s_nact = n;
-  }
-  for (int hh = w; hh < nh; hh += 4) {
-    float M = -INFINITY;
-    for (int j = lane; j < num_splits; j += 64) M = fmaxf(M, s_w[hh][j]);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
-    float L = 0.f;
-    for (int j = lane; j < num_splits; j += 64) {
-      const float m = s_w[hh][j];
-      const float wt = m == -INFINITY ? 0.f : fast_exp2(m - M);
-      s_w[hh][j] = wt;
-      L += m == -INFINITY ? 0.f : wt * s_l[hh][j];   // a slot without a partial holds garbage l
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) L += shfl_xor(L, off);
-    if (lane == 0) s_inv[hh] = M == -INFINITY ? 0.f : 1.f / L;
-  }
-  __syncthreads();
-  const int nact = s_nact;
-  if (nact == 0) return;                        // finished (or zeroed) by the first kernel
-  // Each thread owns up to EPT outputs; for every chunk of CH active splits all EPT x CH loads
-  // are issued before any is consumed (indices past nact repeat the last split with weight 0).
+  int n = sp.count < kMaxSplits ? sp.count : kMaxSplits;     // the plan keeps n_s <= 255
+  n = sp.first + n <= nslots ? n : nslots - sp.first;
+  if (n < 1) return;                             // unreachable for a consistent plan
+  const int64_t slot0 = sp.first;
+  // Each thread owns up to EPT outputs; for every chunk of CH splits all EPT x CH loads are
+  // issued before any is consumed (indices past n repeat the last split with weight 0). The
+  // first chunk does not depend on the statistics, so it goes out together with them.
   constexpr int EPT = 4, CH = 16;
-  for (int e0 = tid; e0 < nh * D; e0 += 256 * EPT) {
-    float O[EPT];
-    const float* accp[EPT];
-    int hh_[EPT];
-    bool ok[EPT];
+  float v[EPT][CH];
+  const float* accp[EPT];
+  int hh_[EPT];
+  bool ok[EPT];
+  auto setup = [&](int e0) {
 #pragma unroll
     for (int q = 0; q < EPT; ++q) {
       const int e = e0 + 256 * q;
       ok[q] = e < nh * D;
       const int ee = ok[q] ? e : 0;
       hh_[q] = ee / D;
-      accp[q] = ws_acc + (base0 + (int64_t)hh_[q] * num_splits) * D + ee % D;
-      O[q] = 0.f;
+      accp[q] = ws_acc + (slot0 * H + head0 + hh_[q]) * D + ee % D;
     }
-    for (int t0 = 0; t0 < nact; t0 += CH) {
-      float v[EPT][CH];
+  };
+  auto load_chunk = [&](int t0) {
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      const int j = (t0 + u) < n ? (t0 + u) : (n - 1);
+#pragma unroll
+      for (int q = 0; q < EPT; ++q) v[q][u] = accp[q][(int64_t)j * H * D];
+    }
+  };
+  setup(tid);
+  load_chunk(0);
+  for (int e = tid; e < nh * n; e += 256) {
+    const int hh = e / n, j = e % n;
+    const int64_t pidx = (slot0 + j) * H + head0 + hh;
+    s_w[hh][j] = ws_m[pidx];
+    s_l[hh][j] = ws_l[pidx];
+  }
+  __syncthreads();
+  for (int hh = w; hh < nh; hh += 4) {
+    float M = -INFINITY;
+    for (int j = lane; j < n; j += 64) M = fmaxf(M, s_w[hh][j]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
+    float L = 0.f;
+    for (int j = lane; j < n; j += 64) {
+      const float wt = fast_exp2(s_w[hh][j] - M);
+      s_w[hh][j] = wt;
+      L += wt * s_l[hh][j];
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) L += shfl_xor(L, off);
+    if (lane == 0) s_inv[hh] = 1.f / L;
+  }
+  __syncthreads();
+  for (int e0 = tid; e0 < nh * D; e0 += 256 * EPT) {
+    if (e0 != tid) {
+      setup(e0);
+      load_chunk(0);
+    }
+    float O[EPT] = {};
+    for (int t0 = 0; t0 < n; t0 += CH) {
+      if (t0 > 0) load_chunk(t0);
 #pragma unroll
       for (int u = 0; u < CH; ++u) {
-        const int j = s_act[(t0 + u) < nact ? (t0 + u) : (nact - 1)];
+        const int j = (t0 + u) < n ? (t0 + u) : (n - 1);
 #pragma unroll
-        for (int q = 0; q < EPT; ++q) v[q][u] = accp[q][(int64_t)j * D];
-      }
-#pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        const int j = s_act[(t0 + u) < nact ? (t0 + u) : (nact - 1)];
-#pragma unroll
-        for (int q = 0; q < EPT; ++q) O[q] += (t0 + u < nact) ? s_w[hh_[q]][j] * v[q][u] : 0.f;
+        for (int q = 0; q < EPT; ++q) O[q] += (t0 + u < n) ? s_w[hh_[q]][j] * v[q][u] : 0.f;
       }
     }
 #pragma unroll
@@ -423,41 +525,59 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(
 #ifndef TS_DECODE_WAVES
 #define TS_DECODE_WAVES 4
 #endif
-#ifndef TS_DECODE_BLOCKS_PER_WAVE
-#define TS_DECODE_BLOCKS_PER_WAVE 4
-#endif
 constexpr int kDecodeWaves = TS_DECODE_WAVES;               // wavefronts per workgroup
-constexpr int kBlocksPerWave = TS_DECODE_BLOCKS_PER_WAVE;   // blocks loaded up front per round
-constexpr int kDefaultPartition = kDecodeWaves * kBlocksPerWave * kBlockSize;   // 256 tokens
+
+// Workgroups of decode_mfma_kernel resident per CU (4 wavefronts each, one per SIMD), from the
+// kernel's VGPR use (512 per SIMD lane): 6 waves per SIMD up to D = 32, 3 at D = 64, 2 at
+// D = 128 (236 VGPRs), 1 at D = 256.
+static int decode_wgs_per_cu(int D) { return D <= 32 ? 6 : (D == 64 ? 3 : (D == 128 ? 2 : 1)); }
 
 struct SplitPlan {
   int version;        // 1, 2 or 3 after resolving AUTO
-  int part_blocks;    // blocks per split
-  int num_splits;
+  int part_blocks;    // v3: blocks per split, 0 = balanced
+  int nx;             // v3 balanced: target split count per (KV head, head group)
+  int nslots;         // v3: launched split slots per (KV head, head group)
+  int cap_blocks;     // v3 fixed partition: blocks of a sequence covered by the launched splits
 };
 
-static SplitPlan plan_decode(int version, int S, int H, int KVH, int max_seq_len, int partition,
-                             int cu_count) {
-  SplitPlan p{version, 1 << 30, 1};
+// Explicit v3 partition (ops/triton_ops.py:50-51): num_splits = ceil(max_seq_len / partition)
+// split slots per sequence; partition = 0 selects the balanced schedule. AUTO splits whenever one
+// workgroup per (sequence, KV head, head group) cannot fill the device and contexts are longer
+// than two minimum splits (the reference's rule, ops/triton_ops.py:44-45, with the CU count and
+// this kernel's residency), and uses the balanced schedule unless a partition is given.
+static SplitPlan plan_decode(int version, int S, int H, int KVH, int D, int max_seq_len,
+                             int partition, int cu_count) {
+  SplitPlan p{version, 0, 0, 0, 0};
   const int G = H / KVH;
   const int HG = (G + 15) / 16;
+  const int64_t groups = (int64_t)KVH * HG;
+  const int64_t wg_slots = (int64_t)cu_count * decode_wgs_per_cu(D);
   if (version == TS_DECODE_AUTO) {
-    // ops/triton_ops.py:44-45: split when the (sequence, KV head) grid cannot fill the device
-    // twice over and the context is long; the CU count replaces the SM count.
-    const bool use_split = (int64_t)S * KVH * HG < 2LL * cu_count && max_seq_len > 1024;
+    const bool use_split = (int64_t)S * groups < wg_slots && max_seq_len > 2 * kMinPartBlocks * kBlockSize;
     p.version = use_split ? TS_DECODE_V3 : TS_DECODE_V2;
   }
-  if (p.version == TS_DECODE_V3) {
-    int part = partition > 0 ? partition : kDefaultPartition;
-    part = ((part + kBlockSize - 1) / kBlockSize) * kBlockSize;
-    p.part_blocks = part / kBlockSize;
-    const int max_blk = (max_seq_len + kBlockSize - 1) / kBlockSize;
-    p.num_splits = (max_blk + p.part_blocks - 1) / p.part_blocks;   // ops/triton_ops.py:50-51
-    if (p.num_splits > 256) {                    // the merge keeps <= 256 split weights in LDS
-      p.part_blocks = (max_blk + 255) / 256;
-      p.num_splits = (max_blk + p.part_blocks - 1) / p.part_blocks;
+  if (p.version != TS_DECODE_V3) return p;
+  const int max_blk = (max_seq_len + kBlockSize - 1) / kBlockSize;
+  if (partition > 0) {
+    p.part_blocks = partition / kBlockSize;
+    int num_splits = (max_blk + p.part_blocks - 1) / p.part_blocks;
+    if (num_splits > kMaxSplits - 1) {            // the merge keeps < 256 split weights in LDS
+      p.part_blocks = (max_blk + kMaxSplits - 2) / (kMaxSplits - 1);
+      num_splits = (max_blk + p.part_blocks - 1) / p.part_blocks;
     }
-    if (p.num_splits < 1) p.num_splits = 1;
+    num_splits = num_splits < 1 ? 1 : num_splits;
+    p.cap_blocks = num_splits * p.part_blocks;
+    p.nslots = S * num_splits;
+  } else {
+#ifdef TS_DECODE_NX
+    int64_t nx = TS_DECODE_NX;                   // tuning override
+#else
+    int64_t nx = wg_slots / groups - S / 2;      // launched slots nx + S ~ resident workgroups
+#endif
+    nx = nx < 16 ? 16 : (nx > kMaxSplits - 1 ? kMaxSplits - 1 : nx);
+    p.nx = (int)nx;
+    p.cap_blocks = 1 << 30;
+    p.nslots = p.nx + S;
   }
   return p;
 }
@@ -468,11 +588,12 @@ struct WsLayout {
   size_t acc, m, l, total;
 };
 
-// [acc: S * H * splits * D fp32][m: S * H * splits][l: S * H * splits]
-static WsLayout ws_layout(const SplitPlan& p, int S, int H, int D) {
+// [acc: slots * H * D fp32][m: slots * H][l: slots * H]; a slot's partial of query head h sits at
+// slot * H + h, so the (KV head, head group) grids share the slot numbering without overlap.
+static WsLayout ws_layout(const SplitPlan& p, int H, int D) {
   WsLayout w{0, 0, 0, 0};
-  if (p.version != TS_DECODE_V3 || p.num_splits <= 1) return w;
-  const size_t n = (size_t)S * H * p.num_splits;
+  if (p.version != TS_DECODE_V3) return w;
+  const size_t n = (size_t)p.nslots * H;
   w.acc = 0;
   w.m = align256(n * D * sizeof(float));
   w.l = w.m + align256(n * sizeof(float));
@@ -493,22 +614,23 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
     return;
   }
   const int HG = (G + 15) / 16;
-  float *ws_acc = nullptr, *ws_m = nullptr, *ws_l = nullptr;
-  if (p.num_splits > 1) {
-    const WsLayout w = ws_layout(p, S, H, D);
-    char* b = static_cast<char*>(ws);
-    ws_acc = reinterpret_cast<float*>(b + w.acc);
-    ws_m = reinterpret_cast<float*>(b + w.m);
-    ws_l = reinterpret_cast<float*>(b + w.l);
+  if (p.version == TS_DECODE_V2) {
+    decode_mfma_kernel<D, kDecodeWaves><<<dim3(S, 1, KVH * HG), kDecodeWaves * 64, 0, st>>>(
+        q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,
+        scale_log2, 0, 0, 0, nullptr, nullptr, nullptr);
+    return;
   }
-  decode_mfma_kernel<D, kDecodeWaves, kBlocksPerWave>
-      <<<dim3(S, p.num_splits, KVH * HG), kDecodeWaves * 64, 0, st>>>(
-          q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, H, KVH, G, HG,
-          scale_log2, p.part_blocks, p.num_splits, ws_acc, ws_m, ws_l);
-  if (p.num_splits > 1) {
-    decode_merge_kernel<D><<<dim3(S, KVH * HG), 256, 0, st>>>(ws_acc, ws_m, ws_l, out, o_st, H,
-                                                              G, HG, p.num_splits);
-  }
+  const WsLayout w = ws_layout(p, H, D);
+  char* b = static_cast<char*>(ws);
+  float* ws_acc = reinterpret_cast<float*>(b + w.acc);
+  float* ws_m = reinterpret_cast<float*>(b + w.m);
+  float* ws_l = reinterpret_cast<float*>(b + w.l);
+  const int cap = p.cap_blocks < max_blocks ? p.cap_blocks : max_blocks;
+  decode_mfma_kernel<D, kDecodeWaves><<<dim3(p.nslots, 1, KVH * HG), kDecodeWaves * 64, 0, st>>>(
+      q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,
+      scale_log2, cap, p.part_blocks, p.nx, ws_acc, ws_m, ws_l);
+  decode_merge_kernel<D><<<dim3(S, KVH * HG), 256, 0, st>>>(
+      ws_acc, ws_m, ws_l, out, o_st, sl, S, H, G, HG, cap, p.part_blocks, p.nx, p.nslots);
 }
 
 static bool supported_head_dim(int D) {
@@ -524,9 +646,9 @@ extern "C" size_t ts_decode_workspace_bytes(int32_t version, int32_t num_seqs, i
                                             int32_t max_seq_len, int32_t partition,
                                             int32_t cu_count) {
   if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
-  const SplitPlan p = plan_decode(version, num_seqs, num_heads, num_kv_heads, max_seq_len,
-                                  partition, cu_count > 0 ? cu_count : 256);
-  return ws_layout(p, num_seqs, num_heads, head_dim).total;
+  const SplitPlan p = plan_decode(version, num_seqs, num_heads, num_kv_heads, head_dim,
+                                  max_seq_len, partition, cu_count > 0 ? cu_count : 256);
+  return ws_layout(p, num_heads, head_dim).total;
 }
 
 extern "C" int ts_decode_attention(int32_t version, const void* q, int64_t q_stride_t,
@@ -561,9 +683,9 @@ extern "C" int ts_decode_attention(int32_t version, const void* q, int64_t q_str
   int cus = 0;
   int st = device_cu_count(&cus);
   if (st != TS_OK) return st;
-  const SplitPlan p = plan_decode(version, num_seqs, num_heads, num_kv_heads, max_seq_len,
-                                  partition, cus);
-  const size_t need = ws_layout(p, num_seqs, num_heads, head_dim).total;
+  const SplitPlan p = plan_decode(version, num_seqs, num_heads, num_kv_heads, head_dim,
+                                  max_seq_len, partition, cus);
+  const size_t need = ws_layout(p, num_heads, head_dim).total;
   TS_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 256)),
              TS_ERR_WORKSPACE, "decode_attention: workspace of %zu bytes (256-aligned) needed, got %zu",
              need, workspace_bytes);

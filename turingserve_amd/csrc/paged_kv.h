@@ -66,4 +66,74 @@ __device__ __forceinline__ half4_t mask_tokens(half4_t v, int tok0, int seq_len)
   return v;
 }
 
+// Token-packed A operand of O^T tile t over a pair of blocks (a, b): lane (c, g) gets tokens
+// 4g .. 4g+3 of each block for dim VW c' + t, taken from the coalesced V rows (two byte permutes
+// per block). Blocks with tokens at or past tok_hi are masked when `tail_*` is set.
+template <int VW, typename VRow>
+__device__ __forceinline__ half8_t vt_operand(const VRow (&va)[4], const VRow (&vb)[4], int t,
+                                              bool tail_a, bool tail_b, int ta, int tb, int tok_hi) {
+  half4_t x = {va[0][t], va[1][t], va[2][t], va[3][t]};
+  half4_t y = {vb[0][t], vb[1][t], vb[2][t], vb[3][t]};
+  if (tail_a) x = mask_tokens(x, ta, tok_hi);
+  if (tail_b) y = mask_tokens(y, tb, tok_hi);
+  return {x[0], x[1], x[2], x[3], y[0], y[1], y[2], y[3]};
+}
+
+// Online softmax with a lazy reference point (in scaled log2 units). A row's reference m moves
+// only when a new score exceeds it by more than kRescaleLog2, so P = 2^(s - m) <= 2^8 stays well
+// inside fp16 (with the same relative rounding as P <= 1) and the O accumulators are rescaled a
+// few times per row instead of at every new maximum. O / l does not depend on the reference
+// point, and merges weight each partial by 2^(m_i - max m), which is exact for any reference.
+constexpr float kRescaleLog2 = 8.f;
+
+// One step over 32 keys (a pair of 16-token blocks) for the 16 rows of a wavefront: sa / sb are
+// the raw S^T tiles (lane (c, g): keys 4g + r of row c; masked keys already -inf) and
+// sl2 = scale * log2(e) > 0. Updates the row's reference m and this lane's partial sum l and
+// returns P^T rounded to fp16 (the B operand of v_mfma_f32_16x16x32_f16: keys 4g .. 4g+3 of
+// block a, then of block b) with the factor alpha the O^T accumulators must be scaled by first
+// when `rescale` is set (alpha is 1 for rows whose reference did not move, 0 on a row's first
+// visible key, where O is still 0).
+struct SoftmaxStep {
+  half8_t p;
+  float alpha;
+  bool rescale;
+};
+
+__device__ __forceinline__ SoftmaxStep softmax_pair(const float4_t& sa, const float4_t& sb,
+                                                    float sl2, float& m, float& l) {
+  const float raw = vmax(vmax(vmax(sa[0], sa[1]), vmax(sa[2], sa[3])),
+                         vmax(vmax(sb[0], sb[1]), vmax(sb[2], sb[3])));
+  const float bm = rows_max(raw) * sl2;            // -inf when every key of the row is masked
+  const bool move = bm > m + kRescaleLog2;         // m = -inf: the first visible key moves it
+  SoftmaxStep st;
+  st.rescale = __ballot(move) != 0;
+  st.alpha = 1.f;
+  if (st.rescale) {
+    st.alpha = move ? fast_exp2(m - bm) : 1.f;     // m = -inf -> 0
+    l *= st.alpha;
+    m = move ? bm : m;
+  }
+  const float neg = m == -INFINITY ? 0.f : -m;     // rows with no visible key: every P is 0
+  float p[8];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    p[r] = fast_exp2(fmaf(sa[r], sl2, neg));
+    p[4 + r] = fast_exp2(fmaf(sb[r], sl2, neg));
+  }
+  l += ((p[0] + p[1]) + (p[2] + p[3])) + ((p[4] + p[5]) + (p[6] + p[7]));
+  st.p = {(half_t)p[0], (half_t)p[1], (half_t)p[2], (half_t)p[3],
+          (half_t)p[4], (half_t)p[5], (half_t)p[6], (half_t)p[7]};
+  return st;
+}
+
+// O^T = alpha O^T + V^T . P^T over the pair for all TILES tiles. The scaling is unconditional
+// (alpha is exactly 1 unless a reference point moved, so the result is the same as skipping it):
+// a conditional multiply before the MFMAs left two accumulator sets live across the branch.
+template <int TILES, typename VOperand>
+__device__ __forceinline__ void pv_update(float4_t (&o)[TILES], const SoftmaxStep& st,
+                                          VOperand vt) {
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) o[t] = mfma16x16x32(vt(t), st.p, o[t] * st.alpha);
+}
+
 }  // namespace ts

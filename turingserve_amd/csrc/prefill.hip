@@ -5,14 +5,17 @@
 // causal mask, ops/reference.py:60-77). Online softmax in fp32; P is rounded to fp16 before
 // the P.V product (ops/triton_prefill_attention.py:57).
 //
-// Workgroup = BM = 64 query rows of one query head, four wavefronts of 16 rows each.
-// Per key tile of BN = 64 keys the workgroup stages K[BN][D] (row-major) and V^T[D][BN]
-// (transposed while storing: two keys packed per 4-byte LDS write) in LDS, gathered through
-// the block table. Each wavefront then computes
-//   S^T[64 keys][16 rows] = K . Q^T        v_mfma_f32_16x16x32_f16, Q^T kept in registers
-//   O^T[D][16 rows]     += V^T . P^T      v_mfma_f32_16x16x32_f16, P^T straight from S^T
-// so every per-row softmax statistic sits in lane column c = lane % 16 (see common.h).
-// Tiles past a wavefront's causal limit are skipped; workgroups are launched longest-first.
+// Workgroup = 32 query rows of one query head and four wavefronts. Every wavefront holds Q^T of
+// all 32 rows (two 16-row column groups) in registers and reads 16-token K/V blocks straight
+// from the paged cache into MFMA operand registers, the way the decode kernel does (K in its
+// natural layout, V as coalesced rows permuted in registers); the wavefronts take the pairs of
+// blocks round-robin, each keeping its next pair in flight while it multiplies the current one:
+//   S^T[32 keys][16 rows] = K . Q^T        two v_mfma_f32_16x16x32_f16 chains per row group
+//   O^T[D][16 rows]     += V^T . P^T      v_mfma_f32_16x16x32_f16 over the 32 keys of the pair
+// so every per-row softmax statistic sits in lane column c = lane % 16 (see common.h). The four
+// partial (m, l, O) states of a row are merged in LDS at the end, so a short chunk on a long
+// prefix still spreads over the whole device without global partials. Pairs past the tile's
+// causal limit are never loaded; workgroups are launched longest-first.
 #include <math.h>
 
 #include "common.h"
@@ -21,188 +24,7 @@
 namespace ts {
 
 constexpr float kLog2eP = 1.4426950408889634f;
-constexpr int kPfBM = 64;
-constexpr int kPfBN = 64;
-constexpr int kPfWaves = 4;
 
-template <int D>
-__global__ void __launch_bounds__(kPfWaves * 64) prefill_kernel(
-    const half_t* __restrict__ q, int64_t q_st, int64_t q_sh, half_t* __restrict__ out,
-    int64_t o_st, int64_t num_tokens, const half_t* __restrict__ kc,
-    const half_t* __restrict__ vc, int64_t NB, const int* __restrict__ bt, int64_t bt_st,
-    int max_blocks, const int* __restrict__ seq_lens, const int* __restrict__ qsl,
-    int num_decode, int H, int KVH, float scale_log2) {
-  constexpr int KP = D + 8;          // padded K row (halfs)
-  constexpr int VP = kPfBN + 8;      // padded V^T row (halfs)
-  constexpr int KK = D >= 32 ? D / 32 : 1;
-  constexpr int TILES = D / 16;
-  constexpr int NT = kPfBN / 16;     // 16-key sub-tiles per key tile
-  __shared__ half_t s_k[kPfBN][KP];
-  __shared__ half_t s_vt[D][VP];
-
-  const int mtile = gridDim.x - 1 - blockIdx.x;       // longest (last) query tiles first
-  const int b = num_decode + blockIdx.y;
-  const int h = blockIdx.z;
-  const int G = H / KVH, kvh = h / G;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
-  const int c = lane & 15, g = lane >> 4;
-
-  const int q_start = qsl[b];
-  int q_len = qsl[b + 1] - q_start;
-  if (q_start < 0 || q_len < 0 || (int64_t)q_start + q_len > num_tokens) q_len = 0;  // bad metadata
-  int seq_len = seq_lens[b];
-  seq_len = seq_len < 0 ? 0 : (seq_len > max_blocks * kBlockSize ? max_blocks * kBlockSize : seq_len);
-  const int m0 = mtile * kPfBM;
-  if (m0 >= q_len) return;
-  const int prefix = seq_len - q_len;
-  const int last_row = (m0 + kPfBM < q_len ? m0 + kPfBM : q_len) - 1;
-  int kv_hi = prefix + last_row + 1;
-  kv_hi = kv_hi < seq_len ? kv_hi : seq_len;
-
-  // This wavefront's rows and their Q^T operand (lane (c, g): row c, dims 32kk + 8g .. +7).
-  const int row = m0 + 16 * w + c;
-  const bool row_ok = row < q_len;
-  const int w_last = (m0 + 16 * w + 15 < q_len ? m0 + 16 * w + 15 : q_len - 1);
-  const int w_kv_hi = prefix + w_last + 1;            // keys this wavefront can see
-  half8_t qf[KK];
-  {
-    const half_t* qp = q + (int64_t)(q_start + (row_ok ? row : 0)) * q_st + (int64_t)h * q_sh;
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      if constexpr (D >= 32) {
-        qf[kk] = row_ok ? ld<half8_t>(qp + 32 * kk + 8 * g) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
-      } else {
-        const half4_t t = row_ok ? ld<half4_t>(qp + 4 * g) : half4_t{0, 0, 0, 0};
-        qf[kk] = {t[0], t[1], t[2], t[3], 0, 0, 0, 0};
-      }
-    }
-  }
-  float4_t o[TILES];
-#pragma unroll
-  for (int t = 0; t < TILES; ++t) o[t] = {0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, l = 0.f;
-  const int abs_row = prefix + row;                    // last key this row may see
-  const int* btrow = bt + (int64_t)b * bt_st;
-  const int64_t head_off = (int64_t)kvh * kBlockSize * D;
-  const int64_t blk_stride = (int64_t)KVH * kBlockSize * D;
-
-  for (int j0 = 0; j0 < kv_hi; j0 += kPfBN) {
-    // ---- stage K (row-major) and V^T into LDS; keys >= seq_len are zero-filled ----
-    constexpr int KCH = D / 8;                          // 16-byte chunks per key row
-    for (int u = tid; u < kPfBN * KCH; u += kPfWaves * 64) {
-      const int kr = u / KCH, cc = u % KCH;
-      const int j = j0 + kr;
-      half8_t val = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (j < seq_len) {
-        const int64_t off = clamp_block(btrow[j >> 4], NB) * blk_stride + head_off +
-                            (int64_t)(j & 15) * D + 8 * cc;
-        val = ld<half8_t>(kc + off);
-      }
-      st<half8_t>(&s_k[kr][8 * cc], val);
-    }
-    for (int u = tid; u < (kPfBN / 2) * KCH; u += kPfWaves * 64) {
-      const int cc = u / (kPfBN / 2), kp = u % (kPfBN / 2);
-      const int j = j0 + 2 * kp;                       // keys j, j + 1 share a KV block
-      half8_t v0 = {0, 0, 0, 0, 0, 0, 0, 0}, v1 = v0;
-      if (j < seq_len) {
-        const int64_t off = clamp_block(btrow[j >> 4], NB) * blk_stride + head_off +
-                            (int64_t)(j & 15) * D + 8 * cc;
-        v0 = ld<half8_t>(vc + off);
-        if (j + 1 < seq_len) v1 = ld<half8_t>(vc + off + D);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) st<half2_t>(&s_vt[8 * cc + e][2 * kp], half2_t{v0[e], v1[e]});
-    }
-    __syncthreads();
-
-    if (j0 < w_kv_hi) {
-      // ---- S^T = K . Q^T for NT sub-tiles of 16 keys ----
-      float4_t sacc[NT];
-#pragma unroll
-      for (int kt = 0; kt < NT; ++kt) {
-        sacc[kt] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < KK; ++kk) {
-          if constexpr (D >= 32) {
-            sacc[kt] = mfma16x16x32(ld<half8_t>(&s_k[16 * kt + c][32 * kk + 8 * g]), qf[kk], sacc[kt]);
-          } else {
-            sacc[kt] = mfma16x16x16(ld<half4_t>(&s_k[16 * kt + c][4 * g]), lo4(qf[kk]), sacc[kt]);
-          }
-        }
-      }
-      // ---- mask, online softmax (row statistics live in lane column c) ----
-      float bmax = -INFINITY;
-#pragma unroll
-      for (int kt = 0; kt < NT; ++kt) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = j0 + 16 * kt + 4 * g + r;
-          const bool ok = row_ok && j < seq_len && j <= abs_row;
-          sacc[kt][r] = ok ? sacc[kt][r] * scale_log2 : -INFINITY;
-          bmax = fmaxf(bmax, sacc[kt][r]);
-        }
-      }
-      bmax = rows_max(bmax);
-      const float m_new = fmaxf(m, bmax);
-      // A row with no visible key in this tile keeps m = -inf: use 0 as the reference point.
-      const float m_ref = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = fast_exp2(m - m_ref);
-      float lsum = 0.f;
-      half4_t pb[NT];
-#pragma unroll
-      for (int kt = 0; kt < NT; ++kt) {
-        float p[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          p[r] = fast_exp2(sacc[kt][r] - m_ref);
-          lsum += p[r];
-        }
-        pb[kt] = {(half_t)p[0], (half_t)p[1], (half_t)p[2], (half_t)p[3]};
-      }
-      l = l * alpha + lsum;
-      m = m_new;
-#pragma unroll
-      for (int t = 0; t < TILES; ++t) o[t] *= alpha;
-      // ---- O^T += V^T . P^T; each 16x16x32 step covers key sub-tiles 2u and 2u + 1 ----
-#pragma unroll
-      for (int u = 0; u < NT / 2; ++u) {
-        const half8_t pu = {pb[2 * u][0], pb[2 * u][1], pb[2 * u][2], pb[2 * u][3],
-                            pb[2 * u + 1][0], pb[2 * u + 1][1], pb[2 * u + 1][2], pb[2 * u + 1][3]};
-#pragma unroll
-        for (int t = 0; t < TILES; ++t) {
-          const half_t* vr = &s_vt[16 * t + c][0];
-          const half4_t a0 = ld<half4_t>(vr + 32 * u + 4 * g);
-          const half4_t a1 = ld<half4_t>(vr + 32 * u + 16 + 4 * g);
-          const half8_t va = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-          o[t] = mfma16x16x32(va, pu, o[t]);
-        }
-      }
-    }
-    __syncthreads();
-  }
-
-  // ---- epilogue: lane (c, g) holds dims 16t + 4g .. +3 of its row ----
-  l = rows_sum(l);
-  if (row_ok) {
-    const float inv = 1.f / (l == 0.f ? 1.f : l);       // a row with no key writes zeros
-    half_t* op = out + (int64_t)(q_start + row) * o_st + (int64_t)h * D;
-#pragma unroll
-    for (int t = 0; t < TILES; ++t) {
-      const half4_t v = {(half_t)(o[t][0] * inv), (half_t)(o[t][1] * inv),
-                         (half_t)(o[t][2] * inv), (half_t)(o[t][3] * inv)};
-      st<half4_t>(op + 16 * t + 4 * g, v);
-    }
-  }
-}
-
-// ------------------------------------------------------------------------------------------
-// Streaming variant (the one launched): a wavefront owns 32 query rows of one head (two 16-row
-// column groups) and reads K/V 16-token blocks straight into registers, the way the decode
-// kernel does (K in MFMA layout, V as coalesced rows permuted in registers), keeping the next
-// two pairs of blocks in flight while the current pair is multiplied. The workgroup's wavefronts take
-// the key pairs round-robin for the same 32 rows and merge their (m, l, acc) in LDS, so a short
-// chunk on a long prefix still spreads over the whole device without global partials.
-// ------------------------------------------------------------------------------------------
 #ifndef TS_PREFILL_ROW_GROUPS
 #define TS_PREFILL_ROW_GROUPS 2
 #endif
@@ -215,7 +37,7 @@ __global__ void __launch_bounds__(NW * 64) prefill_stream_kernel(
     int64_t o_st, int64_t num_tokens, const half_t* __restrict__ kc,
     const half_t* __restrict__ vc, int64_t NB, const int* __restrict__ bt, int64_t bt_st,
     int max_blocks, const int* __restrict__ seq_lens, const int* __restrict__ qsl,
-    int num_decode, int H, int KVH, float scale_log2) {
+    int num_decode, int H, int KVH, float sl2) {
   constexpr int KK = KvRegs<D>::KK, VW = KvRegs<D>::VW, TILES = KvRegs<D>::TILES;
   constexpr int RG = kPsRows / 16;
   constexpr int OROW = D + 4;
@@ -227,13 +49,14 @@ __global__ void __launch_bounds__(NW * 64) prefill_stream_kernel(
   const int b = num_decode + blockIdx.y;
   const int h = blockIdx.z;
   const int G = H / KVH, kvh = h / G;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: keeps loops scalar
   const int c = lane & 15, g = lane >> 4;
 
-  const int q_start = qsl[b];
-  int q_len = qsl[b + 1] - q_start;
+  const int q_start = __builtin_amdgcn_readfirstlane(qsl[b]);
+  int q_len = __builtin_amdgcn_readfirstlane(qsl[b + 1]) - q_start;
   if (q_start < 0 || q_len < 0 || (int64_t)q_start + q_len > num_tokens) q_len = 0;  // bad metadata
-  int seq_len = seq_lens[b];
+  int seq_len = __builtin_amdgcn_readfirstlane(seq_lens[b]);
   seq_len = seq_len < 0 ? 0 : (seq_len > max_blocks * kBlockSize ? max_blocks * kBlockSize : seq_len);
   const int m0 = mtile * kPsRows;
   if (m0 >= q_len) return;
@@ -295,13 +118,7 @@ __global__ void __launch_bounds__(NW * 64) prefill_stream_kernel(
     const bool tail_b = (2 * pi + 2) * kBlockSize > kv_hi;
     half8_t v8[TILES];                                    // V^T operands of the pair
 #pragma unroll
-    for (int t = 0; t < TILES; ++t) {
-      half4_t va = {vr[0][0][t], vr[0][1][t], vr[0][2][t], vr[0][3][t]};
-      half4_t vb = {vr[1][0][t], vr[1][1][t], vr[1][2][t], vr[1][3][t]};
-      if (tail_a) va = mask_tokens(va, ta, kv_hi);
-      if (tail_b) vb = mask_tokens(vb, tb, kv_hi);
-      v8[t] = {va[0], va[1], va[2], va[3], vb[0], vb[1], vb[2], vb[3]};
-    }
+    for (int t = 0; t < TILES; ++t) v8[t] = vt_operand<VW>(vr[0], vr[1], t, tail_a, tail_b, ta, tb, kv_hi);
 #pragma unroll
     for (int rg = 0; rg < RG; ++rg) {
       float4_t sa = zero4, sb = zero4;
@@ -319,63 +136,29 @@ __global__ void __launch_bounds__(NW * 64) prefill_stream_kernel(
       // so no key needs masking.
       const int last_key = (2 * pi + 2) * kBlockSize - 1;
       const bool interior = last_key < kv_hi && last_key <= prefix + m0 + 16 * rg;
-      float sca[4], scb[4];
-      if (interior) {
+      if (!interior) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          sca[r] = sa[r] * scale_log2;
-          scb[r] = sb[r] * scale_log2;
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          sca[r] = (ta + r < kv_hi && ta + r <= lim[rg]) ? sa[r] * scale_log2 : -INFINITY;
-          scb[r] = (tb + r < kv_hi && tb + r <= lim[rg]) ? sb[r] * scale_log2 : -INFINITY;
+          sa[r] = (ta + r < kv_hi && ta + r <= lim[rg]) ? sa[r] : -INFINITY;
+          sb[r] = (tb + r < kv_hi && tb + r <= lim[rg]) ? sb[r] : -INFINITY;
         }
       }
-      const float bmax = rows_max(fmaxf(fmaxf(fmaxf(sca[0], sca[1]), fmaxf(sca[2], sca[3])),
-                                        fmaxf(fmaxf(scb[0], scb[1]), fmaxf(scb[2], scb[3]))));
-      const float m_new = fmaxf(m[rg], bmax);
-      // a row with no visible key so far keeps m = -inf: use 0 as the reference point
-      const float m_ref = m_new == -INFINITY ? 0.f : m_new;
-      const float alpha = fast_exp2(m[rg] - m_ref);
-      // O is rescaled only when some row's running max moved (alpha == 1 exactly otherwise).
-      const bool rescale = __ballot(m_new != m[rg]) != 0;
-      float pa[4], pb[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        pa[r] = fast_exp2(sca[r] - m_ref);
-        pb[r] = fast_exp2(scb[r] - m_ref);
-      }
-      l[rg] = l[rg] * alpha + (((pa[0] + pa[1]) + (pa[2] + pa[3])) + ((pb[0] + pb[1]) + (pb[2] + pb[3])));
-      m[rg] = m_new;
-      const half8_t p8 = {(half_t)pa[0], (half_t)pa[1], (half_t)pa[2], (half_t)pa[3],
-                          (half_t)pb[0], (half_t)pb[1], (half_t)pb[2], (half_t)pb[3]};
-      if (rescale) {
-#pragma unroll
-        for (int t = 0; t < TILES; ++t) o[rg][t] *= alpha;
-      }
-#pragma unroll
-      for (int t = 0; t < TILES; ++t)
-        o[rg][t] = mfma16x16x32(v8[t], p8, o[rg][t]);   // lane (c, g): dims VW (4g + r) + t
+      const SoftmaxStep step = softmax_pair(sa, sb, sl2, m[rg], l[rg]);
+      // lane (c, g) of tile t: dims VW (4g + r) + t
+      pv_update<TILES>(o[rg], step, [&](int t) { return v8[t]; });
     }
   };
-  // Three-deep register ring: the loads of pair p + 2 NW are issued before pair p is computed.
-  // (Occupancy is one wavefront per SIMD at D = 128 anyway, so the ring costs no occupancy.)
-  half8_t k0[2][KK], k1[2][KK], k2[2][KK];
-  VRow v0[2][4], v1[2][4], v2[2][4];
+  // Two-deep register ring: the loads of pair p + NW are issued before pair p is computed.
+  half8_t k0[2][KK], k1[2][KK];
+  VRow v0[2][4], v1[2][4];
   int p = w;
   if (p < npairs) load_pair(p, k0, v0);
-  if (p + NW < npairs) load_pair(p + NW, k1, v1);
-  for (; p < npairs; p += 3 * NW) {
-    if (p + 2 * NW < npairs) load_pair(p + 2 * NW, k2, v2);
+  for (; p < npairs; p += 2 * NW) {
+    if (p + NW < npairs) load_pair(p + NW, k1, v1);
     compute_pair(p, k0, v0);
     if (p + NW >= npairs) break;
-    if (p + 3 * NW < npairs) load_pair(p + 3 * NW, k0, v0);
+    if (p + 2 * NW < npairs) load_pair(p + 2 * NW, k0, v0);
     compute_pair(p + NW, k1, v1);
-    if (p + 2 * NW >= npairs) break;
-    if (p + 4 * NW < npairs) load_pair(p + 4 * NW, k1, v1);
-    compute_pair(p + 2 * NW, k2, v2);
   }
 
   // Merge the NW wavefronts' partial softmax states for the 32 rows in LDS.

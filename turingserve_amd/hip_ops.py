@@ -23,7 +23,7 @@ __all__ = ["kv_write", "paged_attention", "linear", "lm_head_int8", "w8a16_linea
            "decode_attention_v1", "decode_attention_v2", "decode_attention_v3",
            "prefill_attention"]
 
-DEFAULT_PARTITION = 256          # v3 tokens per split when the caller names none
+DEFAULT_PARTITION = 0            # v3 split size when the caller names none: 0 = balanced
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -132,7 +132,8 @@ def decode_attention_v3(q, out, k_cache, v_cache, block_tables, seq_lens, scale,
 
 def _decode(q, out, k_cache, v_cache, meta, scale, version: str | None = None):
     """Decode rows [0, num_decode) of the batch (ops/triton_ops.py:35-57). version None lets the
-    library apply the split rule (split when S * KVH < 2 * CUs and max_seq_len > 1024)."""
+    library choose: balanced split-K when one workgroup per (sequence, KV head) would leave CUs
+    idle and contexts exceed 256 tokens, else one workgroup per (sequence, KV head)."""
     _require(version in N.DECODE_VERSIONS, f"unknown decode version {version!r}")
     S = meta.num_decode
     code = N.DECODE_VERSIONS[version]
