@@ -64,17 +64,21 @@ def test_zero_size_calls_are_no_ops():
 
 def test_workspace_sizes():
     lib = N.lib()
-    # v3 partials for 64 sequences x 12 heads x 16 splits (4096 / 256) x (128 + 2) fp32
-    n = 64 * 12 * 16
-    want = ((n * 128 * 4 + 255) // 256 * 256) + 2 * ((n * 4 + 255) // 256 * 256)
+
+    def v3_bytes(rows_per_seq, S=64, H=12, D=128):
+        n = S * rows_per_seq * H                 # partial rows x heads, each D + 2 fp32
+        a256 = lambda x: (x + 255) // 256 * 256
+        return a256(n * D * 4) + 2 * a256(n * 4) + a256(S * 4)
+
+    # fixed grid: 4096 / 256 = 16 split rows per sequence
+    want = v3_bytes(16)
     assert lib.ts_decode_workspace_bytes(3, 64, 12, 2, 128, 4096, 256, 256) == want
     assert lib.ts_decode_workspace_bytes(2, 64, 12, 2, 128, 4096, 0, 256) == 0
     assert lib.ts_decode_workspace_bytes(1, 64, 12, 2, 128, 4096, 0, 256) == 0
-    # balanced v3 (partition 0): nx = 256 CUs x 2 resident workgroups / 2 KV heads - 64 / 2 = 224
-    # split slots per KV head plus one per sequence, each slot holding all 12 heads
-    nb = (224 + 64) * 12
-    balanced = ((nb * 128 * 4 + 255) // 256 * 256) + 2 * ((nb * 4 + 255) // 256 * 256)
+    # balanced v3 (partition 0): at most 32 split rows per sequence, whatever max_seq_len is
+    balanced = v3_bytes(32)
     assert lib.ts_decode_workspace_bytes(3, 64, 12, 2, 128, 4096, 0, 256) == balanced
+    assert lib.ts_decode_workspace_bytes(3, 64, 12, 2, 128, 32768, 0, 256) == balanced
     # the automatic policy splits 64 x 2 (seq, KV head) workgroups < 512 resident ones, with the
     # fixed grid when a partition is named and the balanced schedule otherwise ...
     assert lib.ts_decode_workspace_bytes(0, 64, 12, 2, 128, 4096, 256, 256) == want

@@ -105,18 +105,24 @@ __global__ void __launch_bounds__(64) decode_v1_kernel(
 // v2 / v3 (ops/triton_decode_attention.py:60-163)
 // ------------------------------------------------------------------------------------------
 // Dense split map of v3. Sequence s has nb_s = ceil(len_s / 16) blocks (len_s clamped to
-// cap_blocks * 16) cut into n_s = ceil(nb_s / P) splits of P blocks; split j of sequence s is
-// slot C_s + j with C_s = sum_{t<s} n_t, so the launched slots carry no idle workgroups. P is
-// the caller's partition, or, when part_blocks == 0, P = max(kMinPartBlocks, ceil(TB / nx)) for
-// the batch's total TB blocks: then sum_s n_s <= nx + S and n_s <= nx whatever the lengths, and
-// every workgroup gets about the same number of blocks (the balanced schedule).
+// cap_blocks * 16) cut into n_s = ceil(nb_s / P_s) splits of P_s blocks; the splits of the batch
+// are numbered densely in sequence order (split j of sequence s is launch slot C_s + j with
+// C_s = sum_{t<s} n_t), so the launch carries no idle workgroups. With a caller partition,
+// P_s = partition. With part_blocks == 0 (the balanced schedule) P = ceil(TB / nx) for the
+// batch's total TB blocks, rounded up to a multiple of kMinPartBlocks (one pair per wavefront,
+// so every wavefront of a full split gets the same number of pairs), and a sequence longer than
+// max_splits * P uses P_s = the multiple of kMinPartBlocks that keeps n_s <= max_splits. Either
+// way sum_s n_s <= nx + S and n_s <= max_splits, and every workgroup gets about the same work.
+// Split j of sequence s leaves its partial in workspace row s * max_splits + j, so the merge
+// can request a sequence's partials without knowing the other sequences' lengths.
 constexpr int kMinPartBlocks = 8;
+constexpr int kBalancedMaxSplits = 32;
 
 struct SplitSlot {
   int seq;     // sequence owning the slot (-1: the slot is past the batch's last split)
   int first;   // C_s
   int count;   // n_s
-  int part;    // P in blocks
+  int part;    // P_s in blocks
   int len;     // clamped seq_len
 };
 
@@ -135,18 +141,24 @@ __device__ __forceinline__ int wave_inclusive_sum(int v, int lane) {
   return v;
 }
 
-// Called by every thread of an NT-thread workgroup (S >= 1). slot >= 0: find the sequence that
-// owns `slot`; slot < 0: report sequence `seq`. s_map holds NT / 64 + 5 ints of LDS.
+__device__ __forceinline__ int round_part(int blocks) {
+  return (blocks + kMinPartBlocks - 1) / kMinPartBlocks * kMinPartBlocks;
+}
+
+// Called by every thread of an NT-thread workgroup (S >= 1): finds the sequence that owns
+// launch slot `slot`. s_map holds NT / 64 + 5 ints of LDS.
 template <int NT>
 __device__ SplitSlot split_lookup(const int* __restrict__ seq_lens, int S, int cap_blocks,
-                                  int part_blocks, int nx, int slot, int seq, int* s_map) {
+                                  int part_blocks, int nx, int max_splits, int slot,
+                                  int* s_map) {
   constexpr int NWV = NT / kWave;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int cap = cap_blocks * kBlockSize;
   auto clamp_len = [&](int len) { return len < 0 ? 0 : (len > cap ? cap : len); };
   const int len0 = tid < S ? clamp_len(seq_lens[tid]) : 0;
+  const bool balanced = part_blocks <= 0;
   int P = part_blocks;
-  if (P <= 0) {
+  if (balanced) {
     int tb = (len0 + kBlockSize - 1) / kBlockSize;
     for (int i = tid + NT; i < S; i += NT) tb += (clamp_len(seq_lens[i]) + kBlockSize - 1) / kBlockSize;
     tb = wave_sum(tb);
@@ -155,21 +167,29 @@ __device__ SplitSlot split_lookup(const int* __restrict__ seq_lens, int S, int c
     int total = 0;
 #pragma unroll
     for (int k = 0; k < NWV; ++k) total += s_map[k];
-    P = (total + nx - 1) / nx;
+    P = round_part((total + nx - 1) / nx);
     P = P > kMinPartBlocks ? P : kMinPartBlocks;
     __syncthreads();
   }
+  auto part_of = [&](int nb) {
+    if (!balanced) return P;
+    const int q = round_part((nb + max_splits - 1) / max_splits);
+    return q > P ? q : P;
+  };
   if (tid == 0) {
     s_map[NWV] = -1;
     s_map[NWV + 1] = 0;
     s_map[NWV + 2] = 0;
     s_map[NWV + 3] = 0;
+    s_map[NWV + 4] = P;
   }
   int base = 0;
   for (int c0 = 0; c0 < S; c0 += NT) {
     const int i = c0 + tid;
     const int len = c0 == 0 ? len0 : (i < S ? clamp_len(seq_lens[i]) : 0);
-    const int n = ((len + kBlockSize - 1) / kBlockSize + P - 1) / P;
+    const int nb = (len + kBlockSize - 1) / kBlockSize;
+    const int ps = part_of(nb);
+    const int n = (nb + ps - 1) / ps;
     const int incl = wave_inclusive_sum(n, lane);
     if (lane == kWave - 1) s_map[w] = incl;
     __syncthreads();
@@ -181,18 +201,18 @@ __device__ SplitSlot split_lookup(const int* __restrict__ seq_lens, int S, int c
       tot += v;
     }
     const int excl = off + incl - n;
-    const bool hit = i < S && (slot >= 0 ? (n > 0 && slot >= excl && slot < excl + n) : i == seq);
-    if (hit) {
+    if (i < S && n > 0 && slot >= excl && slot < excl + n) {
       s_map[NWV] = i;
       s_map[NWV + 1] = excl;
       s_map[NWV + 2] = n;
       s_map[NWV + 3] = len;
+      s_map[NWV + 4] = ps;
     }
     base += tot;
     __syncthreads();
   }
   return {__builtin_amdgcn_readfirstlane(s_map[NWV]), __builtin_amdgcn_readfirstlane(s_map[NWV + 1]),
-          __builtin_amdgcn_readfirstlane(s_map[NWV + 2]), P,
+          __builtin_amdgcn_readfirstlane(s_map[NWV + 2]), __builtin_amdgcn_readfirstlane(s_map[NWV + 4]),
           __builtin_amdgcn_readfirstlane(s_map[NWV + 3])};
 }
 
@@ -210,7 +230,8 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
     int64_t o_st, const half_t* __restrict__ kc, const half_t* __restrict__ vc, int64_t NB,
     const int* __restrict__ bt, int64_t bt_st, int max_blocks, const int* __restrict__ seq_lens,
     int S, int H, int KVH, int G, int HG, float sl2, int cap_blocks, int part_blocks, int nx,
-    float* __restrict__ ws_acc, float* __restrict__ ws_m, float* __restrict__ ws_l) {
+    int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
+    float* __restrict__ ws_l, int* __restrict__ ws_cnt) {
   constexpr int KK = KvRegs<D>::KK;
   constexpr int VW = KvRegs<D>::VW;
   constexpr int TILES = KvRegs<D>::TILES;
@@ -231,16 +252,18 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
   const int head0 = kvh * G + hg * 16;           // first query head of this group
   const bool split = ws_acc != nullptr;
 
-  int s, seq_len, blk_lo, blk_hi, nsplit;
+  int s, seq_len, blk_lo, blk_hi, nsplit, split_j = 0;
   if (split) {
     const SplitSlot sp = split_lookup<NW * 64>(seq_lens, S, cap_blocks, part_blocks, nx,
-                                               blockIdx.x, -1, s_map);
+                                               max_splits, blockIdx.x, s_map);
     if (sp.seq < 0) return;                      // slot past the batch's last split
     s = sp.seq;
     seq_len = sp.len;
     nsplit = sp.count;
+    split_j = (int)blockIdx.x - sp.first;
+    if (split_j == 0 && tid == 0) ws_cnt[s] = nsplit;   // read by the merge kernel
     const int nblk = (seq_len + kBlockSize - 1) / kBlockSize;
-    blk_lo = ((int)blockIdx.x - sp.first) * sp.part;
+    blk_lo = split_j * sp.part;
     blk_hi = (blk_lo + sp.part) < nblk ? (blk_lo + sp.part) : nblk;
   } else {
     s = blockIdx.x;
@@ -402,7 +425,7 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
     if (nsplit == 1) {
       out[(int64_t)s * o_st + (int64_t)(head0 + hh) * D + d] = (half_t)(O / L);
     } else {
-      const int64_t pidx = (int64_t)blockIdx.x * H + head0 + hh;
+      const int64_t pidx = ((int64_t)s * max_splits + split_j) * H + head0 + hh;
       ws_acc[pidx * D + d] = O;
       if (d == 0) {
         ws_m[pidx] = M;
@@ -414,108 +437,71 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
 
 // Merge of the split partials (ops/triton_decode_attention.py:144-163): M = max m_j,
 // w_j = 2^(m_j - M), out = sum w_j acc_j / sum w_j l_j. One workgroup per (sequence, KV head,
-// head group): it recomputes the split map, then loads every (head, split) statistic and the
-// first chunk of partials at once (two dependent memory steps in all for up to 16 splits).
-// Sequences with one split were finished by the first kernel; a sequence with none (seq_len 0)
-// gets zeros here.
+// head group), one thread per 4 output dims of a head. A sequence's partials sit in rows
+// s * max_splits + j, so the split count written by the first kernel, seq_len and the partials
+// of the first kMergeChunk splits are all requested in one memory step (rows past the count are
+// read but ignored). Sequences with one split were finished by the first kernel; a sequence
+// with none (seq_len 0) gets zeros here.
 constexpr int kMaxSplits = 256;
+constexpr int kMergeChunk = 16;
 
 template <int D>
 __global__ void __launch_bounds__(256) decode_merge_kernel(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_m,
-    const float* __restrict__ ws_l, half_t* __restrict__ out, int64_t o_st,
-    const int* __restrict__ seq_lens, int S, int H, int G, int HG, int cap_blocks,
-    int part_blocks, int nx, int nslots) {
-  __shared__ float s_w[16][kMaxSplits];
-  __shared__ float s_l[16][kMaxSplits];
-  __shared__ float s_inv[16];
-  __shared__ int s_map[4 + 5];
+    const float* __restrict__ ws_l, const int* __restrict__ ws_cnt, half_t* __restrict__ out,
+    int64_t o_st, const int* __restrict__ seq_lens, int H, int G, int HG, int max_splits) {
+  constexpr int TPH = D / 4;                     // threads per head (4 dims each)
+  constexpr int HPP = 256 / TPH;                 // heads per pass
+  constexpr int CH = kMergeChunk;
   const int s = blockIdx.x, kvh = blockIdx.y / HG, hg = blockIdx.y % HG;
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x;
   const int nh = (G - hg * 16) < 16 ? (G - hg * 16) : 16;
   const int head0 = kvh * G + hg * 16;
-  const SplitSlot sp = split_lookup<256>(seq_lens, S, cap_blocks, part_blocks, nx, -1, s, s_map);
-  if (sp.count == 1) return;                     // written by the first kernel
-  if (sp.count == 0) {                           // padding row: zeros (ops/reference.py:99,104-105)
-    for (int e = tid; e < nh * D; e += 256)
-      out[(int64_t)s * o_st + (int64_t)(head0 + e / D) * D + e % D] = (half_t)0.f;
-    return;
-  }
-  int n = sp.count < kMaxSplits ? sp.count : kMaxSplits;     // the plan keeps n_s <= 255
-  n = sp.first + n <= nslots ? n : nslots - sp.first;
-  if (n < 1) return;                             // unreachable for a consistent plan
-  const int64_t slot0 = sp.first;
-  // Each thread owns up to EPT outputs; for every chunk of CH splits all EPT x CH loads are
-  // issued before any is consumed (indices past n repeat the last split with weight 0). The
-  // first chunk does not depend on the statistics, so it goes out together with them.
-  constexpr int EPT = 4, CH = 16;
-  float v[EPT][CH];
-  const float* accp[EPT];
-  int hh_[EPT];
-  bool ok[EPT];
-  auto setup = [&](int e0) {
-#pragma unroll
-    for (int q = 0; q < EPT; ++q) {
-      const int e = e0 + 256 * q;
-      ok[q] = e < nh * D;
-      const int ee = ok[q] ? e : 0;
-      hh_[q] = ee / D;
-      accp[q] = ws_acc + (slot0 * H + head0 + hh_[q]) * D + ee % D;
-    }
-  };
-  auto load_chunk = [&](int t0) {
-#pragma unroll
-    for (int u = 0; u < CH; ++u) {
-      const int j = (t0 + u) < n ? (t0 + u) : (n - 1);
-#pragma unroll
-      for (int q = 0; q < EPT; ++q) v[q][u] = accp[q][(int64_t)j * H * D];
-    }
-  };
-  setup(tid);
-  load_chunk(0);
-  for (int e = tid; e < nh * n; e += 256) {
-    const int hh = e / n, j = e % n;
-    const int64_t pidx = (slot0 + j) * H + head0 + hh;
-    s_w[hh][j] = ws_m[pidx];
-    s_l[hh][j] = ws_l[pidx];
-  }
-  __syncthreads();
-  for (int hh = w; hh < nh; hh += 4) {
-    float M = -INFINITY;
-    for (int j = lane; j < n; j += 64) M = fmaxf(M, s_w[hh][j]);
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) M = fmaxf(M, shfl_xor(M, off));
-    float L = 0.f;
-    for (int j = lane; j < n; j += 64) {
-      const float wt = fast_exp2(s_w[hh][j] - M);
-      s_w[hh][j] = wt;
-      L += wt * s_l[hh][j];
-    }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) L += shfl_xor(L, off);
-    if (lane == 0) s_inv[hh] = 1.f / L;
-  }
-  __syncthreads();
-  for (int e0 = tid; e0 < nh * D; e0 += 256 * EPT) {
-    if (e0 != tid) {
-      setup(e0);
-      load_chunk(0);
-    }
-    float O[EPT] = {};
-    for (int t0 = 0; t0 < n; t0 += CH) {
-      if (t0 > 0) load_chunk(t0);
+  const int len = __builtin_amdgcn_readfirstlane(seq_lens[s]);
+  const int cnt = __builtin_amdgcn_readfirstlane(ws_cnt[s]);
+  const int64_t row0 = (int64_t)s * max_splits;
+  for (int hp = 0; hp < nh; hp += HPP) {
+    const int hh = hp + tid / TPH, d0 = (tid % TPH) * 4;
+    const bool active = hh < nh;
+    const int64_t hoff = head0 + (active ? hh : 0);
+    float mv[CH], lv[CH];
+    float4_t av[CH];
+    auto load_chunk = [&](int j0) {
 #pragma unroll
       for (int u = 0; u < CH; ++u) {
-        const int j = (t0 + u) < n ? (t0 + u) : (n - 1);
-#pragma unroll
-        for (int q = 0; q < EPT; ++q) O[q] += (t0 + u < n) ? s_w[hh_[q]][j] * v[q][u] : 0.f;
+        const int j = (j0 + u) < max_splits ? (j0 + u) : (max_splits - 1);
+        const int64_t pidx = (row0 + j) * H + hoff;
+        mv[u] = ws_m[pidx];
+        lv[u] = ws_l[pidx];
+        av[u] = ld<float4_t>(ws_acc + pidx * D + d0);
       }
+    };
+    load_chunk(0);
+    if (len <= 0) {                              // padding row: zeros (ops/reference.py:99,104-105)
+      if (active) st<half4_t>(out + (int64_t)s * o_st + (head0 + hh) * (int64_t)D + d0, half4_t{0, 0, 0, 0});
+      continue;
     }
+    const int n = cnt < 1 ? 1 : (cnt > max_splits ? max_splits : cnt);
+    if (n == 1) return;                          // written by the first kernel
+    float M = -INFINITY, L = 0.f;
+    float4_t O = {0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < n; j0 += CH) {
+      if (j0 > 0) load_chunk(j0);
+      float cm = M;
 #pragma unroll
-    for (int q = 0; q < EPT; ++q) {
-      const int e = e0 + 256 * q;
-      if (ok[q]) out[(int64_t)s * o_st + (int64_t)(head0 + hh_[q]) * D + e % D] = (half_t)(O[q] * s_inv[hh_[q]]);
+      for (int u = 0; u < CH; ++u) cm = (j0 + u < n) ? fmaxf(cm, mv[u]) : cm;
+      const float alpha = fast_exp2(M - cm);     // M = -inf on the first chunk -> 0
+      L *= alpha;
+      O *= alpha;
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const float wt = (j0 + u < n) ? fast_exp2(mv[u] - cm) : 0.f;
+        L += wt * lv[u];
+        O += wt * av[u];
+      }
+      M = cm;
     }
+    if (active) st<half4_t>(out + (int64_t)s * o_st + (head0 + hh) * (int64_t)D + d0, to_half4(O / L));
   }
 }
 
@@ -538,16 +524,17 @@ struct SplitPlan {
   int nx;             // v3 balanced: target split count per (KV head, head group)
   int nslots;         // v3: launched split slots per (KV head, head group)
   int cap_blocks;     // v3 fixed partition: blocks of a sequence covered by the launched splits
+  int max_splits;     // v3: workspace rows per sequence (bound on its split count)
 };
 
 // Explicit v3 partition (ops/triton_ops.py:50-51): num_splits = ceil(max_seq_len / partition)
-// split slots per sequence; partition = 0 selects the balanced schedule. AUTO splits whenever one
-// workgroup per (sequence, KV head, head group) cannot fill the device and contexts are longer
-// than two minimum splits (the reference's rule, ops/triton_ops.py:44-45, with the CU count and
-// this kernel's residency), and uses the balanced schedule unless a partition is given.
+// splits per sequence at most; partition = 0 selects the balanced schedule. AUTO splits whenever
+// one workgroup per (sequence, KV head, head group) cannot fill the device and contexts are
+// longer than two minimum splits (the reference's rule, ops/triton_ops.py:44-45, with the CU
+// count and this kernel's residency), and uses the balanced schedule unless a partition is given.
 static SplitPlan plan_decode(int version, int S, int H, int KVH, int D, int max_seq_len,
                              int partition, int cu_count) {
-  SplitPlan p{version, 0, 0, 0, 0};
+  SplitPlan p{version, 0, 0, 0, 0, 0};
   const int G = H / KVH;
   const int HG = (G + 15) / 16;
   const int64_t groups = (int64_t)KVH * HG;
@@ -561,23 +548,25 @@ static SplitPlan plan_decode(int version, int S, int H, int KVH, int D, int max_
   if (partition > 0) {
     p.part_blocks = partition / kBlockSize;
     int num_splits = (max_blk + p.part_blocks - 1) / p.part_blocks;
-    if (num_splits > kMaxSplits - 1) {            // the merge keeps < 256 split weights in LDS
-      p.part_blocks = (max_blk + kMaxSplits - 2) / (kMaxSplits - 1);
+    if (num_splits > kMaxSplits) {               // bounds the workspace rows per sequence
+      p.part_blocks = (max_blk + kMaxSplits - 1) / kMaxSplits;
       num_splits = (max_blk + p.part_blocks - 1) / p.part_blocks;
     }
     num_splits = num_splits < 1 ? 1 : num_splits;
     p.cap_blocks = num_splits * p.part_blocks;
     p.nslots = S * num_splits;
+    p.max_splits = num_splits;
   } else {
 #ifdef TS_DECODE_NX
     int64_t nx = TS_DECODE_NX;                   // tuning override
 #else
-    int64_t nx = wg_slots / groups - S / 2;      // launched slots nx + S ~ resident workgroups
+    int64_t nx = wg_slots / groups - S;          // launched slots nx + S = resident workgroups
 #endif
-    nx = nx < 16 ? 16 : (nx > kMaxSplits - 1 ? kMaxSplits - 1 : nx);
+    nx = nx < 16 ? 16 : (nx > 4096 ? 4096 : nx);
     p.nx = (int)nx;
     p.cap_blocks = 1 << 30;
     p.nslots = p.nx + S;
+    p.max_splits = kBalancedMaxSplits;
   }
   return p;
 }
@@ -585,19 +574,20 @@ static SplitPlan plan_decode(int version, int S, int H, int KVH, int D, int max_
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct WsLayout {
-  size_t acc, m, l, total;
+  size_t acc, m, l, cnt, total;
 };
 
-// [acc: slots * H * D fp32][m: slots * H][l: slots * H]; a slot's partial of query head h sits at
-// slot * H + h, so the (KV head, head group) grids share the slot numbering without overlap.
-static WsLayout ws_layout(const SplitPlan& p, int H, int D) {
-  WsLayout w{0, 0, 0, 0};
+// [acc: rows * H * D fp32][m: rows * H][l: rows * H][count: S int32] with rows = S * max_splits:
+// split j of sequence s keeps query head h's partial in row s * max_splits + j, column h.
+static WsLayout ws_layout(const SplitPlan& p, int S, int H, int D) {
+  WsLayout w{0, 0, 0, 0, 0};
   if (p.version != TS_DECODE_V3) return w;
-  const size_t n = (size_t)p.nslots * H;
+  const size_t n = (size_t)S * p.max_splits * H;
   w.acc = 0;
   w.m = align256(n * D * sizeof(float));
   w.l = w.m + align256(n * sizeof(float));
-  w.total = w.l + align256(n * sizeof(float));
+  w.cnt = w.l + align256(n * sizeof(float));
+  w.total = w.cnt + align256((size_t)S * sizeof(int));
   return w;
 }
 
@@ -617,20 +607,21 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
   if (p.version == TS_DECODE_V2) {
     decode_mfma_kernel<D, kDecodeWaves><<<dim3(S, 1, KVH * HG), kDecodeWaves * 64, 0, st>>>(
         q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,
-        scale_log2, 0, 0, 0, nullptr, nullptr, nullptr);
+        scale_log2, 0, 0, 0, 0, nullptr, nullptr, nullptr, nullptr);
     return;
   }
-  const WsLayout w = ws_layout(p, H, D);
+  const WsLayout w = ws_layout(p, S, H, D);
   char* b = static_cast<char*>(ws);
   float* ws_acc = reinterpret_cast<float*>(b + w.acc);
   float* ws_m = reinterpret_cast<float*>(b + w.m);
   float* ws_l = reinterpret_cast<float*>(b + w.l);
+  int* ws_cnt = reinterpret_cast<int*>(b + w.cnt);
   const int cap = p.cap_blocks < max_blocks ? p.cap_blocks : max_blocks;
   decode_mfma_kernel<D, kDecodeWaves><<<dim3(p.nslots, 1, KVH * HG), kDecodeWaves * 64, 0, st>>>(
       q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,
-      scale_log2, cap, p.part_blocks, p.nx, ws_acc, ws_m, ws_l);
-  decode_merge_kernel<D><<<dim3(S, KVH * HG), 256, 0, st>>>(
-      ws_acc, ws_m, ws_l, out, o_st, sl, S, H, G, HG, cap, p.part_blocks, p.nx, p.nslots);
+      scale_log2, cap, p.part_blocks, p.nx, p.max_splits, ws_acc, ws_m, ws_l, ws_cnt);
+  decode_merge_kernel<D><<<dim3(S, KVH * HG), 256, 0, st>>>(ws_acc, ws_m, ws_l, ws_cnt, out, o_st,
+                                                             sl, H, G, HG, p.max_splits);
 }
 
 static bool supported_head_dim(int D) {
@@ -648,7 +639,7 @@ extern "C" size_t ts_decode_workspace_bytes(int32_t version, int32_t num_seqs, i
   if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
   const SplitPlan p = plan_decode(version, num_seqs, num_heads, num_kv_heads, head_dim,
                                   max_seq_len, partition, cu_count > 0 ? cu_count : 256);
-  return ws_layout(p, num_heads, head_dim).total;
+  return ws_layout(p, num_seqs, num_heads, head_dim).total;
 }
 
 extern "C" int ts_decode_attention(int32_t version, const void* q, int64_t q_stride_t,
@@ -685,7 +676,7 @@ extern "C" int ts_decode_attention(int32_t version, const void* q, int64_t q_str
   if (st != TS_OK) return st;
   const SplitPlan p = plan_decode(version, num_seqs, num_heads, num_kv_heads, head_dim,
                                   max_seq_len, partition, cus);
-  const size_t need = ws_layout(p, num_heads, head_dim).total;
+  const size_t need = ws_layout(p, num_seqs, num_heads, head_dim).total;
   TS_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 256)),
              TS_ERR_WORKSPACE, "decode_attention: workspace of %zu bytes (256-aligned) needed, got %zu",
              need, workspace_bytes);
