@@ -10,6 +10,9 @@
  *   ts_prefill_attention   <- ops/triton_prefill_attention.py:66-79
  *   ts_paged_attention     <- ops/triton_ops.py:60-71        (twin ops/reference.py:94-111)
  *   ts_w8a16_gemm          <- ops/triton_w8a16.py:38-51 and ops/triton_ops.py:74-91
+ *   ts_rmsnorm             <- ops/triton_rmsnorm.py:30-46   (twins ops/reference.py:13-23)
+ *   ts_rope                <- ops/triton_rope.py:27-31      (twin ops/reference.py:31-42)
+ *   ts_silu_mul            <- ops/triton_silu_mul.py:21-28  (twin ops/reference.py:26-28)
  *                             (twin ops/reference.py:45-47 + quant/int8.py:15-16)
  *
  * Conventions shared by every entry point
@@ -147,6 +150,38 @@ int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const void* scal
                   int32_t scale_is_fp16, const void* bias, void* y, int64_t ldy,
                   int32_t M, int32_t N, int32_t K,
                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * RMSNorm with optional fused residual add, one token row of `hidden` features at a time:
+ *   r = residual ? fp16(x + residual) : x;  out = fp16(w * fp16(r * rsqrt(mean(r^2) + eps)))
+ * with the mean in fp32; residual_out receives r when residual is given (ops/triton_rmsnorm.py:
+ * 10-27). fp16 rows, 16-byte aligned; hidden a multiple of 8, at most 8192.
+ * Replaces ops/triton_rmsnorm.py:30-46 (rmsnorm_residual / rmsnorm).
+ */
+int ts_rmsnorm(const void* x, int64_t x_stride, const void* residual, int64_t residual_stride,
+               const void* weight, void* out, int64_t out_stride, void* residual_out,
+               int64_t residual_out_stride, int64_t num_tokens, int32_t hidden, float eps,
+               void* stream);
+
+/*
+ * In-place rotate-half RoPE on the first num_heads + num_kv_heads heads (q, then k) of each
+ * token row of qkv [T, (H + 2 KVH) * D] fp16: with c, s the fp32 tables [max_position, D / 2]
+ * rounded to fp16 at positions[t] (int64; clamped to the table), x1' = x1 c - x2 s and
+ * x2' = x2 c + x1 s with every product and sum rounded to fp16, the twin's arithmetic
+ * (ops/reference.py:31-42). head_dim a multiple of 8.
+ * Replaces ops/triton_rope.py:27-31.
+ */
+int ts_rope(void* qkv, int64_t qkv_stride, const int64_t* positions, const float* cos_table,
+            const float* sin_table, int64_t max_position, int64_t num_tokens, int32_t num_heads,
+            int32_t num_kv_heads, int32_t head_dim, void* stream);
+
+/*
+ * out[t, i] = fp16(fp16(silu(g)) * u) for gu[t] = [g (intermediate) | u (intermediate)], silu in
+ * fp32 (ops/triton_silu_mul.py:10-18). fp16 rows, 16-byte aligned; intermediate a multiple of 8.
+ * Replaces ops/triton_silu_mul.py:21-28.
+ */
+int ts_silu_mul(const void* gu, int64_t gu_stride, void* out, int64_t out_stride,
+                int64_t num_tokens, int32_t intermediate, void* stream);
 
 #ifdef __cplusplus
 }

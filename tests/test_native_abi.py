@@ -53,6 +53,20 @@ def test_invalid_arguments_return_status_and_message():
         N.check(st, "w8a16")
 
 
+def test_small_op_argument_checks():
+    lib = N.lib()
+    p = ctypes.c_void_p(256)            # never dereferenced: the call fails validation first
+    assert lib.ts_rmsnorm(p, 1536, None, 0, p, p, 1536, None, 0, 4, 12, 1e-6, None) == \
+        N.TS_ERR_UNSUPPORTED and "multiple of 8" in N.last_error()
+    assert lib.ts_rmsnorm(None, 0, None, 0, None, None, 0, None, 0, 4, 64, 1e-6, None) == \
+        N.TS_ERR_INVALID_ARG
+    assert lib.ts_rope(p, 2048, p, p, p, 16, 4, 12, 2, 12, None) == N.TS_ERR_UNSUPPORTED
+    assert lib.ts_silu_mul(p, 100, p, 50, 2, 50, None) == N.TS_ERR_UNSUPPORTED
+    assert lib.ts_rmsnorm(None, 0, None, 0, None, None, 0, None, 0, 0, 64, 1e-6, None) == N.TS_OK
+    assert lib.ts_rope(None, 0, None, None, None, 0, 0, 12, 2, 128, None) == N.TS_OK
+    assert lib.ts_silu_mul(None, 0, None, 0, 0, 64, None) == N.TS_OK
+
+
 def test_zero_size_calls_are_no_ops():
     lib = N.lib()
     assert lib.ts_kv_write(None, None, 0, 0, 0, 0, None, None, 0, None, 0, 2, 64, None) == N.TS_OK

@@ -1,0 +1,203 @@
+// The per-layer elementwise ops around the attention / GEMM hot path, fused for gfx950
+// (ops/triton_rmsnorm.py:10-46, ops/triton_rope.py:10-31, ops/triton_silu_mul.py:10-28; twins
+// ops/reference.py:13-42). All three are HBM-bound row passes: one workgroup reads a token row
+// once with 16-byte vector loads, computes in fp32 and writes the fp16 result once.
+//
+// Rounding follows the reference twins (HF numerics): the residual add is an fp32 add rounded to
+// fp16; RMS is taken in fp32 over the rounded sum and the normalised row is rounded to fp16
+// before the weight multiply; RoPE rounds the fp32 cos / sin tables to fp16 and rounds each
+// product and each sum to fp16 like the twin's fp16 arithmetic (ops/reference.py:31-42; the
+// Triton kernel keeps the products in fp32, which differs from the twin near cancellation);
+// SiLU is computed in fp32 and rounded before the multiply by up.
+#include <math.h>
+
+#include "common.h"
+
+namespace ts {
+
+constexpr int kRowThreads = 256;
+constexpr int kRowVec = 8;                 // halves per 16-byte access
+constexpr int kRmsMaxIter = 4;             // N <= 4 * 256 * 8 = 8192
+
+__device__ __forceinline__ float block_sum_256(float v, float* s_red) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  if (lane == 0) s_red[w] = v;
+  __syncthreads();
+  return (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+}
+
+// One workgroup per token row of N = hidden features.
+template <bool kRes>
+__global__ void __launch_bounds__(kRowThreads) rmsnorm_kernel(
+    const half_t* __restrict__ x, int64_t x_st, const half_t* __restrict__ res, int64_t res_st,
+    const half_t* __restrict__ w, half_t* __restrict__ out, int64_t out_st,
+    half_t* __restrict__ res_out, int64_t res_out_st, int N, float eps) {
+  __shared__ float s_red[kRowThreads / kWave];
+  const int64_t t = blockIdx.x;
+  const int tid = threadIdx.x;
+  half8_t v[kRmsMaxIter];
+  float ss = 0.f;
+#pragma unroll
+  for (int it = 0; it < kRmsMaxIter; ++it) {
+    const int i = (it * kRowThreads + tid) * kRowVec;
+    if (i < N) {
+      half8_t a = ld<half8_t>(x + t * x_st + i);
+      if constexpr (kRes) {
+        const half8_t b = ld<half8_t>(res + t * res_st + i);
+#pragma unroll
+        for (int e = 0; e < kRowVec; ++e) a[e] = (half_t)((float)a[e] + (float)b[e]);
+        st<half8_t>(res_out + t * res_out_st + i, a);
+      }
+      v[it] = a;
+#pragma unroll
+      for (int e = 0; e < kRowVec; ++e) ss += (float)a[e] * (float)a[e];
+    }
+  }
+  const float inv = rsqrtf(block_sum_256(ss, s_red) / (float)N + eps);
+#pragma unroll
+  for (int it = 0; it < kRmsMaxIter; ++it) {
+    const int i = (it * kRowThreads + tid) * kRowVec;
+    if (i < N) {
+      const half8_t wv = ld<half8_t>(w + i);
+      half8_t o;
+#pragma unroll
+      for (int e = 0; e < kRowVec; ++e) {
+        const half_t y = (half_t)((float)v[it][e] * inv);          // cast before the weight
+        o[e] = (half_t)((float)wv[e] * (float)y);
+      }
+      st<half8_t>(out + t * out_st + i, o);
+    }
+  }
+}
+
+// One workgroup per token; the (H + KVH) rotated heads of the row are covered by 256 threads,
+// each owning 4 consecutive frequency indices of one head (8-byte accesses of both halves).
+__global__ void __launch_bounds__(kRowThreads) rope_kernel(
+    half_t* __restrict__ qkv, int64_t qkv_st, const int64_t* __restrict__ positions,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t max_pos,
+    int heads, int D) {
+  // Each product must round to fp16 before the sum, as in the twin: no fused multiply-add.
+#pragma clang fp contract(off)
+  const int64_t t = blockIdx.x;
+  const int half_d = D / 2, per_head = half_d / 4;
+  int64_t pos = positions[t];
+  pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
+  const float* cp = cos_t + pos * half_d;
+  const float* sp = sin_t + pos * half_d;
+  for (int u = threadIdx.x; u < heads * per_head; u += kRowThreads) {
+    const int h = u / per_head, i = (u % per_head) * 4;
+    half_t* base = qkv + t * qkv_st + (int64_t)h * D;
+    const half4_t x1 = ld<half4_t>(base + i);
+    const half4_t x2 = ld<half4_t>(base + half_d + i);
+    const float4_t c4 = ld<float4_t>(cp + i);
+    const float4_t s4 = ld<float4_t>(sp + i);
+    half4_t o1, o2;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      // fp16 x fp16 products are exact in fp32, so each rounds once to fp16, as the twin's
+      // fp16 multiplies do; the sum of two fp16 values then rounds once more.
+      const float c = (float)(half_t)c4[e], s = (float)(half_t)s4[e];
+      const float a = (float)x1[e], b = (float)x2[e];
+      o1[e] = (half_t)((float)(half_t)(a * c) - (float)(half_t)(b * s));
+      o2[e] = (half_t)((float)(half_t)(b * c) + (float)(half_t)(a * s));
+    }
+    st<half4_t>(base + i, o1);
+    st<half4_t>(base + half_d + i, o2);
+  }
+}
+
+// gu = [gate | up] per row (I features each); grid (T, ceil(I / 2048)).
+__global__ void __launch_bounds__(kRowThreads) silu_mul_kernel(
+    const half_t* __restrict__ gu, int64_t gu_st, half_t* __restrict__ out, int64_t out_st,
+    int I) {
+  const int64_t t = blockIdx.x;
+  const int i = (blockIdx.y * kRowThreads + threadIdx.x) * kRowVec;
+  if (i >= I) return;
+  const half8_t g = ld<half8_t>(gu + t * gu_st + i);
+  const half8_t u = ld<half8_t>(gu + t * gu_st + I + i);
+  half8_t o;
+#pragma unroll
+  for (int e = 0; e < kRowVec; ++e) {
+    const float gf = (float)g[e];
+    const half_t sl = (half_t)(gf / (1.f + expf(-gf)));           // silu in fp32, rounded
+    o[e] = (half_t)((float)sl * (float)u[e]);
+  }
+  st<half8_t>(out + t * out_st + i, o);
+}
+
+}  // namespace ts
+
+using namespace ts;
+
+extern "C" int ts_rmsnorm(const void* x, int64_t x_stride, const void* residual,
+                          int64_t residual_stride, const void* weight, void* out,
+                          int64_t out_stride, void* residual_out, int64_t residual_out_stride,
+                          int64_t num_tokens, int32_t hidden, float eps, void* stream) {
+  TS_REQUIRE(num_tokens >= 0, TS_ERR_INVALID_ARG, "rmsnorm: num_tokens %lld < 0",
+             (long long)num_tokens);
+  if (num_tokens == 0) return TS_OK;
+  TS_REQUIRE(x && weight && out && (!residual || residual_out), TS_ERR_INVALID_ARG,
+             "rmsnorm: null pointer argument");
+  TS_REQUIRE(hidden > 0 && hidden % kRowVec == 0 && hidden <= kRmsMaxIter * kRowThreads * kRowVec,
+             TS_ERR_UNSUPPORTED, "rmsnorm: hidden %d must be a multiple of 8 and <= 8192", hidden);
+  TS_REQUIRE(x_stride % kRowVec == 0 && out_stride % kRowVec == 0 &&
+                 (!residual || (residual_stride % kRowVec == 0 && residual_out_stride % kRowVec == 0)) &&
+                 aligned(x, 16) && aligned(out, 16) && aligned(weight, 16) &&
+                 (!residual || (aligned(residual, 16) && aligned(residual_out, 16))),
+             TS_ERR_INVALID_ARG, "rmsnorm: rows must be 16-byte aligned");
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const half_t* xp = static_cast<const half_t*>(x);
+  const half_t* wp = static_cast<const half_t*>(weight);
+  half_t* op = static_cast<half_t*>(out);
+  if (residual) {
+    rmsnorm_kernel<true><<<dim3((unsigned)num_tokens), kRowThreads, 0, s>>>(
+        xp, x_stride, static_cast<const half_t*>(residual), residual_stride, wp, op, out_stride,
+        static_cast<half_t*>(residual_out), residual_out_stride, hidden, eps);
+  } else {
+    rmsnorm_kernel<false><<<dim3((unsigned)num_tokens), kRowThreads, 0, s>>>(
+        xp, x_stride, nullptr, 0, wp, op, out_stride, nullptr, 0, hidden, eps);
+  }
+  return check_launch("rmsnorm");
+}
+
+extern "C" int ts_rope(void* qkv, int64_t qkv_stride, const int64_t* positions,
+                       const float* cos_table, const float* sin_table, int64_t max_position,
+                       int64_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                       int32_t head_dim, void* stream) {
+  TS_REQUIRE(num_tokens >= 0, TS_ERR_INVALID_ARG, "rope: num_tokens %lld < 0", (long long)num_tokens);
+  if (num_tokens == 0) return TS_OK;
+  TS_REQUIRE(qkv && positions && cos_table && sin_table && max_position > 0, TS_ERR_INVALID_ARG,
+             "rope: null pointer or empty table");
+  TS_REQUIRE(num_heads > 0 && num_kv_heads > 0, TS_ERR_INVALID_ARG, "rope: bad head counts");
+  TS_REQUIRE(head_dim % 8 == 0 && head_dim >= 8, TS_ERR_UNSUPPORTED,
+             "rope: head_dim %d must be a multiple of 8", head_dim);
+  TS_REQUIRE(qkv_stride % 4 == 0 && aligned(qkv, 8) && aligned(cos_table, 16) &&
+                 aligned(sin_table, 16),
+             TS_ERR_INVALID_ARG, "rope: misaligned qkv rows or tables");
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  rope_kernel<<<dim3((unsigned)num_tokens), kRowThreads, 0, s>>>(
+      static_cast<half_t*>(qkv), qkv_stride, positions, cos_table, sin_table, max_position,
+      num_heads + num_kv_heads, head_dim);
+  return check_launch("rope");
+}
+
+extern "C" int ts_silu_mul(const void* gu, int64_t gu_stride, void* out, int64_t out_stride,
+                           int64_t num_tokens, int32_t intermediate, void* stream) {
+  TS_REQUIRE(num_tokens >= 0, TS_ERR_INVALID_ARG, "silu_mul: num_tokens %lld < 0",
+             (long long)num_tokens);
+  if (num_tokens == 0) return TS_OK;
+  TS_REQUIRE(gu && out, TS_ERR_INVALID_ARG, "silu_mul: null pointer argument");
+  TS_REQUIRE(intermediate > 0 && intermediate % kRowVec == 0, TS_ERR_UNSUPPORTED,
+             "silu_mul: intermediate %d must be a multiple of 8", intermediate);
+  TS_REQUIRE(gu_stride % kRowVec == 0 && out_stride % kRowVec == 0 && aligned(gu, 16) &&
+                 aligned(out, 16),
+             TS_ERR_INVALID_ARG, "silu_mul: rows must be 16-byte aligned");
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const unsigned gy = (unsigned)((intermediate + kRowThreads * kRowVec - 1) / (kRowThreads * kRowVec));
+  silu_mul_kernel<<<dim3((unsigned)num_tokens, gy), kRowThreads, 0, s>>>(
+      static_cast<const half_t*>(gu), gu_stride, static_cast<half_t*>(out), out_stride,
+      intermediate);
+  return check_launch("silu_mul");
+}

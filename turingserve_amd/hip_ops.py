@@ -2,7 +2,8 @@
 
 Mirrors ops/triton_ops.py (dispatch, decode-version selection, linear routing),
 ops/triton_kv_write.py:28-35, ops/triton_decode_attention.py:169-200,
-ops/triton_prefill_attention.py:66-79 and ops/triton_w8a16.py:38-51. Every op turns its tensors
+ops/triton_prefill_attention.py:66-79, ops/triton_w8a16.py:38-51 and the fused small ops
+(ops/triton_rmsnorm.py:30-46, ops/triton_rope.py:27-31, ops/triton_silu_mul.py:21-28). Every op turns its tensors
 into pointers and strides, allocates outputs and scratch from the torch caching allocator (so the
 calls can be captured into a hipGraph) and launches on torch's current stream. A shape the
 kernels do not support raises ValueError; nothing falls back to another implementation.
@@ -21,7 +22,7 @@ from turingserve_amd.quant import LinearWeight
 
 __all__ = ["kv_write", "paged_attention", "linear", "lm_head_int8", "w8a16_linear",
            "decode_attention_v1", "decode_attention_v2", "decode_attention_v3",
-           "prefill_attention"]
+           "prefill_attention", "rmsnorm", "rmsnorm_residual", "rope_", "silu_mul"]
 
 DEFAULT_PARTITION = 0            # v3 split size when the caller names none: 0 = balanced
 
@@ -244,3 +245,69 @@ def linear(x: torch.Tensor, lw: LinearWeight) -> torch.Tensor:
 def lm_head_int8(h: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     """int8 tied lm head (ops/triton_ops.py:88-91)."""
     return w8a16_linear(h, wq, scale, None)
+
+
+# ------------------------------------------------------------------------------------------
+# fused small ops (ops/triton_rmsnorm.py:30-46, ops/triton_rope.py:27-31,
+# ops/triton_silu_mul.py:21-28)
+# ------------------------------------------------------------------------------------------
+def _rows(x: torch.Tensor, what: str) -> torch.Tensor:
+    _check_gpu(x)
+    _require(x.dim() == 2 and x.dtype == torch.float16, f"{what}: expected fp16 [T, N]")
+    return x if (x.stride(1) == 1 and x.stride(0) % 8 == 0 and x.data_ptr() % 16 == 0) \
+        else x.contiguous()
+
+
+def rmsnorm_residual(x: torch.Tensor, residual: torch.Tensor | None, w: torch.Tensor,
+                     eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """(out, new_residual) with new_residual = x + residual (fp16) or x itself when residual is
+    None, out = rmsnorm(new_residual) (ops/triton_rmsnorm.py:30-46)."""
+    x = _rows(x, "rmsnorm")
+    T, Nf = x.shape
+    out = torch.empty(T, Nf, dtype=x.dtype, device=x.device)
+    w = w.contiguous()
+    _require(w.shape == (Nf,) and w.dtype == torch.float16, "rmsnorm: weight must be fp16 [N]")
+    if residual is None:
+        N.check(N.lib().ts_rmsnorm(_ptr(x), x.stride(0), None, 0, _ptr(w), _ptr(out), out.stride(0),
+                                   None, 0, T, Nf, float(eps), _stream(x)), "rmsnorm")
+        return out, x
+    residual = _rows(residual, "rmsnorm")
+    _require(residual.shape == x.shape, "rmsnorm: residual shape differs from x")
+    res_out = torch.empty_like(out)
+    N.check(N.lib().ts_rmsnorm(_ptr(x), x.stride(0), _ptr(residual), residual.stride(0), _ptr(w),
+                               _ptr(out), out.stride(0), _ptr(res_out), res_out.stride(0), T, Nf,
+                               float(eps), _stream(x)), "rmsnorm")
+    return out, res_out
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    return rmsnorm_residual(x, None, w, eps)[0]
+
+
+def rope_(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
+          H: int, KVH: int, D: int) -> None:
+    """In-place rotate-half RoPE on the q and k heads of qkv [T, (H + 2 KVH) D]; cos / sin are
+    the fp32 tables [max_len, D / 2] (ops/triton_rope.py:27-31)."""
+    _check_gpu(qkv, positions, cos, sin)
+    T = qkv.shape[0]
+    _require(qkv.dim() == 2 and qkv.stride(1) == 1 and qkv.dtype == torch.float16,
+             "rope: qkv must be fp16 rows with unit stride")
+    _require(qkv.shape[1] >= (H + KVH) * D, "rope: qkv is narrower than the q and k heads")
+    _require(cos.dtype == torch.float32 and sin.dtype == torch.float32 and cos.is_contiguous()
+             and sin.is_contiguous() and cos.shape == sin.shape and cos.shape[-1] == D // 2,
+             "rope: tables must be contiguous fp32 [max_len, D / 2]")
+    pos = positions if (positions.dtype == torch.int64 and positions.is_contiguous()) \
+        else positions.to(torch.int64).contiguous()
+    N.check(N.lib().ts_rope(_ptr(qkv), qkv.stride(0), _ptr(pos), _ptr(cos), _ptr(sin),
+                            cos.shape[0], T, H, KVH, D, _stream(qkv)), "rope")
+
+
+def silu_mul(gu: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up for gu = [gate | up] rows (ops/triton_silu_mul.py:21-28)."""
+    gu = _rows(gu, "silu_mul")
+    T, two_i = gu.shape
+    inter = two_i // 2
+    out = torch.empty(T, inter, dtype=gu.dtype, device=gu.device)
+    N.check(N.lib().ts_silu_mul(_ptr(gu), gu.stride(0), _ptr(out), out.stride(0), T, inter,
+                                _stream(gu)), "silu_mul")
+    return out

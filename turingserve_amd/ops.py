@@ -1,8 +1,8 @@
 """Op dispatch: ``get_ops("reference" | "hip")`` returns a namespace of op callables.
 
 Restates ops/__init__.py:12-43 with ``hip`` in place of ``triton``: the hip namespace starts from
-the reference namespace (the dense/masked attention helpers and the fused small ops stay on the
-twins) and overrides the hot-path ops with the gfx950 kernels. ``"triton"`` is accepted as an alias
+the reference namespace (the dense/masked attention helpers stay on the twins) and overrides the
+hot-path ops and the fused small ops with the gfx950 kernels. ``"triton"`` is accepted as an alias
 of ``"hip"`` so an existing ``--kernels triton`` configuration switches backends unchanged.
 """
 
@@ -32,6 +32,10 @@ def _hip() -> SimpleNamespace:
     ns.kv_write = h.kv_write
     ns.paged_attention = h.paged_attention
     ns.lm_head_int8 = h.lm_head_int8
+    ns.rmsnorm = h.rmsnorm
+    ns.rmsnorm_residual = h.rmsnorm_residual
+    ns.rope_ = h.rope_
+    ns.silu_mul = h.silu_mul
     return ns
 
 
