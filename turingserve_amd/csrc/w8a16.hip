@@ -184,7 +184,8 @@ __global__ void __launch_bounds__(256) w8a16_reduce_kernel(
 // writes fp32 partials for w8a16_reduce_kernel.
 constexpr int kTileBK = 64;
 
-template <int BN, int BM>
+
+template <int BN, int BM, int RD>
 __global__ void __launch_bounds__(256) w8a16_tile_kernel(
     const half_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ wq,
     const void* __restrict__ scale, int scale_is_fp16, const half_t* __restrict__ bias,
@@ -208,34 +209,43 @@ __global__ void __launch_bounds__(256) w8a16_tile_kernel(
   const int ke = (kb + k_per_split < K) ? kb + k_per_split : K;
   const int nk = (ke - kb + BK - 1) / BK;
 
-  int2_t wreg[WPT];
-  half8_t xreg[XPT];
-  auto gload = [&](int kt) {
+  // Register ring of RD stages: the global loads of tile kt + RD - 1 are issued before tile kt
+  // is multiplied, so each wait before an LDS store is covered by RD - 1 tiles of MFMA work
+  // instead of one (the per-tile work is far shorter than a memory round trip).
+  static_assert(RD % 2 == 0, "register stages pair with the two LDS buffers");
+  int2_t wreg[RD][WPT];
+  half8_t xreg[RD][XPT];
+  // Every load is issued by every lane at an in-range (clamped) address and out-of-range lanes
+  // are zeroed afterwards: no branch around a load, so the count of loads in flight is static.
+  auto gload = [&](int kt, int2_t (&wr)[WPT], half8_t (&xr)[XPT]) {
     const int k0 = kb + kt * BK;
 #pragma unroll
     for (int i = 0; i < WPT; ++i) {
       const int u = tid + 256 * i, r = u / (BK / 8), cc = u % (BK / 8);
       const int n = n_base + r, k = k0 + 8 * cc;
-      wreg[i] = (n < N && k < ke) ? ld<int2_t>(wq + (int64_t)n * K + k) : int2_t{0, 0};
+      const bool ok = n < N && k < ke;
+      const int2_t v = ld<int2_t>(wq + (int64_t)(n < N ? n : N - 1) * K + (k < K ? k : K - 8));
+      wr[i] = ok ? v : int2_t{0, 0};
     }
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
       const int u = tid + 256 * i, r = u / (BK / 8), cc = u % (BK / 8);
       const int mm = m_base + r, k = k0 + 8 * cc;
-      xreg[i] = (mm < M && k < ke) ? ld<half8_t>(x + (int64_t)mm * ldx + k)
-                                   : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      const bool ok = mm < M && k < ke;
+      const half8_t v = ld<half8_t>(x + (int64_t)(mm < M ? mm : M - 1) * ldx + (k < K ? k : K - 8));
+      xr[i] = ok ? v : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](int buf, const int2_t (&wr)[WPT], const half8_t (&xr)[XPT]) {
 #pragma unroll
     for (int i = 0; i < WPT; ++i) {
       const int u = tid + 256 * i;
-      st<int2_t>(&s_w[buf][u / (BK / 8)][8 * (u % (BK / 8))], wreg[i]);
+      st<int2_t>(&s_w[buf][u / (BK / 8)][8 * (u % (BK / 8))], wr[i]);
     }
 #pragma unroll
     for (int i = 0; i < XPT; ++i) {
       const int u = tid + 256 * i;
-      st<half8_t>(&s_x[buf][u / (BK / 8)][8 * (u % (BK / 8))], xreg[i]);
+      st<half8_t>(&s_x[buf][u / (BK / 8)][8 * (u % (BK / 8))], xr[i]);
     }
   };
 
@@ -245,29 +255,40 @@ __global__ void __launch_bounds__(256) w8a16_tile_kernel(
 #pragma unroll
     for (int j = 0; j < TM; ++j) acc[i][j] = {0.f, 0.f, 0.f, 0.f};
 
-  if (nk > 0) {
-    gload(0);
-    lstore(0);
-  }
-  __syncthreads();
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) gload(kt + 1);              // in flight during the MFMAs below
+  auto mma_tile = [&](int buf) {
 #pragma unroll
     for (int ks = 0; ks < BK / 32; ++ks) {
       half8_t a[TN], b[TM];
 #pragma unroll
       for (int i = 0; i < TN; ++i)
-        a[i] = i8x8_to_half8(ld<int2_t>(&s_w[cur][wn * (BN / 2) + 16 * i + c][32 * ks + 8 * g]));
+        a[i] = i8x8_to_half8(ld<int2_t>(&s_w[buf][wn * (BN / 2) + 16 * i + c][32 * ks + 8 * g]));
 #pragma unroll
-      for (int j = 0; j < TM; ++j) b[j] = ld<half8_t>(&s_x[cur][wm * (BM / 2) + 16 * j + c][32 * ks + 8 * g]);
+      for (int j = 0; j < TM; ++j) b[j] = ld<half8_t>(&s_x[buf][wm * (BM / 2) + 16 * j + c][32 * ks + 8 * g]);
 #pragma unroll
       for (int i = 0; i < TN; ++i)
 #pragma unroll
         for (int j = 0; j < TM; ++j) acc[i][j] = mfma16x16x32(a[i], b[j], acc[i][j]);
     }
-    if (kt + 1 < nk) lstore(cur ^ 1);            // the other buffer was last read before the
-    __syncthreads();                             // previous barrier
+  };
+
+  // Loads are unconditional: a tile past the end of the K range has every lane predicated off
+  // by the k < ke test and yields zeros, so each iteration keeps the same loads in flight and
+  // every wait covers exactly the tile it needs.
+#pragma unroll
+  for (int st_ = 0; st_ < RD - 1; ++st_) gload(st_, wreg[st_], xreg[st_]);
+  lstore(0, wreg[0], xreg[0]);
+  __syncthreads();
+  // Tile kt sits in LDS buffer kt % 2 and came through register stage kt % RD (RD is even, so
+  // both indices are compile-time constants within the unrolled group).
+  for (int kt0 = 0; kt0 < nk; kt0 += RD) {
+#pragma unroll
+    for (int u = 0; u < RD; ++u) {
+      const int kt = kt0 + u;
+      gload(kt + RD - 1, wreg[(u + RD - 1) % RD], xreg[(u + RD - 1) % RD]);
+      if (kt < nk) mma_tile(u & 1);
+      lstore((u + 1) & 1, wreg[(u + 1) % RD], xreg[(u + 1) % RD]);
+      __syncthreads();                           // the other buffer was last read before the
+    }                                            // previous barrier
   }
   // lane (c, g) of tile (i, j) holds Y[m = .. + 16 j + c][n = .. + 16 i + 4g + r]
 #pragma unroll
@@ -437,13 +458,13 @@ extern "C" int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const
     float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const dim3 grid((N + p.bn - 1) / p.bn, (M + p.bm - 1) / p.bm, p.splits);
     if (p.bn == 128 && p.bm == 128)
-      w8a16_tile_kernel<128, 128><<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy,
+      w8a16_tile_kernel<128, 128, 2><<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy,
                                                        M, N, K, p.k_per_split, part);
     else if (p.bn == 128)
-      w8a16_tile_kernel<128, 64><<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy,
+      w8a16_tile_kernel<128, 64, 4><<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy,
                                                       M, N, K, p.k_per_split, part);
     else
-      w8a16_tile_kernel<64, 64><<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy,
+      w8a16_tile_kernel<64, 64, 4><<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy,
                                                      M, N, K, p.k_per_split, part);
     if (p.splits > 1) {
       const int64_t total = (int64_t)M * N;
