@@ -283,6 +283,29 @@ def test_w8a16_config4(M, N, Kd):
     assert err.max() <= 1e-2 and err.mean() <= 1e-3
 
 
+@pytest.mark.parametrize("M", [5, 65, 300])
+@pytest.mark.parametrize("N,Kd", [(36, 24), (132, 200), (200, 1000), (96, 72), (64, 8)])
+@pytest.mark.parametrize("offset", [0, 8])
+def test_w8a16_odd_shapes_and_alignment(M, N, Kd, offset):
+    """K not a multiple of 64 (the split's last K step is partial; K < 64 and K = 8 included),
+    N not a multiple of the tile (a multiple of 4: output rows must be 8-byte aligned), M past
+    the small-M path, and weights 8- but not 16-byte aligned (offset 8): the paths the 1.5B
+    shapes never take."""
+    g = torch.Generator().manual_seed(M * 31 + N * 7 + Kd + offset)
+    w = torch.randn(N, Kd, generator=g) * 0.05
+    wq, sc = OQ.quantize(w.numpy())
+    store = torch.zeros(N * Kd + offset, dtype=torch.int8, device=DEV)
+    wdev = store[offset:].view(N, Kd)
+    wdev.copy_(torch.from_numpy(wq).cuda())
+    assert wdev.data_ptr() % 16 == (offset % 16)
+    x = torch.randn(M, Kd, generator=g).half()
+    bias = (torch.randn(N, generator=g) * 0.1).half()
+    y = K.w8a16_linear(x.cuda(), wdev, torch.from_numpy(sc).cuda(), bias.cuda())
+    ref = OQ.w8a16(x.numpy(), wq, sc, bias.numpy(), np.float64)
+    yn = y.float().cpu().numpy()
+    assert np.linalg.norm(yn - ref) / np.linalg.norm(ref) < 1e-3
+
+
 def test_w8a16_bias_and_linear_routing():
     from turingserve_amd.quant import LinearWeight
 

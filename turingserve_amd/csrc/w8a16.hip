@@ -174,16 +174,24 @@ __global__ void __launch_bounds__(256) w8a16_reduce_kernel(
 }
 
 // ------------------------------------------------------------------------------------------
-// Larger M: LDS-tiled MFMA GEMM, double-buffered.
+// Larger M: LDS-tiled MFMA GEMM.
 // ------------------------------------------------------------------------------------------
 // Workgroup = 4 wavefronts (2 x 2) on a BN (output channels) x BM (activation rows) tile, K step
-// 64. The int8 tile stays int8 in LDS (half the bytes) and is widened when it is read into the A
-// operand. Tile kt + 1 is fetched into registers while tile kt is multiplied out of LDS, then
-// stored into the other LDS buffer: one barrier per K step and the global latency hidden behind
-// the MFMAs. With split-K (gridDim.z > 1) each workgroup covers k_per_split columns of K and
-// writes fp32 partials for w8a16_reduce_kernel.
+// 64. Each thread stages 8-column chunks of both tiles: weight chunks are widened to fp16 once,
+// as they enter LDS (each weight is then read by the two wavefronts that share it without being
+// converted twice), and both tiles are stored as rows of eight 16-byte chunks with chunk kc of
+// row r at position kc ^ (r & 7), an XOR swizzle under which the MFMA operand reads (16 rows x
+// one chunk, eight lanes per LDS cycle) and the staging writes (one row, eight chunks) touch
+// eight distinct bank groups. Global loads run RD - 1 K steps ahead through a register ring, the
+// LDS tiles are double-buffered, and every load is issued by every lane at an in-range address
+// (rows past M or N repeat the last row, whose results are discarded; a K tail past the split
+// end is read at column K - 8 and zeroed) so the loads in flight never depend on a branch. The
+// per-channel scales and the bias are fetched before the loop. (Streaming the weights straight
+// into A-operand registers instead halves the LDS traffic but measured slower: each weight row
+// is then loaded and widened by two wavefronts.) With split-K (gridDim.z > 1) each workgroup
+// covers k_per_split columns of K and writes fp32 partials for w8a16_reduce_kernel.
 constexpr int kTileBK = 64;
-
+constexpr int kTileChunks = kTileBK / 8;          // 16-byte fp16 chunks per tile row
 
 template <int BN, int BM, int RD>
 __global__ void __launch_bounds__(256) w8a16_tile_kernel(
@@ -191,62 +199,83 @@ __global__ void __launch_bounds__(256) w8a16_tile_kernel(
     const void* __restrict__ scale, int scale_is_fp16, const half_t* __restrict__ bias,
     half_t* __restrict__ y, int64_t ldy, int M, int N, int K, int k_per_split,
     float* __restrict__ part) {
-  constexpr int BK = kTileBK;
-  constexpr int WP = BK + 16;                 // padded int8 row (bytes)
-  constexpr int XP = BK + 8;                  // padded fp16 row (halfs)
+  constexpr int BK = kTileBK, CH = kTileChunks;
   constexpr int TN = BN / 32, TM = BM / 32;   // 16 x 16 MFMA tiles per wavefront
-  constexpr int WCH = BN * BK / 8;            // 8-byte chunks of the W tile (K % 8 == 0)
-  constexpr int XCH = BM * BK / 8;            // 16-byte chunks of the X tile
-  constexpr int WPT = WCH / 256, XPT = XCH / 256;
-  static_assert(WPT * 256 == WCH && XPT * 256 == XCH, "tile must split evenly over 256 threads");
-  __shared__ int8_t s_w[2][BN][WP];
-  __shared__ half_t s_x[2][BM][XP];
-  const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
+  constexpr int WPT = BN * CH / 256, XPT = BM * CH / 256;
+  static_assert(WPT * 256 == BN * CH && XPT * 256 == BM * CH, "tile must split over 256 threads");
+  static_assert(RD % 2 == 0, "register stages pair with the two LDS buffers");
+  __shared__ half8_t s_w[2][BN * CH];
+  __shared__ half8_t s_x[2][BM * CH];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c = lane & 15, g = lane >> 4;
   const int wn = w >> 1, wm = w & 1;
   const int n_base = blockIdx.x * BN, m_base = blockIdx.y * BM;
   const int kb = blockIdx.z * k_per_split;
   const int ke = (kb + k_per_split < K) ? kb + k_per_split : K;
   const int nk = (ke - kb + BK - 1) / BK;
+  const bool k_tail = (ke - kb) % BK != 0;          // last step reaches past the split end
 
-  // Register ring of RD stages: the global loads of tile kt + RD - 1 are issued before tile kt
-  // is multiplied, so each wait before an LDS store is covered by RD - 1 tiles of MFMA work
-  // instead of one (the per-tile work is far shorter than a memory round trip).
-  static_assert(RD % 2 == 0, "register stages pair with the two LDS buffers");
+  // Chunk u = tid + 256 i of a tile is row u / CH, columns 8 (u % CH) .. + 7 of the K step.
+  const int kc = tid % CH;
+  const int8_t* wrow[WPT];
+  const half_t* xrow[XPT];
+  int wpos[WPT], xpos[XPT];
+#pragma unroll
+  for (int i = 0; i < WPT; ++i) {
+    const int r = (tid + 256 * i) / CH, n = n_base + r;
+    wrow[i] = wq + (int64_t)(n < N ? n : N - 1) * K;
+    wpos[i] = r * CH + (kc ^ (r & 7));
+  }
+#pragma unroll
+  for (int i = 0; i < XPT; ++i) {
+    const int r = (tid + 256 * i) / CH, mm = m_base + r;
+    xrow[i] = x + (int64_t)(mm < M ? mm : M - 1) * ldx;
+    xpos[i] = r * CH + (kc ^ (r & 7));
+  }
+  // Output-channel scale and bias of this lane's four columns per tile, fetched up front.
+  float sc[TN][4], bs[TN][4];
+#pragma unroll
+  for (int i = 0; i < TN; ++i)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int nn = n_base + wn * (BN / 2) + 16 * i + 4 * g + r;
+      const int nc = nn < N ? nn : N - 1;
+      sc[i][r] = part ? 0.f : load_scale(scale, scale_is_fp16, nc);
+      bs[i][r] = (part || !bias) ? 0.f : (float)bias[nc];
+    }
+
   int2_t wreg[RD][WPT];
   half8_t xreg[RD][XPT];
-  // Every load is issued by every lane at an in-range (clamped) address and out-of-range lanes
-  // are zeroed afterwards: no branch around a load, so the count of loads in flight is static.
+  // Step kt's loads; steps past the split end repeat the last step (a cache hit that is never
+  // used), so every lane issues the same loads in every iteration.
   auto gload = [&](int kt, int2_t (&wr)[WPT], half8_t (&xr)[XPT]) {
-    const int k0 = kb + kt * BK;
+    const int k = kb + (kt < nk ? kt : nk - 1) * BK + 8 * kc;
+    if (k_tail && kt >= nk - 1) {                   // rare: column K - 8 stands in, then zero
+      const bool ok = k < ke;
+      const int ka = ok ? k : K - 8;
 #pragma unroll
-    for (int i = 0; i < WPT; ++i) {
-      const int u = tid + 256 * i, r = u / (BK / 8), cc = u % (BK / 8);
-      const int n = n_base + r, k = k0 + 8 * cc;
-      const bool ok = n < N && k < ke;
-      const int2_t v = ld<int2_t>(wq + (int64_t)(n < N ? n : N - 1) * K + (k < K ? k : K - 8));
-      wr[i] = ok ? v : int2_t{0, 0};
-    }
+      for (int i = 0; i < WPT; ++i) {
+        const int2_t v = ld<int2_t>(wrow[i] + ka);
+        wr[i] = ok ? v : int2_t{0, 0};
+      }
 #pragma unroll
-    for (int i = 0; i < XPT; ++i) {
-      const int u = tid + 256 * i, r = u / (BK / 8), cc = u % (BK / 8);
-      const int mm = m_base + r, k = k0 + 8 * cc;
-      const bool ok = mm < M && k < ke;
-      const half8_t v = ld<half8_t>(x + (int64_t)(mm < M ? mm : M - 1) * ldx + (k < K ? k : K - 8));
-      xr[i] = ok ? v : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      for (int i = 0; i < XPT; ++i) {
+        const half8_t v = ld<half8_t>(xrow[i] + ka);
+        xr[i] = ok ? v : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < WPT; ++i) wr[i] = ld<int2_t>(wrow[i] + k);
+#pragma unroll
+      for (int i = 0; i < XPT; ++i) xr[i] = ld<half8_t>(xrow[i] + k);
     }
   };
   auto lstore = [&](int buf, const int2_t (&wr)[WPT], const half8_t (&xr)[XPT]) {
 #pragma unroll
-    for (int i = 0; i < WPT; ++i) {
-      const int u = tid + 256 * i;
-      st<int2_t>(&s_w[buf][u / (BK / 8)][8 * (u % (BK / 8))], wr[i]);
-    }
+    for (int i = 0; i < WPT; ++i) s_w[buf][wpos[i]] = i8x8_to_half8(wr[i]);
 #pragma unroll
-    for (int i = 0; i < XPT; ++i) {
-      const int u = tid + 256 * i;
-      st<half8_t>(&s_x[buf][u / (BK / 8)][8 * (u % (BK / 8))], xr[i]);
-    }
+    for (int i = 0; i < XPT; ++i) s_x[buf][xpos[i]] = xr[i];
   };
 
   float4_t acc[TN][TM];
@@ -255,15 +284,16 @@ __global__ void __launch_bounds__(256) w8a16_tile_kernel(
 #pragma unroll
     for (int j = 0; j < TM; ++j) acc[i][j] = {0.f, 0.f, 0.f, 0.f};
 
+  // Operand rows are 16 i + c past a multiple of 16, so their swizzle key is c & 7.
   auto mma_tile = [&](int buf) {
 #pragma unroll
     for (int ks = 0; ks < BK / 32; ++ks) {
+      const int pc = (4 * ks + g) ^ (c & 7);
       half8_t a[TN], b[TM];
 #pragma unroll
-      for (int i = 0; i < TN; ++i)
-        a[i] = i8x8_to_half8(ld<int2_t>(&s_w[buf][wn * (BN / 2) + 16 * i + c][32 * ks + 8 * g]));
+      for (int i = 0; i < TN; ++i) a[i] = s_w[buf][(wn * (BN / 2) + 16 * i + c) * CH + pc];
 #pragma unroll
-      for (int j = 0; j < TM; ++j) b[j] = ld<half8_t>(&s_x[buf][wm * (BM / 2) + 16 * j + c][32 * ks + 8 * g]);
+      for (int j = 0; j < TM; ++j) b[j] = s_x[buf][(wm * (BM / 2) + 16 * j + c) * CH + pc];
 #pragma unroll
       for (int i = 0; i < TN; ++i)
 #pragma unroll
@@ -271,14 +301,13 @@ __global__ void __launch_bounds__(256) w8a16_tile_kernel(
     }
   };
 
-  // Loads are unconditional: a tile past the end of the K range has every lane predicated off
-  // by the k < ke test and yields zeros, so each iteration keeps the same loads in flight and
-  // every wait covers exactly the tile it needs.
+  if (nk > 0) {
 #pragma unroll
-  for (int st_ = 0; st_ < RD - 1; ++st_) gload(st_, wreg[st_], xreg[st_]);
-  lstore(0, wreg[0], xreg[0]);
+    for (int st_ = 0; st_ < RD - 1; ++st_) gload(st_, wreg[st_], xreg[st_]);
+    lstore(0, wreg[0], xreg[0]);
+  }
   __syncthreads();
-  // Tile kt sits in LDS buffer kt % 2 and came through register stage kt % RD (RD is even, so
+  // Step kt sits in LDS buffer kt % 2 and came through register stage kt % RD (RD is even, so
   // both indices are compile-time constants within the unrolled group).
   for (int kt0 = 0; kt0 < nk; kt0 += RD) {
 #pragma unroll
@@ -294,13 +323,6 @@ __global__ void __launch_bounds__(256) w8a16_tile_kernel(
 #pragma unroll
   for (int i = 0; i < TN; ++i) {
     const int nn = n_base + wn * (BN / 2) + 16 * i + 4 * g;
-    float sc[4], bs[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const bool ok = nn + r < N;
-      sc[r] = (ok && !part) ? load_scale(scale, scale_is_fp16, nn + r) : 0.f;
-      bs[r] = (ok && !part && bias) ? (float)bias[nn + r] : 0.f;
-    }
 #pragma unroll
     for (int j = 0; j < TM; ++j) {
       const int mm = m_base + wm * (BM / 2) + 16 * j + c;
@@ -317,12 +339,12 @@ __global__ void __launch_bounds__(256) w8a16_tile_kernel(
       }
       half_t* yp = y + (int64_t)mm * ldy + nn;
       if (nn + 3 < N) {
-        const half4_t v = {(half_t)(acc[i][j][0] * sc[0] + bs[0]), (half_t)(acc[i][j][1] * sc[1] + bs[1]),
-                           (half_t)(acc[i][j][2] * sc[2] + bs[2]), (half_t)(acc[i][j][3] * sc[3] + bs[3])};
+        const half4_t v = {(half_t)(acc[i][j][0] * sc[i][0] + bs[i][0]), (half_t)(acc[i][j][1] * sc[i][1] + bs[i][1]),
+                           (half_t)(acc[i][j][2] * sc[i][2] + bs[i][2]), (half_t)(acc[i][j][3] * sc[i][3] + bs[i][3])};
         st<half4_t>(yp, v);
       } else {
         for (int r = 0; r < 4; ++r)
-          if (nn + r < N) yp[r] = (half_t)(acc[i][j][r] * sc[r] + bs[r]);
+          if (nn + r < N) yp[r] = (half_t)(acc[i][j][r] * sc[i][r] + bs[i][r]);
       }
     }
   }
@@ -361,6 +383,17 @@ static GemmPlan plan_gemm(int M, int N, int K, int cus) {
     p.k_per_split = kps;
     return p;
   }
+#ifdef TS_W8A16_FORCE_BN                          // tuning override (bn, bm, splits)
+  if (!p.small) {
+    p.bn = TS_W8A16_FORCE_BN;
+    p.bm = TS_W8A16_FORCE_BM;
+    const int nk = (K + kTileBK - 1) / kTileBK;
+    const int steps = (nk + TS_W8A16_FORCE_SPLITS - 1) / TS_W8A16_FORCE_SPLITS;
+    p.k_per_split = steps * kTileBK;
+    p.splits = (K + p.k_per_split - 1) / p.k_per_split;
+    return p;
+  }
+#endif
   // Largest tile whose grid covers every CU; the smallest tile otherwise.
   static const int tiles[3][2] = {{128, 128}, {128, 64}, {64, 64}};
   int64_t grid = 0;
@@ -457,15 +490,16 @@ extern "C" int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const
   } else {
     float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const dim3 grid((N + p.bn - 1) / p.bn, (M + p.bm - 1) / p.bm, p.splits);
+#define TS_TILE_LAUNCH(BNV, BMV)                                                                  \
+  w8a16_tile_kernel<BNV, BMV, 4><<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, yp,  \
+                                                      ldy, M, N, K, p.k_per_split, part)
     if (p.bn == 128 && p.bm == 128)
-      w8a16_tile_kernel<128, 128, 2><<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy,
-                                                       M, N, K, p.k_per_split, part);
+      TS_TILE_LAUNCH(128, 128);
     else if (p.bn == 128)
-      w8a16_tile_kernel<128, 64, 4><<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy,
-                                                      M, N, K, p.k_per_split, part);
+      TS_TILE_LAUNCH(128, 64);
     else
-      w8a16_tile_kernel<64, 64, 4><<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy,
-                                                     M, N, K, p.k_per_split, part);
+      TS_TILE_LAUNCH(64, 64);
+#undef TS_TILE_LAUNCH
     if (p.splits > 1) {
       const int64_t total = (int64_t)M * N;
       const int64_t want = (total + 255) / 256;
