@@ -206,17 +206,25 @@ def cpu_baseline(st, seconds: float):
 # secondary configurations
 # ------------------------------------------------------------------------------------------
 def time_graph(torch, fn, reps: int, inner: int = 1):
-    """Capture `inner` back-to-back calls in one hipGraph, replay `reps` times, return the mean
-    per-call milliseconds from HIP events."""
+    """Capture `inner` back-to-back calls in one hipGraph, replay it for at least 30 ms of warm-up
+    (the clocks may have dropped while the host was busy, e.g. after the CPU baseline) and time at
+    least `reps` replays and at least 20 ms; return the mean per-call milliseconds from HIP
+    events."""
     fn()
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g):
         for _ in range(inner):
             fn()
-    for _ in range(3):
-        g.replay()
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    g.replay()
+    e.record()
+    torch.cuda.synchronize()
+    one = max(s.elapsed_time(e), 1e-3)
+    for _ in range(max(3, int(30.0 / one) + 1)):
+        g.replay()
+    reps = max(reps, int(20.0 / one) + 1)
     torch.cuda.synchronize()
     s.record()
     for _ in range(reps):
