@@ -100,8 +100,16 @@ def test_workspace_sizes():
     # ... but not contexts of at most two minimum splits or a batch that fills the device
     assert lib.ts_decode_workspace_bytes(0, 64, 12, 2, 128, 256, 0, 256) == 0
     assert lib.ts_decode_workspace_bytes(0, 256, 12, 2, 128, 4096, 0, 256) == 0
-    # W8A16: the large-M path needs none; small M splits K into fp32 partials
+    # W8A16: 128 x 128 tiles that cover the device need no workspace
     assert lib.ts_w8a16_workspace_bytes(2048, 17920, 1536, 256) == 0
+    assert lib.ts_w8a16_workspace_bytes(64, 17920, 1536, 256) == 0      # 140 tiles, 2 per CU
+    # 108 tiles of 128 x 64 for the 1.5B down projection at M = 560: split K in two (70 K
+    # steps each, partials 2 x 560 x 1536 fp32 within the 8 MB floor); a third split would not
+    # fit and K = 1536 (24 steps) never splits
+    assert lib.ts_w8a16_workspace_bytes(560, 1536, 8960, 256) == 2 * 560 * 1536 * 4
+    assert lib.ts_w8a16_workspace_bytes(560, 1536, 1536, 256) == 0
+    # weight streaming at M = 1: 32 workgroups, split into 6 (K / 256) fp32 partial rows
+    assert lib.ts_w8a16_workspace_bytes(1, 2048, 1536, 256) == 6 * 2048 * 4
     ws = lib.ts_w8a16_workspace_bytes(1, 1536, 8960, 256)
     assert ws > 0 and ws % (1536 * 4) == 0
 

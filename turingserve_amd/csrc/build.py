@@ -26,11 +26,17 @@ ARCH = "gfx950"
 COMMON_FLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-std=c++17", "-fPIC", "-Wall", "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
-    # MFMA accumulators in VGPRs (gfx90a+ allows either file): with the default AGPR form the
-    # register allocator copied whole O^T accumulator sets between AGPRs around the rarely taken
-    # softmax rescale branch; the VGPR form needs no copies at the same occupancy.
-    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
+# Per-source flags. Attention kernels keep their MFMA accumulators in VGPRs (gfx90a+ allows
+# either file): with the default AGPR form the register allocator copied whole O^T accumulator
+# sets between AGPRs around the rarely taken softmax rescale branch; the VGPR form needs no
+# copies at the same occupancy. The GEMM keeps the default AGPR form: its widest tile holds 128
+# accumulator registers per lane, which then live in AGPRs beside ~200 VGPRs instead of
+# spilling out of a 256-register VGPR file.
+SOURCE_FLAGS = {
+    "decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
 
 
 def hipcc() -> str:
@@ -42,7 +48,8 @@ def hipcc() -> str:
 
 def _compile(src: str, extra: list[str]) -> str:
     obj = os.path.join(BUILD_DIR, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, *extra, "-c", os.path.join(HERE, src), "-o", obj]
+    cmd = [hipcc(), *COMMON_FLAGS, *SOURCE_FLAGS.get(src, []), *extra, "-c",
+           os.path.join(HERE, src), "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -1,21 +1,21 @@
 // W8A16 GEMM for gfx950: y = x . (wq * scale)^T (+ bias)   (ops/triton_w8a16.py:11-51).
 //
 // The int8 weights are widened to fp16 in registers (exact: |w| <= 127), the contraction runs
-// on v_mfma_f32_16x16x32_f16 with fp32 accumulation and the per-output-channel scale (and
-// the bias) are applied once at the end, as the Triton kernel does.
+// on MFMAs with fp32 accumulation and the per-output-channel scale (and the bias) are applied
+// once at the end, as the Triton kernel does.
 //
 // Everything is computed transposed, Y^T[N][M] = W[N][K] . X^T[K][M], so that both operands
-// are row-contiguous loads: lane (c, g) holds W[n + c][k .. k+7] (8 bytes) as the A operand
-// and X[m + c][k .. k+7] (16 bytes) as the B operand, and the result lane holds
-// Y[m + c][n + 4g .. n + 4g + 3] (see common.h for the operand layouts).
+// are row-contiguous loads (weights as the A operand, activations as the B operand).
 //
-//  * small M (<= 64): HBM-bound weight streaming. One wavefront owns 16 output channels and
-//    a K range; lane (c, g) reads 16 contiguous weight bytes per 64-wide K step (64 bytes per
-//    row and instruction). The K dimension is split over workgroups until the device is full;
-//    fp32 partials are merged (and scaled) by a second kernel.
-//  * larger M: double-buffered LDS-tiled MFMA GEMM (128x128, 128x64 or 64x64 tiles chosen so
-//    the grid covers the CUs, split-K when even the smallest tile does not), K step 64, int8
-//    tile kept as int8 in LDS and widened on read.
+//  * small M (<= 32, see use_small_path): HBM-bound weight streaming on v_mfma_f32_16x16x32_f16. One wavefront
+//    owns 16 output channels and a K range; lane (c, g) reads 16 contiguous weight bytes per
+//    64-wide K step (64 bytes per row and instruction). The K dimension is split over
+//    workgroups until the device is full; fp32 partials are merged (and scaled) by a second
+//    kernel.
+//  * larger M: the wide-tile kernel on v_mfma_f32_32x32x16_f16 (128 x 128 or 128 x 64 tiles of
+//    Y^T, split-K when the grid is short of two workgroups per CU): weights stream straight
+//    into the A operands of the wavefront that owns them, activations are DMA'd into a ring of
+//    LDS stages that all four wavefronts read.
 #include "common.h"
 
 namespace ts {
@@ -51,15 +51,19 @@ __device__ __forceinline__ float load_scale(const void* scale, int scale_is_fp16
 constexpr int kSmWaves = 4;        // wavefronts per workgroup = 4 x 16 output channels
 constexpr int kSmKStep = 64;       // K per step: lane (c, g) covers k + 16g .. k + 16g + 15
 
-// U K steps are loaded before any is multiplied, so each wavefront keeps U x (1 KiB of weights
-// + MT x 2 KiB of activations) in flight instead of waiting one round trip per step.
+// Two register stages of U K steps each: the loads of the next stage (if it starts inside the
+// split) are issued before the current one is multiplied, so each wavefront keeps up to
+// 2U x (1 KiB of weights + MT x 2 KiB of activations) in flight. Every load is at an in-range address (rows past M or N repeat the
+// last row, whose results are not stored; columns past the split end repeat column K - 16 or
+// K - 8) and columns past the split end are zeroed in the widened weights, where they are used:
+// a select on a register whose load is in flight would wait for it.
 template <int MT, bool WIDE>   // MT 16-row m tiles (M <= 16 MT); WIDE: 16-byte weight loads
 __global__ void __launch_bounds__(kSmWaves * 64) w8a16_small_kernel(
     const half_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ wq,
     const void* __restrict__ scale, int scale_is_fp16, const half_t* __restrict__ bias,
     half_t* __restrict__ y, int64_t ldy, int M, int N, int K, int k_per_split,
     float* __restrict__ part) {
-  constexpr int U = MT <= 2 ? 4 : 2;
+  constexpr int U = 4;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int c = lane & 15, g = lane >> 4;
   const int n0 = (blockIdx.x * kSmWaves + w) * 16;
@@ -68,53 +72,66 @@ __global__ void __launch_bounds__(kSmWaves * 64) w8a16_small_kernel(
   const int kb = ks * k_per_split;
   const int ke = (kb + k_per_split < K) ? kb + k_per_split : K;
   const int n = n0 + c;
-  const bool n_ok = n < N;
-  const int8_t* wrow = wq + (int64_t)(n_ok ? n : 0) * K;
+  const int8_t* wrow = wq + (int64_t)(n < N ? n : N - 1) * K;
   const half_t* xrow[MT];
-  bool m_ok[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int mm = mt * 16 + c;
-    m_ok[mt] = mm < M;
-    xrow[mt] = x + (int64_t)(m_ok[mt] ? mm : 0) * ldx;
+    xrow[mt] = x + (int64_t)(mm < M ? mm : M - 1) * ldx;
   }
   float4_t acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = {0.f, 0.f, 0.f, 0.f};
 
-  const half8_t hz = {0, 0, 0, 0, 0, 0, 0, 0};
-  for (int k = kb; k < ke; k += U * kSmKStep) {
+  struct Stage {
     int2_t wa[U], wb[U];
     half8_t xa[U][MT], xb[U][MT];
+  };
+  // lane (c, g), step u of a stage at k: K columns k + 64u + 16g .. +15 in two 8-column pieces
+  // (K % 8 == 0, so a piece is entirely inside or outside [kb, ke)).
+  auto load = [&](int k, Stage& st) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      // lane (c, g): K columns ka .. ka+15 in two 8-element chunks; K % 8 == 0, so a chunk is
-      // entirely inside or outside [kb, ke) (WIDE: K % 16 == 0 and the pair goes together).
       const int ka = k + u * kSmKStep + 16 * g, kb2 = ka + 8;
-      const bool a_ok = ka < ke, b_ok = kb2 < ke;
+      const int xa_col = ka < ke ? ka : K - 8, xb_col = kb2 < ke ? kb2 : K - 8;
       if constexpr (WIDE) {
-        const int4_t v = (n_ok && a_ok) ? ld<int4_t>(wrow + ka) : int4_t{0, 0, 0, 0};
-        wa[u] = {v[0], v[1]};
-        wb[u] = {v[2], v[3]};
+        const int4_t v = ld<int4_t>(wrow + (ka < ke ? ka : K - 16));
+        st.wa[u] = {v[0], v[1]};
+        st.wb[u] = {v[2], v[3]};
       } else {
-        wa[u] = (n_ok && a_ok) ? ld<int2_t>(wrow + ka) : int2_t{0, 0};
-        wb[u] = (n_ok && b_ok) ? ld<int2_t>(wrow + kb2) : int2_t{0, 0};
+        st.wa[u] = ld<int2_t>(wrow + xa_col);
+        st.wb[u] = ld<int2_t>(wrow + xb_col);
       }
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        xa[u][mt] = (m_ok[mt] && a_ok) ? ld<half8_t>(xrow[mt] + ka) : hz;
-        xb[u][mt] = (m_ok[mt] && b_ok) ? ld<half8_t>(xrow[mt] + kb2) : hz;
+        st.xa[u][mt] = ld<half8_t>(xrow[mt] + xa_col);
+        st.xb[u][mt] = ld<half8_t>(xrow[mt] + xb_col);
       }
     }
+  };
+  const half8_t hz = {0, 0, 0, 0, 0, 0, 0, 0};
+  auto compute = [&](int k, const Stage& st) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const half8_t fa = i8x8_to_half8(wa[u]), fb = i8x8_to_half8(wb[u]);
+      const int ka = k + u * kSmKStep + 16 * g;
+      const half8_t fa = ka < ke ? i8x8_to_half8(st.wa[u]) : hz;
+      const half8_t fb = ka + 8 < ke ? i8x8_to_half8(st.wb[u]) : hz;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        acc[mt] = mfma16x16x32(fa, xa[u][mt], acc[mt]);
-        acc[mt] = mfma16x16x32(fb, xb[u][mt], acc[mt]);
+        acc[mt] = mfma16x16x32(fa, st.xa[u][mt], acc[mt]);
+        acc[mt] = mfma16x16x32(fb, st.xb[u][mt], acc[mt]);
       }
     }
+  };
+  constexpr int SK = U * kSmKStep;                 // K per stage
+  Stage s0, s1;
+  load(kb, s0);
+  for (int k = kb; k < ke; k += 2 * SK) {
+    const bool more1 = k + SK < ke, more2 = k + 2 * SK < ke;   // uniform
+    if (more1) load(k + SK, s1);
+    compute(k, s0);
+    if (more2) load(k + 2 * SK, s0);
+    if (more1) compute(k + SK, s1);
   }
   // lane (c, g) holds Y[m = 16 mt + c][n0 + 4g + r]
   const int nn = n0 + 4 * g;
@@ -173,178 +190,295 @@ __global__ void __launch_bounds__(256) w8a16_reduce_kernel(
   }
 }
 
-// ------------------------------------------------------------------------------------------
-// Larger M: LDS-tiled MFMA GEMM.
-// ------------------------------------------------------------------------------------------
-// Workgroup = 4 wavefronts (2 x 2) on a BN (output channels) x BM (activation rows) tile, K step
-// 64. Each thread stages 8-column chunks of both tiles: weight chunks are widened to fp16 once,
-// as they enter LDS (each weight is then read by the two wavefronts that share it without being
-// converted twice), and both tiles are stored as rows of eight 16-byte chunks with chunk kc of
-// row r at position kc ^ (r & 7), an XOR swizzle under which the MFMA operand reads (16 rows x
-// one chunk, eight lanes per LDS cycle) and the staging writes (one row, eight chunks) touch
-// eight distinct bank groups. Global loads run RD - 1 K steps ahead through a register ring, the
-// LDS tiles are double-buffered, and every load is issued by every lane at an in-range address
-// (rows past M or N repeat the last row, whose results are discarded; a K tail past the split
-// end is read at column K - 8 and zeroed) so the loads in flight never depend on a branch. The
-// per-channel scales and the bias are fetched before the loop. (Streaming the weights straight
-// into A-operand registers instead halves the LDS traffic but measured slower: each weight row
-// is then loaded and widened by two wavefronts.) With split-K (gridDim.z > 1) each workgroup
-// covers k_per_split columns of K and writes fp32 partials for w8a16_reduce_kernel.
 constexpr int kTileBK = 64;
 constexpr int kTileChunks = kTileBK / 8;          // 16-byte fp16 chunks per tile row
 
-template <int BN, int BM, int RD>
-__global__ void __launch_bounds__(256) w8a16_tile_kernel(
+// ------------------------------------------------------------------------------------------
+// Larger M, wide tiles: weights straight into registers, activations DMA'd into LDS, 32x32 MFMAs.
+// ------------------------------------------------------------------------------------------
+// Workgroup = 4 wavefronts stacked along N on a (128 WN) x (32 WM) tile of Y^T, K step 64, on
+// v_mfma_f32_32x32x16_f16 (on gfx950 it sustains twice the rate of the 16x16x32 form). Operand
+// layouts, lane l = 32h + r: A holds A[row r][k 8h .. 8h+7], B holds B[k 8h .. 8h+7][col r], and
+// result element e is D[row 8(e / 4) + 4h + e % 4][col r].
+//
+// Each wavefront owns 32 WN weight rows that no other wavefront reads, so it loads them from
+// global memory straight into its A operands: lane (h, r) takes the 32 bytes
+// W[n + r][k + 32h .. + 31] of each 32-row subtile per K step, and the step's MFMA q uses bytes
+// 8q .. 8q+7 (the MFMA reduces over its K slots in any order as long as both operands use the
+// same one). Only the fp16 activation tile goes through LDS, and every wavefront reads all of it:
+// the B operand of MFMA q for lane (h, r) is chunk 4h + q of activation row r. The activations
+// travel by global_load_lds_dwordx4 (each lane's 16 bytes land at the next 16-byte slot of LDS,
+// so they need no registers); a lane picks the chunk its slot must hold under the row swizzle
+// (chunk kc of row r at slot kc ^ (r & 7), conflict-free for the operand reads, which touch
+// rows r .. r+7 at one chunk index each).
+//
+// Loads are issued one step ahead of a ring of PD + 1 LDS stages and weight register stages;
+// each step waits for the batch of the next step (PD - 1 younger batches may stay in flight)
+// and then takes one barrier. The wait and the barrier are written out instead of
+// __syncthreads(), whose release fence would wait for every LDS-bound load in flight; the
+// barrier carries a memory clobber so no load or LDS read moves across it.
+//
+// K tail (only the last split can end inside a K step, and only if K % 64 != 0): weight columns
+// past the split end are zeroed at conversion; activation chunks past it are read at column
+// K - 8 (finite input data whose weights are zero).
+template <int N>
+__device__ __forceinline__ void wait_vmem_below() {
+  // s_waitcnt immediate: vmcnt in bits 3:0 and 15:14; expcnt (bits 6:4) and lgkmcnt (bits 11:8)
+  // left at their maxima. The builtin, unlike inline assembly, tells the compiler's own wait
+  // insertion which loads are complete.
+  static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+// The same with every LDS access of this wavefront complete as well (lgkmcnt 0).
+template <int N>
+__device__ __forceinline__ void wait_vmem_below_lds_done() {
+  static_assert(N >= 0 && N < 64, "vmcnt holds 6 bits");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4));
+}
+__device__ __forceinline__ void workgroup_barrier() { asm volatile("s_barrier" ::: "memory"); }
+
+// Scheduling pattern for one half step: the LDS reads first, the widening of the first weight
+// operand, then MFMAs each followed by an equal share of the remaining VALU work, so that the
+// widening runs in the MFMA shadow instead of in blocks between MFMA runs.
+template <int NMFMA, int NVALU, int NDS>
+__device__ __forceinline__ void interleave_mfma_valu() {
+  constexpr int first = NVALU >= 10 ? 10 : NVALU;
+  constexpr int per = (NVALU - first + NMFMA - 1) / NMFMA;
+  __builtin_amdgcn_sched_group_barrier(0x100, NDS, 0);        // LDS reads
+  if constexpr (first > 0) __builtin_amdgcn_sched_group_barrier(0x002, first, 0);
+#pragma unroll
+  for (int m = 0; m < NMFMA; ++m) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);        // one MFMA
+    if constexpr (per > 0) __builtin_amdgcn_sched_group_barrier(0x002, per, 0);
+  }
+}
+
+typedef float float16_t __attribute__((ext_vector_type(16)));
+
+template <int WN, int WM, int PD, bool WIDE, bool TAIL>
+__global__ void __launch_bounds__(256) w8a16_wide_kernel(
     const half_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ wq,
     const void* __restrict__ scale, int scale_is_fp16, const half_t* __restrict__ bias,
     half_t* __restrict__ y, int64_t ldy, int M, int N, int K, int k_per_split,
     float* __restrict__ part) {
   constexpr int BK = kTileBK, CH = kTileChunks;
-  constexpr int TN = BN / 32, TM = BM / 32;   // 16 x 16 MFMA tiles per wavefront
-  constexpr int WPT = BN * CH / 256, XPT = BM * CH / 256;
-  static_assert(WPT * 256 == BN * CH && XPT * 256 == BM * CH, "tile must split over 256 threads");
-  static_assert(RD % 2 == 0, "register stages pair with the two LDS buffers");
-  __shared__ half8_t s_w[2][BN * CH];
-  __shared__ half8_t s_x[2][BM * CH];
+  constexpr int BN = 128 * WN, BM = 32 * WM;
+  constexpr int XPT = BM * CH / 256;              // activation DMAs per thread per step
+  constexpr int S = PD + 1;                       // LDS stages = weight register stages
+  constexpr int WLD = WIDE ? 2 : 4;               // weight loads per subtile per step
+  constexpr int BATCH = XPT + WN * WLD;           // vector memory loads per thread per step
+  static_assert(XPT * 256 == BM * CH, "activation tile must split over 256 threads");
+  static_assert(BN <= 256, "one scale per thread");
+  static_assert(S >= 2 && S <= 4, "two to four LDS stages");
+  // One array per stage: the compiler's wait insertion then sees that an LDS read of one stage
+  // cannot alias a DMA in flight into another and does not wait for it (stage indices are
+  // constants after unrolling, so stage() folds to one array).
+  __shared__ half8_t s_x0[BM * CH], s_x1[BM * CH], s_x2[S > 2 ? BM * CH : 1], s_x3[S > 3 ? BM * CH : 1];
+  __shared__ float s_sc[BN], s_bs[BN];
+  auto stage = [&](int st) -> half8_t* {
+    return st == 0 ? s_x0 : st == 1 ? s_x1 : st == 2 ? s_x2 : s_x3;
+  };
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int c = lane & 15, g = lane >> 4;
-  const int wn = w >> 1, wm = w & 1;
-  const int n_base = blockIdx.x * BN, m_base = blockIdx.y * BM;
+  const int r = lane & 31, h = lane >> 5;
+  const int n_tile = blockIdx.x * BN;
+  const int n_wave = n_tile + w * 32 * WN;        // this wavefront's first weight row
+  const int m_base = blockIdx.y * BM;
   const int kb = blockIdx.z * k_per_split;
   const int ke = (kb + k_per_split < K) ? kb + k_per_split : K;
   const int nk = (ke - kb + BK - 1) / BK;
-  const bool k_tail = (ke - kb) % BK != 0;          // last step reaches past the split end
 
-  // Chunk u = tid + 256 i of a tile is row u / CH, columns 8 (u % CH) .. + 7 of the K step.
-  const int kc = tid % CH;
-  const int8_t* wrow[WPT];
-  const half_t* xrow[XPT];
-  int wpos[WPT], xpos[XPT];
-#pragma unroll
-  for (int i = 0; i < WPT; ++i) {
-    const int r = (tid + 256 * i) / CH, n = n_base + r;
-    wrow[i] = wq + (int64_t)(n < N ? n : N - 1) * K;
-    wpos[i] = r * CH + (kc ^ (r & 7));
+  // Per-channel scale and bias of the tile, read once into LDS for the epilogue (published by
+  // the barriers of the main loop, which runs at least once).
+  if (tid < BN) {
+    const int nc = n_tile + tid < N ? n_tile + tid : N - 1;
+    s_sc[tid] = part ? 1.f : load_scale(scale, scale_is_fp16, nc);
+    s_bs[tid] = (part || !bias) ? 0.f : (float)bias[nc];
   }
+  const int8_t* wrow[WN];
+#pragma unroll
+  for (int i = 0; i < WN; ++i) {
+    const int n = n_wave + 32 * i + r;
+    wrow[i] = wq + (int64_t)(n < N ? n : N - 1) * K + 32 * h;
+  }
+  // DMA i of thread t fills slot 256 i + t of a stage: row (256 i + t) / 8, position t % 8,
+  // which holds chunk (t % 8) ^ (row & 7) = (t % 8) ^ ((t / 8) & 7) for every i.
+  const int kcx = (tid % CH) ^ ((tid / CH) & 7);
+  const half_t* xrow[XPT];
 #pragma unroll
   for (int i = 0; i < XPT; ++i) {
-    const int r = (tid + 256 * i) / CH, mm = m_base + r;
-    xrow[i] = x + (int64_t)(mm < M ? mm : M - 1) * ldx;
-    xpos[i] = r * CH + (kc ^ (r & 7));
+    const int mm = m_base + (256 * i + tid) / CH;
+    xrow[i] = x + (int64_t)(mm < M ? mm : M - 1) * ldx + 8 * kcx;
   }
-  // Output-channel scale and bias of this lane's four columns per tile, fetched up front.
-  float sc[TN][4], bs[TN][4];
-#pragma unroll
-  for (int i = 0; i < TN; ++i)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int nn = n_base + wn * (BN / 2) + 16 * i + 4 * g + r;
-      const int nc = nn < N ? nn : N - 1;
-      sc[i][r] = part ? 0.f : load_scale(scale, scale_is_fp16, nc);
-      bs[i][r] = (part || !bias) ? 0.f : (float)bias[nc];
-    }
 
-  int2_t wreg[RD][WPT];
-  half8_t xreg[RD][XPT];
-  // Step kt's loads; steps past the split end repeat the last step (a cache hit that is never
-  // used), so every lane issues the same loads in every iteration.
-  auto gload = [&](int kt, int2_t (&wr)[WPT], half8_t (&xr)[XPT]) {
-    const int k = kb + (kt < nk ? kt : nk - 1) * BK + 8 * kc;
-    if (k_tail && kt >= nk - 1) {                   // rare: column K - 8 stands in, then zero
-      const bool ok = k < ke;
-      const int ka = ok ? k : K - 8;
+  // Step kt's loads (steps past the split end repeat the last one), all at in-range addresses.
+  // Weight piece p (8 bytes each) of lane (h, r) is columns 32h + 8p .. + 7 of the step.
+  auto issue = [&](int kt, int st, int4_t (&wr)[WN][2]) {
+    const int k = kb + (kt < nk ? kt : nk - 1) * BK;
+    const int kx = !TAIL || k + 8 * kcx < ke ? k : K - 8 - 8 * kcx;
 #pragma unroll
-      for (int i = 0; i < WPT; ++i) {
-        const int2_t v = ld<int2_t>(wrow[i] + ka);
-        wr[i] = ok ? v : int2_t{0, 0};
-      }
+    for (int i = 0; i < XPT; ++i)
+      __builtin_amdgcn_global_load_lds((const void*)(xrow[i] + kx),
+                                       (__attribute__((address_space(3))) void*)(stage(st) + 256 * i + 64 * w),
+                                       16, 0, 0);
+    if constexpr (WIDE) {
+      const int k0 = !TAIL || k + 32 * h < ke ? k : K - 16 - 32 * h;
+      const int k1 = !TAIL || k + 32 * h + 16 < ke ? k + 16 : K - 16 - 32 * h;
 #pragma unroll
-      for (int i = 0; i < XPT; ++i) {
-        const half8_t v = ld<half8_t>(xrow[i] + ka);
-        xr[i] = ok ? v : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      for (int i = 0; i < WN; ++i) {
+        wr[i][0] = ld<int4_t>(wrow[i] + k0);
+        wr[i][1] = ld<int4_t>(wrow[i] + k1);
       }
     } else {
+      int kp[4];
 #pragma unroll
-      for (int i = 0; i < WPT; ++i) wr[i] = ld<int2_t>(wrow[i] + k);
+      for (int q = 0; q < 4; ++q) kp[q] = !TAIL || k + 32 * h + 8 * q < ke ? k + 8 * q : K - 8 - 32 * h;
 #pragma unroll
-      for (int i = 0; i < XPT; ++i) xr[i] = ld<half8_t>(xrow[i] + k);
-    }
-  };
-  auto lstore = [&](int buf, const int2_t (&wr)[WPT], const half8_t (&xr)[XPT]) {
-#pragma unroll
-    for (int i = 0; i < WPT; ++i) s_w[buf][wpos[i]] = i8x8_to_half8(wr[i]);
-#pragma unroll
-    for (int i = 0; i < XPT; ++i) s_x[buf][xpos[i]] = xr[i];
-  };
-
-  float4_t acc[TN][TM];
-#pragma unroll
-  for (int i = 0; i < TN; ++i)
-#pragma unroll
-    for (int j = 0; j < TM; ++j) acc[i][j] = {0.f, 0.f, 0.f, 0.f};
-
-  // Operand rows are 16 i + c past a multiple of 16, so their swizzle key is c & 7.
-  auto mma_tile = [&](int buf) {
-#pragma unroll
-    for (int ks = 0; ks < BK / 32; ++ks) {
-      const int pc = (4 * ks + g) ^ (c & 7);
-      half8_t a[TN], b[TM];
-#pragma unroll
-      for (int i = 0; i < TN; ++i) a[i] = s_w[buf][(wn * (BN / 2) + 16 * i + c) * CH + pc];
-#pragma unroll
-      for (int j = 0; j < TM; ++j) b[j] = s_x[buf][(wm * (BM / 2) + 16 * j + c) * CH + pc];
-#pragma unroll
-      for (int i = 0; i < TN; ++i)
-#pragma unroll
-        for (int j = 0; j < TM; ++j) acc[i][j] = mfma16x16x32(a[i], b[j], acc[i][j]);
-    }
-  };
-
-  if (nk > 0) {
-#pragma unroll
-    for (int st_ = 0; st_ < RD - 1; ++st_) gload(st_, wreg[st_], xreg[st_]);
-    lstore(0, wreg[0], xreg[0]);
-  }
-  __syncthreads();
-  // Step kt sits in LDS buffer kt % 2 and came through register stage kt % RD (RD is even, so
-  // both indices are compile-time constants within the unrolled group).
-  for (int kt0 = 0; kt0 < nk; kt0 += RD) {
-#pragma unroll
-    for (int u = 0; u < RD; ++u) {
-      const int kt = kt0 + u;
-      gload(kt + RD - 1, wreg[(u + RD - 1) % RD], xreg[(u + RD - 1) % RD]);
-      if (kt < nk) mma_tile(u & 1);
-      lstore((u + 1) & 1, wreg[(u + 1) % RD], xreg[(u + 1) % RD]);
-      __syncthreads();                           // the other buffer was last read before the
-    }                                            // previous barrier
-  }
-  // lane (c, g) of tile (i, j) holds Y[m = .. + 16 j + c][n = .. + 16 i + 4g + r]
-#pragma unroll
-  for (int i = 0; i < TN; ++i) {
-    const int nn = n_base + wn * (BN / 2) + 16 * i + 4 * g;
-#pragma unroll
-    for (int j = 0; j < TM; ++j) {
-      const int mm = m_base + wm * (BM / 2) + 16 * j + c;
-      if (mm >= M) continue;
-      if (part) {
-        float* dst = part + ((int64_t)blockIdx.z * M + mm) * N + nn;
-        if (nn + 3 < N) {
-          st<float4_t>(dst, acc[i][j]);
-        } else {
-          for (int r = 0; r < 4; ++r)
-            if (nn + r < N) dst[r] = acc[i][j][r];
-        }
-        continue;
+      for (int i = 0; i < WN; ++i) {
+        const int2_t p0 = ld<int2_t>(wrow[i] + kp[0]), p1 = ld<int2_t>(wrow[i] + kp[1]);
+        const int2_t p2 = ld<int2_t>(wrow[i] + kp[2]), p3 = ld<int2_t>(wrow[i] + kp[3]);
+        wr[i][0] = {p0[0], p0[1], p1[0], p1[1]};
+        wr[i][1] = {p2[0], p2[1], p3[0], p3[1]};
       }
-      half_t* yp = y + (int64_t)mm * ldy + nn;
-      if (nn + 3 < N) {
-        const half4_t v = {(half_t)(acc[i][j][0] * sc[i][0] + bs[i][0]), (half_t)(acc[i][j][1] * sc[i][1] + bs[i][1]),
-                           (half_t)(acc[i][j][2] * sc[i][2] + bs[i][2]), (half_t)(acc[i][j][3] * sc[i][3] + bs[i][3])};
-        st<half4_t>(yp, v);
-      } else {
-        for (int r = 0; r < 4; ++r)
-          if (nn + r < N) yp[r] = (half_t)(acc[i][j][r] * sc[i][r] + bs[i][r]);
+    }
+  };
+
+  float16_t acc[WN][WM];
+#pragma unroll
+  for (int i = 0; i < WN; ++i)
+#pragma unroll
+    for (int j = 0; j < WM; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.f;
+
+  // B operands of MFMAs q0 and q0 + 1 of a step.
+  auto read_b = [&](int st, int q0, half8_t (&b)[2][WM]) {
+    const half8_t* sx = stage(st);
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int j = 0; j < WM; ++j) b[q][j] = sx[(32 * j + r) * CH + ((4 * h + q0 + q) ^ (r & 7))];
+  };
+  // A operands of MFMAs q0 and q0 + 1 of step kt (K tail columns zeroed).
+  auto convert = [&](const int4_t (&wr)[WN][2], int kt, int q0, half8_t (&a)[2][WN]) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      const int p = q0 + q;
+      const bool ok = !TAIL || kb + kt * BK + 32 * h + 8 * p < ke;
+#pragma unroll
+      for (int i = 0; i < WN; ++i) {
+        const int4_t v = wr[i][p >> 1];
+        const int lo = (p & 1) * 2;
+        a[q][i] = i8x8_to_half8(int2_t{ok ? v[lo] : 0, ok ? v[lo + 1] : 0});
+      }
+    }
+  };
+  auto mma = [&](const half8_t (&a)[2][WN], const half8_t (&b)[2][WM]) {
+#pragma unroll
+    for (int q = 0; q < 2; ++q)
+#pragma unroll
+      for (int i = 0; i < WN; ++i)
+#pragma unroll
+        for (int j = 0; j < WM; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[q][i], b[q][j], acc[i][j], 0, 0, 0);
+  };
+
+  int4_t wreg[S][WN][2];
+  half8_t b0[2][WM], b1[2][WM];
+  // Step t lives in LDS stage and weight registers t % S, constants of the loops unrolled by S.
+  // The prologue issues steps 0 .. S-1 and waits for step 0; each main-loop iteration computes
+  // step kt and then issues step kt + S into the stage and registers it has just released. The
+  // main loop holds only whole groups of S steps and no branch, so the compiler's wait
+  // accounting stays exact across its back edge (the prologue leaves the same loads in flight as
+  // a group does); the last nk % S steps follow it, after waiting for everything.
+  //
+  // Each step is split into two halves (MFMAs q = 0, 1 and q = 2, 3) so that LDS reads overlap
+  // MFMAs instead of following the barrier in lock step on all four wavefronts: the second
+  // half's B operands are read while the first half multiplies, and the next step's first-half
+  // B operands while the second half multiplies. The barrier between the halves publishes step
+  // kt + 1's activations (its batch has landed on every wavefront) and guarantees that every
+  // wavefront has finished its reads of step kt's LDS stage (the wait before it includes this
+  // wavefront's LDS reads; both halves' A operands are widened before it), so step kt + S's
+  // batch is issued right after it into that stage and those registers.
+#pragma unroll
+  for (int u = 0; u < S; ++u) issue(u, u, wreg[u]);
+  wait_vmem_below_lds_done<PD * BATCH>();
+  workgroup_barrier();
+  read_b(0, 0, b0);
+  int kt0 = 0;
+  for (; kt0 + S <= nk; kt0 += S) {
+#pragma unroll
+    for (int u = 0; u < S; ++u) {
+      const int kt = kt0 + u;
+      half8_t a0[2][WN], a1[2][WN];
+      read_b(u, 2, b1);
+      convert(wreg[u], kt, 0, a0);
+      convert(wreg[u], kt, 2, a1);
+      mma(a0, b0);
+      interleave_mfma_valu<2 * WN * WM, 40 * WN, 2 * WM>();
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vmem_below_lds_done<(PD - 1) * BATCH>();   // step kt + 1's batch has landed
+      workgroup_barrier();
+      issue(kt + S, u, wreg[u]);                      // step kt's stage and registers
+      read_b((u + 1) % S, 0, b0);                     // past the last step: never used
+      mma(a1, b1);
+      interleave_mfma_valu<2 * WN * WM, 0, 2 * WM>();
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < S - 1; ++u) {
+    const int kt = kt0 + u;
+    if (kt < nk) {
+      half8_t a[2][WN];
+      read_b(u, 2, b1);
+      convert(wreg[u], kt, 0, a);
+      mma(a, b0);
+      wait_vmem_below_lds_done<0>();
+      workgroup_barrier();
+      read_b((u + 1) % S, 0, b0);
+      convert(wreg[u], kt, 2, a);
+      mma(a, b1);
+    }
+  }
+  // No DMA may still be writing this workgroup's LDS when it exits.
+  wait_vmem_below<0>();
+  // lane (h, r) of subtile (i, j), element e = 4a + c: Y[m][n] with m = m_base + 32 j + r and
+  // n = n_wave + 32 i + 8a + 4h + c; the four c are one 8-byte store.
+#pragma unroll
+  for (int i = 0; i < WN; ++i) {
+#pragma unroll
+    for (int a4 = 0; a4 < 4; ++a4) {
+      const int nl = w * 32 * WN + 32 * i + 8 * a4 + 4 * h;   // column within the tile
+      const int nn = n_tile + nl;
+      if (nn >= N) continue;
+      const float4_t sc = *reinterpret_cast<const float4_t*>(&s_sc[nl]);
+      const float4_t bs = *reinterpret_cast<const float4_t*>(&s_bs[nl]);
+#pragma unroll
+      for (int j = 0; j < WM; ++j) {
+        const int mm = m_base + 32 * j + r;
+        if (mm >= M) continue;
+        const float4_t v = {acc[i][j][4 * a4], acc[i][j][4 * a4 + 1], acc[i][j][4 * a4 + 2],
+                            acc[i][j][4 * a4 + 3]};
+        if (part) {
+          float* dst = part + ((int64_t)blockIdx.z * M + mm) * N + nn;
+          if (nn + 3 < N) {
+            st<float4_t>(dst, v);
+          } else {
+            for (int c = 0; c < 4; ++c)
+              if (nn + c < N) dst[c] = v[c];
+          }
+          continue;
+        }
+        half_t* yp = y + (int64_t)mm * ldy + nn;
+        if (nn + 3 < N) {
+          const half4_t o = {(half_t)(v[0] * sc[0] + bs[0]), (half_t)(v[1] * sc[1] + bs[1]),
+                             (half_t)(v[2] * sc[2] + bs[2]), (half_t)(v[3] * sc[3] + bs[3])};
+          st<half4_t>(yp, o);
+        } else {
+          for (int c = 0; c < 4; ++c)
+            if (nn + c < N) yp[c] = (half_t)(v[c] * sc[c] + bs[c]);
+        }
       }
     }
   }
@@ -353,27 +487,39 @@ __global__ void __launch_bounds__(256) w8a16_tile_kernel(
 // ------------------------------------------------------------------------------------------
 // Host side
 // ------------------------------------------------------------------------------------------
-constexpr int kSmallMMax = 64;
+constexpr int kSmallMMax = 32;
+
+// The weight-streaming kernel re-reads the activations once per wavefront (M x K x 2 bytes per
+// 16 output channels), so its cost grows with M x N; the wide kernel shares them through LDS
+// but pays a fixed ~10 us for the shortest K. Measured on the 1.5B projections, streaming wins
+// for M <= 8 everywhere and up to M = 32 on the narrow, short-K ones (M x N <= 64K, K <= 2048).
+static bool use_small_path(int M, int N, int K) {
+  if (M <= 8) return true;
+  return M <= kSmallMMax && (int64_t)M * N <= 65536 && K <= 2048;
+}
+constexpr int kWidePrefetch = 3;                  // K steps of loads in flight (wide kernel)
 
 struct GemmPlan {
   bool small;
   int mt;          // m tiles (small path)
-  int bn, bm;      // tile shape (tile path)
+  int bn, bm;      // tile shape (wide path): 128 x 128 or 128 x 64
   int splits;      // K splits
   int k_per_split;
 };
 
 static GemmPlan plan_gemm(int M, int N, int K, int cus) {
-  GemmPlan p{M <= kSmallMMax, (M + 15) / 16, 0, 0, 1, K};
+  GemmPlan p{use_small_path(M, N, K), (M + 15) / 16, 0, 0, 1, K};
   if (p.small) {
     // Fill the device with wavefronts (about eight per CU) by splitting K, keeping at least
-    // 256 K per split and the partial traffic (splits * M * N * 4 bytes) below 1/8 of the
-    // weight bytes.
+    // 256 K per split and the fp32 partials (splits * M * N * 4 bytes) within a quarter of the
+    // weight bytes or 2 MB.
     const int64_t wgs = (N + 16 * kSmWaves - 1) / (16 * kSmWaves);
     const int64_t target_wgs = 2LL * cus;
     int splits = (int)((target_wgs + wgs - 1) / wgs);
     const int max_by_k = K / 256 > 1 ? K / 256 : 1;
-    const int max_by_traffic = (int)((int64_t)K / (32LL * M) > 1 ? (int64_t)K / (32LL * M) : 1);
+    const int64_t budget = (int64_t)N * K / 4 > (2LL << 20) ? (int64_t)N * K / 4 : (2LL << 20);
+    const int64_t by_traffic64 = budget / ((int64_t)M * N * 4);
+    const int max_by_traffic = by_traffic64 > 1 ? (int)by_traffic64 : 1;
     if (splits > max_by_k) splits = max_by_k;
     if (splits > max_by_traffic) splits = max_by_traffic;
     if (splits < 1) splits = 1;
@@ -383,41 +529,35 @@ static GemmPlan plan_gemm(int M, int N, int K, int cus) {
     p.k_per_split = kps;
     return p;
   }
+  const int nk = (K + kTileBK - 1) / kTileBK;
+  int splits = 1;
 #ifdef TS_W8A16_FORCE_BN                          // tuning override (bn, bm, splits)
-  if (!p.small) {
-    p.bn = TS_W8A16_FORCE_BN;
-    p.bm = TS_W8A16_FORCE_BM;
-    const int nk = (K + kTileBK - 1) / kTileBK;
-    const int steps = (nk + TS_W8A16_FORCE_SPLITS - 1) / TS_W8A16_FORCE_SPLITS;
-    p.k_per_split = steps * kTileBK;
-    p.splits = (K + p.k_per_split - 1) / p.k_per_split;
-    return p;
+  p.bn = TS_W8A16_FORCE_BN;
+  p.bm = TS_W8A16_FORCE_BM;
+  splits = TS_W8A16_FORCE_SPLITS;
+#else
+  // 128 x 128 tiles (two workgroups per CU; the most work per CU of the shapes measured) once
+  // they cover half the CUs. Otherwise 128 x 64 tiles, split over K while the grid holds fewer
+  // than two workgroups per CU, each split keeps at least 32 K steps (below that the reduction
+  // costs more than the split saves) and the fp32 partials (written and read once more by the
+  // reduction) stay within half the weight bytes or 8 MB.
+  p.bn = 128;
+  const int64_t n_tiles = (N + 127) / 128;
+  if (n_tiles * ((M + 127) / 128) * 2 >= cus) {
+    p.bm = 128;
+  } else {
+    p.bm = 64;
+    const int64_t tiles = n_tiles * ((M + 63) / 64);
+    const int64_t part_budget = (int64_t)N * K / 2 > (8LL << 20) ? (int64_t)N * K / 2 : (8LL << 20);
+    while (tiles * splits < 2LL * cus && nk / (splits + 1) >= 32 &&
+           (int64_t)(splits + 1) * M * N * 4 <= part_budget)
+      ++splits;
   }
 #endif
-  // Largest tile whose grid covers every CU; the smallest tile otherwise.
-  static const int tiles[3][2] = {{128, 128}, {128, 64}, {64, 64}};
-  int64_t grid = 0;
-  for (int t = 0; t < 3; ++t) {
-    p.bn = tiles[t][0];
-    p.bm = tiles[t][1];
-    grid = (int64_t)((N + p.bn - 1) / p.bn) * ((M + p.bm - 1) / p.bm);
-    if (grid >= cus) break;
-  }
-  // Still short of the CU count: split K, keeping >= 4 K steps per split and the fp32 partial
-  // traffic (splits * M * N * 4 bytes) within half the weight bytes.
-  if (grid < cus) {
-    const int nk = (K + kTileBK - 1) / kTileBK;
-    int splits = (int)((cus + grid - 1) / grid);
-    const int by_k = nk / 4 > 1 ? nk / 4 : 1;
-    const int64_t by_traffic64 = ((int64_t)N * K / 2) / ((int64_t)M * N * 4);
-    const int by_traffic = by_traffic64 > 1 ? (int)by_traffic64 : 1;
-    if (splits > by_k) splits = by_k;
-    if (splits > by_traffic) splits = by_traffic;
-    if (splits > 1) {
-      const int steps = (nk + splits - 1) / splits;
-      p.k_per_split = steps * kTileBK;
-      p.splits = (K + p.k_per_split - 1) / p.k_per_split;
-    }
+  if (splits > 1) {
+    const int steps = (nk + splits - 1) / splits;
+    p.k_per_split = steps * kTileBK;
+    p.splits = (K + p.k_per_split - 1) / p.k_per_split;
   }
   return p;
 }
@@ -477,8 +617,6 @@ extern "C" int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const
     switch (p.mt) {
       TS_SM_CASE(1)
       TS_SM_CASE(2)
-      TS_SM_CASE(3)
-      TS_SM_CASE(4)
     }
 #undef TS_SM_CASE
     if (p.splits > 1) {
@@ -490,16 +628,20 @@ extern "C" int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const
   } else {
     float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const dim3 grid((N + p.bn - 1) / p.bn, (M + p.bm - 1) / p.bm, p.splits);
-#define TS_TILE_LAUNCH(BNV, BMV)                                                                  \
-  w8a16_tile_kernel<BNV, BMV, 4><<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, yp,  \
-                                                      ldy, M, N, K, p.k_per_split, part)
-    if (p.bn == 128 && p.bm == 128)
-      TS_TILE_LAUNCH(128, 128);
-    else if (p.bn == 128)
-      TS_TILE_LAUNCH(128, 64);
-    else
-      TS_TILE_LAUNCH(64, 64);
-#undef TS_TILE_LAUNCH
+    const bool fast = K % kTileBK == 0 && aligned(wq, 16);   // 16-byte weight loads, no K tail
+#define TS_WIDE_LAUNCH(WNV, WMV)                                                                   \
+  if (fast)                                                                                        \
+    w8a16_wide_kernel<WNV, WMV, kWidePrefetch, true, false><<<grid, 256, 0, s>>>(                   \
+        xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part);             \
+  else                                                                                             \
+    w8a16_wide_kernel<WNV, WMV, kWidePrefetch, false, true><<<grid, 256, 0, s>>>(                   \
+        xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part)
+    if (p.bm == 128) {
+      TS_WIDE_LAUNCH(1, 4);
+    } else {
+      TS_WIDE_LAUNCH(1, 2);
+    }
+#undef TS_WIDE_LAUNCH
     if (p.splits > 1) {
       const int64_t total = (int64_t)M * N;
       const int64_t want = (total + 255) / 256;
