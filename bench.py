@@ -44,7 +44,7 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "w8a16", "mixed"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "w8a16", "logits", "mixed"], default=None,
                     help="run one workload alone (for profiling); prints its result as JSON")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="copy a 256 MiB buffer 8 times (the known-size kernel that scales the "
@@ -277,6 +277,32 @@ def bench_w8a16(torch, K, synth):
     return rows
 
 
+def bench_logits(torch, K):
+    """Logits of one config 5 step: the 49 sampling rows (48 decodes + the chunk's last token) of
+    560 hidden rows through the tied Qwen2.5-1.5B lm head (151936 x 1536). The fused int8 path
+    (one gather + W8A16 + fp32 launch) beside the unfused composition the reference runs (torch
+    gather, W8A16, .float()) and the fp16 head on the vendor BLAS; weight bytes per call over the
+    time, against 8 TB/s."""
+    dev = torch.device("cuda", 0)
+    V, H, T, S = 151936, 1536, 560, 49
+    g = torch.Generator(device=dev).manual_seed(0)
+    embed = (torch.randn(V, H, generator=g, device=dev) * 0.02).half()
+    amax = embed.float().abs().amax(dim=1).clamp_min(1e-8)
+    sc = (amax / 127.0).contiguous()
+    wq = torch.round(embed.float() / sc[:, None]).clamp(-127, 127).to(torch.int8).contiguous()
+    hidden = torch.randn(T, H, generator=g, device=dev).half()
+    idx = torch.sort(torch.randperm(T, generator=g, device=dev)[:S]).values
+    out = {}
+    for name, fn, wbytes in (
+            ("int8_fused", lambda: K.logits_int8(hidden, idx, wq, sc), V * H),
+            ("int8_unfused", lambda: K.lm_head_int8(hidden[idx], wq, sc).float(), V * H),
+            ("fp16_blas", lambda: (hidden[idx] @ embed.T).float(), 2 * V * H)):
+        ms = time_graph(torch, fn, reps=10, inner=5)
+        out[name] = {"us": round(ms * 1e3, 2), "weight_GBps": round(wbytes / ms / 1e6, 1),
+                     "hbm_frac": round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
+    return {"rows": S, "vocab": V, "hidden": H, **out}
+
+
 def bench_mixed(torch, synth, reps: int = 5):
     """Config 5: one mixed forward step of a random-init Qwen2 at the Qwen2.5-1.5B dimensions
     (28 layers, W8A16 linears, tied fp16 lm head) over 48 decodes with contexts log-uniform in
@@ -368,9 +394,10 @@ def main() -> int:
                           "copy_bytes_written_per_launch": a.numel(), "launches": 8}))
         return 0
     _native.lib()
-    if args.only in ("prefill", "w8a16", "mixed"):
+    if args.only in ("prefill", "w8a16", "logits", "mixed"):
         fn = {"prefill": lambda: bench_prefill(torch, K, synth),
               "w8a16": lambda: bench_w8a16(torch, K, synth),
+              "logits": lambda: bench_logits(torch, K),
               "mixed": lambda: bench_mixed(torch, synth)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return 0
@@ -417,6 +444,8 @@ def main() -> int:
         extra = {"prefill_config3": bench_prefill(torch, K, synth)}
         log("extra: config 4 W8A16")
         extra["w8a16_config4"] = bench_w8a16(torch, K, synth)
+        log("extra: config 5 logits")
+        extra["logits_config5"] = bench_logits(torch, K)
         log("extra: config 5 mixed step")
         extra["mixed_config5"] = bench_mixed(torch, synth)
         out["extra"] = extra

@@ -10,6 +10,8 @@
  *   ts_prefill_attention   <- ops/triton_prefill_attention.py:66-79
  *   ts_paged_attention     <- ops/triton_ops.py:60-71        (twin ops/reference.py:94-111)
  *   ts_w8a16_gemm          <- ops/triton_w8a16.py:38-51 and ops/triton_ops.py:74-91
+ *   ts_logits_int8         <- model/qwen2.py:94-99 with ops/triton_ops.py:88-91 (gather, int8
+ *                             lm head and .float() fused)
  *   ts_rmsnorm             <- ops/triton_rmsnorm.py:30-46   (twins ops/reference.py:13-23)
  *   ts_rope                <- ops/triton_rope.py:27-31      (twin ops/reference.py:31-42)
  *   ts_silu_mul            <- ops/triton_silu_mul.py:21-28  (twin ops/reference.py:26-28)
@@ -150,6 +152,27 @@ int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const void* scal
                   int32_t scale_is_fp16, const void* bias, void* y, int64_t ldy,
                   int32_t M, int32_t N, int32_t K,
                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * Logits of the sampling rows through the int8 tied lm head, in one launch (plus the split-K
+ * reduction when num_samples is small): for s < num_samples,
+ *   logits[s][v] = (float) fp16( sum_k hidden[sample_indices[s]][k] * wq[v][k] * scale[v] )
+ * which is what the reference computes as hidden[sample_indices] (a gather), lm_head_int8
+ * (the W8A16 product, fp16 result) and .float(): model/qwen2.py:94-99 with
+ * ops/triton_ops.py:88-91. hidden fp16 [hidden_rows, hidden_size] (row stride hidden_stride,
+ * 16-byte aligned rows); sample_indices int64 on the device (clamped to [0, hidden_rows));
+ * wq int8 [vocab, hidden_size] and scale as for ts_w8a16_gemm; logits fp32
+ * [num_samples, vocab] with a row stride that is a multiple of 4. The values equal those of
+ * ts_w8a16_gemm on the gathered rows, widened to fp32.
+ * Workspace: ts_logits_int8_workspace_bytes() bytes.
+ */
+size_t ts_logits_int8_workspace_bytes(int32_t num_samples, int32_t vocab, int32_t hidden_size,
+                                      int32_t cu_count);
+int ts_logits_int8(const void* hidden, int64_t hidden_stride, int64_t hidden_rows,
+                   const int64_t* sample_indices, int32_t num_samples, const int8_t* wq,
+                   const void* scale, int32_t scale_is_fp16, float* logits, int64_t logits_stride,
+                   int32_t vocab, int32_t hidden_size, void* workspace, size_t workspace_bytes,
+                   void* stream);
 
 /*
  * RMSNorm with optional fused residual add, one token row of `hidden` features at a time:

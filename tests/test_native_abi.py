@@ -67,6 +67,24 @@ def test_small_op_argument_checks():
     assert lib.ts_silu_mul(None, 0, None, 0, 0, 64, None) == N.TS_OK
 
 
+def test_logits_argument_checks():
+    lib = N.lib()
+    p = ctypes.c_void_p(256)            # never dereferenced: the call fails validation first
+    # hidden_size not a multiple of 8; null pointers; misaligned logits rows; no samples: no-op
+    assert lib.ts_logits_int8(p, 1540, 4, p, 2, p, p, 0, p, 1000, 1000, 1540, None, 0, None) == \
+        N.TS_ERR_UNSUPPORTED and "multiple of 8" in N.last_error()
+    assert lib.ts_logits_int8(None, 1536, 4, None, 2, None, None, 0, None, 1000, 1000, 1536, None,
+                              0, None) == N.TS_ERR_INVALID_ARG
+    assert lib.ts_logits_int8(p, 1536, 4, p, 2, p, p, 0, p, 1002, 1001, 1536, None, 0, None) == \
+        N.TS_ERR_INVALID_ARG and "logits rows" in N.last_error()
+    assert lib.ts_logits_int8(None, 0, 0, None, 0, None, None, 0, None, 0, 1000, 1536, None, 0,
+                              None) == N.TS_OK
+    # the gathered product is planned exactly like the GEMM on those rows
+    for S in (1, 49, 300):
+        assert lib.ts_logits_int8_workspace_bytes(S, 151936, 1536, 256) == \
+            lib.ts_w8a16_workspace_bytes(S, 151936, 1536, 256)
+
+
 def test_zero_size_calls_are_no_ops():
     lib = N.lib()
     assert lib.ts_kv_write(None, None, 0, 0, 0, 0, None, None, 0, None, 0, 2, 64, None) == N.TS_OK
@@ -102,7 +120,7 @@ def test_workspace_sizes():
     assert lib.ts_decode_workspace_bytes(0, 256, 12, 2, 128, 4096, 0, 256) == 0
     # W8A16: 128 x 128 tiles that cover the device need no workspace
     assert lib.ts_w8a16_workspace_bytes(2048, 17920, 1536, 256) == 0
-    assert lib.ts_w8a16_workspace_bytes(64, 17920, 1536, 256) == 0      # 140 tiles, 2 per CU
+    assert lib.ts_w8a16_workspace_bytes(64, 17920, 1536, 256) == 0      # 140 tiles of 128 x 64
     # 108 tiles of 128 x 64 for the 1.5B down projection at M = 560: split K in two (70 K
     # steps each, partials 2 x 560 x 1536 fp32 within the 8 MB floor); a third split would not
     # fit and K = 1536 (24 steps) never splits

@@ -45,6 +45,46 @@ __device__ __forceinline__ float load_scale(const void* scale, int scale_is_fp16
                        : static_cast<const float*>(scale)[n];
 }
 
+// Optional extras of the logits entry point: activation row r of the product is
+// x[rows[r]] (clamped to [0, x_rows)) instead of x[r], and the result goes to the fp32 matrix yf
+// as the fp16-rounded value widened (what the reference's fp16 product followed by .float()
+// holds) instead of to the fp16 matrix y.
+struct GemmIo {
+  const int64_t* rows;
+  int64_t x_rows;
+  float* yf;
+  int64_t ldyf;
+};
+
+__device__ __forceinline__ int64_t x_row(const GemmIo& io, int r) {
+  if (!io.rows) return r;
+  const int64_t v = io.rows[r];
+  return v < 0 ? 0 : (v >= io.x_rows ? io.x_rows - 1 : v);
+}
+
+// Output columns nn .. nn + 3 of row mm (those below N) from their fp32 values.
+__device__ __forceinline__ void store_out4(const GemmIo& io, half_t* y, int64_t ldy, int mm, int nn,
+                                           int N, const float (&v)[4]) {
+  const half4_t hv = {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+  if (io.yf) {
+    float* dst = io.yf + (int64_t)mm * io.ldyf + nn;
+    if (nn + 3 < N) {
+      st<float4_t>(dst, float4_t{(float)hv[0], (float)hv[1], (float)hv[2], (float)hv[3]});
+    } else {
+      for (int r = 0; r < 4; ++r)
+        if (nn + r < N) dst[r] = (float)hv[r];
+    }
+  } else {
+    half_t* dst = y + (int64_t)mm * ldy + nn;
+    if (nn + 3 < N) {
+      st<half4_t>(dst, hv);
+    } else {
+      for (int r = 0; r < 4; ++r)
+        if (nn + r < N) dst[r] = hv[r];
+    }
+  }
+}
+
 // ------------------------------------------------------------------------------------------
 // Small M: split-K weight streaming.
 // ------------------------------------------------------------------------------------------
@@ -62,7 +102,7 @@ __global__ void __launch_bounds__(kSmWaves * 64) w8a16_small_kernel(
     const half_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ wq,
     const void* __restrict__ scale, int scale_is_fp16, const half_t* __restrict__ bias,
     half_t* __restrict__ y, int64_t ldy, int M, int N, int K, int k_per_split,
-    float* __restrict__ part) {
+    float* __restrict__ part, GemmIo io) {
   constexpr int U = 4;
   const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63;
   const int c = lane & 15, g = lane >> 4;
@@ -77,7 +117,7 @@ __global__ void __launch_bounds__(kSmWaves * 64) w8a16_small_kernel(
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
     const int mm = mt * 16 + c;
-    xrow[mt] = x + (int64_t)(mm < M ? mm : M - 1) * ldx;
+    xrow[mt] = x + x_row(io, mm < M ? mm : M - 1) * ldx;
   }
   float4_t acc[MT];
 #pragma unroll
@@ -147,15 +187,9 @@ __global__ void __launch_bounds__(kSmWaves * 64) w8a16_small_kernel(
     for (int mt = 0; mt < MT; ++mt) {
       const int mm = mt * 16 + c;
       if (mm >= M) continue;
-      half_t* yp = y + (int64_t)mm * ldy + nn;
-      if (nn + 3 < N) {
-        const half4_t v = {(half_t)(acc[mt][0] * sc[0] + bs[0]), (half_t)(acc[mt][1] * sc[1] + bs[1]),
-                           (half_t)(acc[mt][2] * sc[2] + bs[2]), (half_t)(acc[mt][3] * sc[3] + bs[3])};
-        st<half4_t>(yp, v);
-      } else {
-        for (int r = 0; r < 4; ++r)
-          if (nn + r < N) yp[r] = (half_t)(acc[mt][r] * sc[r] + bs[r]);
-      }
+      const float v[4] = {acc[mt][0] * sc[0] + bs[0], acc[mt][1] * sc[1] + bs[1],
+                          acc[mt][2] * sc[2] + bs[2], acc[mt][3] * sc[3] + bs[3]};
+      store_out4(io, y, ldy, mm, nn, N, v);
     }
   } else {
     float* pp = part + (int64_t)ks * M * N;
@@ -177,7 +211,8 @@ __global__ void __launch_bounds__(kSmWaves * 64) w8a16_small_kernel(
 // Sum of the split-K partials, then scale, bias and fp16 conversion.
 __global__ void __launch_bounds__(256) w8a16_reduce_kernel(
     const float* __restrict__ part, int splits, const void* __restrict__ scale, int scale_is_fp16,
-    const half_t* __restrict__ bias, half_t* __restrict__ y, int64_t ldy, int M, int N) {
+    const half_t* __restrict__ bias, half_t* __restrict__ y, int64_t ldy, int M, int N,
+    GemmIo io) {
   const int64_t total = (int64_t)M * N;
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
@@ -186,7 +221,11 @@ __global__ void __launch_bounds__(256) w8a16_reduce_kernel(
     for (int k = 0; k < splits; ++k) s += part[(int64_t)k * total + i];
     float v = s * load_scale(scale, scale_is_fp16, nn);
     if (bias) v += (float)bias[nn];
-    y[(int64_t)mm * ldy + nn] = (half_t)v;
+    const half_t hv = (half_t)v;
+    if (io.yf)
+      io.yf[(int64_t)mm * io.ldyf + nn] = (float)hv;
+    else
+      y[(int64_t)mm * ldy + nn] = hv;
   }
 }
 
@@ -260,7 +299,7 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
     const half_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ wq,
     const void* __restrict__ scale, int scale_is_fp16, const half_t* __restrict__ bias,
     half_t* __restrict__ y, int64_t ldy, int M, int N, int K, int k_per_split,
-    float* __restrict__ part) {
+    float* __restrict__ part, GemmIo io) {
   constexpr int BK = kTileBK, CH = kTileChunks;
   constexpr int BN = 128 * WN, BM = 32 * WM;
   constexpr int XPT = BM * CH / 256;              // activation DMAs per thread per step
@@ -308,7 +347,7 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
 #pragma unroll
   for (int i = 0; i < XPT; ++i) {
     const int mm = m_base + (256 * i + tid) / CH;
-    xrow[i] = x + (int64_t)(mm < M ? mm : M - 1) * ldx + 8 * kcx;
+    xrow[i] = x + x_row(io, mm < M ? mm : M - 1) * ldx + 8 * kcx;
   }
 
   // Step kt's loads (steps past the split end repeat the last one), all at in-range addresses.
@@ -470,15 +509,9 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
           }
           continue;
         }
-        half_t* yp = y + (int64_t)mm * ldy + nn;
-        if (nn + 3 < N) {
-          const half4_t o = {(half_t)(v[0] * sc[0] + bs[0]), (half_t)(v[1] * sc[1] + bs[1]),
-                             (half_t)(v[2] * sc[2] + bs[2]), (half_t)(v[3] * sc[3] + bs[3])};
-          st<half4_t>(yp, o);
-        } else {
-          for (int c = 0; c < 4; ++c)
-            if (nn + c < N) yp[c] = (half_t)(v[c] * sc[c] + bs[c]);
-        }
+        const float o[4] = {v[0] * sc[0] + bs[0], v[1] * sc[1] + bs[1], v[2] * sc[2] + bs[2],
+                            v[3] * sc[3] + bs[3]};
+        store_out4(io, y, ldy, mm, nn, N, o);
       }
     }
   }
@@ -537,13 +570,14 @@ static GemmPlan plan_gemm(int M, int N, int K, int cus) {
   splits = TS_W8A16_FORCE_SPLITS;
 #else
   // 128 x 128 tiles (two workgroups per CU; the most work per CU of the shapes measured) once
-  // they cover half the CUs. Otherwise 128 x 64 tiles, split over K while the grid holds fewer
+  // they cover half the CUs and M is past 64 (below that most of their rows would be padding).
+  // Otherwise 128 x 64 tiles, split over K while the grid holds fewer
   // than two workgroups per CU, each split keeps at least 32 K steps (below that the reduction
   // costs more than the split saves) and the fp32 partials (written and read once more by the
   // reduction) stay within half the weight bytes or 8 MB.
   p.bn = 128;
   const int64_t n_tiles = (N + 127) / 128;
-  if (n_tiles * ((M + 127) / 128) * 2 >= cus) {
+  if (M > 64 && n_tiles * ((M + 127) / 128) * 2 >= cus) {
     p.bm = 128;
   } else {
     p.bm = 64;
@@ -575,6 +609,70 @@ extern "C" size_t ts_w8a16_workspace_bytes(int32_t M, int32_t N, int32_t K, int3
   return gemm_workspace(plan_gemm(M, N, K, cu_count > 0 ? cu_count : 256), M, N);
 }
 
+// Validated launch shared by the GEMM and logits entry points.
+static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const void* scale,
+                        int32_t scale_is_fp16, const half_t* bp, half_t* yp, int64_t ldy,
+                        int32_t M, int32_t N, int32_t K, void* workspace, size_t workspace_bytes,
+                        hipStream_t s, const GemmIo& io) {
+  int cus = 0;
+  int st = device_cu_count(&cus);
+  if (st != TS_OK) return st;
+  const GemmPlan p = plan_gemm(M, N, K, cus);
+  const size_t need = gemm_workspace(p, M, N);
+  TS_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
+             TS_ERR_WORKSPACE, "w8a16: workspace of %zu bytes needed, got %zu", need,
+             workspace_bytes);
+  if (p.small) {
+    float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    const dim3 grid((N + 16 * kSmWaves - 1) / (16 * kSmWaves), p.splits);
+    const bool wide = K % 16 == 0 && aligned(wq, 16);
+#define TS_SM_CASE(MTV)                                                                          \
+  case MTV:                                                                                      \
+    if (wide)                                                                                    \
+      w8a16_small_kernel<MTV, true><<<grid, kSmWaves * 64, 0, s>>>(                             \
+          xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part, io);    \
+    else                                                                                         \
+      w8a16_small_kernel<MTV, false><<<grid, kSmWaves * 64, 0, s>>>(                            \
+          xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part, io);    \
+    break;
+    switch (p.mt) {
+      TS_SM_CASE(1)
+      TS_SM_CASE(2)
+    }
+#undef TS_SM_CASE
+    if (p.splits > 1) {
+      const int64_t total = (int64_t)M * N;
+      const int64_t want = (total + 255) / 256;
+      w8a16_reduce_kernel<<<(int)(want < 4096 ? want : 4096), 256, 0, s>>>(
+          part, p.splits, scale, scale_is_fp16, bp, yp, ldy, M, N, io);
+    }
+  } else {
+    float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
+    const dim3 grid((N + p.bn - 1) / p.bn, (M + p.bm - 1) / p.bm, p.splits);
+    const bool fast = K % kTileBK == 0 && aligned(wq, 16);   // 16-byte weight loads, no K tail
+#define TS_WIDE_LAUNCH(WNV, WMV)                                                                   \
+  if (fast)                                                                                        \
+    w8a16_wide_kernel<WNV, WMV, kWidePrefetch, true, false><<<grid, 256, 0, s>>>(                   \
+        xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part, io);         \
+  else                                                                                             \
+    w8a16_wide_kernel<WNV, WMV, kWidePrefetch, false, true><<<grid, 256, 0, s>>>(                   \
+        xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part, io)
+    if (p.bm == 128) {
+      TS_WIDE_LAUNCH(1, 4);
+    } else {
+      TS_WIDE_LAUNCH(1, 2);
+    }
+#undef TS_WIDE_LAUNCH
+    if (p.splits > 1) {
+      const int64_t total = (int64_t)M * N;
+      const int64_t want = (total + 255) / 256;
+      w8a16_reduce_kernel<<<(int)(want < 4096 ? want : 4096), 256, 0, s>>>(
+          part, p.splits, scale, scale_is_fp16, bp, yp, ldy, M, N, io);
+    }
+  }
+  return TS_OK;
+}
+
 extern "C" int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const void* scale,
                              int32_t scale_is_fp16, const void* bias, void* y, int64_t ldy,
                              int32_t M, int32_t N, int32_t K, void* workspace,
@@ -589,65 +687,41 @@ extern "C" int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const
              TS_ERR_INVALID_ARG, "w8a16: x must be 16-byte aligned rows (ldx %% 8 == 0), wq 8-byte aligned");
   TS_REQUIRE(!(ldy % 4) && aligned(y, 8), TS_ERR_INVALID_ARG,
              "w8a16: y rows must be 8-byte aligned (ldy %% 4 == 0)");
-  int cus = 0;
-  int st = device_cu_count(&cus);
+  const GemmIo io{nullptr, 0, nullptr, 0};
+  const int st = w8a16_launch(static_cast<const half_t*>(x), ldx, wq, scale, scale_is_fp16,
+                              static_cast<const half_t*>(bias), static_cast<half_t*>(y), ldy, M,
+                              N, K, workspace, workspace_bytes,
+                              reinterpret_cast<hipStream_t>(stream), io);
   if (st != TS_OK) return st;
-  const GemmPlan p = plan_gemm(M, N, K, cus);
-  const size_t need = gemm_workspace(p, M, N);
-  TS_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
-             TS_ERR_WORKSPACE, "w8a16: workspace of %zu bytes needed, got %zu", need,
-             workspace_bytes);
-  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  const half_t* xp = static_cast<const half_t*>(x);
-  const half_t* bp = static_cast<const half_t*>(bias);
-  half_t* yp = static_cast<half_t*>(y);
-  if (p.small) {
-    float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
-    const dim3 grid((N + 16 * kSmWaves - 1) / (16 * kSmWaves), p.splits);
-    const bool wide = K % 16 == 0 && aligned(wq, 16);
-#define TS_SM_CASE(MTV)                                                                          \
-  case MTV:                                                                                      \
-    if (wide)                                                                                    \
-      w8a16_small_kernel<MTV, true><<<grid, kSmWaves * 64, 0, s>>>(                             \
-          xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part);        \
-    else                                                                                         \
-      w8a16_small_kernel<MTV, false><<<grid, kSmWaves * 64, 0, s>>>(                            \
-          xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part);        \
-    break;
-    switch (p.mt) {
-      TS_SM_CASE(1)
-      TS_SM_CASE(2)
-    }
-#undef TS_SM_CASE
-    if (p.splits > 1) {
-      const int64_t total = (int64_t)M * N;
-      const int64_t want = (total + 255) / 256;
-      w8a16_reduce_kernel<<<(int)(want < 4096 ? want : 4096), 256, 0, s>>>(
-          part, p.splits, scale, scale_is_fp16, bp, yp, ldy, M, N);
-    }
-  } else {
-    float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
-    const dim3 grid((N + p.bn - 1) / p.bn, (M + p.bm - 1) / p.bm, p.splits);
-    const bool fast = K % kTileBK == 0 && aligned(wq, 16);   // 16-byte weight loads, no K tail
-#define TS_WIDE_LAUNCH(WNV, WMV)                                                                   \
-  if (fast)                                                                                        \
-    w8a16_wide_kernel<WNV, WMV, kWidePrefetch, true, false><<<grid, 256, 0, s>>>(                   \
-        xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part);             \
-  else                                                                                             \
-    w8a16_wide_kernel<WNV, WMV, kWidePrefetch, false, true><<<grid, 256, 0, s>>>(                   \
-        xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part)
-    if (p.bm == 128) {
-      TS_WIDE_LAUNCH(1, 4);
-    } else {
-      TS_WIDE_LAUNCH(1, 2);
-    }
-#undef TS_WIDE_LAUNCH
-    if (p.splits > 1) {
-      const int64_t total = (int64_t)M * N;
-      const int64_t want = (total + 255) / 256;
-      w8a16_reduce_kernel<<<(int)(want < 4096 ? want : 4096), 256, 0, s>>>(
-          part, p.splits, scale, scale_is_fp16, bp, yp, ldy, M, N);
-    }
-  }
   return check_launch("w8a16_gemm");
+}
+
+extern "C" size_t ts_logits_int8_workspace_bytes(int32_t num_samples, int32_t vocab,
+                                                  int32_t hidden_size, int32_t cu_count) {
+  return ts_w8a16_workspace_bytes(num_samples, vocab, hidden_size, cu_count);
+}
+
+extern "C" int ts_logits_int8(const void* hidden, int64_t hidden_stride, int64_t hidden_rows,
+                              const int64_t* sample_indices, int32_t num_samples, const int8_t* wq,
+                              const void* scale, int32_t scale_is_fp16, float* logits,
+                              int64_t logits_stride, int32_t vocab, int32_t hidden_size,
+                              void* workspace, size_t workspace_bytes, void* stream) {
+  TS_REQUIRE(num_samples >= 0 && vocab > 0 && hidden_size > 0, TS_ERR_INVALID_ARG,
+             "logits_int8: bad shape S=%d V=%d H=%d", num_samples, vocab, hidden_size);
+  if (num_samples == 0) return TS_OK;
+  TS_REQUIRE(hidden && sample_indices && wq && scale && logits && hidden_rows > 0,
+             TS_ERR_INVALID_ARG, "logits_int8: null pointer argument or no hidden rows");
+  TS_REQUIRE(hidden_size % 8 == 0, TS_ERR_UNSUPPORTED,
+             "logits_int8: hidden_size=%d is not a multiple of 8", hidden_size);
+  TS_REQUIRE(hidden_stride >= hidden_size && hidden_stride % 8 == 0 && aligned(hidden, 16) &&
+                 aligned(wq, 8) && aligned(sample_indices, 8),
+             TS_ERR_INVALID_ARG, "logits_int8: hidden must be 16-byte aligned rows, wq 8-byte aligned");
+  TS_REQUIRE(logits_stride >= vocab && logits_stride % 4 == 0 && aligned(logits, 16),
+             TS_ERR_INVALID_ARG, "logits_int8: logits rows must be 16-byte aligned (stride %% 4 == 0)");
+  const GemmIo io{sample_indices, hidden_rows, logits, logits_stride};
+  const int st = w8a16_launch(static_cast<const half_t*>(hidden), hidden_stride, wq, scale,
+                              scale_is_fp16, nullptr, nullptr, 0, num_samples, vocab, hidden_size,
+                              workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream), io);
+  if (st != TS_OK) return st;
+  return check_launch("logits_int8");
 }

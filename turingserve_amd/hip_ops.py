@@ -20,7 +20,7 @@ import torch.nn.functional as F
 from turingserve_amd import _native as N
 from turingserve_amd.quant import LinearWeight
 
-__all__ = ["kv_write", "paged_attention", "linear", "lm_head_int8", "w8a16_linear",
+__all__ = ["kv_write", "paged_attention", "linear", "lm_head_int8", "logits_int8", "w8a16_linear",
            "decode_attention_v1", "decode_attention_v2", "decode_attention_v3",
            "prefill_attention", "rmsnorm", "rmsnorm_residual", "rope_", "silu_mul"]
 
@@ -245,6 +245,37 @@ def linear(x: torch.Tensor, lw: LinearWeight) -> torch.Tensor:
 def lm_head_int8(h: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     """int8 tied lm head (ops/triton_ops.py:88-91)."""
     return w8a16_linear(h, wq, scale, None)
+
+
+def logits_int8(hidden: torch.Tensor, sample_indices: torch.Tensor, wq: torch.Tensor,
+                scale: torch.Tensor) -> torch.Tensor:
+    """Logits of the sampling rows, [S, V] fp32, through the int8 tied lm head in one launch:
+    equal to lm_head_int8(hidden[sample_indices], wq, scale).float() (model/qwen2.py:94-99)."""
+    _check_gpu(hidden, sample_indices, wq, scale)
+    _require(hidden.dim() == 2 and hidden.dtype == torch.float16, "logits_int8: hidden must be fp16 [T, H]")
+    if not (hidden.stride(1) == 1 and hidden.stride(0) % 8 == 0 and hidden.data_ptr() % 16 == 0):
+        hidden = hidden.contiguous()
+    T, Hd = hidden.shape
+    V, Kw = wq.shape
+    _require(Kw == Hd, f"logits_int8: hidden has {Hd} features, weight has {Kw}")
+    _require(wq.dtype == torch.int8 and wq.is_contiguous(), "logits_int8: weight must be int8 row-major")
+    _require(scale.dtype in (torch.float32, torch.float16) and scale.numel() == V,
+             "logits_int8: scale must be fp32 or fp16 [V]")
+    idx = sample_indices.reshape(-1).to(torch.int64).contiguous()
+    S = idx.numel()
+    out = torch.empty(S, V, dtype=torch.float32, device=hidden.device)
+    if S == 0:
+        return out
+    _require(T > 0, "logits_int8: no hidden rows to sample from")
+    sc = scale.contiguous()
+    cus = N.cu_count(hidden.device.index or 0)
+    ws_bytes = N.lib().ts_logits_int8_workspace_bytes(S, V, Hd, cus)
+    ws = _workspace(ws_bytes, hidden.device)
+    N.check(N.lib().ts_logits_int8(_ptr(hidden), hidden.stride(0), T, _ptr(idx), S, _ptr(wq),
+                                   _ptr(sc), 1 if sc.dtype == torch.float16 else 0, _ptr(out),
+                                   out.stride(0), V, Hd, _ptr(ws), ws_bytes, _stream(hidden)),
+            "logits_int8")
+    return out
 
 
 # ------------------------------------------------------------------------------------------

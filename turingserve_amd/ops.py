@@ -32,6 +32,7 @@ def _hip() -> SimpleNamespace:
     ns.kv_write = h.kv_write
     ns.paged_attention = h.paged_attention
     ns.lm_head_int8 = h.lm_head_int8
+    ns.logits_int8 = h.logits_int8
     ns.rmsnorm = h.rmsnorm
     ns.rmsnorm_residual = h.rmsnorm_residual
     ns.rope_ = h.rope_

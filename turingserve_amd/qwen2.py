@@ -169,7 +169,11 @@ class Qwen2Model:
         return x
 
     def compute_logits(self, hidden: torch.Tensor, sample_indices: torch.Tensor) -> torch.Tensor:
-        """Logits of the sampling rows only, [S, V] fp32 (model/qwen2.py:94-99)."""
+        """Logits of the sampling rows only, [S, V] fp32 (model/qwen2.py:94-99). With the int8
+        lm head, a backend that has logits_int8 gathers, multiplies and widens in one launch
+        (same values as lm_head_int8 on the gathered rows followed by .float())."""
+        if self.w.embed_q is not None and hasattr(self.ops, "logits_int8"):
+            return self.ops.logits_int8(hidden, sample_indices, *self.w.embed_q)
         h = hidden[sample_indices]
         if self.w.embed_q is not None and hasattr(self.ops, "lm_head_int8"):
             return self.ops.lm_head_int8(h, *self.w.embed_q).float()
