@@ -44,7 +44,8 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "w8a16", "logits", "mixed"], default=None,
+    ap.add_argument("--only", choices=["decode", "prefill", "w8a16", "logits", "metadata", "mixed"],
+                    default=None,
                     help="run one workload alone (for profiling); prints its result as JSON")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="copy a 256 MiB buffer 8 times (the known-size kernel that scales the "
@@ -303,6 +304,45 @@ def bench_logits(torch, K):
     return {"rows": S, "vocab": V, "hidden": H, **out}
 
 
+def bench_metadata(torch, synth):
+    """Step metadata of the config 5 batch (48 decodes with contexts log-uniform in [256, 4096]
+    and a 512-token chunk): the host builder (numpy per item and seven host-to-device copies,
+    runner/input_builder.py:81-150) against the device builder (one packed upload and one
+    kernel). Host microseconds until build() returns (what the step loop pays before it can
+    launch the forward) and microseconds until the metadata is on the device."""
+    import time as _t
+
+    from turingserve_amd.metadata import BatchItem, DeviceInputBuilder, InputBuilder, SeqState
+
+    dev = torch.device("cuda", 0)
+    g = torch.Generator().manual_seed(0)
+    ctx = synth.log_uniform_ints(48, 256, 4096, g)
+    free = list(range(1, 20000))
+    items = []
+    for c in ctx:
+        s = SeqState(list(range(c)), [free.pop() for _ in range(-(-c // 16))])
+        items.append(BatchItem(s, c - 1, [s.token_ids[-1]]))
+    s = SeqState(list(range(1549)), [free.pop() for _ in range(-(-1549 // 16))])
+    items.append(BatchItem(s, 1037, s.token_ids[1037:1549]))
+    out = {"tokens": 560, "seqs": 49}
+    for name, b in (("host_builder", InputBuilder(2048, 64, 512, dev)),
+                    ("device_builder", DeviceInputBuilder(2048, 64, 512, dev))):
+        for _ in range(20):
+            b.build(items)
+        torch.cuda.synchronize()
+        host, total, n = 0.0, 0.0, 200
+        for _ in range(n):
+            t0 = _t.perf_counter()
+            b.build(items)
+            t1 = _t.perf_counter()
+            torch.cuda.synchronize()
+            t2 = _t.perf_counter()
+            host += t1 - t0
+            total += t2 - t0
+        out[name] = {"host_us": round(host / n * 1e6, 1), "ready_us": round(total / n * 1e6, 1)}
+    return out
+
+
 def bench_mixed(torch, synth, reps: int = 5):
     """Config 5: one mixed forward step of a random-init Qwen2 at the Qwen2.5-1.5B dimensions
     (28 layers, W8A16 linears, tied fp16 lm head) over 48 decodes with contexts log-uniform in
@@ -394,10 +434,11 @@ def main() -> int:
                           "copy_bytes_written_per_launch": a.numel(), "launches": 8}))
         return 0
     _native.lib()
-    if args.only in ("prefill", "w8a16", "logits", "mixed"):
+    if args.only in ("prefill", "w8a16", "logits", "metadata", "mixed"):
         fn = {"prefill": lambda: bench_prefill(torch, K, synth),
               "w8a16": lambda: bench_w8a16(torch, K, synth),
               "logits": lambda: bench_logits(torch, K),
+              "metadata": lambda: bench_metadata(torch, synth),
               "mixed": lambda: bench_mixed(torch, synth)}[args.only]
         print(json.dumps({args.only: fn()}), flush=True)
         return 0
@@ -446,6 +487,8 @@ def main() -> int:
         extra["w8a16_config4"] = bench_w8a16(torch, K, synth)
         log("extra: config 5 logits")
         extra["logits_config5"] = bench_logits(torch, K)
+        log("extra: config 5 step metadata")
+        extra["metadata_config5"] = bench_metadata(torch, synth)
         log("extra: config 5 mixed step")
         extra["mixed_config5"] = bench_mixed(torch, synth)
         out["extra"] = extra

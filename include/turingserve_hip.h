@@ -12,6 +12,8 @@
  *   ts_w8a16_gemm          <- ops/triton_w8a16.py:38-51 and ops/triton_ops.py:74-91
  *   ts_logits_int8         <- model/qwen2.py:94-99 with ops/triton_ops.py:88-91 (gather, int8
  *                             lm head and .float() fused)
+ *   ts_step_metadata       <- runner/input_builder.py:81-150 (host arrays + seven copies) and
+ *                             the decode-graph padding of runner/cuda_graphs.py:62-78
  *   ts_rmsnorm             <- ops/triton_rmsnorm.py:30-46   (twins ops/reference.py:13-23)
  *   ts_rope                <- ops/triton_rope.py:27-31      (twin ops/reference.py:31-42)
  *   ts_silu_mul            <- ops/triton_silu_mul.py:21-28  (twin ops/reference.py:26-28)
@@ -173,6 +175,32 @@ int ts_logits_int8(const void* hidden, int64_t hidden_stride, int64_t hidden_row
                    const void* scale, int32_t scale_is_fp16, float* logits, int64_t logits_stride,
                    int32_t vocab, int32_t hidden_size, void* workspace, size_t workspace_bytes,
                    void* stream);
+
+/*
+ * One step's attention metadata built on the device from a compact packed int32 upload
+ * (replaces the host builder of runner/input_builder.py:81-150 and the padding copies of
+ * runner/cuda_graphs.py:62-78). `packed` (device memory) holds, in order:
+ *   num_seqs descriptors of 5 int32 {start, n_tokens, sample (0 none, 1 last, 2 all),
+ *   table_offset, table_len}, then num_tokens token ids, then num_block_ids block ids (the
+ *   sequences' block tables concatenated; table_offset / table_len index them).
+ * Writes, for the token rows in sequence order (row offset off_i = n_0 + ... + n_{i-1}):
+ *   input_ids[row] = token, positions[row] = start + t,
+ *   slot_mapping[row] = table[pos / 16] * 16 + pos % 16 (-1 when pos / 16 >= table_len);
+ * per sequence: query_start_loc[i + 1] = off_i + n_i (query_start_loc[0] = 0),
+ *   seq_lens[i] = start + n_i, block_tables row i (stride bt_stride) = the table padded with
+ *   block 0 to bt_width entries; sample_indices (may be NULL) = the last row of each 'last'
+ *   sequence with n_i > 0 and every row of each 'all' sequence, in order.
+ * Sequences num_seqs .. pad_seqs - 1 become padding rows of a captured decode graph: one token
+ * (id 0, position 0, slot -1) each after the real rows, seq_len 0, a zero table row, and
+ * query_start_loc advancing by one. Output sizes: num_tokens + pad_seqs - num_seqs token rows,
+ * pad_seqs + 1 query_start_loc entries, pad_seqs seq_lens and table rows.
+ * Block ids past num_block_ids read as 0 and token rows past num_tokens are not written.
+ */
+int ts_step_metadata(const int32_t* packed, int32_t num_seqs, int64_t num_tokens,
+                     int64_t num_block_ids, int32_t pad_seqs, int32_t bt_width, int64_t bt_stride,
+                     int64_t* input_ids, int64_t* positions, int64_t* slot_mapping,
+                     int32_t* query_start_loc, int32_t* seq_lens, int32_t* block_tables,
+                     int64_t* sample_indices, void* stream);
 
 /*
  * RMSNorm with optional fused residual add, one token row of `hidden` features at a time:

@@ -78,3 +78,57 @@ def test_stale_block_table_rows_are_cleared():
     two = SeqState(list(range(20)), [1, 2])
     m = b.build([BatchItem(short, 0, [1]), BatchItem(two, 19, [19])]).meta
     assert m.block_tables.tolist() == [[3, 0], [1, 2]]
+
+
+def _expand(words: np.ndarray, B: int, T: int, width: int):
+    """Straightforward expansion of pack_step's upload, following ts_step_metadata's contract."""
+    desc = words[:5 * B].reshape(B, 5).astype(np.int64)
+    toks = words[5 * B:5 * B + T].astype(np.int64)
+    blocks = words[5 * B + T:].astype(np.int64)
+    ids, pos, slot, qsl, sl, bt, smp = [], [], [], [0], [], [], []
+    off = 0
+    for start, n, mode, t_off, t_len in desc:
+        table = blocks[t_off:t_off + t_len]
+        for t in range(n):
+            p = start + t
+            ids.append(toks[off + t])
+            pos.append(p)
+            slot.append(table[p // 16] * 16 + p % 16 if p // 16 < t_len else -1)
+        if mode == 1 and n > 0:
+            smp.append(off + n - 1)
+        elif mode == 2:
+            smp += list(range(off, off + n))
+        off += n
+        qsl.append(off)
+        sl.append(start + n)
+        bt.append(list(table) + [0] * (width - t_len))
+    return ids, pos, slot, qsl, sl, bt, smp
+
+
+def test_pack_step_upload_expands_to_the_simple_builder():
+    from turingserve_amd.metadata import pack_step
+
+    rng = random.Random(1)
+    blocks = Blocks(400, seed=1)
+    for _ in range(100):
+        items = []
+        for _i in range(rng.randint(1, 8)):
+            n_prompt = rng.randint(1, 120)
+            s = SeqState([rng.randrange(150000) for _ in range(n_prompt)])
+            start = rng.randint(0, n_prompt - 1)
+            n = rng.randint(1, n_prompt - start)
+            blocks.grow(s, start + n + rng.randint(0, 40))      # tables may run ahead
+            items.append(BatchItem(s, start, s.token_ids[start:start + n],
+                                   rng.choice(["last", "none", "all"])))
+        items.sort(key=lambda it: len(it.tokens) != 1)
+        words, T, NB, S = pack_step(items)
+        assert words.dtype == np.int32 and words.size == 5 * len(items) + T + NB
+        a = build_simple(items, "cpu")
+        width = a.meta.block_tables.shape[1]
+        ids, pos, slot, qsl, sl, bt, smp = _expand(words, len(items), T, width)
+        assert ids == a.input_ids.tolist() and pos == a.positions.tolist()
+        assert slot == a.meta.slot_mapping.tolist() and qsl == a.meta.query_start_loc.tolist()
+        assert sl == a.meta.seq_lens.tolist() and bt == a.meta.block_tables.tolist()
+        assert smp == a.sample_indices.tolist() and S == len(smp)
+        for it in items:
+            blocks.release(it.seq)

@@ -51,6 +51,8 @@ SIGNATURES = {
     "ts_w8a16_gemm": (ctypes.c_int, [_p, _i64, _p, _p, _i32, _p, _p, _i64, _i32, _i32, _i32, _p,
                                      _sz, _p]),
     "ts_logits_int8_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
+    "ts_step_metadata": (ctypes.c_int, [_p, _i32, _i64, _i64, _i32, _i32, _i64, _p, _p, _p, _p,
+                                        _p, _p, _p, _p]),
     "ts_logits_int8": (ctypes.c_int, [_p, _i64, _i64, _p, _i32, _p, _p, _i32, _p, _i64, _i32,
                                       _i32, _p, _sz, _p]),
     "ts_rmsnorm": (ctypes.c_int, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i32, _f32,

@@ -14,7 +14,8 @@ from dataclasses import dataclass, field
 import torch
 
 from turingserve_amd.graphs import HipGraphRunner
-from turingserve_amd.metadata import BatchItem, InputBuilder, SeqState
+from turingserve_amd.metadata import (BatchItem, DeviceInputBuilder, InputBuilder, SeqState,
+                                      num_decode_rows)
 
 BLOCK = 16
 
@@ -55,15 +56,17 @@ class Request:
 
 class GreedyEngine:
     def __init__(self, model, num_blocks: int, max_num_batched_tokens: int = 256,
-                 max_num_seqs: int = 32, max_model_len: int = 1024, graph_sizes=()) -> None:
+                 max_num_seqs: int = 32, max_model_len: int = 1024, graph_sizes=(),
+                 device_metadata: bool = False) -> None:
         self.model = model
         self.kv = model.new_kv_cache(num_blocks)
         self.alloc = BlockAllocator(num_blocks)
         self.budget = max_num_batched_tokens
         self.max_seqs = max_num_seqs
         self.max_blocks = -(-max_model_len // BLOCK)
-        self.builder = InputBuilder(max_num_batched_tokens, max_num_seqs, self.max_blocks,
-                                    model.device)
+        self.device_metadata = device_metadata
+        make = DeviceInputBuilder if device_metadata else InputBuilder
+        self.builder = make(max_num_batched_tokens, max_num_seqs, self.max_blocks, model.device)
         self.graphs = None
         if graph_sizes:
             self.graphs = HipGraphRunner(model, self.kv, tuple(graph_sizes), self.max_blocks,
@@ -98,12 +101,15 @@ class GreedyEngine:
     def step(self, running: list[Request]) -> None:
         sched = self._schedule(running)
         items = [it for _, it in sched]
-        inp = self.builder.build(items)
-        pure_decode = inp.meta.num_decode == len(items) and all(it.sample == "last" for it in items)
+        pure_decode = num_decode_rows(items) == len(items) and all(it.sample == "last" for it in items)
         if pure_decode and self.graphs is not None and self.graphs.can_replay(len(items)):
-            logits = self.graphs.replay(inp, len(items))
+            if self.device_metadata:
+                logits = self.graphs.replay_items(items, self.builder)
+            else:
+                logits = self.graphs.replay(self.builder.build(items), len(items))
             self.graph_steps += 1
         else:
+            inp = self.builder.build(items)
             hidden = self.model.forward(inp.input_ids, inp.positions, inp.meta, self.kv)
             logits = self.model.compute_logits(hidden, inp.sample_indices)
         top = logits.topk(2, dim=-1)

@@ -173,3 +173,113 @@ class InputBuilder:
             num_decode=num_decode_rows(items), max_query_len=max(n_tok),
             max_seq_len=int(sl[:B].max()))
         return ModelInput(self.d_ids[:T], self.d_pos[:T], meta, self.d_sample[:ns])
+
+
+SAMPLE_CODES = {"none": 0, "last": 1, "all": 2}
+DESC_WORDS = 5
+
+
+def pack_step(items: list[BatchItem], out: np.ndarray | None = None) -> tuple[np.ndarray, int, int, int]:
+    """The compact int32 upload that ts_step_metadata expands on the device: per item the
+    descriptor {start, n_tokens, sample code, table offset, table length}, then every token id,
+    then every block table, concatenated. Written into `out` (e.g. a pinned buffer's view) when
+    given. Returns (packed words, num_tokens, num_block_ids, num_samples); an item with no tokens
+    samples nothing."""
+    B = len(items)
+    n_tok = np.fromiter((len(it.tokens) for it in items), np.int64, B)
+    t_len = np.fromiter((len(it.seq.block_table) for it in items), np.int64, B)
+    T, NB = int(n_tok.sum()), int(t_len.sum())
+    total = DESC_WORDS * B + T + NB
+    buf = np.empty(total, np.int32) if out is None else out[:total]
+    desc = buf[:DESC_WORDS * B].reshape(B, DESC_WORDS)
+    desc[:, 0] = np.fromiter((it.start for it in items), np.int64, B)
+    desc[:, 1] = n_tok
+    codes = np.fromiter((SAMPLE_CODES[it.sample] for it in items), np.int64, B)
+    desc[:, 2] = codes
+    desc[:, 3] = np.cumsum(t_len) - t_len
+    desc[:, 4] = t_len
+    o = DESC_WORDS * B
+    for it in items:
+        n = len(it.tokens)
+        buf[o:o + n] = it.tokens
+        o += n
+    for it in items:
+        n = len(it.seq.block_table)
+        buf[o:o + n] = it.seq.block_table
+        o += n
+    S = int(((codes == 1) & (n_tok > 0)).sum() + n_tok[codes == 2].sum())
+    return buf, T, NB, S
+
+
+class DeviceInputBuilder:
+    """Builds the step's metadata on the GPU (ts_step_metadata) from one packed upload instead of
+    the host arrays and seven copies of InputBuilder (runner/input_builder.py:81-150); the same
+    ModelInput contract. The pinned upload buffer is rewritten only after the previous step's
+    sampler synchronisation, as with InputBuilder. build_into() writes a pure-decode batch
+    straight into a captured graph's static buffers, padded to the graph size
+    (runner/cuda_graphs.py:62-78)."""
+
+    def __init__(self, max_tokens: int, max_seqs: int, max_blocks_per_seq: int, device) -> None:
+        from turingserve_amd import _native
+
+        self._native = _native
+        _native.lib()                               # fail now, loudly, if the library is missing
+        self.device = torch.device(device)
+        i32, i64 = torch.int32, torch.int64
+        self.max_tokens, self.max_seqs, self.max_blocks = max_tokens, max_seqs, max_blocks_per_seq
+        cap = DESC_WORDS * max_seqs + max_tokens + max_seqs * max_blocks_per_seq
+        self.h_packed = torch.zeros(cap, dtype=i32, pin_memory=True)
+        self.d_packed = torch.zeros(cap, dtype=i32, device=self.device)
+        dev = lambda *shape, dtype: torch.zeros(*shape, dtype=dtype, device=self.device)
+        self.d_ids, self.d_pos = dev(max_tokens, dtype=i64), dev(max_tokens, dtype=i64)
+        self.d_slot, self.d_sample = dev(max_tokens, dtype=i64), dev(max_tokens, dtype=i64)
+        self.d_qsl, self.d_sl = dev(max_seqs + 1, dtype=i32), dev(max_seqs, dtype=i32)
+        self.d_bt = dev(max_seqs, max_blocks_per_seq, dtype=i32)
+
+    def _upload(self, items: list[BatchItem]) -> tuple[int, int, int, int]:
+        B = len(items)
+        if B > self.max_seqs:
+            raise ValueError(f"batch of {B} sequences exceeds the builder's {self.max_seqs}")
+        width = max(1, max((len(it.seq.block_table) for it in items), default=1))
+        if width > self.max_blocks:
+            raise ValueError(f"block table of {width} blocks exceeds {self.max_blocks}")
+        if sum(len(it.tokens) for it in items) > self.max_tokens:
+            raise ValueError("batch exceeds max_num_batched_tokens")
+        words, T, NB, S = pack_step(items, self.h_packed.numpy())
+        n = words.size
+        self.d_packed[:n].copy_(self.h_packed[:n], non_blocking=True)
+        return T, NB, S, width
+
+    def _launch(self, B, pad, T, NB, width, ids, pos, slot, qsl, sl, bt, sample) -> None:
+        N = self._native
+        stream = torch.cuda.current_stream(self.device).cuda_stream
+        ptr = lambda t: None if t is None else t.data_ptr()
+        N.check(N.lib().ts_step_metadata(ptr(self.d_packed), B, T, NB, pad, width, bt.stride(0),
+                                         ptr(ids), ptr(pos), ptr(slot), ptr(qsl), ptr(sl),
+                                         ptr(bt), ptr(sample), stream), "step_metadata")
+
+    def build(self, items: list[BatchItem]) -> ModelInput:
+        B = len(items)
+        T, NB, S, width = self._upload(items)
+        self._launch(B, B, T, NB, width, self.d_ids, self.d_pos, self.d_slot, self.d_qsl,
+                     self.d_sl, self.d_bt, self.d_sample)
+        n_tok = [len(it.tokens) for it in items]
+        meta = AttentionMetadata(
+            query_start_loc=self.d_qsl[:B + 1], seq_lens=self.d_sl[:B],
+            block_tables=self.d_bt[:B, :width], slot_mapping=self.d_slot[:T],
+            num_decode=num_decode_rows(items), max_query_len=max(n_tok),
+            max_seq_len=max(it.start + n for it, n in zip(items, n_tok)))
+        return ModelInput(self.d_ids[:T], self.d_pos[:T], meta, self.d_sample[:S])
+
+    def build_into(self, items: list[BatchItem], pad_to: int, ids: torch.Tensor,
+                   pos: torch.Tensor, slot: torch.Tensor, qsl: torch.Tensor, seq_lens: torch.Tensor,
+                   block_tables: torch.Tensor) -> None:
+        """Pure-decode items (one token each) into static buffers of a graph captured for pad_to
+        rows: rows len(items) .. pad_to - 1 become padding rows; the table rows are written over
+        the buffers' full width."""
+        B = len(items)
+        if any(len(it.tokens) != 1 for it in items) or not B <= pad_to <= ids.numel():
+            raise ValueError("build_into: one token per item and len(items) <= pad_to <= buffer rows")
+        T, NB, S, _ = self._upload(items)
+        self._launch(B, pad_to, T, NB, block_tables.shape[1], ids, pos, slot, qsl, seq_lens,
+                     block_tables, None)
