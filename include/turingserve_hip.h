@@ -10,6 +10,7 @@
  *   ts_prefill_attention   <- ops/triton_prefill_attention.py:66-79
  *   ts_paged_attention     <- ops/triton_ops.py:60-71        (twin ops/reference.py:94-111)
  *   ts_w8a16_gemm          <- ops/triton_w8a16.py:38-51 and ops/triton_ops.py:74-91
+ *   ts_w8a16_gemm_v        <- the same with the tuned per-bucket config (autopilot/tuner.py)
  *   ts_logits_int8         <- model/qwen2.py:94-99 with ops/triton_ops.py:88-91 (gather, int8
  *                             lm head and .float() fused)
  *   ts_step_metadata       <- runner/input_builder.py:81-150 (host arrays + seven copies) and
@@ -154,6 +155,22 @@ int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const void* scal
                   int32_t scale_is_fp16, const void* bias, void* y, int64_t ldy,
                   int32_t M, int32_t N, int32_t K,
                   void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The same product with a named kernel variant, the choice a tuning table makes for a shape
+ * bucket (the role of the reference's per-bucket W8A16 configs, autopilot/tuner.py:116-134 and
+ * ops/triton_ops.py:74-86): variant 0 = the library's own plan (as ts_w8a16_gemm), 1 = weight
+ * streaming (M <= 32 only), 2 = 128 x 64 wide tiles, 3 = 128 x 128 wide tiles; splits = the
+ * number of K splits (0 = the variant's own rule, at most 256; splits > 1 sum fp32 partials in
+ * the workspace). Every variant computes the same product up to fp32 summation order.
+ * Unavailable combinations return TS_ERR_UNSUPPORTED.
+ */
+size_t ts_w8a16_workspace_bytes_v(int32_t M, int32_t N, int32_t K, int32_t variant,
+                                  int32_t splits, int32_t cu_count);
+int ts_w8a16_gemm_v(const void* x, int64_t ldx, const int8_t* wq, const void* scale,
+                    int32_t scale_is_fp16, const void* bias, void* y, int64_t ldy,
+                    int32_t M, int32_t N, int32_t K, int32_t variant, int32_t splits,
+                    void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Logits of the sampling rows through the int8 tied lm head, in one launch (plus the split-K

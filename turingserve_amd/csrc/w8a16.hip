@@ -540,54 +540,65 @@ struct GemmPlan {
   int k_per_split;
 };
 
-static GemmPlan plan_gemm(int M, int N, int K, int cus) {
-  GemmPlan p{use_small_path(M, N, K), (M + 15) / 16, 0, 0, 1, K};
+// Variants a caller (a tuning table) may name instead of the planner's choice.
+enum GemmVariant : int { kVarAuto = 0, kVarStream = 1, kVarWide64 = 2, kVarWide128 = 3 };
+constexpr int kMaxSplits = 256;
+
+// Weight streaming: fill the device with wavefronts (about eight per CU) by splitting K,
+// keeping at least 256 K per split and the fp32 partials (splits * M * N * 4 bytes) within a
+// quarter of the weight bytes or 2 MB.
+static int stream_splits(int M, int N, int K, int cus) {
+  const int64_t wgs = (N + 16 * kSmWaves - 1) / (16 * kSmWaves);
+  const int64_t target_wgs = 2LL * cus;
+  int splits = (int)((target_wgs + wgs - 1) / wgs);
+  const int max_by_k = K / 256 > 1 ? K / 256 : 1;
+  const int64_t budget = (int64_t)N * K / 4 > (2LL << 20) ? (int64_t)N * K / 4 : (2LL << 20);
+  const int64_t by_traffic64 = budget / ((int64_t)M * N * 4);
+  const int max_by_traffic = by_traffic64 > 1 ? (int)by_traffic64 : 1;
+  if (splits > max_by_k) splits = max_by_k;
+  if (splits > max_by_traffic) splits = max_by_traffic;
+  return splits < 1 ? 1 : splits;
+}
+
+// 128 x 64 wide tiles: split over K while the grid holds fewer than two workgroups per CU, each
+// split keeps at least 32 K steps (below that the reduction costs more than the split saves)
+// and the fp32 partials (written and read once more by the reduction) stay within half the
+// weight bytes or 8 MB.
+static int wide64_splits(int M, int N, int K, int cus) {
+  const int nk = (K + kTileBK - 1) / kTileBK;
+  const int64_t tiles = (int64_t)((N + 127) / 128) * ((M + 63) / 64);
+  const int64_t part_budget = (int64_t)N * K / 2 > (8LL << 20) ? (int64_t)N * K / 2 : (8LL << 20);
+  int splits = 1;
+  while (tiles * splits < 2LL * cus && nk / (splits + 1) >= 32 &&
+         (int64_t)(splits + 1) * M * N * 4 <= part_budget)
+    ++splits;
+  return splits;
+}
+
+// The plan of a variant with `splits` K splits (0: the variant's own rule). kVarAuto: weight
+// streaming when use_small_path says so; else 128 x 128 tiles (two workgroups per CU; the most
+// work per CU of the shapes measured) once they cover half the CUs and M is past 64 (below
+// that most of their rows would be padding); else 128 x 64 tiles.
+static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int splits) {
+  if (variant == kVarAuto) {
+    const int64_t n_tiles = (N + 127) / 128;
+    variant = use_small_path(M, N, K)                                       ? kVarStream
+              : (M > 64 && n_tiles * ((M + 127) / 128) * 2 >= cus) ? kVarWide128
+                                                                        : kVarWide64;
+    splits = 0;
+  }
+  GemmPlan p{variant == kVarStream, (M + 15) / 16, 128, variant == kVarWide128 ? 128 : 64, 1, K};
   if (p.small) {
-    // Fill the device with wavefronts (about eight per CU) by splitting K, keeping at least
-    // 256 K per split and the fp32 partials (splits * M * N * 4 bytes) within a quarter of the
-    // weight bytes or 2 MB.
-    const int64_t wgs = (N + 16 * kSmWaves - 1) / (16 * kSmWaves);
-    const int64_t target_wgs = 2LL * cus;
-    int splits = (int)((target_wgs + wgs - 1) / wgs);
-    const int max_by_k = K / 256 > 1 ? K / 256 : 1;
-    const int64_t budget = (int64_t)N * K / 4 > (2LL << 20) ? (int64_t)N * K / 4 : (2LL << 20);
-    const int64_t by_traffic64 = budget / ((int64_t)M * N * 4);
-    const int max_by_traffic = by_traffic64 > 1 ? (int)by_traffic64 : 1;
-    if (splits > max_by_k) splits = max_by_k;
-    if (splits > max_by_traffic) splits = max_by_traffic;
-    if (splits < 1) splits = 1;
+    if (splits == 0) splits = stream_splits(M, N, K, cus);
     int kps = (K + splits - 1) / splits;
     kps = (kps + kSmKStep - 1) / kSmKStep * kSmKStep;
     p.splits = (K + kps - 1) / kps;
     p.k_per_split = kps;
     return p;
   }
+  if (splits == 0) splits = variant == kVarWide64 ? wide64_splits(M, N, K, cus) : 1;
   const int nk = (K + kTileBK - 1) / kTileBK;
-  int splits = 1;
-#ifdef TS_W8A16_FORCE_BN                          // tuning override (bn, bm, splits)
-  p.bn = TS_W8A16_FORCE_BN;
-  p.bm = TS_W8A16_FORCE_BM;
-  splits = TS_W8A16_FORCE_SPLITS;
-#else
-  // 128 x 128 tiles (two workgroups per CU; the most work per CU of the shapes measured) once
-  // they cover half the CUs and M is past 64 (below that most of their rows would be padding).
-  // Otherwise 128 x 64 tiles, split over K while the grid holds fewer
-  // than two workgroups per CU, each split keeps at least 32 K steps (below that the reduction
-  // costs more than the split saves) and the fp32 partials (written and read once more by the
-  // reduction) stay within half the weight bytes or 8 MB.
-  p.bn = 128;
-  const int64_t n_tiles = (N + 127) / 128;
-  if (M > 64 && n_tiles * ((M + 127) / 128) * 2 >= cus) {
-    p.bm = 128;
-  } else {
-    p.bm = 64;
-    const int64_t tiles = n_tiles * ((M + 63) / 64);
-    const int64_t part_budget = (int64_t)N * K / 2 > (8LL << 20) ? (int64_t)N * K / 2 : (8LL << 20);
-    while (tiles * splits < 2LL * cus && nk / (splits + 1) >= 32 &&
-           (int64_t)(splits + 1) * M * N * 4 <= part_budget)
-      ++splits;
-  }
-#endif
+  if (splits > nk) splits = nk;
   if (splits > 1) {
     const int steps = (nk + splits - 1) / splits;
     p.k_per_split = steps * kTileBK;
@@ -595,6 +606,8 @@ static GemmPlan plan_gemm(int M, int N, int K, int cus) {
   }
   return p;
 }
+
+static GemmPlan plan_gemm(int M, int N, int K, int cus) { return plan_gemm_v(M, N, K, cus, kVarAuto, 0); }
 
 static size_t gemm_workspace(const GemmPlan& p, int M, int N) {
   return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
@@ -609,15 +622,27 @@ extern "C" size_t ts_w8a16_workspace_bytes(int32_t M, int32_t N, int32_t K, int3
   return gemm_workspace(plan_gemm(M, N, K, cu_count > 0 ? cu_count : 256), M, N);
 }
 
+static bool variant_valid(int variant, int splits, int M) {
+  return variant >= kVarAuto && variant <= kVarWide128 && splits >= 0 && splits <= kMaxSplits &&
+         (variant != kVarStream || M <= kSmallMMax);
+}
+
+extern "C" size_t ts_w8a16_workspace_bytes_v(int32_t M, int32_t N, int32_t K, int32_t variant,
+                                             int32_t splits, int32_t cu_count) {
+  if (M <= 0 || N <= 0 || K <= 0 || !variant_valid(variant, splits, M)) return 0;
+  return gemm_workspace(plan_gemm_v(M, N, K, cu_count > 0 ? cu_count : 256, variant, splits), M,
+                        N);
+}
+
 // Validated launch shared by the GEMM and logits entry points.
 static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const void* scale,
                         int32_t scale_is_fp16, const half_t* bp, half_t* yp, int64_t ldy,
                         int32_t M, int32_t N, int32_t K, void* workspace, size_t workspace_bytes,
-                        hipStream_t s, const GemmIo& io) {
+                        hipStream_t s, const GemmIo& io, int variant, int splits) {
   int cus = 0;
   int st = device_cu_count(&cus);
   if (st != TS_OK) return st;
-  const GemmPlan p = plan_gemm(M, N, K, cus);
+  const GemmPlan p = plan_gemm_v(M, N, K, cus, variant, splits);
   const size_t need = gemm_workspace(p, M, N);
   TS_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
              TS_ERR_WORKSPACE, "w8a16: workspace of %zu bytes needed, got %zu", need,
@@ -673,12 +698,14 @@ static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const v
   return TS_OK;
 }
 
-extern "C" int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const void* scale,
-                             int32_t scale_is_fp16, const void* bias, void* y, int64_t ldy,
-                             int32_t M, int32_t N, int32_t K, void* workspace,
-                             size_t workspace_bytes, void* stream) {
+static int w8a16_gemm_checked(const void* x, int64_t ldx, const int8_t* wq, const void* scale,
+                              int32_t scale_is_fp16, const void* bias, void* y, int64_t ldy,
+                              int32_t M, int32_t N, int32_t K, int32_t variant, int32_t splits,
+                              void* workspace, size_t workspace_bytes, void* stream) {
   TS_REQUIRE(M >= 0 && N > 0 && K > 0, TS_ERR_INVALID_ARG, "w8a16: bad shape M=%d N=%d K=%d", M,
              N, K);
+  TS_REQUIRE(variant_valid(variant, splits, M < 1 ? 1 : M), TS_ERR_UNSUPPORTED,
+             "w8a16: variant %d with %d splits is not available for M=%d", variant, splits, M);
   if (M == 0) return TS_OK;
   TS_REQUIRE(x && wq && scale && y, TS_ERR_INVALID_ARG, "w8a16: null pointer argument");
   TS_REQUIRE(K % 8 == 0, TS_ERR_UNSUPPORTED, "w8a16: K=%d is not a multiple of 8", K);
@@ -691,9 +718,25 @@ extern "C" int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const
   const int st = w8a16_launch(static_cast<const half_t*>(x), ldx, wq, scale, scale_is_fp16,
                               static_cast<const half_t*>(bias), static_cast<half_t*>(y), ldy, M,
                               N, K, workspace, workspace_bytes,
-                              reinterpret_cast<hipStream_t>(stream), io);
+                              reinterpret_cast<hipStream_t>(stream), io, variant, splits);
   if (st != TS_OK) return st;
   return check_launch("w8a16_gemm");
+}
+
+extern "C" int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const void* scale,
+                             int32_t scale_is_fp16, const void* bias, void* y, int64_t ldy,
+                             int32_t M, int32_t N, int32_t K, void* workspace,
+                             size_t workspace_bytes, void* stream) {
+  return w8a16_gemm_checked(x, ldx, wq, scale, scale_is_fp16, bias, y, ldy, M, N, K, kVarAuto, 0,
+                            workspace, workspace_bytes, stream);
+}
+
+extern "C" int ts_w8a16_gemm_v(const void* x, int64_t ldx, const int8_t* wq, const void* scale,
+                               int32_t scale_is_fp16, const void* bias, void* y, int64_t ldy,
+                               int32_t M, int32_t N, int32_t K, int32_t variant, int32_t splits,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+  return w8a16_gemm_checked(x, ldx, wq, scale, scale_is_fp16, bias, y, ldy, M, N, K, variant,
+                            splits, workspace, workspace_bytes, stream);
 }
 
 extern "C" size_t ts_logits_int8_workspace_bytes(int32_t num_samples, int32_t vocab,
@@ -721,7 +764,8 @@ extern "C" int ts_logits_int8(const void* hidden, int64_t hidden_stride, int64_t
   const GemmIo io{sample_indices, hidden_rows, logits, logits_stride};
   const int st = w8a16_launch(static_cast<const half_t*>(hidden), hidden_stride, wq, scale,
                               scale_is_fp16, nullptr, nullptr, 0, num_samples, vocab, hidden_size,
-                              workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream), io);
+                              workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream), io,
+                              kVarAuto, 0);
   if (st != TS_OK) return st;
   return check_launch("logits_int8");
 }

@@ -18,6 +18,7 @@ import torch
 import torch.nn.functional as F
 
 from turingserve_amd import _native as N
+from turingserve_amd import tuner
 from turingserve_amd.quant import LinearWeight
 
 __all__ = ["kv_write", "paged_attention", "linear", "lm_head_int8", "logits_int8", "w8a16_linear",
@@ -170,9 +171,11 @@ def prefill_attention(q, out, k_cache, v_cache, meta, scale, block_m: int = 64,
 # ------------------------------------------------------------------------------------------
 def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, meta,
                     scale: float, decode_version: str | None = None,
-                    partition: int = DEFAULT_PARTITION) -> torch.Tensor:
+                    partition: int | None = None) -> torch.Tensor:
     """q [T, H, D] -> [T, H*D]: decode kernel on rows [0, num_decode), prefill kernel on the
-    remaining sequences, one library call."""
+    remaining sequences, one library call. Unless the caller names a decode version, the active
+    variant table's choice for (num_decode, max_seq_len) applies, then the library's own
+    policy with the balanced split (partition 0)."""
     T, H, D = q.shape
     out = torch.empty(T, H * D, dtype=q.dtype, device=q.device)
     if T == 0:
@@ -185,6 +188,12 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     bt, sl, qsl = _i32(meta.block_tables), _i32(meta.seq_lens), _i32(meta.query_start_loc)
     B = sl.shape[0]
     S = meta.num_decode
+    if decode_version is None and S > 0:
+        tv, tp = tuner.decode_choice(S, int(meta.max_seq_len))
+        if tv is not None:
+            decode_version = tv
+            partition = tp if partition is None else partition
+    partition = DEFAULT_PARTITION if partition is None else partition
     code = N.DECODE_VERSIONS[decode_version]
     ws_bytes = 0
     if S > 0:
@@ -205,7 +214,10 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
 # ------------------------------------------------------------------------------------------
 def w8a16_linear(x: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor,
                  bias: torch.Tensor | None, cfg=None) -> torch.Tensor:
-    """y = x . (wq * scale)^T + bias, x fp16 [M, K], wq int8 [N, K], scale fp32 or fp16 [N]."""
+    """y = x . (wq * scale)^T + bias, x fp16 [M, K], wq int8 [N, K], scale fp32 or fp16 [N].
+    cfg = (variant, splits) of ts_w8a16_gemm_v (the reference passes its tuned Triton config in
+    this position, ops/triton_ops.py:80-86); None takes the active variant table's choice for
+    (N, K, M's bucket), or the library's own plan."""
     x = x.contiguous()
     M, K = x.shape
     Nn, Kw = wq.shape
@@ -224,12 +236,21 @@ def w8a16_linear(x: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor,
         _require(bias.numel() == Nn, "w8a16: bias must be [N]")
         b = bias.to(torch.float16).contiguous()
     cus = N.cu_count(x.device.index or 0)
-    ws_bytes = N.lib().ts_w8a16_workspace_bytes(M, Nn, K, cus)
+    variant, splits = tuner.w8a16_choice(Nn, K, M) if cfg is None else (int(cfg[0]), int(cfg[1]))
+    if variant == 0 and splits == 0:
+        ws_bytes = N.lib().ts_w8a16_workspace_bytes(M, Nn, K, cus)
+        ws = _workspace(ws_bytes, x.device)
+        N.check(N.lib().ts_w8a16_gemm(_ptr(x), x.stride(0), _ptr(wq), _ptr(sc),
+                                      1 if sc.dtype == torch.float16 else 0, _ptr(b), _ptr(y),
+                                      y.stride(0), M, Nn, K, _ptr(ws), ws_bytes, _stream(x)),
+                "w8a16_gemm")
+        return y
+    ws_bytes = N.lib().ts_w8a16_workspace_bytes_v(M, Nn, K, variant, splits, cus)
     ws = _workspace(ws_bytes, x.device)
-    N.check(N.lib().ts_w8a16_gemm(_ptr(x), x.stride(0), _ptr(wq), _ptr(sc),
-                                  1 if sc.dtype == torch.float16 else 0, _ptr(b), _ptr(y),
-                                  y.stride(0), M, Nn, K, _ptr(ws), ws_bytes, _stream(x)),
-            "w8a16_gemm")
+    N.check(N.lib().ts_w8a16_gemm_v(_ptr(x), x.stride(0), _ptr(wq), _ptr(sc),
+                                    1 if sc.dtype == torch.float16 else 0, _ptr(b), _ptr(y),
+                                    y.stride(0), M, Nn, K, variant, splits, _ptr(ws), ws_bytes,
+                                    _stream(x)), "w8a16_gemm_v")
     return y
 
 
