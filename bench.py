@@ -343,6 +343,20 @@ def bench_metadata(torch, synth):
     return out
 
 
+def tune_for_mixed(torch):
+    """A variant table measured for the config 5 step's shapes: the four Qwen2.5-1.5B projections
+    at M = 560 and the decode kernel for 48 rows at the step's 4096-token bound."""
+    from turingserve_amd import tuner
+    from turingserve_amd.qwen2 import QWEN25_15B as c
+
+    D = c.head_dim
+    shapes = [(c.qkv_dim, c.hidden_size), (c.hidden_size, c.num_heads * D),
+              (2 * c.intermediate_size, c.hidden_size), (c.hidden_size, c.intermediate_size)]
+    t = tuner.tune_w8a16(torch, shapes, [560], "cuda")
+    tuner.tune_decode(torch, c.num_heads, c.num_kv_heads, D, [48], [4096], "cuda", t)
+    return t
+
+
 def bench_mixed(torch, synth, reps: int = 5):
     """Config 5: one mixed forward step of a random-init Qwen2 at the Qwen2.5-1.5B dimensions
     (28 layers, W8A16 linears, tied fp16 lm head) over 48 decodes with contexts log-uniform in
@@ -491,6 +505,15 @@ def main() -> int:
         extra["metadata_config5"] = bench_metadata(torch, synth)
         log("extra: config 5 mixed step")
         extra["mixed_config5"] = bench_mixed(torch, synth)
+        log("extra: config 5 mixed step with a measured variant table")
+        from turingserve_amd import tuner
+        table = tune_for_mixed(torch)
+        tuner.set_active(table)
+        try:
+            extra["mixed_config5_tuned"] = {**bench_mixed(torch, synth),
+                                            "choices": table.tables}
+        finally:
+            tuner.set_active(tuner.VariantTable())
         out["extra"] = extra
     print(json.dumps(out), flush=True)
     return 0

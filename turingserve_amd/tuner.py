@@ -5,8 +5,9 @@
 Each kernel has candidate variants per shape bucket; tune() times every candidate with HIP events
 over graph-captured calls and keeps the fastest; the winners are stored in a JSON file keyed by
 GPU, CU count, model dimensions and library / torch versions. At run time the ops look their
-bucket up, rounding each dimension up to the smallest recorded bucket (as lookup_rounded does in
-the reference); a miss takes the library's own plan.
+bucket up, rounding up to the smallest recorded bucket (as lookup_rounded does in the
+reference; for W8A16 only M rounds, N and K must match); a miss takes the library's own plan.
+tune() records the M buckets below the engine's token budget and the budget itself.
 
     kernel "decode": key "S,L"   (decode rows, max_seq_len)  -> {"version": "v2" | "v3",
                                                                   "partition": 0 | 256 | ...}
@@ -96,14 +97,19 @@ def set_active(table: VariantTable) -> None:
 
 
 def w8a16_choice(N: int, K: int, M: int) -> tuple[int, int]:
-    """(variant, splits) for a W8A16 product: the tuned choice of N, K and M's bucket, or the
-    library's own plan (0, 0)."""
+    """(variant, splits) for a W8A16 product: the choice recorded for this N and K at the
+    smallest recorded M >= M, or the library's own plan (0, 0)."""
     table = ACTIVE.tables.get("w8a16")
     if not table:
         return 0, 0
-    c = table.get(f"{N},{K},{round_up_bucket(W8A16_M_BUCKETS, M)}")
-    if c is None:
+    best = None
+    for name, choice in table.items():
+        n, k, m = (int(v) for v in name.split(","))
+        if n == N and k == K and m >= M and (best is None or m < best[0]):
+            best = (m, choice)
+    if best is None:
         return 0, 0
+    c = best[1]
     variant, splits = int(c["variant"]), int(c["splits"])
     if variant == 1 and M > 32:                     # streaming exists for M <= 32 only
         return 0, 0
@@ -239,6 +245,48 @@ def tune(torch, cfg, max_num_seqs: int, max_model_len: int, max_num_batched_toke
         shapes = sorted({(cfg.qkv_dim, cfg.hidden_size), (cfg.hidden_size, cfg.num_heads * D),
                          (2 * cfg.intermediate_size, cfg.hidden_size),
                          (cfg.hidden_size, cfg.intermediate_size)})
-        ms = [m for m in W8A16_M_BUCKETS if m <= max_num_batched_tokens]
+        ms = [m for m in W8A16_M_BUCKETS if m < max_num_batched_tokens] + [max_num_batched_tokens]
         tune_w8a16(torch, shapes, ms, device, table)
     return table
+
+
+def main(argv=None) -> int:
+    """Tune this GPU for a model configuration and write the table:
+        python -m turingserve_amd.tuner --model qwen2.5-1.5b --out <dir> [--max-num-seqs 64]
+            [--max-model-len 4096] [--max-num-batched-tokens 560] [--w8a16-only]"""
+    import argparse
+
+    import torch
+
+    from turingserve_amd import _native
+    from turingserve_amd.qwen2 import QWEN25_15B, TINY_G2, TINY_G7
+
+    models = {"qwen2.5-1.5b": QWEN25_15B, "tiny-g2": TINY_G2, "tiny-g7": TINY_G7}
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--model", choices=sorted(models), default="qwen2.5-1.5b")
+    ap.add_argument("--out", required=True)
+    ap.add_argument("--max-num-seqs", type=int, default=64)
+    ap.add_argument("--max-model-len", type=int, default=4096)
+    ap.add_argument("--max-num-batched-tokens", type=int, default=560)
+    ap.add_argument("--w8a16-only", action="store_true")
+    a = ap.parse_args(argv)
+    cfg = models[a.model]
+    dev = "cuda"
+    if a.w8a16_only:
+        table = VariantTable(meta={"gpu": torch.cuda.get_device_name(dev)})
+        D = cfg.head_dim
+        shapes = sorted({(cfg.qkv_dim, cfg.hidden_size), (cfg.hidden_size, cfg.num_heads * D),
+                         (2 * cfg.intermediate_size, cfg.hidden_size),
+                         (cfg.hidden_size, cfg.intermediate_size)})
+        ms = [m for m in W8A16_M_BUCKETS if m < a.max_num_batched_tokens] + [a.max_num_batched_tokens]
+        tune_w8a16(torch, shapes, ms, dev, table)
+    else:
+        table = tune(torch, cfg, a.max_num_seqs, a.max_model_len, a.max_num_batched_tokens, dev)
+    key = cache_key(torch.cuda.get_device_name(dev), _native.cu_count(0), a.model,
+                    _native.version(), torch.__version__)
+    print(save_cache(a.out, key, table), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
