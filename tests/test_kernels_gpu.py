@@ -149,6 +149,32 @@ def test_decode_v3_partitions(partition):
     assert (out[6] == 0).all()
 
 
+def test_decode_v3_merge_ignores_stale_workspace():
+    """The merge requests a fixed chunk of partial rows per sequence before it knows the split
+    count; rows past the count hold whatever an earlier call left, NaN included, and must not
+    reach the output (a zero weight times NaN would). The workspace is filled with NaN bytes and
+    the library is called through its C ABI."""
+    from turingserve_amd import _native as N
+
+    H, KVH, D = 12, 2, 128
+    lens = [4096, 3, 700, 1500, 0, 64]
+    q, kc, vc, qsl, sl, bt = make_paged(lens, H, KVH, D, seed=13)
+    n = len(lens)
+    q_d, kc_d, vc_d, bt_d, sl_d = q.cuda(), kc.cuda(), vc.cuda(), bt.cuda(), sl.cuda()
+    out = torch.empty(n, H * D, device=DEV, dtype=torch.float16)
+    lib = N.lib()
+    for partition in (0, 256):
+        ws_bytes = lib.ts_decode_workspace_bytes(3, n, H, KVH, D, 4096, partition, N.cu_count(0))
+        ws = torch.full((ws_bytes,), 0xFF, dtype=torch.uint8, device=DEV)    # NaN floats
+        N.check(lib.ts_decode_attention(
+            3, q_d.data_ptr(), q_d.stride(0), q_d.stride(1), out.data_ptr(), out.stride(0),
+            kc_d.data_ptr(), vc_d.data_ptr(), kc.shape[0], bt_d.data_ptr(), bt_d.stride(0),
+            bt.shape[1], sl_d.data_ptr(), n, H, KVH, D, D ** -0.5, 4096, partition,
+            ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream), "decode")
+        assert_attn(out, oracle_attn(q, kc, vc, qsl, sl, bt, D ** -0.5), f"stale ws {partition}")
+        assert (out[4] == 0).all()
+
+
 def test_decode_stale_nan_beyond_seq_len():
     """Cache slots past seq_len in the last block may hold anything (a reused block); NaN there
     must not reach the output (the twin slices [:seq_len], ops/reference.py:108-109)."""

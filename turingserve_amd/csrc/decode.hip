@@ -495,9 +495,11 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(
       O *= alpha;
 #pragma unroll
       for (int u = 0; u < CH; ++u) {
-        const float wt = (j0 + u < n) ? fast_exp2(mv[u] - cm) : 0.f;
-        L += wt * lv[u];
-        O += wt * av[u];
+        // rows past n are skipped, not weighted by 0: their stale contents may be inf or NaN
+        const float wt = fast_exp2(mv[u] - cm);
+        L = (j0 + u < n) ? L + wt * lv[u] : L;
+        const float4_t o2 = O + wt * av[u];
+        O = (j0 + u < n) ? o2 : O;
       }
       M = cm;
     }
