@@ -11,6 +11,8 @@
  *   ts_paged_attention     <- ops/triton_ops.py:60-71        (twin ops/reference.py:94-111)
  *   ts_w8a16_gemm          <- ops/triton_w8a16.py:38-51 and ops/triton_ops.py:74-91
  *   ts_w8a16_gemm_v        <- the same with the tuned per-bucket config (autopilot/tuner.py)
+ *   ts_w8a16_glu           <- model/qwen2.py:35-36, silu_mul(linear(x, gate_up)) fused
+ *                             (ops/triton_ops.py:74-91 + ops/triton_silu_mul.py:21-28)
  *   ts_logits_int8         <- model/qwen2.py:94-99 with ops/triton_ops.py:88-91 (gather, int8
  *                             lm head and .float() fused)
  *   ts_step_metadata       <- runner/input_builder.py:81-150 (host arrays + seven copies) and
@@ -171,6 +173,27 @@ int ts_w8a16_gemm_v(const void* x, int64_t ldx, const int8_t* wq, const void* sc
                     int32_t scale_is_fp16, const void* bias, void* y, int64_t ldy,
                     int32_t M, int32_t N, int32_t K, int32_t variant, int32_t splits,
                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * The gated MLP activation from the fused gate_up W8A16 linear, in one call:
+ *   out[m][i] = fp16( fp16(silu(g)) * u ),  g = G[m][i], u = G[m][I + i],
+ *   G = fp16( x . (wq * scale)^T + bias ), an [M, 2I] product never written to memory,
+ * where silu(g) = g / (1 + exp(-g)) in fp32. This is model/qwen2.py:35-36's
+ * silu_mul(linear(x, gate_up)) (ops/triton_silu_mul.py:21-28 after ops/triton_ops.py:74-91)
+ * and equals, bit for bit, ts_silu_mul applied to ts_w8a16_gemm_v's output with the same
+ * variant and splits: the product is planned for the [M, 2I] shape, and each gate value meets
+ * its up value in the GEMM epilogue (or in the split-K reduction). wq int8 [2 * intermediate, K]
+ * = [gate rows; up rows], scale / bias [2 * intermediate]; out fp16 [M, intermediate] with a
+ * row stride that is a multiple of 4; x and variant / splits as for ts_w8a16_gemm_v.
+ * Workspace: ts_w8a16_glu_workspace_bytes() bytes (the split-K partials, as for
+ * ts_w8a16_gemm_v on the [M, 2I] shape).
+ */
+size_t ts_w8a16_glu_workspace_bytes(int32_t M, int32_t intermediate, int32_t K, int32_t variant,
+                                    int32_t splits, int32_t cu_count);
+int ts_w8a16_glu(const void* x, int64_t ldx, const int8_t* wq, const void* scale,
+                 int32_t scale_is_fp16, const void* bias, void* out, int64_t ldo,
+                 int32_t M, int32_t intermediate, int32_t K, int32_t variant, int32_t splits,
+                 void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Logits of the sampling rows through the int8 tied lm head, in one launch (plus the split-K

@@ -85,6 +85,26 @@ def test_logits_argument_checks():
             lib.ts_w8a16_workspace_bytes(S, 151936, 1536, 256)
 
 
+def test_glu_argument_checks_and_workspace():
+    lib = N.lib()
+    p = ctypes.c_void_p(256)            # never dereferenced: the call fails validation first
+    assert lib.ts_w8a16_glu(p, 1540, p, p, 0, None, p, 8960, 4, 8960, 1540, 0, 0, None, 0,
+                            None) == N.TS_ERR_UNSUPPORTED and "multiple of 8" in N.last_error()
+    assert lib.ts_w8a16_glu(p, 1536, p, p, 0, None, p, 8962, 4, 8960, 1536, 0, 0, None, 0,
+                            None) == N.TS_ERR_INVALID_ARG and "out rows" in N.last_error()
+    assert lib.ts_w8a16_glu(p, 1536, p, p, 0, None, p, 8960, 64, 8960, 1536, 1, 0, None, 0,
+                            None) == N.TS_ERR_UNSUPPORTED                # streaming is M <= 32
+    assert lib.ts_w8a16_glu(None, 0, None, None, 0, None, None, 0, 0, 8960, 1536, 0, 0, None, 0,
+                            None) == N.TS_OK
+    # planned as the [M, 2I] product: the same split-K partials as ts_w8a16_gemm_v's
+    for M, v, s in ((560, 0, 0), (2048, 0, 0), (64, 2, 3), (200, 3, 1), (4, 1, 1), (4, 1, 3)):
+        assert lib.ts_w8a16_glu_workspace_bytes(M, 8960, 1536, v, s, 256) == \
+            lib.ts_w8a16_workspace_bytes_v(M, 17920, 1536, v, s, 256)
+    assert lib.ts_w8a16_glu_workspace_bytes(1, 8960, 1536, 0, 0, 256) == \
+        lib.ts_w8a16_workspace_bytes_v(1, 17920, 1536, 0, 0, 256) > 0
+    assert lib.ts_w8a16_glu_workspace_bytes(4, 8960, 1536, 1, 1, 256) == 0
+
+
 def test_zero_size_calls_are_no_ops():
     lib = N.lib()
     assert lib.ts_kv_write(None, None, 0, 0, 0, 0, None, None, 0, None, 0, 2, 64, None) == N.TS_OK

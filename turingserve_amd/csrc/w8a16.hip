@@ -48,13 +48,25 @@ __device__ __forceinline__ float load_scale(const void* scale, int scale_is_fp16
 // Optional extras of the logits entry point: activation row r of the product is
 // x[rows[r]] (clamped to [0, x_rows)) instead of x[r], and the result goes to the fp32 matrix yf
 // as the fp16-rounded value widened (what the reference's fp16 product followed by .float()
-// holds) instead of to the fp16 matrix y.
+// holds) instead of to the fp16 matrix y. glu = I > 0 selects the gated-MLP output of the
+// fused gate_up entry point: the weights are [gate; up] (N = 2I rows) and y[m][i] =
+// silu(Y[m][i]) * Y[m][I + i], an [M, I] matrix.
 struct GemmIo {
   const int64_t* rows;
   int64_t x_rows;
   float* yf;
   int64_t ldyf;
+  int glu;
 };
+
+// silu(gate) * up from the fp16 GEMM outputs, with the rounding points of the unfused pair
+// (the silu_mul kernel, ops/reference.py:40-42): SiLU in fp32 rounded to fp16, then the product
+// rounded to fp16.
+__device__ __forceinline__ half_t silu_mul_h(half_t g, half_t u) {
+  const float gf = (float)g;
+  const half_t sl = (half_t)(gf / (1.f + expf(-gf)));
+  return (half_t)((float)sl * (float)u);
+}
 
 __device__ __forceinline__ int64_t x_row(const GemmIo& io, int r) {
   if (!io.rows) return r;
@@ -108,11 +120,22 @@ __global__ void __launch_bounds__(kSmWaves * 64) w8a16_small_kernel(
   const int c = lane & 15, g = lane >> 4;
   const int n0 = (blockIdx.x * kSmWaves + w) * 16;
   const int ks = blockIdx.y;
-  if (n0 >= N) return;
+  // GLU mode (N = 2I): wavefronts 0, 1 take gate rows g0 + 16w .. + 15 and wavefronts 2, 3
+  // the matching up rows, so each gate value meets its up value in this workgroup. Every
+  // wavefront then stays to the end (the epilogue has a barrier); rows past I are clamped.
+  const int glu = io.glu;
+  const int g0 = blockIdx.x * (kSmWaves / 2) * 16;
+  auto weight_row = [&](int j) {                   // weight row of this wavefront's row j
+    if (glu) {
+      const int i = g0 + (w & 1) * 16 + j;
+      return (w >= kSmWaves / 2 ? glu : 0) + (i < glu ? i : glu - 1);
+    }
+    return n0 + j < N ? n0 + j : N - 1;
+  };
+  if (!glu && n0 >= N) return;
   const int kb = ks * k_per_split;
   const int ke = (kb + k_per_split < K) ? kb + k_per_split : K;
-  const int n = n0 + c;
-  const int8_t* wrow = wq + (int64_t)(n < N ? n : N - 1) * K;
+  const int8_t* wrow = wq + (int64_t)weight_row(c) * K;
   const half_t* xrow[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) {
@@ -173,8 +196,54 @@ __global__ void __launch_bounds__(kSmWaves * 64) w8a16_small_kernel(
     if (more2) load(k + 2 * SK, s0);
     if (more1) compute(k + SK, s1);
   }
-  // lane (c, g) holds Y[m = 16 mt + c][n0 + 4g + r]
-  const int nn = n0 + 4 * g;
+  // lane (c, g) holds Y[m = 16 mt + c][weight_row(4g + r)]
+  if (glu && !part) {
+    // Up wavefronts pass their fp16 results to the gate wavefronts through LDS, in register
+    // order; the values are formed exactly as the plain epilogue below forms them.
+    __shared__ half4_t s_xch[2][MT][64];
+    float sc[4], bs[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int nr = weight_row(4 * g + r);
+      sc[r] = load_scale(scale, scale_is_fp16, nr);
+      bs[r] = bias ? (float)bias[nr] : 0.f;
+    }
+    auto value = [&](int mt) {
+      const float v[4] = {acc[mt][0] * sc[0] + bs[0], acc[mt][1] * sc[1] + bs[1],
+                          acc[mt][2] * sc[2] + bs[2], acc[mt][3] * sc[3] + bs[3]};
+      return half4_t{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+    };
+    const int hw = w & 1;
+    if (w >= kSmWaves / 2) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) s_xch[hw][mt][lane] = value(mt);
+    }
+    __syncthreads();
+    if (w < kSmWaves / 2) {
+      const int col = g0 + hw * 16 + 4 * g;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int mm = mt * 16 + c;
+        if (mm >= M || col >= glu) continue;
+        const half4_t gv = value(mt), uv = s_xch[hw][mt][lane];
+        const half4_t o = {silu_mul_h(gv[0], uv[0]), silu_mul_h(gv[1], uv[1]),
+                           silu_mul_h(gv[2], uv[2]), silu_mul_h(gv[3], uv[3])};
+        half_t* dst = y + (int64_t)mm * ldy + col;
+        if (col + 3 < glu) {
+          st<half4_t>(dst, o);
+        } else {
+          for (int r = 0; r < 4; ++r)
+            if (col + r < glu) dst[r] = o[r];
+        }
+      }
+    }
+    return;
+  }
+  // GLU partials go to the weight row's column of the [M, 2I] product (valid while the gate
+  // index is below I); otherwise column n0 + 4g + r.
+  const int nn = glu ? weight_row(4 * g) : n0 + 4 * g;
+  const int nend = glu ? (w >= kSmWaves / 2 ? 2 * glu : glu) : N;
+  const bool run_ok = !glu || g0 + (w & 1) * 16 + 4 * g < glu;
   if (part == nullptr) {
     float sc[4], bs[4];
 #pragma unroll
@@ -196,16 +265,28 @@ __global__ void __launch_bounds__(kSmWaves * 64) w8a16_small_kernel(
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const int mm = mt * 16 + c;
-      if (mm >= M) continue;
+      if (mm >= M || !run_ok) continue;
       float* dst = pp + (int64_t)mm * N + nn;
-      if (nn + 3 < N) {
+      if (nn + 3 < nend) {
         st<float4_t>(dst, acc[mt]);
       } else {
         for (int r = 0; r < 4; ++r)
-          if (nn + r < N) dst[r] = acc[mt][r];
+          if (nn + r < nend) dst[r] = acc[mt][r];
       }
     }
   }
+}
+
+// Element i of the [M, N] product from its split-K partials: sum, scale, bias, fp16.
+__device__ __forceinline__ half_t reduce_partials(const float* __restrict__ part, int splits,
+                                                  int64_t total, int64_t i,
+                                                  const void* __restrict__ scale, int scale_is_fp16,
+                                                  const half_t* __restrict__ bias, int nn) {
+  float s = 0.f;
+  for (int k = 0; k < splits; ++k) s += part[(int64_t)k * total + i];
+  float v = s * load_scale(scale, scale_is_fp16, nn);
+  if (bias) v += (float)bias[nn];
+  return (half_t)v;
 }
 
 // Sum of the split-K partials, then scale, bias and fp16 conversion.
@@ -217,15 +298,26 @@ __global__ void __launch_bounds__(256) w8a16_reduce_kernel(
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
        i += (int64_t)gridDim.x * blockDim.x) {
     const int mm = (int)(i / N), nn = (int)(i % N);
-    float s = 0.f;
-    for (int k = 0; k < splits; ++k) s += part[(int64_t)k * total + i];
-    float v = s * load_scale(scale, scale_is_fp16, nn);
-    if (bias) v += (float)bias[nn];
-    const half_t hv = (half_t)v;
+    const half_t hv = reduce_partials(part, splits, total, i, scale, scale_is_fp16, bias, nn);
     if (io.yf)
       io.yf[(int64_t)mm * io.ldyf + nn] = (float)hv;
     else
       y[(int64_t)mm * ldy + nn] = hv;
+  }
+}
+
+// The gated-MLP form: partials of the [M, 2I] gate_up product in, y[m][i] = silu(gate) * up out.
+__global__ void __launch_bounds__(256) w8a16_glu_reduce_kernel(
+    const float* __restrict__ part, int splits, const void* __restrict__ scale, int scale_is_fp16,
+    const half_t* __restrict__ bias, half_t* __restrict__ y, int64_t ldy, int M, int I) {
+  const int64_t N = 2 * (int64_t)I, total = (int64_t)M * N, outs = (int64_t)M * I;
+  for (int64_t o = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; o < outs;
+       o += (int64_t)gridDim.x * blockDim.x) {
+    const int mm = (int)(o / I), ii = (int)(o % I);
+    const int64_t i = (int64_t)mm * N + ii;
+    const half_t g = reduce_partials(part, splits, total, i, scale, scale_is_fp16, bias, ii);
+    const half_t u = reduce_partials(part, splits, total, i + I, scale, scale_is_fp16, bias, I + ii);
+    y[(int64_t)mm * ldy + ii] = silu_mul_h(g, u);
   }
 }
 
@@ -321,8 +413,21 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r = lane & 31, h = lane >> 5;
   const int n_tile = blockIdx.x * BN;
-  const int n_wave = n_tile + w * 32 * WN;        // this wavefront's first weight row
   const int m_base = blockIdx.y * BM;
+  // Weight row of tile column nl (clamped into the matrix). In GLU mode the tile holds the gate
+  // rows g0 .. g0 + BN/2 - 1 in its first half (wavefronts 0, 1) and the matching up rows in
+  // its second half (wavefronts 2, 3), so each gate value and its up value meet in one workgroup.
+  const int glu = io.glu;
+  const int g0 = blockIdx.x * (BN / 2);
+  auto weight_row = [&](int nl) {
+    if (glu) {
+      const int i = g0 + nl % (BN / 2);
+      return (nl >= BN / 2 ? glu : 0) + (i < glu ? i : glu - 1);
+    }
+    const int n = n_tile + nl;
+    return n < N ? n : N - 1;
+  };
+  static_assert(WN == 1, "GLU mode pairs wavefronts 0, 1 with 2, 3 (32 rows each)");
   const int kb = blockIdx.z * k_per_split;
   const int ke = (kb + k_per_split < K) ? kb + k_per_split : K;
   const int nk = (ke - kb + BK - 1) / BK;
@@ -330,16 +435,13 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
   // Per-channel scale and bias of the tile, read once into LDS for the epilogue (published by
   // the barriers of the main loop, which runs at least once).
   if (tid < BN) {
-    const int nc = n_tile + tid < N ? n_tile + tid : N - 1;
+    const int nc = weight_row(tid);
     s_sc[tid] = part ? 1.f : load_scale(scale, scale_is_fp16, nc);
     s_bs[tid] = (part || !bias) ? 0.f : (float)bias[nc];
   }
   const int8_t* wrow[WN];
 #pragma unroll
-  for (int i = 0; i < WN; ++i) {
-    const int n = n_wave + 32 * i + r;
-    wrow[i] = wq + (int64_t)(n < N ? n : N - 1) * K + 32 * h;
-  }
+  for (int i = 0; i < WN; ++i) wrow[i] = wq + (int64_t)weight_row(w * 32 * WN + 32 * i + r) * K + 32 * h;
   // DMA i of thread t fills slot 256 i + t of a stage: row (256 i + t) / 8, position t % 8,
   // which holds chunk (t % 8) ^ (row & 7) = (t % 8) ^ ((t / 8) & 7) for every i.
   const int kcx = (tid % CH) ^ ((tid / CH) & 7);
@@ -483,14 +585,66 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
   // No DMA may still be writing this workgroup's LDS when it exits.
   wait_vmem_below<0>();
   // lane (h, r) of subtile (i, j), element e = 4a + c: Y[m][n] with m = m_base + 32 j + r and
-  // n = n_wave + 32 i + 8a + 4h + c; the four c are one 8-byte store.
+  // n = weight_row(32 WN w + 32 i + 8a + 4h + c); the four c are one 8-byte store.
+  if (glu && !part) {
+    // Every wavefront puts its fp16 results in LDS (gate values in stage 0, up values in stage
+    // 1, both idle now) in register order, slot ((half, j, a), lane); then wavefronts w and w + 2
+    // share column half w % 2, w < 2 finishing subtiles j < WM / 2 and w >= 2 the rest, each
+    // lane at the same (row, columns) its slot came from.
+    __syncthreads();                                  // every wavefront is done with the stages
+    half4_t* xg = reinterpret_cast<half4_t*>(s_x0);   // 2 halves x WM x 4 x 64 lanes x 8 B each
+    half4_t* xu = reinterpret_cast<half4_t*>(s_x1);
+    static_assert(sizeof(s_x0) == 2 * WM * 4 * 64 * sizeof(half4_t), "exchange fits one stage");
+    static_assert(WM % 2 == 0, "subtiles split between the two wavefronts of a half");
+    const int half_w = w & 1;
+    const bool is_up = w >= 2;
+#pragma unroll
+    for (int j = 0; j < WM; ++j)
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        const int nl = w * 32 + 8 * a4 + 4 * h;
+        const float4_t sc = *reinterpret_cast<const float4_t*>(&s_sc[nl]);
+        const float4_t bs = *reinterpret_cast<const float4_t*>(&s_bs[nl]);
+        const float o[4] = {acc[0][j][4 * a4] * sc[0] + bs[0], acc[0][j][4 * a4 + 1] * sc[1] + bs[1],
+                            acc[0][j][4 * a4 + 2] * sc[2] + bs[2], acc[0][j][4 * a4 + 3] * sc[3] + bs[3]};
+        const half4_t hv = {(half_t)o[0], (half_t)o[1], (half_t)o[2], (half_t)o[3]};
+        (is_up ? xu : xg)[((half_w * WM + j) * 4 + a4) * 64 + lane] = hv;
+      }
+    __syncthreads();
+#pragma unroll
+    for (int jj = 0; jj < WM / 2; ++jj) {
+      const int j = (is_up ? WM / 2 : 0) + jj;
+      const int mm = m_base + 32 * j + r;
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        const int col = g0 + 32 * half_w + 8 * a4 + 4 * h;
+        if (mm >= M || col >= glu) continue;
+        const int slot = ((half_w * WM + j) * 4 + a4) * 64 + lane;
+        const half4_t gv = xg[slot], uv = xu[slot];
+        const half4_t o = {silu_mul_h(gv[0], uv[0]), silu_mul_h(gv[1], uv[1]), silu_mul_h(gv[2], uv[2]),
+                           silu_mul_h(gv[3], uv[3])};
+        half_t* dst = y + (int64_t)mm * ldy + col;
+        if (col + 3 < glu) {
+          st<half4_t>(dst, o);
+        } else {
+          for (int c = 0; c < 4; ++c)
+            if (col + c < glu) dst[c] = o[c];
+        }
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < WN; ++i) {
 #pragma unroll
     for (int a4 = 0; a4 < 4; ++a4) {
       const int nl = w * 32 * WN + 32 * i + 8 * a4 + 4 * h;   // column within the tile
-      const int nn = n_tile + nl;
-      if (nn >= N) continue;
+      // GLU partials: column of the [M, 2I] product; the four columns are valid together or
+      // stop at I (the gate index of each half is what may run past the matrix)
+      const int gi = g0 + nl % (BN / 2);
+      const int nn = glu ? (nl >= BN / 2 ? glu : 0) + gi : n_tile + nl;
+      const int nend = glu ? nn - gi + glu : N;        // first column past this run
+      if (nn >= nend) continue;
       const float4_t sc = *reinterpret_cast<const float4_t*>(&s_sc[nl]);
       const float4_t bs = *reinterpret_cast<const float4_t*>(&s_bs[nl]);
 #pragma unroll
@@ -501,11 +655,11 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
                             acc[i][j][4 * a4 + 3]};
         if (part) {
           float* dst = part + ((int64_t)blockIdx.z * M + mm) * N + nn;
-          if (nn + 3 < N) {
+          if (nn + 3 < nend) {
             st<float4_t>(dst, v);
           } else {
             for (int c = 0; c < 4; ++c)
-              if (nn + c < N) dst[c] = v[c];
+              if (nn + c < nend) dst[c] = v[c];
           }
           continue;
         }
@@ -609,6 +763,7 @@ static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int split
 
 static GemmPlan plan_gemm(int M, int N, int K, int cus) { return plan_gemm_v(M, N, K, cus, kVarAuto, 0); }
 
+// fp32 partials [splits][M][N] of split-K (in GLU mode N = 2I).
 static size_t gemm_workspace(const GemmPlan& p, int M, int N) {
   return p.splits > 1 ? (size_t)p.splits * M * N * sizeof(float) : 0;
 }
@@ -643,13 +798,26 @@ static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const v
   int st = device_cu_count(&cus);
   if (st != TS_OK) return st;
   const GemmPlan p = plan_gemm_v(M, N, K, cus, variant, splits);
+  const bool glu = io.glu > 0;                    // N = 2 * io.glu, y is [M, io.glu]
   const size_t need = gemm_workspace(p, M, N);
   TS_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
              TS_ERR_WORKSPACE, "w8a16: workspace of %zu bytes needed, got %zu", need,
              workspace_bytes);
+  auto reduce = [&](float* part) {
+    if (glu) {
+      const int64_t want = ((int64_t)M * io.glu + 255) / 256;
+      w8a16_glu_reduce_kernel<<<(int)(want < 4096 ? want : 4096), 256, 0, s>>>(
+          part, p.splits, scale, scale_is_fp16, bp, yp, ldy, M, io.glu);
+    } else {
+      const int64_t want = ((int64_t)M * N + 255) / 256;
+      w8a16_reduce_kernel<<<(int)(want < 4096 ? want : 4096), 256, 0, s>>>(
+          part, p.splits, scale, scale_is_fp16, bp, yp, ldy, M, N, io);
+    }
+  };
   if (p.small) {
     float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
-    const dim3 grid((N + 16 * kSmWaves - 1) / (16 * kSmWaves), p.splits);
+    const int rows_per_wg = glu ? 16 * kSmWaves / 2 : 16 * kSmWaves;   // GLU: gate columns
+    const dim3 grid(((glu ? io.glu : N) + rows_per_wg - 1) / rows_per_wg, p.splits);
     const bool wide = K % 16 == 0 && aligned(wq, 16);
 #define TS_SM_CASE(MTV)                                                                          \
   case MTV:                                                                                      \
@@ -665,15 +833,11 @@ static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const v
       TS_SM_CASE(2)
     }
 #undef TS_SM_CASE
-    if (p.splits > 1) {
-      const int64_t total = (int64_t)M * N;
-      const int64_t want = (total + 255) / 256;
-      w8a16_reduce_kernel<<<(int)(want < 4096 ? want : 4096), 256, 0, s>>>(
-          part, p.splits, scale, scale_is_fp16, bp, yp, ldy, M, N, io);
-    }
+    if (part) reduce(part);
   } else {
     float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
-    const dim3 grid((N + p.bn - 1) / p.bn, (M + p.bm - 1) / p.bm, p.splits);
+    const int tiles_n = glu ? (io.glu + p.bn / 2 - 1) / (p.bn / 2) : (N + p.bn - 1) / p.bn;
+    const dim3 grid(tiles_n, (M + p.bm - 1) / p.bm, p.splits);
     const bool fast = K % kTileBK == 0 && aligned(wq, 16);   // 16-byte weight loads, no K tail
 #define TS_WIDE_LAUNCH(WNV, WMV)                                                                   \
   if (fast)                                                                                        \
@@ -688,12 +852,7 @@ static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const v
       TS_WIDE_LAUNCH(1, 2);
     }
 #undef TS_WIDE_LAUNCH
-    if (p.splits > 1) {
-      const int64_t total = (int64_t)M * N;
-      const int64_t want = (total + 255) / 256;
-      w8a16_reduce_kernel<<<(int)(want < 4096 ? want : 4096), 256, 0, s>>>(
-          part, p.splits, scale, scale_is_fp16, bp, yp, ldy, M, N, io);
-    }
+    if (part) reduce(part);
   }
   return TS_OK;
 }
@@ -714,7 +873,7 @@ static int w8a16_gemm_checked(const void* x, int64_t ldx, const int8_t* wq, cons
              TS_ERR_INVALID_ARG, "w8a16: x must be 16-byte aligned rows (ldx %% 8 == 0), wq 8-byte aligned");
   TS_REQUIRE(!(ldy % 4) && aligned(y, 8), TS_ERR_INVALID_ARG,
              "w8a16: y rows must be 8-byte aligned (ldy %% 4 == 0)");
-  const GemmIo io{nullptr, 0, nullptr, 0};
+  const GemmIo io{nullptr, 0, nullptr, 0, 0};
   const int st = w8a16_launch(static_cast<const half_t*>(x), ldx, wq, scale, scale_is_fp16,
                               static_cast<const half_t*>(bias), static_cast<half_t*>(y), ldy, M,
                               N, K, workspace, workspace_bytes,
@@ -761,11 +920,43 @@ extern "C" int ts_logits_int8(const void* hidden, int64_t hidden_stride, int64_t
              TS_ERR_INVALID_ARG, "logits_int8: hidden must be 16-byte aligned rows, wq 8-byte aligned");
   TS_REQUIRE(logits_stride >= vocab && logits_stride % 4 == 0 && aligned(logits, 16),
              TS_ERR_INVALID_ARG, "logits_int8: logits rows must be 16-byte aligned (stride %% 4 == 0)");
-  const GemmIo io{sample_indices, hidden_rows, logits, logits_stride};
+  const GemmIo io{sample_indices, hidden_rows, logits, logits_stride, 0};
   const int st = w8a16_launch(static_cast<const half_t*>(hidden), hidden_stride, wq, scale,
                               scale_is_fp16, nullptr, nullptr, 0, num_samples, vocab, hidden_size,
                               workspace, workspace_bytes, reinterpret_cast<hipStream_t>(stream), io,
                               kVarAuto, 0);
   if (st != TS_OK) return st;
   return check_launch("logits_int8");
+}
+
+extern "C" size_t ts_w8a16_glu_workspace_bytes(int32_t M, int32_t intermediate, int32_t K,
+                                               int32_t variant, int32_t splits, int32_t cu_count) {
+  if (M <= 0 || intermediate <= 0 || K <= 0 || !variant_valid(variant, splits, M)) return 0;
+  const int N = 2 * intermediate;
+  return gemm_workspace(plan_gemm_v(M, N, K, cu_count > 0 ? cu_count : 256, variant, splits), M,
+                        N);
+}
+
+extern "C" int ts_w8a16_glu(const void* x, int64_t ldx, const int8_t* wq, const void* scale,
+                            int32_t scale_is_fp16, const void* bias, void* out, int64_t ldo,
+                            int32_t M, int32_t intermediate, int32_t K, int32_t variant,
+                            int32_t splits, void* workspace, size_t workspace_bytes, void* stream) {
+  TS_REQUIRE(M >= 0 && intermediate > 0 && intermediate <= (1 << 29) && K > 0, TS_ERR_INVALID_ARG,
+             "w8a16_glu: bad shape M=%d I=%d K=%d", M, intermediate, K);
+  TS_REQUIRE(variant_valid(variant, splits, M < 1 ? 1 : M), TS_ERR_UNSUPPORTED,
+             "w8a16_glu: variant %d with %d splits is not available for M=%d", variant, splits, M);
+  if (M == 0) return TS_OK;
+  TS_REQUIRE(x && wq && scale && out, TS_ERR_INVALID_ARG, "w8a16_glu: null pointer argument");
+  TS_REQUIRE(K % 8 == 0, TS_ERR_UNSUPPORTED, "w8a16_glu: K=%d is not a multiple of 8", K);
+  TS_REQUIRE(ldx >= K && ldx % 8 == 0 && aligned(x, 16) && aligned(wq, 8), TS_ERR_INVALID_ARG,
+             "w8a16_glu: x must be 16-byte aligned rows (ldx %% 8 == 0), wq 8-byte aligned");
+  TS_REQUIRE(ldo >= intermediate && !(ldo % 4) && aligned(out, 8), TS_ERR_INVALID_ARG,
+             "w8a16_glu: out rows must be 8-byte aligned (ldo %% 4 == 0)");
+  const GemmIo io{nullptr, 0, nullptr, 0, intermediate};
+  const int st = w8a16_launch(static_cast<const half_t*>(x), ldx, wq, scale, scale_is_fp16,
+                              static_cast<const half_t*>(bias), static_cast<half_t*>(out), ldo, M,
+                              2 * intermediate, K, workspace, workspace_bytes,
+                              reinterpret_cast<hipStream_t>(stream), io, variant, splits);
+  if (st != TS_OK) return st;
+  return check_launch("w8a16_glu");
 }

@@ -23,7 +23,8 @@ from turingserve_amd.quant import LinearWeight
 
 __all__ = ["kv_write", "paged_attention", "linear", "lm_head_int8", "logits_int8", "w8a16_linear",
            "decode_attention_v1", "decode_attention_v2", "decode_attention_v3",
-           "prefill_attention", "rmsnorm", "rmsnorm_residual", "rope_", "silu_mul"]
+           "prefill_attention", "rmsnorm", "rmsnorm_residual", "rope_", "silu_mul", "w8a16_glu",
+           "gate_up_silu"]
 
 DEFAULT_PARTITION = 0            # v3 split size when the caller names none: 0 = balanced
 
@@ -252,6 +253,52 @@ def w8a16_linear(x: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor,
                                     y.stride(0), M, Nn, K, variant, splits, _ptr(ws), ws_bytes,
                                     _stream(x)), "w8a16_gemm_v")
     return y
+
+
+def w8a16_glu(x: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor,
+               bias: torch.Tensor | None = None, cfg=None) -> torch.Tensor:
+    """silu(gate) * up of the fused gate_up W8A16 linear in one library call: wq int8 [2I, K] =
+    [gate; up], out fp16 [M, I]. Equal, bit for bit, to silu_mul(w8a16_linear(x, wq, scale,
+    bias, cfg)) (model/qwen2.py:35-36 with ops/triton_silu_mul.py:21-28): the product is planned
+    for the [M, 2I] shape, so the same split and tile choice applies, and the [M, 2I]
+    intermediate is never written. cfg as for w8a16_linear (the table entry of the gate_up
+    shape)."""
+    x = x.contiguous()
+    M, K = x.shape
+    Nn, Kw = wq.shape
+    _require(Kw == K, f"w8a16_glu: x has K={K}, weight has K={Kw}")
+    _require(Nn % 2 == 0, "w8a16_glu: weight must hold [gate; up] (an even number of rows)")
+    _require(x.dtype == torch.float16, "w8a16_glu: activations must be fp16")
+    _require(wq.dtype == torch.int8 and wq.is_contiguous(), "w8a16_glu: weight must be int8 row-major")
+    _require(scale.dtype in (torch.float32, torch.float16) and scale.numel() == Nn,
+             "w8a16_glu: scale must be fp32 or fp16 [2I]")
+    inter = Nn // 2
+    out = torch.empty(M, inter, dtype=x.dtype, device=x.device)
+    if M == 0:
+        return out
+    _check_gpu(x, wq, scale)
+    sc = scale.contiguous()
+    b = None
+    if bias is not None:
+        _require(bias.numel() == Nn, "w8a16_glu: bias must be [2I]")
+        b = bias.to(torch.float16).contiguous()
+    cus = N.cu_count(x.device.index or 0)
+    variant, splits = tuner.w8a16_choice(Nn, K, M) if cfg is None else (int(cfg[0]), int(cfg[1]))
+    ws_bytes = N.lib().ts_w8a16_glu_workspace_bytes(M, inter, K, variant, splits, cus)
+    ws = _workspace(ws_bytes, x.device)
+    N.check(N.lib().ts_w8a16_glu(_ptr(x), x.stride(0), _ptr(wq), _ptr(sc),
+                                 1 if sc.dtype == torch.float16 else 0, _ptr(b), _ptr(out),
+                                 out.stride(0), M, inter, K, variant, splits, _ptr(ws), ws_bytes,
+                                 _stream(x)), "w8a16_glu")
+    return out
+
+
+def gate_up_silu(x: torch.Tensor, lw: LinearWeight) -> torch.Tensor:
+    """silu_mul(linear(x, gate_up)) (model/qwen2.py:36): one fused call for int8 weights, the
+    two calls otherwise."""
+    if not lw.quantized:
+        return silu_mul(F.linear(x, lw.w, lw.b))
+    return w8a16_glu(x, lw.w, lw.scale, lw.b)
 
 
 def linear(x: torch.Tensor, lw: LinearWeight) -> torch.Tensor:

@@ -37,6 +37,7 @@ def _hip() -> SimpleNamespace:
     ns.rmsnorm_residual = h.rmsnorm_residual
     ns.rope_ = h.rope_
     ns.silu_mul = h.silu_mul
+    ns.gate_up_silu = h.gate_up_silu
     return ns
 
 

@@ -143,7 +143,10 @@ class Qwen2Model:
         return q, k, v
 
     def _mlp(self, x, lw):
-        return self.ops.linear(self.ops.silu_mul(self.ops.linear(x, lw.gu)), lw.down)
+        gate_up_silu = getattr(self.ops, "gate_up_silu", None)       # fused on the hip backend
+        act = (gate_up_silu(x, lw.gu) if gate_up_silu is not None
+               else self.ops.silu_mul(self.ops.linear(x, lw.gu)))
+        return self.ops.linear(act, lw.down)
 
     @torch.inference_mode()
     def forward(self, input_ids, positions, meta, kv_cache):
