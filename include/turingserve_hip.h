@@ -19,6 +19,7 @@
  *                             the decode-graph padding of runner/cuda_graphs.py:62-78
  *   ts_rmsnorm             <- ops/triton_rmsnorm.py:30-46   (twins ops/reference.py:13-23)
  *   ts_rope                <- ops/triton_rope.py:27-31      (twin ops/reference.py:31-42)
+ *   ts_rope_kv_write       <- rope then kv_write of one layer, fused (model/qwen2.py:26-28, :89)
  *   ts_silu_mul            <- ops/triton_silu_mul.py:21-28  (twin ops/reference.py:26-28)
  *                             (twin ops/reference.py:45-47 + quant/int8.py:15-16)
  *
@@ -265,6 +266,21 @@ int ts_rmsnorm(const void* x, int64_t x_stride, const void* residual, int64_t re
 int ts_rope(void* qkv, int64_t qkv_stride, const int64_t* positions, const float* cos_table,
             const float* sin_table, int64_t max_position, int64_t num_tokens, int32_t num_heads,
             int32_t num_kv_heads, int32_t head_dim, void* stream);
+
+/*
+ * ts_rope followed by ts_kv_write of the rotated k heads and the v heads of the same qkv rows,
+ * in one pass over each row (the per-layer sequence rope -> kv_write of model/qwen2.py:26-28
+ * and :89, ops/triton_rope.py:27-31 then ops/triton_kv_write.py:28-35): the q and k heads of
+ * qkv [T, (H + 2 KVH) D] are rotated in place, and for slot_mapping[t] in [0, num_blocks * 16)
+ * k_cache / v_cache [num_blocks, KVH, 16, D] receive row t's rotated k and its v at that slot.
+ * The same bits as the two calls. qkv rows, caches and tables 16-byte aligned (qkv_stride a
+ * multiple of 8); head_dim a multiple of 8.
+ */
+int ts_rope_kv_write(void* qkv, int64_t qkv_stride, const int64_t* positions,
+                     const float* cos_table, const float* sin_table, int64_t max_position,
+                     int64_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
+                     int32_t head_dim, void* k_cache, void* v_cache, int64_t num_blocks,
+                     const int64_t* slot_mapping, void* stream);
 
 /*
  * out[t, i] = fp16(fp16(silu(g)) * u) for gu[t] = [g (intermediate) | u (intermediate)], silu in

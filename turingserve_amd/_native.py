@@ -64,6 +64,8 @@ SIGNATURES = {
     "ts_rmsnorm": (ctypes.c_int, [_p, _i64, _p, _i64, _p, _p, _i64, _p, _i64, _i64, _i32, _f32,
                                   _p]),
     "ts_rope": (ctypes.c_int, [_p, _i64, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _p]),
+    "ts_rope_kv_write": (ctypes.c_int, [_p, _i64, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _p,
+                                        _p, _i64, _p, _p]),
     "ts_silu_mul": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _i32, _p]),
 }
 

@@ -72,14 +72,29 @@ __global__ void __launch_bounds__(kRowThreads) rmsnorm_kernel(
   }
 }
 
+// Rotate-half RoPE of 4 consecutive frequency indices: x1 from the first half of the head, x2
+// from the second, c4 / s4 the fp32 table entries.
+__device__ __forceinline__ void rope4(half4_t x1, half4_t x2, float4_t c4, float4_t s4,
+                                      half4_t& o1, half4_t& o2) {
+  // Each product must round to fp16 before the sum, as in the twin: no fused multiply-add.
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    // fp16 x fp16 products are exact in fp32, so each rounds once to fp16, as the twin's
+    // fp16 multiplies do; the sum of two fp16 values then rounds once more.
+    const float c = (float)(half_t)c4[e], s = (float)(half_t)s4[e];
+    const float a = (float)x1[e], b = (float)x2[e];
+    o1[e] = (half_t)((float)(half_t)(a * c) - (float)(half_t)(b * s));
+    o2[e] = (half_t)((float)(half_t)(b * c) + (float)(half_t)(a * s));
+  }
+}
+
 // One workgroup per token; the (H + KVH) rotated heads of the row are covered by 256 threads,
 // each owning 4 consecutive frequency indices of one head (8-byte accesses of both halves).
 __global__ void __launch_bounds__(kRowThreads) rope_kernel(
     half_t* __restrict__ qkv, int64_t qkv_st, const int64_t* __restrict__ positions,
     const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t max_pos,
     int heads, int D) {
-  // Each product must round to fp16 before the sum, as in the twin: no fused multiply-add.
-#pragma clang fp contract(off)
   const int64_t t = blockIdx.x;
   const int half_d = D / 2, per_head = half_d / 4;
   int64_t pos = positions[t];
@@ -89,22 +104,54 @@ __global__ void __launch_bounds__(kRowThreads) rope_kernel(
   for (int u = threadIdx.x; u < heads * per_head; u += kRowThreads) {
     const int h = u / per_head, i = (u % per_head) * 4;
     half_t* base = qkv + t * qkv_st + (int64_t)h * D;
-    const half4_t x1 = ld<half4_t>(base + i);
-    const half4_t x2 = ld<half4_t>(base + half_d + i);
-    const float4_t c4 = ld<float4_t>(cp + i);
-    const float4_t s4 = ld<float4_t>(sp + i);
     half4_t o1, o2;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      // fp16 x fp16 products are exact in fp32, so each rounds once to fp16, as the twin's
-      // fp16 multiplies do; the sum of two fp16 values then rounds once more.
-      const float c = (float)(half_t)c4[e], s = (float)(half_t)s4[e];
-      const float a = (float)x1[e], b = (float)x2[e];
-      o1[e] = (half_t)((float)(half_t)(a * c) - (float)(half_t)(b * s));
-      o2[e] = (half_t)((float)(half_t)(b * c) + (float)(half_t)(a * s));
-    }
+    rope4(ld<half4_t>(base + i), ld<half4_t>(base + half_d + i), ld<float4_t>(cp + i),
+          ld<float4_t>(sp + i), o1, o2);
     st<half4_t>(base + i, o1);
     st<half4_t>(base + half_d + i, o2);
+  }
+}
+
+// RoPE and the cache write of one token row in one pass: the q and k heads are rotated in
+// place as rope_kernel does, and when the token's slot lies in the cache the rotated k heads
+// and the v heads are also written to K / V cache slot (block slot / 16, row slot % 16), as
+// kv_write_kernel copies them. The row is read once and the rotated k is never re-read.
+__global__ void __launch_bounds__(kRowThreads) rope_kv_write_kernel(
+    half_t* __restrict__ qkv, int64_t qkv_st, const int64_t* __restrict__ positions,
+    const float* __restrict__ cos_t, const float* __restrict__ sin_t, int64_t max_pos, int H,
+    int KVH, int D, half_t* __restrict__ kc, half_t* __restrict__ vc, int64_t num_slots,
+    const int64_t* __restrict__ slots) {
+  const int64_t t = blockIdx.x;
+  const int half_d = D / 2, per_head = half_d / 4;
+  int64_t pos = positions[t];
+  pos = pos < 0 ? 0 : (pos >= max_pos ? max_pos - 1 : pos);
+  const float* cp = cos_t + pos * half_d;
+  const float* sp = sin_t + pos * half_d;
+  const int64_t slot = slots[t];
+  const bool cached = slot >= 0 && slot < num_slots;            // -1 = padding row
+  const int64_t cache_row = ((slot >> 4) * KVH * kBlockSize + (slot & 15)) * D;  // + head * 16 D
+  half_t* row = qkv + t * qkv_st;
+  for (int u = threadIdx.x; u < (H + KVH) * per_head; u += kRowThreads) {
+    const int h = u / per_head, i = (u % per_head) * 4;
+    half_t* base = row + (int64_t)h * D;
+    half4_t o1, o2;
+    rope4(ld<half4_t>(base + i), ld<half4_t>(base + half_d + i), ld<float4_t>(cp + i),
+          ld<float4_t>(sp + i), o1, o2);
+    st<half4_t>(base + i, o1);
+    st<half4_t>(base + half_d + i, o2);
+    if (h >= H && cached) {
+      half_t* dst = kc + cache_row + (int64_t)(h - H) * kBlockSize * D;
+      st<half4_t>(dst + i, o1);
+      st<half4_t>(dst + half_d + i, o2);
+    }
+  }
+  if (!cached) return;
+  const int pieces = D / kRowVec;
+  const half_t* vrow = row + (int64_t)(H + KVH) * D;
+  for (int u = threadIdx.x; u < KVH * pieces; u += kRowThreads) {
+    const int kh = u / pieces, p = (u % pieces) * kRowVec;
+    st<half8_t>(vc + cache_row + (int64_t)kh * kBlockSize * D + p,
+                ld<half8_t>(vrow + (int64_t)kh * D + p));
   }
 }
 
@@ -181,6 +228,33 @@ extern "C" int ts_rope(void* qkv, int64_t qkv_stride, const int64_t* positions,
       static_cast<half_t*>(qkv), qkv_stride, positions, cos_table, sin_table, max_position,
       num_heads + num_kv_heads, head_dim);
   return check_launch("rope");
+}
+
+extern "C" int ts_rope_kv_write(void* qkv, int64_t qkv_stride, const int64_t* positions,
+                                const float* cos_table, const float* sin_table,
+                                int64_t max_position, int64_t num_tokens, int32_t num_heads,
+                                int32_t num_kv_heads, int32_t head_dim, void* k_cache,
+                                void* v_cache, int64_t num_blocks, const int64_t* slot_mapping,
+                                void* stream) {
+  TS_REQUIRE(num_tokens >= 0, TS_ERR_INVALID_ARG, "rope_kv_write: num_tokens %lld < 0",
+             (long long)num_tokens);
+  if (num_tokens == 0) return TS_OK;
+  TS_REQUIRE(qkv && positions && cos_table && sin_table && max_position > 0 && k_cache &&
+                 v_cache && slot_mapping && num_blocks > 0,
+             TS_ERR_INVALID_ARG, "rope_kv_write: null pointer, empty table or empty cache");
+  TS_REQUIRE(num_heads > 0 && num_kv_heads > 0, TS_ERR_INVALID_ARG, "rope_kv_write: bad head counts");
+  TS_REQUIRE(head_dim % 8 == 0 && head_dim >= 8, TS_ERR_UNSUPPORTED,
+             "rope_kv_write: head_dim %d must be a multiple of 8", head_dim);
+  TS_REQUIRE(qkv_stride >= (int64_t)(num_heads + 2 * num_kv_heads) * head_dim &&
+                 qkv_stride % 8 == 0 && aligned(qkv, 16) && aligned(k_cache, 16) &&
+                 aligned(v_cache, 16) && aligned(cos_table, 16) && aligned(sin_table, 16),
+             TS_ERR_INVALID_ARG, "rope_kv_write: qkv rows, caches and tables must be 16-byte aligned");
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  rope_kv_write_kernel<<<dim3((unsigned)num_tokens), kRowThreads, 0, s>>>(
+      static_cast<half_t*>(qkv), qkv_stride, positions, cos_table, sin_table, max_position,
+      num_heads, num_kv_heads, head_dim, static_cast<half_t*>(k_cache),
+      static_cast<half_t*>(v_cache), num_blocks * kBlockSize, slot_mapping);
+  return check_launch("rope_kv_write");
 }
 
 extern "C" int ts_silu_mul(const void* gu, int64_t gu_stride, void* out, int64_t out_stride,

@@ -24,7 +24,7 @@ from turingserve_amd.quant import LinearWeight
 __all__ = ["kv_write", "paged_attention", "linear", "lm_head_int8", "logits_int8", "w8a16_linear",
            "decode_attention_v1", "decode_attention_v2", "decode_attention_v3",
            "prefill_attention", "rmsnorm", "rmsnorm_residual", "rope_", "silu_mul", "w8a16_glu",
-           "gate_up_silu"]
+           "gate_up_silu", "rope_kv_write_"]
 
 DEFAULT_PARTITION = 0            # v3 split size when the caller names none: 0 = balanced
 
@@ -399,6 +399,37 @@ def rope_(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor, sin: to
         else positions.to(torch.int64).contiguous()
     N.check(N.lib().ts_rope(_ptr(qkv), qkv.stride(0), _ptr(pos), _ptr(cos), _ptr(sin),
                             cos.shape[0], T, H, KVH, D, _stream(qkv)), "rope")
+
+
+def rope_kv_write_(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor,
+                   sin: torch.Tensor, H: int, KVH: int, D: int, k_cache: torch.Tensor,
+                   v_cache: torch.Tensor, slot_mapping: torch.Tensor) -> bool:
+    """rope_(qkv, ...) then kv_write(k, v, k_cache, v_cache, slot_mapping) of qkv's k and v
+    heads, in one pass over each token row (ops/triton_rope.py:27-31 then
+    ops/triton_kv_write.py:28-35); the same bits as the two calls. Returns False, having done
+    nothing, when qkv's layout does not allow the fused pass (rows not 16-byte aligned): the
+    caller then makes the two calls."""
+    _check_gpu(qkv, positions, cos, sin, k_cache, v_cache, slot_mapping)
+    T = qkv.shape[0]
+    if not (qkv.dim() == 2 and qkv.stride(1) == 1 and qkv.stride(0) % 8 == 0 and
+            qkv.data_ptr() % 16 == 0 and k_cache.is_contiguous() and v_cache.is_contiguous()):
+        return False
+    _require(qkv.dtype == torch.float16 and qkv.shape[1] >= (H + 2 * KVH) * D,
+             "rope_kv_write: qkv must be fp16 [T, (H + 2 KVH) D]")
+    NB, ckvh, cd = _check_cache(k_cache, v_cache)
+    _require(ckvh == KVH and cd == D, "rope_kv_write: cache shape mismatch")
+    _require(cos.dtype == torch.float32 and sin.dtype == torch.float32 and cos.is_contiguous()
+             and sin.is_contiguous() and cos.shape == sin.shape and cos.shape[-1] == D // 2,
+             "rope_kv_write: tables must be contiguous fp32 [max_len, D / 2]")
+    _require(slot_mapping.shape[0] >= T, "rope_kv_write: slot_mapping shorter than qkv")
+    pos = positions if (positions.dtype == torch.int64 and positions.is_contiguous()) \
+        else positions.to(torch.int64).contiguous()
+    slots = slot_mapping if (slot_mapping.dtype == torch.int64 and slot_mapping.is_contiguous()) \
+        else slot_mapping.to(torch.int64).contiguous()
+    N.check(N.lib().ts_rope_kv_write(_ptr(qkv), qkv.stride(0), _ptr(pos), _ptr(cos), _ptr(sin),
+                                     cos.shape[0], T, H, KVH, D, _ptr(k_cache), _ptr(v_cache),
+                                     NB, _ptr(slots), _stream(qkv)), "rope_kv_write")
+    return True
 
 
 def silu_mul(gu: torch.Tensor) -> torch.Tensor:

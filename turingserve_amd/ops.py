@@ -38,6 +38,7 @@ def _hip() -> SimpleNamespace:
     ns.rope_ = h.rope_
     ns.silu_mul = h.silu_mul
     ns.gate_up_silu = h.gate_up_silu
+    ns.rope_kv_write_ = h.rope_kv_write_
     return ns
 
 

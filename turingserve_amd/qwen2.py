@@ -131,15 +131,24 @@ class Qwen2Model:
         self.rotary = RotaryCache(cfg.head_dim, cfg.rope_theta,
                                   max_model_len or cfg.max_position_embeddings, device)
 
-    def _qkv(self, x, lw, positions):
+    def _qkv(self, x, lw, positions, k_cache, v_cache, slot_mapping):
+        """q, k, v views of the rotated qkv activation, with the new K / V rows already in the
+        layer's cache (model/qwen2.py:26-28 and :89: rope, then kv_write). A backend with
+        rope_kv_write_ rotates and writes them in one pass."""
         c = self.cfg
         qkv = self.ops.linear(x, lw.qkv)
-        self.ops.rope_(qkv, positions, self.rotary.cos, self.rotary.sin, c.num_heads,
-                       c.num_kv_heads, c.head_dim)
+        fused = getattr(self.ops, "rope_kv_write_", None)
+        args = (qkv, positions, self.rotary.cos, self.rotary.sin, c.num_heads, c.num_kv_heads,
+                c.head_dim)
+        written = fused is not None and fused(*args, k_cache, v_cache, slot_mapping)
+        if not written:
+            self.ops.rope_(*args)
         T, H, KVH, D = qkv.shape[0], c.num_heads, c.num_kv_heads, c.head_dim
         q = qkv[:, : H * D].view(T, H, D)
         k = qkv[:, H * D:(H + KVH) * D].view(T, KVH, D)
         v = qkv[:, (H + KVH) * D:].view(T, KVH, D)
+        if not written:
+            self.ops.kv_write(k, v, k_cache, v_cache, slot_mapping)
         return q, k, v
 
     def _mlp(self, x, lw):
@@ -161,9 +170,8 @@ class Qwen2Model:
                 x = ops.rmsnorm(h, lw.w_in, c.rms_norm_eps)
             else:
                 x, residual = ops.rmsnorm_residual(h, residual, lw.w_in, c.rms_norm_eps)
-            q, k, v = self._qkv(x, lw, positions)
             k_cache, v_cache = kv_cache[layer, 0], kv_cache[layer, 1]
-            ops.kv_write(k, v, k_cache, v_cache, meta.slot_mapping)
+            q, _, _ = self._qkv(x, lw, positions, k_cache, v_cache, meta.slot_mapping)
             a = ops.paged_attention(q, k_cache, v_cache, meta, self.scale)
             h = ops.linear(a, lw.o)
             x, residual = ops.rmsnorm_residual(h, residual, lw.w_post, c.rms_norm_eps)
