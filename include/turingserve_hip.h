@@ -8,6 +8,7 @@
  *   ts_decode_attention    <- ops/triton_ops.py:35-57 (_decode) and
  *                             ops/triton_decode_attention.py:169-200 (v1 / v2 / v3 launchers)
  *   ts_prefill_attention   <- ops/triton_prefill_attention.py:66-79
+ *   ts_prefill_attention_ws   (the same with split key ranges, + ts_prefill_workspace_bytes)
  *   ts_paged_attention     <- ops/triton_ops.py:60-71        (twin ops/reference.py:94-111)
  *   ts_w8a16_gemm          <- ops/triton_w8a16.py:38-51 and ops/triton_ops.py:74-91
  *   ts_w8a16_gemm_v        <- the same with the tuned per-bucket config (autopilot/tuner.py)
@@ -118,6 +119,7 @@ int ts_decode_attention(int32_t version,
  * absolute position prefix + i, prefix = seq_lens[b] - q_len; it attends to keys
  * j <= prefix + i (bottom-right causal mask) read through block_tables[b].
  * num_tokens bounds every q / out row the kernel touches.
+ * Without a workspace every 128-row query tile runs as one workgroup.
  * Replaces ops/triton_prefill_attention.py:66-79.
  */
 int ts_prefill_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
@@ -130,8 +132,30 @@ int ts_prefill_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                          float scale, void* stream);
 
 /*
+ * The same with a workspace of ts_prefill_workspace_bytes() bytes (16-byte aligned): at
+ * head_dim 128 the key range of a long query tile is then split over several workgroups whose
+ * fp32 partials a merge kernel combines, so short chunks on long prefixes still fill the
+ * device. max_seq_len: a host-side upper bound of the prefill sequences' seq_lens. A smaller
+ * workspace (or none) runs the tiles unsplit. Same results up to fp32 summation order.
+ * Replaces ops/triton_prefill_attention.py:66-79 (the launch grid of :72-79).
+ */
+size_t ts_prefill_workspace_bytes(int32_t num_prefill, int32_t num_heads, int32_t head_dim,
+                                  int32_t max_query_len, int32_t max_seq_len, int32_t cu_count);
+int ts_prefill_attention_ws(const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                            void* out, int64_t out_stride_t, int64_t num_tokens,
+                            const void* k_cache, const void* v_cache, int64_t num_blocks,
+                            const int32_t* block_tables, int64_t bt_stride,
+                            int32_t max_blocks_per_seq, const int32_t* seq_lens,
+                            const int32_t* query_start_loc, int32_t num_seqs, int32_t num_decode,
+                            int32_t max_query_len, int32_t max_seq_len, int32_t num_heads,
+                            int32_t num_kv_heads, int32_t head_dim, float scale,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * paged_attention: decode kernel on rows [0, num_decode), prefill kernel on the remaining
- * sequences; one call per layer. Workspace as ts_decode_workspace_bytes(TS_DECODE_AUTO, ...).
+ * sequences; one call per layer. The two run one after the other on `stream` and share the
+ * workspace: the larger of ts_decode_workspace_bytes(decode_version, ...) and
+ * ts_prefill_workspace_bytes(num_seqs - num_decode, ...) bytes.
  * Replaces ops/triton_ops.py:60-71.
  */
 int ts_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,

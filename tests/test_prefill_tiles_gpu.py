@@ -1,0 +1,124 @@
+"""The LDS-tiled prefill path (head_dim 128) against the oracle (needs an MI355X).
+
+128-row query tiles share each staged 64-key step; long key ranges are split over several
+workgroups whose fp32 partials a merge kernel combines (ts_prefill_attention_ws). Both forms
+are checked against the oracle (ops/reference.py:60-77, 94-111) with the attention criterion of
+the other kernel tests, on shapes that put the diagonal, the key tail and the split boundaries in
+every position of a step; a NaN-filled workspace and NaN cache rows past seq_len must not reach
+the output.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+import pytest
+import torch
+
+from turingserve_amd import _native as N
+from turingserve_amd import hip_ops as K
+from turingserve_amd import synth
+
+from .test_kernels_gpu import DEV, assert_attn, make_paged, meta_of, oracle_attn
+
+pytestmark = pytest.mark.gpu
+H, KVH, D = 12, 2, 128
+
+
+def run_prefill(q, kc, vc, qsl, sl, bt, meta, ws: torch.Tensor | None, ws_bytes: int | None = None):
+    out = torch.full((q.shape[0], H * D), float("nan"), dtype=torch.float16, device=DEV)
+    B = sl.shape[0]
+    common = (q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), out.stride(0), q.shape[0],
+              kc.data_ptr(), vc.data_ptr(), kc.shape[0], bt.data_ptr(), bt.stride(0), bt.shape[1],
+              sl.data_ptr(), qsl.data_ptr(), B, meta.num_decode, int(meta.max_query_len))
+    stream = torch.cuda.current_stream().cuda_stream
+    if ws is None:
+        N.check(N.lib().ts_prefill_attention(*common, H, KVH, D, D ** -0.5, stream), "prefill")
+    else:
+        nb = ws.numel() if ws_bytes is None else ws_bytes
+        N.check(N.lib().ts_prefill_attention_ws(*common, int(meta.max_seq_len), H, KVH, D,
+                                                D ** -0.5, ws.data_ptr(), nb, stream), "prefill")
+    torch.cuda.synchronize()
+    return out
+
+
+def setup(q_lens, prefixes, seed=0):
+    seq = [p + n for p, n in zip(prefixes, q_lens)]
+    q, kc, vc, qsl, sl, bt = make_paged(seq, H, KVH, D, list(q_lens), seed=seed)
+    meta = meta_of(qsl, sl, bt, 0, list(q_lens), q.shape[0])
+    dev = [x.to(DEV) for x in (q, kc, vc, qsl, sl, bt)]
+    ref = oracle_attn(q, kc, vc, qsl, sl, bt, D ** -0.5)
+    return dev, meta, ref
+
+
+def ws_bytes_for(meta, P):
+    return N.lib().ts_prefill_workspace_bytes(P, H, D, int(meta.max_query_len),
+                                              int(meta.max_seq_len), N.cu_count(0))
+
+
+@pytest.mark.parametrize("q_lens,prefixes", [
+    ([1], [0]), ([63], [1]), ([128], [0]), ([129], [63]), ([200], [64]), ([512], [1037]),
+    ([700], [3000]), ([2048], [0]), ([17], [4000]), ([5, 300, 128], [0, 900, 2500]),
+])
+def test_tiled_prefill_split_and_unsplit(q_lens, prefixes):
+    (q, kc, vc, qsl, sl, bt), meta, ref = setup(q_lens, prefixes)
+    out1 = run_prefill(q, kc, vc, qsl, sl, bt, meta, None)
+    assert_attn(out1, ref, "unsplit")
+    nb = ws_bytes_for(meta, len(q_lens))
+    ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=DEV)
+    out2 = run_prefill(q, kc, vc, qsl, sl, bt, meta, ws)
+    assert_attn(out2, ref, "split")
+
+
+def test_tiled_prefill_splits_when_it_should():
+    """A short chunk on a long prefix gets a split plan (the case the split path is for), and a
+    workspace one byte short runs unsplit with the same result quality."""
+    (q, kc, vc, qsl, sl, bt), meta, ref = setup([512], [1037], seed=3)
+    nb = ws_bytes_for(meta, 1)
+    assert nb > 0
+    ws = torch.empty(nb, dtype=torch.uint8, device=DEV)
+    assert_attn(run_prefill(q, kc, vc, qsl, sl, bt, meta, ws, nb - 1), ref, "short workspace")
+    assert_attn(run_prefill(q, kc, vc, qsl, sl, bt, meta, ws, nb), ref, "split")
+
+
+def test_tiled_prefill_stale_nan_workspace():
+    """Partials of empty splits and rows past q_len are never read: a NaN-filled workspace
+    gives the same result."""
+    (q, kc, vc, qsl, sl, bt), meta, ref = setup([300, 40], [1900, 333], seed=4)
+    nb = ws_bytes_for(meta, 2)
+    ws = torch.full((nb // 4 + 1,), float("nan"), dtype=torch.float32, device=DEV)
+    out = run_prefill(q, kc, vc, qsl, sl, bt, meta, ws.view(torch.uint8), nb)
+    assert_attn(out, ref, "nan workspace")
+
+
+def test_tiled_prefill_nan_beyond_seq_len():
+    """Cache rows past seq_len inside the last block hold NaN (a reused block): masked keys
+    and zeroed V rows keep them out of the output."""
+    q_lens, prefixes = [77], [250]           # seq_len 327: last block half used
+    (q, kc, vc, qsl, sl, bt), meta, ref = setup(q_lens, prefixes, seed=6)
+    seq = prefixes[0] + q_lens[0]
+    last = int(bt[0, (seq - 1) // 16])
+    kc[last, :, seq % 16:] = float("nan")
+    vc[last, :, seq % 16:] = float("nan")
+    out1 = run_prefill(q, kc, vc, qsl, sl, bt, meta, None)
+    assert_attn(out1, ref, "nan tail unsplit")
+    ws = torch.empty(max(ws_bytes_for(meta, 1), 16), dtype=torch.uint8, device=DEV)
+    assert_attn(run_prefill(q, kc, vc, qsl, sl, bt, meta, ws), ref, "nan tail split")
+
+
+def test_tiled_prefill_chunked_prompt_through_paged_attention():
+    """A 3000-token prompt in 1024-token chunks (the shape of config 3, shortened so the oracle
+    stays quick): each chunk's K/V written first, then paged_attention over the cache so far."""
+    for ci, (prefix, n) in enumerate(synth.config3_chunks(prompt=3000, chunk=1024)):
+        st = synth.config3(ci, seed=0, prompt=3000, chunk=1024)
+        kc, vc = st.k_cache.to(DEV), st.v_cache.to(DEV)
+        qkv = st.qkv.to(DEV)
+        q, k, v = st.views(qkv)
+        meta = st.meta(DEV)
+        K.kv_write(k, v, kc, vc, meta.slot_mapping)
+        out = K.paged_attention(q, kc, vc, meta, st.D ** -0.5)
+        qn = q.float().cpu().half().numpy()
+        ref = oracle_attn(torch.from_numpy(qn), kc.cpu(), vc.cpu(), meta.query_start_loc.cpu(),
+                          meta.seq_lens.cpu(), meta.block_tables.cpu(), st.D ** -0.5)
+        assert_attn(out, ref, f"chunk {ci} (prefix {prefix}, {n} rows)")

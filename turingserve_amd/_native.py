@@ -44,6 +44,10 @@ SIGNATURES = {
     "ts_prefill_attention": (ctypes.c_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _i64,
                                             _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
                                             _f32, _p]),
+    "ts_prefill_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "ts_prefill_attention_ws": (ctypes.c_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p,
+                                               _i64, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32,
+                                               _i32, _i32, _f32, _p, _sz, _p]),
     "ts_paged_attention": (ctypes.c_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _i64,
                                           _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
                                           _f32, _i32, _i32, _p, _sz, _p]),

@@ -79,11 +79,13 @@ extern "C" int ts_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
     if (st != TS_OK) return st;
   }
   if (num_seqs > num_decode) {
-    int st = ts_prefill_attention(q, q_stride_t, q_stride_h, out, out_stride_t, num_tokens,
-                                  k_cache, v_cache, num_blocks, block_tables, bt_stride,
-                                  max_blocks_per_seq, seq_lens, query_start_loc, num_seqs,
-                                  num_decode, max_query_len, num_heads, num_kv_heads, head_dim,
-                                  scale, stream);
+    // Stream-ordered after the decode kernels, so the prefill reuses the same workspace.
+    int st = ts_prefill_attention_ws(q, q_stride_t, q_stride_h, out, out_stride_t, num_tokens,
+                                     k_cache, v_cache, num_blocks, block_tables, bt_stride,
+                                     max_blocks_per_seq, seq_lens, query_start_loc, num_seqs,
+                                     num_decode, max_query_len, max_seq_len, num_heads,
+                                     num_kv_heads, head_dim, scale, workspace, workspace_bytes,
+                                     stream);
     if (st != TS_OK) return st;
   }
   return TS_OK;

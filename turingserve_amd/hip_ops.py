@@ -160,11 +160,21 @@ def prefill_attention(q, out, k_cache, v_cache, meta, scale, block_m: int = 64,
     _require(qd == D and q.stride(2) == 1 and q.dtype == torch.float16,
              "prefill: q must be fp16 [T, H, D] with unit stride over D")
     bt, sl, qsl = _i32(meta.block_tables), _i32(meta.seq_lens), _i32(meta.query_start_loc)
-    N.check(N.lib().ts_prefill_attention(
+    ws_bytes = _prefill_ws_bytes(B - meta.num_decode, H, D, meta, q.device)
+    ws = _workspace(ws_bytes, q.device)
+    N.check(N.lib().ts_prefill_attention_ws(
         _ptr(q), q.stride(0), q.stride(1), _ptr(out), out.stride(0), T, _ptr(k_cache),
         _ptr(v_cache), NB, _ptr(bt), bt.stride(0), bt.shape[1], _ptr(sl), _ptr(qsl), B,
-        meta.num_decode, int(meta.max_query_len), H, KVH, D, float(scale), _stream(q)),
-        "prefill_attention")
+        meta.num_decode, int(meta.max_query_len), int(meta.max_seq_len), H, KVH, D,
+        float(scale), _ptr(ws), ws_bytes, _stream(q)), "prefill_attention")
+
+
+def _prefill_ws_bytes(P: int, H: int, D: int, meta, device) -> int:
+    """Workspace of the split prefill path (0 when the batch has no prefill rows)."""
+    if P <= 0:
+        return 0
+    return N.lib().ts_prefill_workspace_bytes(P, H, D, int(meta.max_query_len),
+                                              int(meta.max_seq_len), N.cu_count(device.index or 0))
 
 
 # ------------------------------------------------------------------------------------------
@@ -201,6 +211,8 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
         cus = N.cu_count(q.device.index or 0)
         ws_bytes = N.lib().ts_decode_workspace_bytes(code, S, H, KVH, D, meta.max_seq_len,
                                                      partition, cus)
+    # the prefill kernels run after the decode kernels on the same stream and reuse the buffer
+    ws_bytes = max(ws_bytes, _prefill_ws_bytes(B - S, H, D, meta, q.device))
     ws = _workspace(ws_bytes, q.device)
     N.check(N.lib().ts_paged_attention(
         _ptr(q), q.stride(0), q.stride(1), _ptr(out), out.stride(0), T, _ptr(k_cache),
