@@ -10,6 +10,7 @@
  *   ts_prefill_attention   <- ops/triton_prefill_attention.py:66-79
  *   ts_prefill_attention_ws   (the same with split key ranges, + ts_prefill_workspace_bytes)
  *   ts_paged_attention     <- ops/triton_ops.py:60-71        (twin ops/reference.py:94-111)
+ *                             (+ ts_paged_attention_workspace_bytes)
  *   ts_w8a16_gemm          <- ops/triton_w8a16.py:38-51 and ops/triton_ops.py:74-91
  *   ts_w8a16_gemm_v        <- the same with the tuned per-bucket config (autopilot/tuner.py)
  *   ts_w8a16_glu           <- model/qwen2.py:35-36, silu_mul(linear(x, gate_up)) fused
@@ -152,19 +153,31 @@ int ts_prefill_attention_ws(const void* q, int64_t q_stride_t, int64_t q_stride_
                             void* workspace, size_t workspace_bytes, void* stream);
 
 /*
- * paged_attention: decode kernel on rows [0, num_decode), prefill kernel on the remaining
- * sequences; one call per layer. The two run one after the other on `stream` and share the
- * workspace: the larger of ts_decode_workspace_bytes(decode_version, ...) and
- * ts_prefill_workspace_bytes(num_seqs - num_decode, ...) bytes.
+ * paged_attention: decode attention on rows [0, num_decode), chunked-prefill attention on the
+ * remaining sequences; one call per layer. With a workspace of
+ * ts_paged_attention_workspace_bytes() bytes (256-byte aligned), head_dim 128, the automatic
+ * (or v3) decode policy with partition 0 and both kinds of rows present, the two run in ONE
+ * launch (prefill tiles and decode splits side by side) followed by one merge launch;
+ * otherwise they run one after the other on `stream`, sharing the workspace (then the larger
+ * of ts_decode_workspace_bytes() and ts_prefill_workspace_bytes() suffices). Same results
+ * either way, up to fp32 summation order. max_seq_len bounds every seq_len (decode policy);
+ * max_prefill_seq_len bounds the prefill rows' seq_lens (the prefill split plan; 0 = use
+ * max_seq_len).
  * Replaces ops/triton_ops.py:60-71.
  */
+size_t ts_paged_attention_workspace_bytes(int32_t num_seqs, int32_t num_decode,
+                                          int32_t max_query_len, int32_t max_seq_len,
+                                          int32_t max_prefill_seq_len, int32_t num_heads,
+                                          int32_t num_kv_heads, int32_t head_dim,
+                                          int32_t decode_version, int32_t partition,
+                                          int32_t cu_count);
 int ts_paged_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,
                        void* out, int64_t out_stride_t, int64_t num_tokens,
                        const void* k_cache, const void* v_cache, int64_t num_blocks,
                        const int32_t* block_tables, int64_t bt_stride, int32_t max_blocks_per_seq,
                        const int32_t* seq_lens, const int32_t* query_start_loc,
                        int32_t num_seqs, int32_t num_decode, int32_t max_query_len,
-                       int32_t max_seq_len,
+                       int32_t max_seq_len, int32_t max_prefill_seq_len,
                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                        float scale, int32_t decode_version, int32_t partition,
                        void* workspace, size_t workspace_bytes, void* stream);

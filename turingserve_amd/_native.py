@@ -48,9 +48,11 @@ SIGNATURES = {
     "ts_prefill_attention_ws": (ctypes.c_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p,
                                                _i64, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32,
                                                _i32, _i32, _f32, _p, _sz, _p]),
+    "ts_paged_attention_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
+                                                  _i32, _i32, _i32]),
     "ts_paged_attention": (ctypes.c_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _i64,
                                           _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _i32,
-                                          _f32, _i32, _i32, _p, _sz, _p]),
+                                          _i32, _f32, _i32, _i32, _p, _sz, _p]),
     "ts_w8a16_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "ts_w8a16_gemm": (ctypes.c_int, [_p, _i64, _p, _p, _i32, _p, _p, _i64, _i32, _i32, _i32, _p,
                                      _sz, _p]),

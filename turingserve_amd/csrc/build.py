@@ -20,7 +20,8 @@ PKG = os.path.dirname(HERE)
 LIB_DIR = os.path.join(PKG, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libturingserve_hip.so")
 BUILD_DIR = os.path.join(HERE, "_build")
-SOURCES = ["capi.hip", "kv_write.hip", "decode.hip", "prefill.hip", "w8a16.hip", "small_ops.hip",
+SOURCES = ["capi.hip", "kv_write.hip", "decode.hip", "prefill.hip", "ragged.hip", "w8a16.hip",
+           "small_ops.hip",
            "metadata.hip"]
 ARCH = "gfx950"
 
@@ -37,6 +38,7 @@ COMMON_FLAGS = [
 SOURCE_FLAGS = {
     "decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
     "prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+    "ragged.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
 }
 
 

@@ -1,0 +1,668 @@
+// Paged decode attention for gfx950: the v1 / v2 / v3 family of
+// ops/triton_decode_attention.py:1-200 with the policy of ops/triton_ops.py:35-57.
+//
+//  v1  one wavefront per (sequence, query head); VALU dot products and 64-lane shuffles.
+//      Reads every KV block once per query head; kept as the simple, any-group-size variant.
+//  v2  one workgroup per (sequence, KV head, group of <= 16 query heads): the whole GQA group
+//      shares each 16-token K/V block, which is read from HBM exactly once per KV head.
+//  v3  v2 split over context partitions of `partition` tokens ("flash-decoding"): partials
+//      (m, l, acc) in fp32 go to the workspace and a merge kernel combines them (sequences
+//      that fit one split are finished by the first kernel).
+//
+// Inner loop of v2/v3 (one wavefront, a pair of 16-token blocks; lane l = 16 g + c):
+//   S^T[16 tok][16 heads] = K[16 tok][D] . Q^T[D][16 heads]       v_mfma_f32_16x16x32_f16
+//   K lane (c, g) loads K[tok c][32kk + 8g .. +7]: 16-byte loads, 64 contiguous bytes per token
+//   per instruction; Q^T uses the same dim permutation, so no shuffles are needed.
+//   The result leaves lane (c, g) holding tokens 4g..4g+3 of head c: every per-head softmax
+//   statistic (running max m, sum l, rescale alpha) lives in lane column c.
+//   V rows are loaded coalesced (lane (c, g): tokens 4g..4g+3, dims 8c..8c+7 at D = 128) and
+//   tile t of O^T takes dims {8i + t}, so each lane's token-packed operand is two byte
+//   permutes of what it loaded: O^T[D][16 heads] += V^T . P^T runs on v_mfma_f32_16x16x32_f16
+//   over both blocks of the pair with no transpose; P is rounded to fp16 first, exactly like
+//   ops/triton_decode_attention.py:91. Afterwards lane (c, g) owns dims 32g .. 32g+31 of head c.
+// The waves of a workgroup take consecutive blocks and merge their (m, l, acc) in LDS.
+#pragma once
+
+#include <math.h>
+
+#include <type_traits>
+
+#include "common.h"
+#include "paged_kv.h"
+namespace ts {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ------------------------------------------------------------------------------------------
+// v1 (ops/triton_decode_attention.py:23-54)
+// ------------------------------------------------------------------------------------------
+template <int D>
+__global__ void __launch_bounds__(64) decode_v1_kernel(
+    const half_t* __restrict__ q, int64_t q_st, int64_t q_sh, half_t* __restrict__ out,
+    int64_t o_st, const half_t* __restrict__ kc, const half_t* __restrict__ vc, int64_t NB,
+    const int* __restrict__ bt, int64_t bt_st, int max_blocks, const int* __restrict__ seq_lens,
+    int H, int KVH, float scale_log2) {
+  constexpr int DQ = D / 4;                    // dims per lane: 4 lanes share one token row
+  const int s = blockIdx.x, h = blockIdx.y;
+  const int G = H / KVH, kvh = h / G;
+  const int lane = threadIdx.x, tok = lane >> 2, part = lane & 3;
+  int seq_len = seq_lens[s];
+  seq_len = seq_len < 0 ? 0 : (seq_len > max_blocks * kBlockSize ? max_blocks * kBlockSize : seq_len);
+  float qv[DQ], acc[DQ];
+  const half_t* qp = q + (int64_t)s * q_st + (int64_t)h * q_sh + part * DQ;
+#pragma unroll
+  for (int d = 0; d < DQ; ++d) {
+    qv[d] = (float)qp[d];
+    acc[d] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  const int nblk = (seq_len + kBlockSize - 1) / kBlockSize;
+  for (int i = 0; i < nblk; ++i) {
+    const int phys = clamp_block(bt[(int64_t)s * bt_st + i], NB);
+    const int64_t row = (((int64_t)phys * KVH + kvh) * kBlockSize + tok) * D + part * DQ;
+    float sc = 0.f;
+#pragma unroll
+    for (int d = 0; d < DQ; ++d) sc += qv[d] * (float)kc[row + d];
+    sc += shfl_xor(sc, 1);
+    sc += shfl_xor(sc, 2);
+    const bool valid = i * kBlockSize + tok < seq_len;
+    sc = valid ? sc * scale_log2 : -INFINITY;
+    float bm = sc;
+    bm = fmaxf(bm, shfl_xor(bm, 4));
+    bm = fmaxf(bm, shfl_xor(bm, 8));
+    bm = fmaxf(bm, shfl_xor(bm, 16));
+    bm = fmaxf(bm, shfl_xor(bm, 32));
+    const float m_new = fmaxf(m, bm);          // finite: token 0 of the block is valid
+    const float alpha = fast_exp2(m - m_new);
+    const float p = valid ? fast_exp2(sc - m_new) : 0.f;
+    float ps = p;                              // sum over the 16 tokens (lanes of equal part)
+    ps += shfl_xor(ps, 4);
+    ps += shfl_xor(ps, 8);
+    ps += shfl_xor(ps, 16);
+    ps += shfl_xor(ps, 32);
+    l = l * alpha + ps;
+#pragma unroll
+    for (int d = 0; d < DQ; ++d) acc[d] = acc[d] * alpha + (valid ? p * (float)vc[row + d] : 0.f);
+    m = m_new;
+  }
+#pragma unroll
+  for (int d = 0; d < DQ; ++d) {
+    float a = acc[d];
+    a += shfl_xor(a, 4);
+    a += shfl_xor(a, 8);
+    a += shfl_xor(a, 16);
+    a += shfl_xor(a, 32);
+    acc[d] = a;
+  }
+  const float inv = 1.f / (l == 0.f ? 1.f : l);   // seq_len 0 -> zeros
+  if (tok == 0) {
+    half_t* op = out + (int64_t)s * o_st + (int64_t)h * D + part * DQ;
+#pragma unroll
+    for (int d = 0; d < DQ; ++d) op[d] = (half_t)(acc[d] * inv);
+  }
+}
+
+// ------------------------------------------------------------------------------------------
+// v2 / v3 (ops/triton_decode_attention.py:60-163)
+// ------------------------------------------------------------------------------------------
+// Dense split map of v3. Sequence s has nb_s = ceil(len_s / 16) blocks (len_s clamped to
+// cap_blocks * 16) cut into n_s = ceil(nb_s / P_s) splits of P_s blocks; the splits of the batch
+// are numbered densely in sequence order (split j of sequence s is launch slot C_s + j with
+// C_s = sum_{t<s} n_t), so the launch carries no idle workgroups. With a caller partition,
+// P_s = partition. With part_blocks == 0 (the balanced schedule) P = ceil(TB / nx) for the
+// batch's total TB blocks, rounded up to a multiple of kMinPartBlocks (one pair per wavefront,
+// so every wavefront of a full split gets the same number of pairs), and a sequence longer than
+// max_splits * P uses P_s = the multiple of kMinPartBlocks that keeps n_s <= max_splits. Either
+// way sum_s n_s <= nx + S and n_s <= max_splits, and every workgroup gets about the same work.
+// Split j of sequence s leaves its partial in workspace row s * max_splits + j, so the merge
+// can request a sequence's partials without knowing the other sequences' lengths.
+constexpr int kMinPartBlocks = 8;
+constexpr int kBalancedMaxSplits = 32;
+
+struct SplitSlot {
+  int seq;     // sequence owning the slot (-1: the slot is past the batch's last split)
+  int first;   // C_s
+  int count;   // n_s
+  int part;    // P_s in blocks
+  int len;     // clamped seq_len
+};
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ int wave_inclusive_sum(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < kWave; d <<= 1) {
+    const int t = __shfl_up(v, d, kWave);
+    if (lane >= d) v += t;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int round_part(int blocks) {
+  return (blocks + kMinPartBlocks - 1) / kMinPartBlocks * kMinPartBlocks;
+}
+
+// Called by every thread of an NT-thread workgroup (S >= 1): finds the sequence that owns
+// launch slot `slot`. s_map holds NT / 64 + 5 ints of LDS.
+template <int NT>
+__device__ SplitSlot split_lookup(const int* __restrict__ seq_lens, int S, int cap_blocks,
+                                  int part_blocks, int nx, int max_splits, int slot,
+                                  int* s_map) {
+  constexpr int NWV = NT / kWave;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  const int cap = cap_blocks * kBlockSize;
+  auto clamp_len = [&](int len) { return len < 0 ? 0 : (len > cap ? cap : len); };
+  const int len0 = tid < S ? clamp_len(seq_lens[tid]) : 0;
+  const bool balanced = part_blocks <= 0;
+  int P = part_blocks;
+  if (balanced) {
+    int tb = (len0 + kBlockSize - 1) / kBlockSize;
+    for (int i = tid + NT; i < S; i += NT) tb += (clamp_len(seq_lens[i]) + kBlockSize - 1) / kBlockSize;
+    tb = wave_sum(tb);
+    if (lane == 0) s_map[w] = tb;
+    __syncthreads();
+    int total = 0;
+#pragma unroll
+    for (int k = 0; k < NWV; ++k) total += s_map[k];
+    P = round_part((total + nx - 1) / nx);
+    P = P > kMinPartBlocks ? P : kMinPartBlocks;
+    __syncthreads();
+  }
+  auto part_of = [&](int nb) {
+    if (!balanced) return P;
+    const int q = round_part((nb + max_splits - 1) / max_splits);
+    return q > P ? q : P;
+  };
+  if (tid == 0) {
+    s_map[NWV] = -1;
+    s_map[NWV + 1] = 0;
+    s_map[NWV + 2] = 0;
+    s_map[NWV + 3] = 0;
+    s_map[NWV + 4] = P;
+  }
+  int base = 0;
+  for (int c0 = 0; c0 < S; c0 += NT) {
+    const int i = c0 + tid;
+    const int len = c0 == 0 ? len0 : (i < S ? clamp_len(seq_lens[i]) : 0);
+    const int nb = (len + kBlockSize - 1) / kBlockSize;
+    const int ps = part_of(nb);
+    const int n = (nb + ps - 1) / ps;
+    const int incl = wave_inclusive_sum(n, lane);
+    if (lane == kWave - 1) s_map[w] = incl;
+    __syncthreads();
+    int off = base, tot = 0;
+#pragma unroll
+    for (int k = 0; k < NWV; ++k) {
+      const int v = s_map[k];
+      off += k < w ? v : 0;
+      tot += v;
+    }
+    const int excl = off + incl - n;
+    if (i < S && n > 0 && slot >= excl && slot < excl + n) {
+      s_map[NWV] = i;
+      s_map[NWV + 1] = excl;
+      s_map[NWV + 2] = n;
+      s_map[NWV + 3] = len;
+      s_map[NWV + 4] = ps;
+    }
+    base += tot;
+    __syncthreads();
+  }
+  return {__builtin_amdgcn_readfirstlane(s_map[NWV]), __builtin_amdgcn_readfirstlane(s_map[NWV + 1]),
+          __builtin_amdgcn_readfirstlane(s_map[NWV + 2]), __builtin_amdgcn_readfirstlane(s_map[NWV + 4]),
+          __builtin_amdgcn_readfirstlane(s_map[NWV + 3])};
+}
+
+// One workgroup = NW wavefronts = one (split slot, KV head, head group) in v3 or one (sequence,
+// KV head, head group) in v2 (ws_acc == nullptr). The blocks of the range are consumed in pairs,
+// pair p by wavefront p % NW: two S^T chains, one online-softmax step per 32 tokens and the P.V
+// product as v_mfma_f32_16x16x32_f16 over the pair. Each wavefront keeps the next pair's loads in
+// flight while it multiplies the current one; block-table entries are wave-uniform scalar loads
+// issued a pair further ahead, so they never wait behind the K/V vector loads. The wavefronts
+// merge their (m, l, acc) in LDS; a sequence with one split writes its output here, otherwise
+// the split's partial goes to the workspace for decode_merge_kernel.
+// LDS of one decode workgroup: per-wavefront O^T rows, m and l, and the split lookup's scratch.
+template <int D, int NW>
+struct DecodeLds {
+  static constexpr int OROW = D + 4;
+  static constexpr int M = NW * 16 * OROW * 4;
+  static constexpr int L = M + NW * 16 * 4;
+  static constexpr int MAP = L + NW * 16 * 4;
+  static constexpr int BYTES = MAP + (NW + 5) * 4;
+};
+
+template <int D, int NW>
+__device__ __forceinline__ void decode_mfma_body(
+    const half_t* __restrict__ q, int64_t q_st, int64_t q_sh, half_t* __restrict__ out,
+    int64_t o_st, const half_t* __restrict__ kc, const half_t* __restrict__ vc, int64_t NB,
+    const int* __restrict__ bt, int64_t bt_st, int max_blocks, const int* __restrict__ seq_lens,
+    int S, int H, int KVH, int G, int HG, float sl2, int cap_blocks, int part_blocks, int nx,
+    int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
+    float* __restrict__ ws_l, int* __restrict__ ws_cnt,
+    int bx, int bz, char* __restrict__ lds) {
+  constexpr int KK = KvRegs<D>::KK;
+  constexpr int VW = KvRegs<D>::VW;
+  constexpr int TILES = KvRegs<D>::TILES;
+  constexpr int OROW = D + 4;                    // padded LDS row (floats) against bank conflicts
+  typedef typename HalfVec<VW>::type VRow;
+  float (*s_o)[16][OROW] = reinterpret_cast<float (*)[16][OROW]>(lds);
+  float (*s_m)[16] = reinterpret_cast<float (*)[16]>(lds + DecodeLds<D, NW>::M);
+  float (*s_l)[16] = reinterpret_cast<float (*)[16]>(lds + DecodeLds<D, NW>::L);
+  int* s_map = reinterpret_cast<int*>(lds + DecodeLds<D, NW>::MAP);
+
+  const int kvh = bz / HG, hg = bz % HG;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15, g = lane >> 4;
+  const int hq = hg * 16 + c;                    // query head within the GQA group
+  const bool head_ok = hq < G;
+  const int nh = (G - hg * 16) < 16 ? (G - hg * 16) : 16;   // real heads in this group
+  const int head0 = kvh * G + hg * 16;           // first query head of this group
+  const bool split = ws_acc != nullptr;
+
+  int s, seq_len, blk_lo, blk_hi, nsplit, split_j = 0;
+  if (split) {
+    const SplitSlot sp = split_lookup<NW * 64>(seq_lens, S, cap_blocks, part_blocks, nx,
+                                               max_splits, bx, s_map);
+    if (sp.seq < 0) return;                      // slot past the batch's last split
+    s = sp.seq;
+    seq_len = sp.len;
+    nsplit = sp.count;
+    split_j = bx - sp.first;
+    if (split_j == 0 && tid == 0) ws_cnt[s] = nsplit;   // read by the merge kernel
+    const int nblk = (seq_len + kBlockSize - 1) / kBlockSize;
+    blk_lo = split_j * sp.part;
+    blk_hi = (blk_lo + sp.part) < nblk ? (blk_lo + sp.part) : nblk;
+  } else {
+    s = bx;
+    seq_len = seq_lens[s];
+    seq_len = seq_len < 0 ? 0 : (seq_len > max_blocks * kBlockSize ? max_blocks * kBlockSize : seq_len);
+    seq_len = __builtin_amdgcn_readfirstlane(seq_len);
+    nsplit = 1;
+    blk_lo = 0;
+    blk_hi = (seq_len + kBlockSize - 1) / kBlockSize;
+    if (seq_len == 0) {                          // padding row: zeros (ops/reference.py:99,104-105)
+      for (int e = tid; e < nh * D; e += NW * 64)
+        out[(int64_t)s * o_st + (int64_t)(head0 + e / D) * D + e % D] = (half_t)0.f;
+      return;
+    }
+  }
+  // Tokens this range may use: a pair's second block can lie past the range (it then repeats
+  // the range's last block, a cache hit) while its tokens are still below seq_len.
+  const int tok_hi = blk_hi * kBlockSize < seq_len ? blk_hi * kBlockSize : seq_len;
+  const int npairs = (blk_hi - blk_lo + 1) >> 1;
+  const int* btrow = bt + (int64_t)s * bt_st;
+  auto blk_id = [&](int p, int j) {
+    int bi = blk_lo + 2 * p + j;
+    bi = bi < blk_hi ? bi : blk_hi - 1;
+    return clamp_block(btrow[bi], NB);
+  };
+
+  half8_t qf[KK];
+  {
+    const half_t* qp = q + (int64_t)s * q_st + (int64_t)(kvh * G + hq) * q_sh;
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      if constexpr (D >= 32) {
+        qf[kk] = head_ok ? ld<half8_t>(qp + 32 * kk + 8 * g) : half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+      } else {
+        const half4_t t = head_ok ? ld<half4_t>(qp + 4 * g) : half4_t{0, 0, 0, 0};
+        qf[kk] = {t[0], t[1], t[2], t[3], 0, 0, 0, 0};
+      }
+    }
+  }
+  const float4_t zero4 = {0.f, 0.f, 0.f, 0.f};
+  float4_t o[TILES];
+#pragma unroll
+  for (int t = 0; t < TILES; ++t) o[t] = zero4;
+  float m = -INFINITY, l = 0.f;
+
+  const int64_t head_off = (int64_t)kvh * kBlockSize * D;
+  const int64_t blk_stride = (int64_t)KVH * kBlockSize * D;
+  // Register budget per wavefront: K of one pair (refilled for the next pair as soon as the
+  // S^T MFMAs have consumed it) and V of two pairs (the next pair's V is requested a whole
+  // iteration before its P.V product). At D = 128 this keeps the kernel at two wavefronts per
+  // SIMD; the remaining latency is hidden by the other resident wavefronts. The refills are
+  // unconditional (past a wavefront's last pair they repeat its current pair, a cache hit) so
+  // every iteration has the same loads in flight and each wait covers exactly what it needs.
+  // Block-table entries are scalar loads issued two pairs ahead.
+  auto load_k = [&](const int (&id)[2], half8_t (&kf)[2][KK]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) load_k_block<D>(kc + id[j] * blk_stride + head_off, c, g, kf[j]);
+  };
+  auto load_v = [&](const int (&id)[2], VRow (&vr)[2][4]) {
+#pragma unroll
+    for (int j = 0; j < 2; ++j) load_v_rows<D>(vc + id[j] * blk_stride + head_off, c, g, vr[j]);
+  };
+  auto ids_of = [&](int pp, int (&id)[2]) {
+    id[0] = blk_id(pp, 0);
+    id[1] = blk_id(pp, 1);
+  };
+  half8_t kf[2][KK];
+  VRow vA[2][4], vB[2][4];
+  int idk[2] = {0, 0}, idv[2] = {0, 0};        // next K refill / next V refill (two pairs on)
+  auto last_or = [&](int pp, int fallback) { return pp < npairs ? pp : fallback; };
+  // Pair p: S^T from kf, refill kf with pair p + NW, softmax, P.V from vr, refill vr with pair
+  // p + 2 NW.
+  auto step = [&](int p, VRow (&vr)[2][4]) {
+    int idk_next[2], idv_next[2];
+    ids_of(last_or(p + 2 * NW, last_or(p + NW, p)), idk_next);
+    ids_of(last_or(p + 3 * NW, last_or(p + 2 * NW, last_or(p + NW, p))), idv_next);
+    const int ba = blk_lo + 2 * p;
+    const int ta = ba * kBlockSize + 4 * g, tb = ta + kBlockSize;
+    float4_t sa = zero4, sb = zero4;             // S^T = K . Q^T: two independent MFMA chains
+#pragma unroll
+    for (int kk = 0; kk < KK; ++kk) {
+      if constexpr (D >= 32) {
+        sa = mfma16x16x32(kf[0][kk], qf[kk], sa);
+        sb = mfma16x16x32(kf[1][kk], qf[kk], sb);
+      } else {
+        sa = mfma16x16x16(lo4(kf[0][kk]), lo4(qf[kk]), sa);
+        sb = mfma16x16x16(lo4(kf[1][kk]), lo4(qf[kk]), sb);
+      }
+    }
+    load_k(idk, kf);
+    // Only the last pair of a range can reach past tok_hi (token 0 of block a never does), so
+    // the masked form is a separate, rarely taken path and the common one carries no selects.
+    auto finish = [&](auto masked) {
+      constexpr bool kMasked = decltype(masked)::value;
+      const bool tail_a = kMasked && (ba + 1) * kBlockSize > tok_hi;
+      if constexpr (kMasked) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          sa[r] = ta + r < tok_hi ? sa[r] : -INFINITY;
+          sb[r] = tb + r < tok_hi ? sb[r] : -INFINITY;
+        }
+      }
+      const SoftmaxStep st = softmax_pair(sa, sb, sl2, m, l);
+      // lane (c, g) of tile t: dims VW (4g + r) + t of head c
+      pv_update<TILES>(o, st, [&](int t) {
+        return vt_operand<VW>(vr[0], vr[1], t, tail_a, kMasked, ta, tb, tok_hi);
+      });
+    };
+    if ((ba + 2) * kBlockSize > tok_hi)
+      finish(std::true_type());
+    else
+      finish(std::false_type());
+    load_v(idv, vr);
+    idk[0] = idk_next[0];
+    idk[1] = idk_next[1];
+    idv[0] = idv_next[0];
+    idv[1] = idv_next[1];
+  };
+  int p = w;
+  if (p < npairs) {
+    int id0[2], id1[2];
+    ids_of(p, id0);
+    ids_of(last_or(p + NW, p), id1);
+    load_k(id0, kf);
+    load_v(id0, vA);
+    load_v(id1, vB);
+    ids_of(last_or(p + NW, p), idk);
+    ids_of(last_or(p + 2 * NW, last_or(p + NW, p)), idv);
+  }
+  for (; p < npairs; p += 2 * NW) {
+    step(p, vA);
+    if (p + NW >= npairs) break;
+    step(p + NW, vB);
+  }
+  l = rows_sum(l);
+
+  // Merge the NW wavefronts of this workgroup in LDS.
+  if (g == 0) {
+    s_m[w][c] = m;
+    s_l[w][c] = l;
+  }
+#pragma unroll
+  for (int t = 0; t < TILES; ++t)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) s_o[w][c][VW * (4 * g + r) + t] = o[t][r];
+  __syncthreads();
+  for (int e = tid; e < nh * D; e += NW * 64) {
+    const int hh = e / D, d = e % D;
+    float M = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, s_m[ww][hh]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) {
+      const float wt = fast_exp2(s_m[ww][hh] - M);    // idle wavefront: m = -inf -> 0
+      L += wt * s_l[ww][hh];
+      O += wt * s_o[ww][hh][d];
+    }
+    if (nsplit == 1) {
+      out[(int64_t)s * o_st + (int64_t)(head0 + hh) * D + d] = (half_t)(O / L);
+    } else {
+      const int64_t pidx = ((int64_t)s * max_splits + split_j) * H + head0 + hh;
+      ws_acc[pidx * D + d] = O;
+      if (d == 0) {
+        ws_m[pidx] = M;
+        ws_l[pidx] = L;
+      }
+    }
+  }
+}
+
+template <int D, int NW>
+__global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
+    const half_t* __restrict__ q, int64_t q_st, int64_t q_sh, half_t* __restrict__ out,
+    int64_t o_st, const half_t* __restrict__ kc, const half_t* __restrict__ vc, int64_t NB,
+    const int* __restrict__ bt, int64_t bt_st, int max_blocks, const int* __restrict__ seq_lens,
+    int S, int H, int KVH, int G, int HG, float sl2, int cap_blocks, int part_blocks, int nx,
+    int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
+    float* __restrict__ ws_l, int* __restrict__ ws_cnt) {
+  __shared__ __attribute__((aligned(16))) char lds[DecodeLds<D, NW>::BYTES];
+  decode_mfma_body<D, NW>(q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, seq_lens, S,
+                          H, KVH, G, HG, sl2, cap_blocks, part_blocks, nx, max_splits, ws_acc,
+                          ws_m, ws_l, ws_cnt, (int)blockIdx.x, (int)blockIdx.z, lds);
+}
+
+// Merge of the split partials (ops/triton_decode_attention.py:144-163): M = max m_j,
+// w_j = 2^(m_j - M), out = sum w_j acc_j / sum w_j l_j. One workgroup per (sequence, KV head,
+// head group), one thread per 4 output dims of a head. A sequence's partials sit in rows
+// s * max_splits + j, so the split count written by the first kernel, seq_len and the partials
+// of the first kMergeChunk splits are all requested in one memory step (rows past the count are
+// read but ignored). Sequences with one split were finished by the first kernel; a sequence
+// with none (seq_len 0) gets zeros here.
+constexpr int kMaxSplits = 256;
+constexpr int kMergeChunk = 16;
+
+template <int D>
+__device__ __forceinline__ void decode_merge_body(
+    const float* __restrict__ ws_acc, const float* __restrict__ ws_m,
+    const float* __restrict__ ws_l, const int* __restrict__ ws_cnt, half_t* __restrict__ out,
+    int64_t o_st, const int* __restrict__ seq_lens, int H, int G, int HG, int max_splits, int bx, int by) {
+  constexpr int TPH = D / 4;                     // threads per head (4 dims each)
+  constexpr int HPP = 256 / TPH;                 // heads per pass
+  constexpr int CH = kMergeChunk;
+  const int s = bx, kvh = by / HG, hg = by % HG;
+  const int tid = threadIdx.x;
+  const int nh = (G - hg * 16) < 16 ? (G - hg * 16) : 16;
+  const int head0 = kvh * G + hg * 16;
+  const int len = __builtin_amdgcn_readfirstlane(seq_lens[s]);
+  const int cnt = __builtin_amdgcn_readfirstlane(ws_cnt[s]);
+  const int64_t row0 = (int64_t)s * max_splits;
+  for (int hp = 0; hp < nh; hp += HPP) {
+    const int hh = hp + tid / TPH, d0 = (tid % TPH) * 4;
+    const bool active = hh < nh;
+    const int64_t hoff = head0 + (active ? hh : 0);
+    float mv[CH], lv[CH];
+    float4_t av[CH];
+    auto load_chunk = [&](int j0) {
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        const int j = (j0 + u) < max_splits ? (j0 + u) : (max_splits - 1);
+        const int64_t pidx = (row0 + j) * H + hoff;
+        mv[u] = ws_m[pidx];
+        lv[u] = ws_l[pidx];
+        av[u] = ld<float4_t>(ws_acc + pidx * D + d0);
+      }
+    };
+    load_chunk(0);
+    if (len <= 0) {                              // padding row: zeros (ops/reference.py:99,104-105)
+      if (active) st<half4_t>(out + (int64_t)s * o_st + (head0 + hh) * (int64_t)D + d0, half4_t{0, 0, 0, 0});
+      continue;
+    }
+    const int n = cnt < 1 ? 1 : (cnt > max_splits ? max_splits : cnt);
+    if (n == 1) return;                          // written by the first kernel
+    float M = -INFINITY, L = 0.f;
+    float4_t O = {0.f, 0.f, 0.f, 0.f};
+    for (int j0 = 0; j0 < n; j0 += CH) {
+      if (j0 > 0) load_chunk(j0);
+      float cm = M;
+#pragma unroll
+      for (int u = 0; u < CH; ++u) cm = (j0 + u < n) ? fmaxf(cm, mv[u]) : cm;
+      const float alpha = fast_exp2(M - cm);     // M = -inf on the first chunk -> 0
+      L *= alpha;
+      O *= alpha;
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        // rows past n are skipped, not weighted by 0: their stale contents may be inf or NaN
+        const float wt = fast_exp2(mv[u] - cm);
+        L = (j0 + u < n) ? L + wt * lv[u] : L;
+        const float4_t o2 = O + wt * av[u];
+        O = (j0 + u < n) ? o2 : O;
+      }
+      M = cm;
+    }
+    if (active) st<half4_t>(out + (int64_t)s * o_st + (head0 + hh) * (int64_t)D + d0, to_half4(O / L));
+  }
+}
+
+template <int D>
+__global__ void __launch_bounds__(256) decode_merge_kernel(
+    const float* __restrict__ ws_acc, const float* __restrict__ ws_m,
+    const float* __restrict__ ws_l, const int* __restrict__ ws_cnt, half_t* __restrict__ out,
+    int64_t o_st, const int* __restrict__ seq_lens, int H, int G, int HG, int max_splits) {
+  decode_merge_body<D>(ws_acc, ws_m, ws_l, ws_cnt, out, o_st, seq_lens, H, G, HG, max_splits,
+                       (int)blockIdx.x, (int)blockIdx.y);
+}
+
+// ------------------------------------------------------------------------------------------
+// Host side
+// ------------------------------------------------------------------------------------------
+#ifndef TS_DECODE_WAVES
+#define TS_DECODE_WAVES 4
+#endif
+constexpr int kDecodeWaves = TS_DECODE_WAVES;               // wavefronts per workgroup
+
+// Workgroups of decode_mfma_kernel resident per CU (4 wavefronts each, one per SIMD), from the
+// kernel's VGPR use (512 per SIMD lane): 6 waves per SIMD up to D = 32, 3 at D = 64, 2 at
+// D = 128 (236 VGPRs), 1 at D = 256.
+static int decode_wgs_per_cu(int D) { return D <= 32 ? 6 : (D == 64 ? 3 : (D == 128 ? 2 : 1)); }
+
+struct SplitPlan {
+  int version;        // 1, 2 or 3 after resolving AUTO
+  int part_blocks;    // v3: blocks per split, 0 = balanced
+  int nx;             // v3 balanced: target split count per (KV head, head group)
+  int nslots;         // v3: launched split slots per (KV head, head group)
+  int cap_blocks;     // v3 fixed partition: blocks of a sequence covered by the launched splits
+  int max_splits;     // v3: workspace rows per sequence (bound on its split count)
+};
+
+// Explicit v3 partition (ops/triton_ops.py:50-51): num_splits = ceil(max_seq_len / partition)
+// splits per sequence at most; partition = 0 selects the balanced schedule. AUTO splits whenever
+// one workgroup per (sequence, KV head, head group) cannot fill the device and contexts are
+// longer than two minimum splits (the reference's rule, ops/triton_ops.py:44-45, with the CU
+// count and this kernel's residency), and uses the balanced schedule unless a partition is given.
+static SplitPlan plan_decode(int version, int S, int H, int KVH, int D, int max_seq_len,
+                             int partition, int cu_count) {
+  SplitPlan p{version, 0, 0, 0, 0, 0};
+  const int G = H / KVH;
+  const int HG = (G + 15) / 16;
+  const int64_t groups = (int64_t)KVH * HG;
+  const int64_t wg_slots = (int64_t)cu_count * decode_wgs_per_cu(D);
+  if (version == TS_DECODE_AUTO) {
+    const bool use_split = (int64_t)S * groups < wg_slots && max_seq_len > 2 * kMinPartBlocks * kBlockSize;
+    p.version = use_split ? TS_DECODE_V3 : TS_DECODE_V2;
+  }
+  if (p.version != TS_DECODE_V3) return p;
+  const int max_blk = (max_seq_len + kBlockSize - 1) / kBlockSize;
+  if (partition > 0) {
+    p.part_blocks = partition / kBlockSize;
+    int num_splits = (max_blk + p.part_blocks - 1) / p.part_blocks;
+    if (num_splits > kMaxSplits) {               // bounds the workspace rows per sequence
+      p.part_blocks = (max_blk + kMaxSplits - 1) / kMaxSplits;
+      num_splits = (max_blk + p.part_blocks - 1) / p.part_blocks;
+    }
+    num_splits = num_splits < 1 ? 1 : num_splits;
+    p.cap_blocks = num_splits * p.part_blocks;
+    p.nslots = S * num_splits;
+    p.max_splits = num_splits;
+  } else {
+#ifdef TS_DECODE_NX
+    int64_t nx = TS_DECODE_NX;                   // tuning override
+#else
+    int64_t nx = wg_slots / groups - S;          // launched slots nx + S = resident workgroups
+#endif
+    nx = nx < 16 ? 16 : (nx > 4096 ? 4096 : nx);
+    p.nx = (int)nx;
+    p.cap_blocks = 1 << 30;
+    p.nslots = p.nx + S;
+    p.max_splits = kBalancedMaxSplits;
+  }
+  return p;
+}
+
+static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+struct WsLayout {
+  size_t acc, m, l, cnt, total;
+};
+
+// [acc: rows * H * D fp32][m: rows * H][l: rows * H][count: S int32] with rows = S * max_splits:
+// split j of sequence s keeps query head h's partial in row s * max_splits + j, column h.
+static WsLayout ws_layout(const SplitPlan& p, int S, int H, int D) {
+  WsLayout w{0, 0, 0, 0, 0};
+  if (p.version != TS_DECODE_V3) return w;
+  const size_t n = (size_t)S * p.max_splits * H;
+  w.acc = 0;
+  w.m = align256(n * D * sizeof(float));
+  w.l = w.m + align256(n * sizeof(float));
+  w.cnt = w.l + align256(n * sizeof(float));
+  w.total = w.cnt + align256((size_t)S * sizeof(int));
+  return w;
+}
+
+template <int D>
+static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, int64_t q_st,
+                          int64_t q_sh, half_t* out, int64_t o_st, const half_t* kc,
+                          const half_t* vc, int64_t NB, const int* bt, int64_t bt_st,
+                          int max_blocks, const int* sl, int S, int H, int KVH, float scale_log2,
+                          void* ws) {
+  const int G = H / KVH;
+  if (p.version == TS_DECODE_V1) {
+    decode_v1_kernel<D><<<dim3(S, H), 64, 0, st>>>(q, q_st, q_sh, out, o_st, kc, vc, NB, bt,
+                                                   bt_st, max_blocks, sl, H, KVH, scale_log2);
+    return;
+  }
+  const int HG = (G + 15) / 16;
+  if (p.version == TS_DECODE_V2) {
+    decode_mfma_kernel<D, kDecodeWaves><<<dim3(S, 1, KVH * HG), kDecodeWaves * 64, 0, st>>>(
+        q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,
+        scale_log2, 0, 0, 0, 0, nullptr, nullptr, nullptr, nullptr);
+    return;
+  }
+  const WsLayout w = ws_layout(p, S, H, D);
+  char* b = static_cast<char*>(ws);
+  float* ws_acc = reinterpret_cast<float*>(b + w.acc);
+  float* ws_m = reinterpret_cast<float*>(b + w.m);
+  float* ws_l = reinterpret_cast<float*>(b + w.l);
+  int* ws_cnt = reinterpret_cast<int*>(b + w.cnt);
+  const int cap = p.cap_blocks < max_blocks ? p.cap_blocks : max_blocks;
+  decode_mfma_kernel<D, kDecodeWaves><<<dim3(p.nslots, 1, KVH * HG), kDecodeWaves * 64, 0, st>>>(
+      q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,
+      scale_log2, cap, p.part_blocks, p.nx, p.max_splits, ws_acc, ws_m, ws_l, ws_cnt);
+  decode_merge_kernel<D><<<dim3(S, KVH * HG), 256, 0, st>>>(ws_acc, ws_m, ws_l, ws_cnt, out, o_st,
+                                                             sl, H, G, HG, p.max_splits);
+}
+
+static bool supported_head_dim(int D) {
+  return D == 16 || D == 32 || D == 64 || D == 128 || D == 256;
+}
+
+}  // namespace ts

@@ -165,7 +165,7 @@ def prefill_attention(q, out, k_cache, v_cache, meta, scale, block_m: int = 64,
     N.check(N.lib().ts_prefill_attention_ws(
         _ptr(q), q.stride(0), q.stride(1), _ptr(out), out.stride(0), T, _ptr(k_cache),
         _ptr(v_cache), NB, _ptr(bt), bt.stride(0), bt.shape[1], _ptr(sl), _ptr(qsl), B,
-        meta.num_decode, int(meta.max_query_len), int(meta.max_seq_len), H, KVH, D,
+        meta.num_decode, int(meta.max_query_len), _prefill_seq_bound(meta), H, KVH, D,
         float(scale), _ptr(ws), ws_bytes, _stream(q)), "prefill_attention")
 
 
@@ -174,7 +174,13 @@ def _prefill_ws_bytes(P: int, H: int, D: int, meta, device) -> int:
     if P <= 0:
         return 0
     return N.lib().ts_prefill_workspace_bytes(P, H, D, int(meta.max_query_len),
-                                              int(meta.max_seq_len), N.cu_count(device.index or 0))
+                                              _prefill_seq_bound(meta), N.cu_count(device.index or 0))
+
+
+def _prefill_seq_bound(meta) -> int:
+    """Host bound of the prefill rows' seq_lens (the builders record it; else max_seq_len)."""
+    b = int(getattr(meta, "max_prefill_seq_len", 0) or 0)
+    return b if b > 0 else int(meta.max_seq_len)
 
 
 # ------------------------------------------------------------------------------------------
@@ -206,18 +212,15 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
             partition = tp if partition is None else partition
     partition = DEFAULT_PARTITION if partition is None else partition
     code = N.DECODE_VERSIONS[decode_version]
-    ws_bytes = 0
-    if S > 0:
-        cus = N.cu_count(q.device.index or 0)
-        ws_bytes = N.lib().ts_decode_workspace_bytes(code, S, H, KVH, D, meta.max_seq_len,
-                                                     partition, cus)
-    # the prefill kernels run after the decode kernels on the same stream and reuse the buffer
-    ws_bytes = max(ws_bytes, _prefill_ws_bytes(B - S, H, D, meta, q.device))
+    ws_bytes = N.lib().ts_paged_attention_workspace_bytes(
+        B, S, int(meta.max_query_len), int(meta.max_seq_len), _prefill_seq_bound(meta), H, KVH, D,
+        code, int(partition), N.cu_count(q.device.index or 0))
     ws = _workspace(ws_bytes, q.device)
     N.check(N.lib().ts_paged_attention(
         _ptr(q), q.stride(0), q.stride(1), _ptr(out), out.stride(0), T, _ptr(k_cache),
         _ptr(v_cache), NB, _ptr(bt), bt.stride(0), bt.shape[1], _ptr(sl), _ptr(qsl), B, S,
-        int(meta.max_query_len), int(meta.max_seq_len), H, KVH, D, float(scale), code,
+        int(meta.max_query_len), int(meta.max_seq_len), _prefill_seq_bound(meta), H, KVH, D,
+        float(scale), code,
         int(partition), _ptr(ws), ws_bytes, _stream(q)), "paged_attention")
     return out
 

@@ -27,6 +27,9 @@ class AttentionMetadata:
     max_query_len: int
     max_seq_len: int
     in_graph: bool = False            # set while capturing / replaying a hipGraph
+    # Host bound of the prefill rows' seq_lens (0: unknown, max_seq_len applies). Not a field of
+    # the reference's metadata: it only sizes the prefill kernel's split plan.
+    max_prefill_seq_len: int = 0
 
 
 @dataclass
@@ -93,7 +96,8 @@ def build_simple(items: list[BatchItem], device) -> ModelInput:
         block_tables=torch.tensor(tables, dtype=torch.int32, device=device),
         slot_mapping=torch.tensor(slots, dtype=torch.int64, device=device),
         num_decode=num_decode_rows(items), max_query_len=max(len(i.tokens) for i in items),
-        max_seq_len=max(seq_lens))
+        max_seq_len=max(seq_lens),
+        max_prefill_seq_len=max(seq_lens[num_decode_rows(items):], default=0))
     return ModelInput(torch.tensor(ids, dtype=torch.int64, device=device),
                       torch.tensor(pos, dtype=torch.int64, device=device), meta,
                       torch.tensor(sample, dtype=torch.int64, device=device))
@@ -171,7 +175,8 @@ class InputBuilder:
             query_start_loc=self.d_qsl[:B + 1], seq_lens=self.d_sl[:B],
             block_tables=self.d_bt[:B, :width], slot_mapping=self.d_slot[:T],
             num_decode=num_decode_rows(items), max_query_len=max(n_tok),
-            max_seq_len=int(sl[:B].max()))
+            max_seq_len=int(sl[:B].max()),
+            max_prefill_seq_len=int(sl[num_decode_rows(items):B].max(initial=0)))
         return ModelInput(self.d_ids[:T], self.d_pos[:T], meta, self.d_sample[:ns])
 
 
@@ -268,7 +273,9 @@ class DeviceInputBuilder:
             query_start_loc=self.d_qsl[:B + 1], seq_lens=self.d_sl[:B],
             block_tables=self.d_bt[:B, :width], slot_mapping=self.d_slot[:T],
             num_decode=num_decode_rows(items), max_query_len=max(n_tok),
-            max_seq_len=max(it.start + n for it, n in zip(items, n_tok)))
+            max_seq_len=max(it.start + n for it, n in zip(items, n_tok)),
+            max_prefill_seq_len=max((it.start + n for it, n in
+                                     list(zip(items, n_tok))[num_decode_rows(items):]), default=0))
         return ModelInput(self.d_ids[:T], self.d_pos[:T], meta, self.d_sample[:S])
 
     def build_into(self, items: list[BatchItem], pad_to: int, ids: torch.Tensor,
