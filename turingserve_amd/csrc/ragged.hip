@@ -49,6 +49,17 @@ struct RaggedArgs {
   int dm_launch, pm_x;
 };
 
+// Tuning overrides (eighths of the resident slots): the prefill plan's round, and the decode
+// splits' share (8: as many as on an idle device; otherwise the slots the prefill leaves).
+#ifndef TS_RAGGED_PF_SHARE
+#define TS_RAGGED_PF_SHARE 4
+#endif
+#ifndef TS_RAGGED_DEC_SHARE
+#define TS_RAGGED_DEC_SHARE 0
+#endif
+constexpr int kRaggedPfShare = TS_RAGGED_PF_SHARE;
+constexpr int kRaggedDecShare = TS_RAGGED_DEC_SHARE;
+
 constexpr int kRaggedLds = 2 * TileLayout<128>::STAGE > DecodeLds<128, kDecodeWaves>::BYTES
                                ? 2 * TileLayout<128>::STAGE
                                : DecodeLds<128, kDecodeWaves>::BYTES;
@@ -104,12 +115,13 @@ static RaggedPlan ragged_plan(int num_seqs, int num_decode, int max_query_len, i
   const int cus = cu_count > 0 ? cu_count : 256;
   const int64_t slots = (int64_t)cus * decode_wgs_per_cu(D);
   const int pf_seq = max_prefill_seq_len > 0 ? max_prefill_seq_len : max_seq_len;
-  r.pf = tile_plan(P, H, D, max_query_len, pf_seq, cus, true, slots / 2);
+  r.pf = tile_plan(P, H, D, max_query_len, pf_seq, cus, true, slots * kRaggedPfShare / 8);
   r.dec = plan_decode(decode_version, num_decode, H, KVH, D, max_seq_len, 0, cus);
   if (r.dec.version != TS_DECODE_V3) return r;
   const int G = H / KVH, HG = (G + 15) / 16;
   const int64_t groups = (int64_t)KVH * HG;
-  int64_t nx = (slots - r.pf.est_wg) / groups - num_decode;
+  const int64_t dec_slots = kRaggedDecShare == 0 ? slots - r.pf.est_wg : slots * kRaggedDecShare / 8;
+  int64_t nx = dec_slots / groups - num_decode;
   nx = nx < 16 ? 16 : (nx > 4096 ? 4096 : nx);
   r.dec.nx = (int)nx;
   r.dec.nslots = r.dec.nx + num_decode;
