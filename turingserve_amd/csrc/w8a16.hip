@@ -541,6 +541,15 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
   // wavefront has finished its reads of step kt's LDS stage (the wait before it includes this
   // wavefront's LDS reads; both halves' A operands are widened before it), so step kt + S's
   // batch is issued right after it into that stage and those registers.
+  //
+  // The explicit waits count vector-memory operations, which retire in issue order on one
+  // counter whatever their kind. Each batch issues its activation DMAs before its weight loads:
+  // the compiler may sink the prologue's last weight loads (registers only the main loop reads)
+  // below the first wait, and with this order that only removes operations the wait's count
+  // already allows to be outstanding, never ones between the awaited DMAs and the wait. (A
+  // weights-first order, tried for a deeper weight-only register ring, broke exactly there; the
+  // deeper ring gains nothing anyway, since the in-order counter makes every wait for step
+  // kt + 1's activations also wait for all weights issued before them.)
 #pragma unroll
   for (int u = 0; u < S; ++u) issue(u, u, wreg[u]);
   wait_vmem_below_lds_done<PD * BATCH>();
