@@ -5,7 +5,9 @@
 Headline workload (the configuration the metric is quoted on): pure-decode paged attention at the
 Qwen2.5-1.5B attention shape -- 12 query / 2 KV heads, head_dim 128, block 16, 64 sequences with
 contexts log-uniform in [128, 4096], 16384 cache blocks, fp16. One *step* is one layer's work:
-kv_write of the 64 new K/V rows, then decode attention over every cached token. Steps rotate over
+kv_write of the 64 new K/V rows, then decode attention over every cached token (by default in
+one launch, ts_decode_attention_kv_write; --separate-kv-write times the two launches, and the
+other form is reported beside the headline either way). Steps rotate over
 8 layer caches (2 GiB in total, far above the 256 MB Infinity Cache) so each step reads its KV
 from HBM, and every step is a hipGraph replay (pure-decode steps are graph-captured, as the
 reference's CudaGraphRunner does). Inputs are resident in HBM before timing starts.
@@ -41,6 +43,9 @@ def parse_args():
     ap.add_argument("--layers", type=int, default=8, help="layer caches rotated over")
     ap.add_argument("--partition", type=int, default=0, help="v3 split size (0 = library policy)")
     ap.add_argument("--decode-version", default="auto", choices=["auto", "v1", "v2", "v3"])
+    ap.add_argument("--separate-kv-write", action="store_true",
+                    help="time the decode step as kv_write + attention launches instead of the "
+                         "fused ts_decode_attention_kv_write")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true")
@@ -117,27 +122,52 @@ def bench_decode(args, torch, K, synth):
         outs[l] = K.paged_attention(q, kv[l, 0], kv[l, 1], meta, scale, decode_version=version,
                                     partition=args.partition or K.DEFAULT_PARTITION)
 
-    for l in range(L):                      # eager warm-up (library, workspace, allocator)
+    def fused_step(l):                      # kv_write fused into the attention launch
+        outs[l] = K.decode_kv_write_attention(q, k, v, kv[l, 0], kv[l, 1], meta, scale,
+                                              decode_version=version,
+                                              partition=args.partition or K.DEFAULT_PARTITION)
+
+    def two_call_step(l):
         kv_step(l)
         attn_step(l)
+
+    step_fn = two_call_step if args.separate_kv_write else fused_step
+    for l in range(L):                      # eager warm-up (library, workspace, allocator)
+        two_call_step(l)
+        fused_step(l)
     torch.cuda.synchronize()
     # One replay = L steps (every layer's kv_write + attention), the way a model's layer stack
-    # sits in one graph; a second graph holds the L attention calls alone for the kernel timing.
+    # sits in one graph; a second graph holds the L attention calls alone for the kernel timing
+    # and a third the other form of the step (two launches or one) for comparison.
     pool = torch.cuda.graph_pool_handle()
     g_step = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_step, pool=pool):
         for l in range(L):
-            kv_step(l)
-            attn_step(l)
+            step_fn(l)
     step_outs = list(outs)
     g_attn = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_attn, pool=pool):
         for l in range(L):
             attn_step(l)
+    g_other = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_other, pool=pool):
+        for l in range(L):
+            (fused_step if args.separate_kv_write else two_call_step)(l)
     torch.cuda.synchronize()
     for _ in range(max(1, args.warmup // L)):
         g_step.replay()
     replays = max(1, -(-args.steps // L))
+
+    def timed(graph):
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+               for _ in range(replays)]
+        for i in range(replays):
+            evs[i][0].record()
+            graph.replay()
+            evs[i][1].record()
+        torch.cuda.synchronize()
+        return [a.elapsed_time(b) / L for a, b in evs]
+
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
           for _ in range(replays)]
     torch.cuda.synchronize()
@@ -149,15 +179,9 @@ def bench_decode(args, torch, K, synth):
     torch.cuda.synchronize()
     t1 = time.perf_counter()
     step_ev_ms = statistics.fmean(a.elapsed_time(b) for a, b in ev) / L
-    a_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-            for _ in range(replays)]
-    for i in range(replays):
-        a_ev[i][0].record()
-        g_attn.replay()
-        a_ev[i][1].record()
-    torch.cuda.synchronize()
-    attn_ms = [a.elapsed_time(b) / L for a, b in a_ev]
-    # graph == eager: the last layer's output of the step graph against an eager call
+    attn_ms = timed(g_attn)
+    other_ms = statistics.fmean(timed(g_other))
+    # graph == eager: the last layer's output of the step graph against an eager two-call step
     ref_out = K.paged_attention(q, kv[L - 1, 0], kv[L - 1, 1], meta, scale,
                                 decode_version=version,
                                 partition=args.partition or K.DEFAULT_PARTITION)
@@ -169,8 +193,10 @@ def bench_decode(args, torch, K, synth):
         "step_s": step_s, "steps": steps_timed, "bytes": b, "step_ev_ms": step_ev_ms,
         "attn_ms_mean": statistics.fmean(attn_ms), "attn_ms_median": statistics.median(attn_ms),
         "graph_equals_eager": same, "mean_ctx": float(st.seq_lens.float().mean()),
+        "fused": not args.separate_kv_write,
+        ("step_two_launch_ms" if not args.separate_kv_write else "step_fused_ms"): other_ms,
     }
-    del kv, g_step, g_attn
+    del kv, g_step, g_attn, g_other
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return st, res
@@ -465,8 +491,11 @@ def main() -> int:
     value = b["step"] / r["step_s"] / 1e9
     attn_s = r["attn_ms_mean"] / 1e3
     achieved = b["attention"] / attn_s / 1e9
-    log(f"step {r['step_s'] * 1e6:.2f} us (events {r['step_ev_ms'] * 1e3:.2f} us)  attention "
-        f"{r['attn_ms_mean'] * 1e3:.2f} us ({achieved:.0f} GB/s)  graph==eager {r['graph_equals_eager']}")
+    other_key = "step_two_launch_ms" if r["fused"] else "step_fused_ms"
+    log(f"step {r['step_s'] * 1e6:.2f} us (events {r['step_ev_ms'] * 1e3:.2f} us, "
+        f"{'fused' if r['fused'] else 'two launches'}; {other_key} {r[other_key] * 1e3:.2f} us)  "
+        f"attention {r['attn_ms_mean'] * 1e3:.2f} us ({achieved:.0f} GB/s)  "
+        f"graph==eager {r['graph_equals_eager']}")
     traffic = traffic_from_profiles("decode_c2_traffic")
     out = {
         "metric": "paged-attn HBM GB/s (% of peak) + mixed-step tokens/s @ Qwen2.5-1.5B shape",
@@ -479,6 +508,8 @@ def main() -> int:
                    "num_seqs": st.num_decode, "mean_context": round(r["mean_ctx"], 1),
                    "max_context": st.max_seq_len, "num_blocks": st.k_cache.shape[0],
                    "layers_rotated": args.layers, "hipgraph": True,
+                   "kv_write": "fused into the attention launch" if r["fused"] else "own launch",
+                   other_key.replace("_ms", "_us"): round(r[other_key] * 1e3, 3),
                    "bytes_per_step": b["step"], "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": "decode attention (paged_attention, decode rows)",
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

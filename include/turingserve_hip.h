@@ -7,6 +7,7 @@
  *   ts_kv_write            <- ops/triton_kv_write.py:28-35   (twin ops/reference.py:50-57)
  *   ts_decode_attention    <- ops/triton_ops.py:35-57 (_decode) and
  *                             ops/triton_decode_attention.py:169-200 (v1 / v2 / v3 launchers)
+ *   ts_decode_attention_kv_write  (kv_write + decode attention of a pure-decode step, fused)
  *   ts_prefill_attention   <- ops/triton_prefill_attention.py:66-79
  *   ts_prefill_attention_ws   (the same with split key ranges, + ts_prefill_workspace_bytes)
  *   ts_paged_attention     <- ops/triton_ops.py:60-71        (twin ops/reference.py:94-111)
@@ -113,6 +114,32 @@ int ts_decode_attention(int32_t version,
                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                         float scale, int32_t max_seq_len, int32_t partition,
                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * ts_kv_write of the step's new rows followed by ts_decode_attention, as one launch: the
+ * decode-only layer step of model/qwen2.py:26-28 with ops/triton_kv_write.py:28-35 and
+ * ops/triton_ops.py:60-71 (pure decode). Row i of k / v ([num_seqs, num_kv_heads, head_dim],
+ * strides in elements) goes to slot_mapping[i] exactly as ts_kv_write writes it, and the
+ * attention then sees it. Precondition (what every input builder produces, incl. the graph
+ * padding of runner/cuda_graphs.py:62-78): slot_mapping[i] is the slot of position
+ * seq_lens[i] - 1, and a row with seq_lens[i] == 0 carries slot -1 (such a row is not written).
+ * The write is fused for v2 / v3 with at most 16 query heads per KV head and 16-byte aligned
+ * rows; otherwise it runs as ts_kv_write's own launch before the attention. Same workspace as
+ * ts_decode_attention (ts_decode_workspace_bytes()).
+ */
+int ts_decode_attention_kv_write(int32_t version,
+                                 const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                                 const void* k, const void* v, int64_t k_stride_t,
+                                 int64_t k_stride_h, int64_t v_stride_t, int64_t v_stride_h,
+                                 const int64_t* slot_mapping,
+                                 void* out, int64_t out_stride_t,
+                                 void* k_cache, void* v_cache, int64_t num_blocks,
+                                 const int32_t* block_tables, int64_t bt_stride,
+                                 int32_t max_blocks_per_seq, const int32_t* seq_lens,
+                                 int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                 int32_t head_dim, float scale, int32_t max_seq_len,
+                                 int32_t partition, void* workspace, size_t workspace_bytes,
+                                 void* stream);
 
 /*
  * Chunked-prefill attention for sequences num_decode .. num_seqs-1 of the flat batch.

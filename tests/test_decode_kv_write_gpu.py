@@ -1,0 +1,139 @@
+"""kv_write fused into the decode attention launch (ts_decode_attention_kv_write) against the
+two separate calls and the oracle (needs an MI355X).
+
+A pure-decode layer step is kv_write of the new K/V rows (ops/triton_kv_write.py:28-35) and
+then paged attention over every cached token including them (ops/triton_ops.py:60-71). The
+fused entry point must leave bit-identical caches and return bit-identical outputs to
+K.kv_write followed by K.paged_attention with the same decode policy (the attention arithmetic
+is the same kernel's), and match the oracle (ops/reference.py:50-57 then :94-111) with the
+attention criterion of the other kernel tests. Cases where the write cannot be fused (v1,
+more than 16 query heads per KV head) take the two-launch route inside the library and must
+give the same results.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import paged as OP
+from turingserve_amd import hip_ops as K
+from turingserve_amd import synth
+from turingserve_amd.metadata import AttentionMetadata
+
+from .test_kernels_gpu import DEV, assert_attn, make_paged
+
+pytestmark = pytest.mark.gpu
+
+
+def decode_step(ctx, H, KVH, D, seed, pad=()):
+    """A decode step: sequence i has ctx[i] tokens after it (its new token at position
+    ctx[i] - 1, slot from its block table); rows in `pad` are graph padding (seq_len 0,
+    slot -1). q, k, v are strided views of one qkv buffer, as the model produces them."""
+    g = torch.Generator().manual_seed(seed + 1000)
+    ctx = list(ctx)
+    for i in pad:
+        ctx[i] = 0
+    _, kc, vc, qsl, sl, bt = make_paged(ctx, H, KVH, D, seed=seed)
+    B = len(ctx)
+    qkv = torch.randn(B, (H + 2 * KVH) * D, generator=g).half()
+    slots = torch.tensor([int(bt[i, (c - 1) // 16]) * 16 + (c - 1) % 16 if c > 0 else -1
+                          for i, c in enumerate(ctx)], dtype=torch.int64)
+    return qkv, kc, vc, qsl, sl, bt, slots
+
+
+def views(qkv, H, KVH, D):
+    B = qkv.shape[0]
+    q = qkv[:, :H * D].view(B, H, D)
+    k = qkv[:, H * D:(H + KVH) * D].view(B, KVH, D)
+    v = qkv[:, (H + KVH) * D:].view(B, KVH, D)
+    return q, k, v
+
+
+def meta_for(qsl, sl, bt, slots):
+    B = sl.shape[0]
+    return AttentionMetadata(qsl.to(DEV), sl.to(DEV), bt.to(DEV), slots.to(DEV), B, 1,
+                             max(1, int(sl.max())))
+
+
+def run_both(case, H, KVH, D, version, partition):
+    qkv, kc, vc, qsl, sl, bt, slots = case
+    meta = meta_for(qsl, sl, bt, slots)
+    q, k, v = views(qkv.to(DEV), H, KVH, D)
+    scale = D ** -0.5
+    kc1, vc1 = kc.to(DEV), vc.to(DEV)
+    K.kv_write(k, v, kc1, vc1, meta.slot_mapping)
+    ref = K.paged_attention(q, kc1, vc1, meta, scale, decode_version=version, partition=partition)
+    kc2, vc2 = kc.to(DEV), vc.to(DEV)
+    out = K.decode_kv_write_attention(q, k, v, kc2, vc2, meta, scale, decode_version=version,
+                                      partition=partition)
+    torch.cuda.synchronize()
+    return out, ref, (kc1, vc1), (kc2, vc2)
+
+
+@pytest.mark.parametrize("H,KVH,D,version,partition", [
+    (12, 2, 128, None, None),       # config 2 heads: balanced split-K, fused
+    (12, 2, 128, "v2", None),       # one workgroup per (sequence, KV head), fused
+    (12, 2, 128, "v3", 512),        # the reference's fixed partition grid, fused
+    (12, 2, 128, "v1", None),       # no MFMA kernel: kv_write's own launch first
+    (14, 2, 64, None, None),        # Qwen2.5-0.5B heads
+    (32, 1, 128, None, None),       # 32 query heads per KV head: two head groups, two launches
+    (4, 4, 16, None, None),         # smallest head_dim, no GQA
+])
+def test_fused_matches_separate_calls_and_oracle(H, KVH, D, version, partition):
+    g = torch.Generator().manual_seed(H * 100 + D)
+    ctx = synth.log_uniform_ints(64, 17, 4096, g)
+    ctx[3], ctx[7], ctx[11] = 1, 16, 33       # a one-token context and block boundaries
+    case = decode_step(ctx, H, KVH, D, seed=H + D)
+    out, ref, (kc1, vc1), (kc2, vc2) = run_both(case, H, KVH, D, version, partition)
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2), "caches differ"
+    assert torch.equal(out, ref), "fused output differs from kv_write + paged_attention"
+    qkv, kc, vc, qsl, sl, bt, slots = case
+    q, k, v = views(qkv, H, KVH, D)
+    kcn, vcn = kc.numpy().copy(), vc.numpy().copy()
+    OP.kv_write(k.numpy(), v.numpy(), kcn, vcn, slots.numpy())
+    oref = OP.paged_attention(q.numpy(), kcn, vcn, qsl.numpy(), sl.numpy(), bt.numpy(), D ** -0.5)
+    assert_attn(out, oref, "fused decode")
+
+
+def test_fused_padding_rows():
+    """Graph padding rows (seq_len 0, slot -1) are written as zeros and touch no cache row."""
+    H, KVH, D = 12, 2, 128
+    g = torch.Generator().manual_seed(5)
+    ctx = synth.log_uniform_ints(48, 100, 3000, g)
+    case = decode_step(ctx, H, KVH, D, seed=5, pad=(0, 17, 47))
+    out, ref, (kc1, vc1), (kc2, vc2) = run_both(case, H, KVH, D, None, None)
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+    assert torch.equal(out, ref)
+    for i in (0, 17, 47):
+        assert torch.equal(out[i], torch.zeros_like(out[i]))
+
+
+def test_fused_config2_graph_replays():
+    """The config 2 step captured in a graph: every replay (with eager work between them)
+    equals the eager fused call and the two-call step."""
+    st = synth.config2(seed=3)
+    qkv = st.qkv.to(DEV)
+    q, k, v = st.views(qkv)
+    meta = st.meta(DEV)
+    meta.in_graph = True
+    scale = st.D ** -0.5
+    kc, vc = st.k_cache.to(DEV), st.v_cache.to(DEV)
+    K.kv_write(k, v, kc, vc, meta.slot_mapping)
+    ref = K.paged_attention(q, kc, vc, meta, scale)
+    kc2, vc2 = st.k_cache.to(DEV), st.v_cache.to(DEV)
+    eager = K.decode_kv_write_attention(q, k, v, kc2, vc2, meta, scale)
+    assert torch.equal(eager, ref) and torch.equal(kc2, kc) and torch.equal(vc2, vc)
+    outs = []
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        outs.append(K.decode_kv_write_attention(q, k, v, kc2, vc2, meta, scale))
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(outs[0], ref)
+        scratch = torch.randn(1 << 20, device=DEV).sum()     # eager work between replays
+        torch.cuda.synchronize()
+        assert torch.isfinite(scratch)
+    assert torch.equal(kc2, kc) and torch.equal(vc2, vc)

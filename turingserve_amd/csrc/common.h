@@ -29,6 +29,9 @@ typedef int int2_t __attribute__((ext_vector_type(2)));
 
 constexpr int kBlockSize = 16;    // tokens per KV block (config.py:74-75)
 constexpr int kWave = 64;         // CDNA wavefront width
+// s_waitcnt operand waiting for every vector memory operation of the wavefront (loads and
+// stores: vmcnt 0; expcnt and lgkmcnt at their maxima, i.e. not waited for).
+constexpr int kWaitVmcntZero = (7 << 4) | (15 << 8);
 
 __device__ __forceinline__ float4_t mfma16x16x16(half4_t a, half4_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);

@@ -14,15 +14,14 @@ extern "C" size_t ts_decode_workspace_bytes(int32_t version, int32_t num_seqs, i
   return ws_layout(p, num_seqs, num_heads, head_dim).total;
 }
 
-extern "C" int ts_decode_attention(int32_t version, const void* q, int64_t q_stride_t,
-                                   int64_t q_stride_h, void* out, int64_t out_stride_t,
-                                   const void* k_cache, const void* v_cache, int64_t num_blocks,
-                                   const int32_t* block_tables, int64_t bt_stride,
-                                   int32_t max_blocks_per_seq, const int32_t* seq_lens,
-                                   int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
-                                   int32_t head_dim, float scale, int32_t max_seq_len,
-                                   int32_t partition, void* workspace, size_t workspace_bytes,
-                                   void* stream) {
+// Shared by the two entry points; nr.k set: kv_write fused into the attention launch.
+static int decode_entry(int32_t version, const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                        void* out, int64_t out_stride_t, const void* k_cache, const void* v_cache,
+                        int64_t num_blocks, const int32_t* block_tables, int64_t bt_stride,
+                        int32_t max_blocks_per_seq, const int32_t* seq_lens, int32_t num_seqs,
+                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
+                        int32_t max_seq_len, int32_t partition, void* workspace,
+                        size_t workspace_bytes, void* stream, const NewRows& nr) {
   TS_REQUIRE(version >= TS_DECODE_AUTO && version <= TS_DECODE_V3, TS_ERR_INVALID_ARG,
              "decode_attention: unknown version %d", version);
   TS_REQUIRE(num_seqs >= 0, TS_ERR_INVALID_ARG, "decode_attention: num_seqs %d < 0", num_seqs);
@@ -53,6 +52,25 @@ extern "C" int ts_decode_attention(int32_t version, const void* q, int64_t q_str
              TS_ERR_WORKSPACE, "decode_attention: workspace of %zu bytes (256-aligned) needed, got %zu",
              need, workspace_bytes);
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (nr.k) {
+    // The fused write needs the MFMA kernels with one head group per KV head (so the workgroup
+    // that writes a block is the only one reading it) and 16-byte row pieces; otherwise the
+    // rows go through kv_write's own launch first.
+    const bool fused = p.version != TS_DECODE_V1 && num_heads / num_kv_heads <= 16 &&
+                       head_dim % 8 == 0 && nr.k_st % 8 == 0 && nr.k_sh % 8 == 0 &&
+                       nr.v_st % 8 == 0 && nr.v_sh % 8 == 0 && aligned(nr.k, 16) &&
+                       aligned(nr.v, 16) && aligned(k_cache, 16) && aligned(v_cache, 16);
+    if (!fused) {
+      st = ts_kv_write(nr.k, nr.v, nr.k_st, nr.k_sh, nr.v_st, nr.v_sh, const_cast<void*>(k_cache),
+                       const_cast<void*>(v_cache), num_blocks, nr.slots, num_seqs, num_kv_heads,
+                       head_dim, stream);
+      if (st != TS_OK) return st;
+      return decode_entry(version, q, q_stride_t, q_stride_h, out, out_stride_t, k_cache, v_cache,
+                          num_blocks, block_tables, bt_stride, max_blocks_per_seq, seq_lens,
+                          num_seqs, num_heads, num_kv_heads, head_dim, scale, max_seq_len,
+                          partition, workspace, workspace_bytes, stream, NewRows{});
+    }
+  }
   const float sl2 = scale * kLog2e;
   const half_t* qp = static_cast<const half_t*>(q);
   half_t* op = static_cast<half_t*>(out);
@@ -62,7 +80,7 @@ extern "C" int ts_decode_attention(int32_t version, const void* q, int64_t q_str
   case DD:                                                                                      \
     launch_decode<DD>(p, s, qp, q_stride_t, q_stride_h, op, out_stride_t, kp, vp, num_blocks,  \
                       block_tables, bt_stride, max_blocks_per_seq, seq_lens, num_seqs, num_heads, \
-                      num_kv_heads, sl2, workspace);                                            \
+                      num_kv_heads, sl2, workspace, nr);                                        \
     break;
   switch (head_dim) {
     TS_DECODE_CASE(16)
@@ -73,4 +91,43 @@ extern "C" int ts_decode_attention(int32_t version, const void* q, int64_t q_str
   }
 #undef TS_DECODE_CASE
   return check_launch("decode_attention");
+}
+
+extern "C" int ts_decode_attention(int32_t version, const void* q, int64_t q_stride_t,
+                                   int64_t q_stride_h, void* out, int64_t out_stride_t,
+                                   const void* k_cache, const void* v_cache, int64_t num_blocks,
+                                   const int32_t* block_tables, int64_t bt_stride,
+                                   int32_t max_blocks_per_seq, const int32_t* seq_lens,
+                                   int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                   int32_t head_dim, float scale, int32_t max_seq_len,
+                                   int32_t partition, void* workspace, size_t workspace_bytes,
+                                   void* stream) {
+  return decode_entry(version, q, q_stride_t, q_stride_h, out, out_stride_t, k_cache, v_cache,
+                      num_blocks, block_tables, bt_stride, max_blocks_per_seq, seq_lens, num_seqs,
+                      num_heads, num_kv_heads, head_dim, scale, max_seq_len, partition, workspace,
+                      workspace_bytes, stream, NewRows{});
+}
+
+extern "C" int ts_decode_attention_kv_write(
+    int32_t version, const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k,
+    const void* v, int64_t k_stride_t, int64_t k_stride_h, int64_t v_stride_t,
+    int64_t v_stride_h, const int64_t* slot_mapping, void* out, int64_t out_stride_t,
+    void* k_cache, void* v_cache, int64_t num_blocks, const int32_t* block_tables,
+    int64_t bt_stride, int32_t max_blocks_per_seq, const int32_t* seq_lens, int32_t num_seqs,
+    int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seq_len,
+    int32_t partition, void* workspace, size_t workspace_bytes, void* stream) {
+  TS_REQUIRE(num_seqs >= 0, TS_ERR_INVALID_ARG, "decode_attention_kv_write: num_seqs %d < 0",
+             num_seqs);
+  if (num_seqs == 0) return TS_OK;
+  TS_REQUIRE(k && v && slot_mapping, TS_ERR_INVALID_ARG,
+             "decode_attention_kv_write: null pointer argument");
+  TS_REQUIRE(k_stride_t >= 0 && k_stride_h >= 0 && v_stride_t >= 0 && v_stride_h >= 0,
+             TS_ERR_INVALID_ARG, "decode_attention_kv_write: negative stride");
+  const NewRows nr{static_cast<const half_t*>(k), static_cast<const half_t*>(v), k_stride_t,
+                   k_stride_h, v_stride_t, v_stride_h, slot_mapping,
+                   num_blocks * (int64_t)kBlockSize};
+  return decode_entry(version, q, q_stride_t, q_stride_h, out, out_stride_t, k_cache, v_cache,
+                      num_blocks, block_tables, bt_stride, max_blocks_per_seq, seq_lens, num_seqs,
+                      num_heads, num_kv_heads, head_dim, scale, max_seq_len, partition, workspace,
+                      workspace_bytes, stream, nr);
 }

@@ -235,7 +235,16 @@ struct DecodeLds {
   static constexpr int BYTES = MAP + (NW + 5) * 4;
 };
 
-template <int D, int NW>
+// The step's new K/V rows (one per decode row), for the launch that also performs kv_write.
+struct NewRows {
+  const half_t* k;
+  const half_t* v;
+  int64_t k_st, k_sh, v_st, v_sh;
+  const int64_t* slots;     // slot_mapping [S] (-1: padding row, not written)
+  int64_t num_slots;        // NB * 16: slots at or past it are not written (as kv_write)
+};
+
+template <int D, int NW, bool WRITE = false>
 __device__ __forceinline__ void decode_mfma_body(
     const half_t* __restrict__ q, int64_t q_st, int64_t q_sh, half_t* __restrict__ out,
     int64_t o_st, const half_t* __restrict__ kc, const half_t* __restrict__ vc, int64_t NB,
@@ -243,7 +252,7 @@ __device__ __forceinline__ void decode_mfma_body(
     int S, int H, int KVH, int G, int HG, float sl2, int cap_blocks, int part_blocks, int nx,
     int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
     float* __restrict__ ws_l, int* __restrict__ ws_cnt,
-    int bx, int bz, char* __restrict__ lds) {
+    int bx, int bz, char* __restrict__ lds, const NewRows& nr = NewRows{}) {
   constexpr int KK = KvRegs<D>::KK;
   constexpr int VW = KvRegs<D>::VW;
   constexpr int TILES = KvRegs<D>::TILES;
@@ -289,6 +298,29 @@ __device__ __forceinline__ void decode_mfma_body(
       for (int e = tid; e < nh * D; e += NW * 64)
         out[(int64_t)s * o_st + (int64_t)(head0 + e / D) * D + e % D] = (half_t)0.f;
       return;
+    }
+  }
+  if constexpr (WRITE) {
+    // kv_write of sequence s's new row (ops/reference.py:50-57) for this KV head, by the
+    // workgroup whose range ends the sequence (it holds position seq_len - 1, where every input
+    // builder puts slot_mapping[s]; the launch has one head group per KV head, so no other
+    // workgroup reads that block). The rows are stored before any wavefront requests K/V:
+    // the stores complete in L2 (vmcnt 0) before the barrier, and no wavefront of this CU has
+    // requested those lines in this kernel, so the loads after it see the new row. The cache
+    // pointers are the same restrict pointers the loads use, so the compiler orders them too.
+    if (split_j == nsplit - 1) {
+      const int64_t slot = nr.slots[s];
+      if (slot >= 0 && slot < nr.num_slots && tid < D / 4) {
+        constexpr int PIECES = D / 8;              // 16-byte pieces per row
+        const int j = tid / PIECES, pc = tid % PIECES;   // j: 0 = K, 1 = V
+        const half_t* src = j ? nr.v + (int64_t)s * nr.v_st + (int64_t)kvh * nr.v_sh
+                              : nr.k + (int64_t)s * nr.k_st + (int64_t)kvh * nr.k_sh;
+        half_t* dst = const_cast<half_t*>(j ? vc : kc) +
+                      (((slot >> 4) * KVH + kvh) * kBlockSize + (slot & 15)) * D;
+        st<half8_t>(dst + 8 * pc, ld<half8_t>(src + 8 * pc));
+      }
+      __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
+      __syncthreads();
     }
   }
   // Tokens this range may use: a pair's second block can lie past the range (it then repeats
@@ -447,18 +479,19 @@ __device__ __forceinline__ void decode_mfma_body(
   }
 }
 
-template <int D, int NW>
+template <int D, int NW, bool WRITE = false>
 __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
     const half_t* __restrict__ q, int64_t q_st, int64_t q_sh, half_t* __restrict__ out,
     int64_t o_st, const half_t* __restrict__ kc, const half_t* __restrict__ vc, int64_t NB,
     const int* __restrict__ bt, int64_t bt_st, int max_blocks, const int* __restrict__ seq_lens,
     int S, int H, int KVH, int G, int HG, float sl2, int cap_blocks, int part_blocks, int nx,
     int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
-    float* __restrict__ ws_l, int* __restrict__ ws_cnt) {
+    float* __restrict__ ws_l, int* __restrict__ ws_cnt, const NewRows nr) {
   __shared__ __attribute__((aligned(16))) char lds[DecodeLds<D, NW>::BYTES];
-  decode_mfma_body<D, NW>(q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, seq_lens, S,
-                          H, KVH, G, HG, sl2, cap_blocks, part_blocks, nx, max_splits, ws_acc,
-                          ws_m, ws_l, ws_cnt, (int)blockIdx.x, (int)blockIdx.z, lds);
+  decode_mfma_body<D, NW, WRITE>(q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks,
+                                 seq_lens, S, H, KVH, G, HG, sl2, cap_blocks, part_blocks, nx,
+                                 max_splits, ws_acc, ws_m, ws_l, ws_cnt, (int)blockIdx.x,
+                                 (int)blockIdx.z, lds, nr);
 }
 
 // Merge of the split partials (ops/triton_decode_attention.py:144-163): M = max m_j,
@@ -628,13 +661,16 @@ static WsLayout ws_layout(const SplitPlan& p, int S, int H, int D) {
   return w;
 }
 
+// With nr.k set (kv_write fused into the launch; v2 / v3 with one head group per KV head only)
+// the MFMA kernel first writes the new rows, as in decode_mfma_body.
 template <int D>
 static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, int64_t q_st,
                           int64_t q_sh, half_t* out, int64_t o_st, const half_t* kc,
                           const half_t* vc, int64_t NB, const int* bt, int64_t bt_st,
                           int max_blocks, const int* sl, int S, int H, int KVH, float scale_log2,
-                          void* ws) {
+                          void* ws, const NewRows& nr = NewRows{}) {
   const int G = H / KVH;
+  const bool write = nr.k != nullptr;
   if (p.version == TS_DECODE_V1) {
     decode_v1_kernel<D><<<dim3(S, H), 64, 0, st>>>(q, q_st, q_sh, out, o_st, kc, vc, NB, bt,
                                                    bt_st, max_blocks, sl, H, KVH, scale_log2);
@@ -642,9 +678,15 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
   }
   const int HG = (G + 15) / 16;
   if (p.version == TS_DECODE_V2) {
-    decode_mfma_kernel<D, kDecodeWaves><<<dim3(S, 1, KVH * HG), kDecodeWaves * 64, 0, st>>>(
-        q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,
-        scale_log2, 0, 0, 0, 0, nullptr, nullptr, nullptr, nullptr);
+#define TS_V2_LAUNCH(W)                                                                          \
+  decode_mfma_kernel<D, kDecodeWaves, W><<<dim3(S, 1, KVH * HG), kDecodeWaves * 64, 0, st>>>(    \
+      q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,        \
+      scale_log2, 0, 0, 0, 0, nullptr, nullptr, nullptr, nullptr, nr)
+    if (write)
+      TS_V2_LAUNCH(true);
+    else
+      TS_V2_LAUNCH(false);
+#undef TS_V2_LAUNCH
     return;
   }
   const WsLayout w = ws_layout(p, S, H, D);
@@ -654,9 +696,16 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
   float* ws_l = reinterpret_cast<float*>(b + w.l);
   int* ws_cnt = reinterpret_cast<int*>(b + w.cnt);
   const int cap = p.cap_blocks < max_blocks ? p.cap_blocks : max_blocks;
-  decode_mfma_kernel<D, kDecodeWaves><<<dim3(p.nslots, 1, KVH * HG), kDecodeWaves * 64, 0, st>>>(
-      q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,
-      scale_log2, cap, p.part_blocks, p.nx, p.max_splits, ws_acc, ws_m, ws_l, ws_cnt);
+#define TS_V3_LAUNCH(W)                                                                          \
+  decode_mfma_kernel<D, kDecodeWaves, W><<<dim3(p.nslots, 1, KVH * HG), kDecodeWaves * 64, 0,    \
+                                           st>>>(                                                \
+      q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,        \
+      scale_log2, cap, p.part_blocks, p.nx, p.max_splits, ws_acc, ws_m, ws_l, ws_cnt, nr)
+  if (write)
+    TS_V3_LAUNCH(true);
+  else
+    TS_V3_LAUNCH(false);
+#undef TS_V3_LAUNCH
   decode_merge_kernel<D><<<dim3(S, KVH * HG), 256, 0, st>>>(ws_acc, ws_m, ws_l, ws_cnt, out, o_st,
                                                              sl, H, G, HG, p.max_splits);
 }

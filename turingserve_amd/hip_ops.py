@@ -225,6 +225,54 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     return out
 
 
+def decode_kv_write_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                              k_cache: torch.Tensor, v_cache: torch.Tensor, meta, scale: float,
+                              decode_version: str | None = None,
+                              partition: int | None = None) -> torch.Tensor:
+    """A pure-decode layer step in one launch: kv_write(k, v, caches, meta.slot_mapping) and
+    then paged_attention(q, caches, meta, scale) (model/qwen2.py:26-28 with
+    ops/triton_ops.py:60-71), returning the same [T, H*D] and leaving the same cache. q [T, H, D],
+    k, v [T, KVH, D] (strided views of the qkv rows allowed). Every row must be a decode row, and
+    slot_mapping[i] the slot of position seq_lens[i] - 1 (-1 where seq_lens[i] == 0), as every
+    input builder produces."""
+    T, H, D = q.shape
+    out = torch.empty(T, H * D, dtype=q.dtype, device=q.device)
+    if T == 0:
+        return out
+    _check_gpu(q, k, v, k_cache, v_cache)
+    NB, KVH, cd = _check_cache(k_cache, v_cache)
+    _require(cd == D and q.stride(2) == 1 and q.dtype == torch.float16,
+             "decode_kv_write_attention: q must be fp16 [T, H, D] with unit stride over D")
+    _require(k.shape == (T, KVH, D) and v.shape == k.shape, "decode_kv_write_attention: k, v shape")
+    _require(k.dtype == torch.float16 and v.dtype == torch.float16 and k.stride(2) == 1
+             and v.stride(2) == 1, "decode_kv_write_attention: k, v must be fp16 rows")
+    _require(decode_version in N.DECODE_VERSIONS, f"unknown decode version {decode_version!r}")
+    S = meta.num_decode
+    _require(S == T and meta.seq_lens.shape[0] == S,
+             "decode_kv_write_attention: every row must be a decode row")
+    bt, sl = _i32(meta.block_tables), _i32(meta.seq_lens)
+    sm = meta.slot_mapping
+    slots = sm if (sm.dtype == torch.int64 and sm.is_contiguous()) else sm.to(torch.int64).contiguous()
+    _require(slots.shape[0] >= T, "decode_kv_write_attention: slot_mapping shorter than q")
+    if decode_version is None:
+        tv, tp = tuner.decode_choice(S, int(meta.max_seq_len))
+        if tv is not None:
+            decode_version = tv
+            partition = tp if partition is None else partition
+    code = N.DECODE_VERSIONS[decode_version]
+    part = (DEFAULT_PARTITION if partition is None else partition) if code in (0, 3) else 0
+    ws_bytes = N.lib().ts_decode_workspace_bytes(code, S, H, KVH, D, int(meta.max_seq_len), part,
+                                                 N.cu_count(q.device.index or 0))
+    ws = _workspace(ws_bytes, q.device)
+    N.check(N.lib().ts_decode_attention_kv_write(
+        code, _ptr(q), q.stride(0), q.stride(1), _ptr(k), _ptr(v), k.stride(0), k.stride(1),
+        v.stride(0), v.stride(1), _ptr(slots), _ptr(out), out.stride(0), _ptr(k_cache),
+        _ptr(v_cache), NB, _ptr(bt), bt.stride(0), bt.shape[1], _ptr(sl), S, H, KVH, D,
+        float(scale), int(meta.max_seq_len), int(part), _ptr(ws), ws_bytes, _stream(q)),
+        "decode_kv_write_attention")
+    return out
+
+
 # ------------------------------------------------------------------------------------------
 # W8A16 (ops/triton_w8a16.py:38-51, ops/triton_ops.py:74-91)
 # ------------------------------------------------------------------------------------------
