@@ -67,6 +67,9 @@ def test_variant_workspace_sizes_and_checks():
             lib.ts_w8a16_workspace_bytes(*shape, 256)
     assert lib.ts_w8a16_workspace_bytes_v(560, 1536, 1536, 2, 2, 256) == 2 * 560 * 1536 * 4
     assert lib.ts_w8a16_workspace_bytes_v(560, 1536, 1536, 3, 1, 256) == 0
+    assert lib.ts_w8a16_workspace_bytes_v(560, 1536, 1536, 4, 0, 256) == 0   # 128 x 32: no split
+    assert lib.ts_w8a16_workspace_bytes_v(560, 1536, 1536, 4, 3, 256) == 3 * 560 * 1536 * 4
+    assert lib.ts_w8a16_glu_workspace_bytes(560, 768, 1536, 4, 2, 256) == 2 * 560 * 1536 * 4
     assert lib.ts_w8a16_workspace_bytes_v(8, 1536, 1536, 1, 3, 256) == 3 * 8 * 1536 * 4
     assert lib.ts_w8a16_workspace_bytes_v(64, 1536, 1536, 1, 0, 256) == 0    # not available
     p = ctypes.c_void_p(256)

@@ -12,7 +12,7 @@
 //    64-wide K step (64 bytes per row and instruction). The K dimension is split over
 //    workgroups until the device is full; fp32 partials are merged (and scaled) by a second
 //    kernel.
-//  * larger M: the wide-tile kernel on v_mfma_f32_32x32x16_f16 (128 x 128 or 128 x 64 tiles of
+//  * larger M: the wide-tile kernel on v_mfma_f32_32x32x16_f16 (128 x 128, 128 x 64 or 128 x 32 tiles of
 //    Y^T, split-K when the grid is short of two workgroups per CU): weights stream straight
 //    into the A operands of the wavefront that owns them, activations are DMA'd into a ring of
 //    LDS stages that all four wavefronts read.
@@ -595,53 +595,55 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
   wait_vmem_below<0>();
   // lane (h, r) of subtile (i, j), element e = 4a + c: Y[m][n] with m = m_base + 32 j + r and
   // n = weight_row(32 WN w + 32 i + 8a + 4h + c); the four c are one 8-byte store.
-  if (glu && !part) {
-    // Every wavefront puts its fp16 results in LDS (gate values in stage 0, up values in stage
-    // 1, both idle now) in register order, slot ((half, j, a), lane); then wavefronts w and w + 2
-    // share column half w % 2, w < 2 finishing subtiles j < WM / 2 and w >= 2 the rest, each
-    // lane at the same (row, columns) its slot came from.
-    __syncthreads();                                  // every wavefront is done with the stages
-    half4_t* xg = reinterpret_cast<half4_t*>(s_x0);   // 2 halves x WM x 4 x 64 lanes x 8 B each
-    half4_t* xu = reinterpret_cast<half4_t*>(s_x1);
-    static_assert(sizeof(s_x0) == 2 * WM * 4 * 64 * sizeof(half4_t), "exchange fits one stage");
-    static_assert(WM % 2 == 0, "subtiles split between the two wavefronts of a half");
-    const int half_w = w & 1;
-    const bool is_up = w >= 2;
-#pragma unroll
-    for (int j = 0; j < WM; ++j)
-#pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
-        const int nl = w * 32 + 8 * a4 + 4 * h;
-        const float4_t sc = *reinterpret_cast<const float4_t*>(&s_sc[nl]);
-        const float4_t bs = *reinterpret_cast<const float4_t*>(&s_bs[nl]);
-        const float o[4] = {acc[0][j][4 * a4] * sc[0] + bs[0], acc[0][j][4 * a4 + 1] * sc[1] + bs[1],
-                            acc[0][j][4 * a4 + 2] * sc[2] + bs[2], acc[0][j][4 * a4 + 3] * sc[3] + bs[3]};
-        const half4_t hv = {(half_t)o[0], (half_t)o[1], (half_t)o[2], (half_t)o[3]};
-        (is_up ? xu : xg)[((half_w * WM + j) * 4 + a4) * 64 + lane] = hv;
-      }
-    __syncthreads();
-#pragma unroll
-    for (int jj = 0; jj < WM / 2; ++jj) {
-      const int j = (is_up ? WM / 2 : 0) + jj;
-      const int mm = m_base + 32 * j + r;
-#pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
-        const int col = g0 + 32 * half_w + 8 * a4 + 4 * h;
-        if (mm >= M || col >= glu) continue;
-        const int slot = ((half_w * WM + j) * 4 + a4) * 64 + lane;
-        const half4_t gv = xg[slot], uv = xu[slot];
-        const half4_t o = {silu_mul_h(gv[0], uv[0]), silu_mul_h(gv[1], uv[1]), silu_mul_h(gv[2], uv[2]),
-                           silu_mul_h(gv[3], uv[3])};
-        half_t* dst = y + (int64_t)mm * ldy + col;
-        if (col + 3 < glu) {
-          st<half4_t>(dst, o);
-        } else {
-          for (int c = 0; c < 4; ++c)
-            if (col + c < glu) dst[c] = o[c];
+  if constexpr (WM % 2 == 0) {         // GLU tiles pair subtiles (no 32-row GLU tiles)
+    if (glu && !part) {
+      // Every wavefront puts its fp16 results in LDS (gate values in stage 0, up values in stage
+      // 1, both idle now) in register order, slot ((half, j, a), lane); then wavefronts w and w + 2
+      // share column half w % 2, w < 2 finishing subtiles j < WM / 2 and w >= 2 the rest, each
+      // lane at the same (row, columns) its slot came from.
+      __syncthreads();                                  // every wavefront is done with the stages
+      half4_t* xg = reinterpret_cast<half4_t*>(s_x0);   // 2 halves x WM x 4 x 64 lanes x 8 B each
+      half4_t* xu = reinterpret_cast<half4_t*>(s_x1);
+      static_assert(sizeof(s_x0) == 2 * WM * 4 * 64 * sizeof(half4_t), "exchange fits one stage");
+      static_assert(WM % 2 == 0, "subtiles split between the two wavefronts of a half");
+      const int half_w = w & 1;
+      const bool is_up = w >= 2;
+  #pragma unroll
+      for (int j = 0; j < WM; ++j)
+  #pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4) {
+          const int nl = w * 32 + 8 * a4 + 4 * h;
+          const float4_t sc = *reinterpret_cast<const float4_t*>(&s_sc[nl]);
+          const float4_t bs = *reinterpret_cast<const float4_t*>(&s_bs[nl]);
+          const float o[4] = {acc[0][j][4 * a4] * sc[0] + bs[0], acc[0][j][4 * a4 + 1] * sc[1] + bs[1],
+                              acc[0][j][4 * a4 + 2] * sc[2] + bs[2], acc[0][j][4 * a4 + 3] * sc[3] + bs[3]};
+          const half4_t hv = {(half_t)o[0], (half_t)o[1], (half_t)o[2], (half_t)o[3]};
+          (is_up ? xu : xg)[((half_w * WM + j) * 4 + a4) * 64 + lane] = hv;
+        }
+      __syncthreads();
+  #pragma unroll
+      for (int jj = 0; jj < WM / 2; ++jj) {
+        const int j = (is_up ? WM / 2 : 0) + jj;
+        const int mm = m_base + 32 * j + r;
+  #pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4) {
+          const int col = g0 + 32 * half_w + 8 * a4 + 4 * h;
+          if (mm >= M || col >= glu) continue;
+          const int slot = ((half_w * WM + j) * 4 + a4) * 64 + lane;
+          const half4_t gv = xg[slot], uv = xu[slot];
+          const half4_t o = {silu_mul_h(gv[0], uv[0]), silu_mul_h(gv[1], uv[1]), silu_mul_h(gv[2], uv[2]),
+                             silu_mul_h(gv[3], uv[3])};
+          half_t* dst = y + (int64_t)mm * ldy + col;
+          if (col + 3 < glu) {
+            st<half4_t>(dst, o);
+          } else {
+            for (int c = 0; c < 4; ++c)
+              if (col + c < glu) dst[c] = o[c];
+          }
         }
       }
+      return;
     }
-    return;
   }
 #pragma unroll
   for (int i = 0; i < WN; ++i) {
@@ -698,13 +700,13 @@ constexpr int kWidePrefetch = 3;                  // K steps of loads in flight 
 struct GemmPlan {
   bool small;
   int mt;          // m tiles (small path)
-  int bn, bm;      // tile shape (wide path): 128 x 128 or 128 x 64
+  int bn, bm;      // tile shape (wide path): 128 x 128, 128 x 64 or 128 x 32
   int splits;      // K splits
   int k_per_split;
 };
 
 // Variants a caller (a tuning table) may name instead of the planner's choice.
-enum GemmVariant : int { kVarAuto = 0, kVarStream = 1, kVarWide64 = 2, kVarWide128 = 3 };
+enum GemmVariant : int { kVarAuto = 0, kVarStream = 1, kVarWide64 = 2, kVarWide128 = 3, kVarWide32 = 4 };
 constexpr int kMaxSplits = 256;
 
 // Weight streaming: fill the device with wavefronts (about eight per CU) by splitting K,
@@ -741,16 +743,24 @@ static int wide64_splits(int M, int N, int K, int cus) {
 // The plan of a variant with `splits` K splits (0: the variant's own rule). kVarAuto: weight
 // streaming when use_small_path says so; else 128 x 128 tiles (two workgroups per CU; the most
 // work per CU of the shapes measured) once they cover half the CUs and M is past 64 (below
-// that most of their rows would be padding); else 128 x 64 tiles.
+// that most of their rows would be padding); else 128 x 64 tiles, or 128 x 32 tiles (four
+// workgroups per CU) when M is past 64 but 128 x 64 tiles would cover fewer than half the CUs
+// with no K split (short K): twice the workgroups for the same weights, which measured ~13 %
+// faster on the 1536 x 1536 and 2048 x 1536 products at M = 256 and the former at M = 560.
+// 128 x 32 tiles never split K by their own rule, and GLU mode plans them as 128 x 64.
 static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int splits) {
   if (variant == kVarAuto) {
     const int64_t n_tiles = (N + 127) / 128;
     variant = use_small_path(M, N, K)                                       ? kVarStream
               : (M > 64 && n_tiles * ((M + 127) / 128) * 2 >= cus) ? kVarWide128
                                                                         : kVarWide64;
+    if (variant == kVarWide64 && M > 64 && n_tiles * ((M + 63) / 64) * 2 < cus &&
+        wide64_splits(M, N, K, cus) == 1)
+      variant = kVarWide32;
     splits = 0;
   }
-  GemmPlan p{variant == kVarStream, (M + 15) / 16, 128, variant == kVarWide128 ? 128 : 64, 1, K};
+  GemmPlan p{variant == kVarStream, (M + 15) / 16, 128,
+             variant == kVarWide128 ? 128 : (variant == kVarWide32 ? 32 : 64), 1, K};
   if (p.small) {
     if (splits == 0) splits = stream_splits(M, N, K, cus);
     int kps = (K + splits - 1) / splits;
@@ -787,7 +797,7 @@ extern "C" size_t ts_w8a16_workspace_bytes(int32_t M, int32_t N, int32_t K, int3
 }
 
 static bool variant_valid(int variant, int splits, int M) {
-  return variant >= kVarAuto && variant <= kVarWide128 && splits >= 0 && splits <= kMaxSplits &&
+  return variant >= kVarAuto && variant <= kVarWide32 && splits >= 0 && splits <= kMaxSplits &&
          (variant != kVarStream || M <= kSmallMMax);
 }
 
@@ -806,8 +816,9 @@ static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const v
   int cus = 0;
   int st = device_cu_count(&cus);
   if (st != TS_OK) return st;
-  const GemmPlan p = plan_gemm_v(M, N, K, cus, variant, splits);
   const bool glu = io.glu > 0;                    // N = 2 * io.glu, y is [M, io.glu]
+  GemmPlan p = plan_gemm_v(M, N, K, cus, variant, splits);
+  if (glu && p.bm == 32) p.bm = 64;               // GLU tiles pair 32-row subtiles (same splits)
   const size_t need = gemm_workspace(p, M, N);
   TS_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
              TS_ERR_WORKSPACE, "w8a16: workspace of %zu bytes needed, got %zu", need,
@@ -857,8 +868,10 @@ static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const v
         xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part, io)
     if (p.bm == 128) {
       TS_WIDE_LAUNCH(1, 4);
-    } else {
+    } else if (p.bm == 64) {
       TS_WIDE_LAUNCH(1, 2);
+    } else {
+      TS_WIDE_LAUNCH(1, 1);
     }
 #undef TS_WIDE_LAUNCH
     if (part) reduce(part);
