@@ -50,7 +50,8 @@ def parse_args():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["decode", "prefill", "w8a16", "logits", "metadata", "mixed"],
+    ap.add_argument("--only", choices=["decode", "prefill", "w8a16", "logits", "metadata", "mixed",
+                                       "decode_model"],
                     default=None,
                     help="run one workload alone (for profiling); prints its result as JSON")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -451,6 +452,69 @@ def bench_mixed(torch, synth, reps: int = 5):
             "logits_finite": finite}
 
 
+def bench_decode_model(torch, synth, reps: int = 10):
+    """A pure-decode step of the whole model: config 2's 64 sequences (contexts log-uniform in
+    [128, 4096]) through a random-init Qwen2 at the Qwen2.5-1.5B dimensions (28 layers, W8A16
+    linears), graph-replayed as pure-decode steps are; tokens/s = 64 / step time. Timed with each
+    layer's rope + kv_write + attention as one launch and, for comparison, as the separate calls
+    (rope_kv_write, then paged_attention)."""
+    import random as _r
+
+    from turingserve_amd import get_ops
+    from turingserve_amd.metadata import BatchItem, InputBuilder, SeqState
+    from turingserve_amd.qwen2 import QWEN25_15B, Qwen2Model, random_weights
+
+    dev = torch.device("cuda", 0)
+    cfg = QWEN25_15B
+    g = torch.Generator().manual_seed(0)
+    ctx = synth.log_uniform_ints(64, 128, 4096, g)
+    w = random_weights(cfg, dev, quantization="int8", init_std=0.02, seed=0)
+    ops_plain = get_ops("hip")
+    del ops_plain.decode_rope_kv_write_attention
+    models = {"fused": Qwen2Model(cfg, w, get_ops("hip"), dev, max_model_len=8192),
+              "separate": Qwen2Model(cfg, w, ops_plain, dev, max_model_len=8192)}
+    nb = sum(-(-c // 16) for c in ctx) + 8
+    kv = models["fused"].new_kv_cache(nb)
+    kv.normal_(0.0, 0.5)
+    rng = _r.Random(0)
+    free = list(range(1, nb))
+    rng.shuffle(free)
+    items = []
+    for c in ctx:
+        s = SeqState([rng.randrange(cfg.vocab_size) for _ in range(c)])
+        s.block_table = [free.pop() for _ in range(-(-c // 16))]
+        items.append(BatchItem(s, c - 1, [s.token_ids[-1]], "last"))
+    inp = InputBuilder(1024, 64, 512, dev).build(items)
+    T = inp.input_ids.shape[0]
+    res = {"tokens_per_step": T}
+    outs = {}
+    for name, model in models.items():
+        def step(model=model):
+            hidden = model.forward(inp.input_ids, inp.positions, inp.meta, kv)
+            return model.compute_logits(hidden, inp.sample_indices)
+
+        step()
+        torch.cuda.synchronize()
+        g_ = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_):
+            out = step()
+        g_.replay()
+        torch.cuda.synchronize()
+        outs[name] = out.clone()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            g_.replay()
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t0) / reps
+        res[f"{name}_graph_ms"] = round(dt * 1e3, 3)
+        res[f"{name}_tokens_per_s"] = round(T / dt, 1)
+        del g_
+    res["fused_equals_separate"] = bool(torch.equal(outs["fused"], outs["separate"]))
+    del models, w, kv
+    torch.cuda.empty_cache()
+    return res
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -475,8 +539,9 @@ def main() -> int:
                           "copy_bytes_written_per_launch": a.numel(), "launches": 8}))
         return 0
     _native.lib()
-    if args.only in ("prefill", "w8a16", "logits", "metadata", "mixed"):
-        fn = {"prefill": lambda: bench_prefill(torch, K, synth),
+    if args.only in ("prefill", "w8a16", "logits", "metadata", "mixed", "decode_model"):
+        fn = {"decode_model": lambda: bench_decode_model(torch, synth),
+              "prefill": lambda: bench_prefill(torch, K, synth),
               "w8a16": lambda: bench_w8a16(torch, K, synth),
               "logits": lambda: bench_logits(torch, K),
               "metadata": lambda: bench_metadata(torch, synth),
@@ -546,6 +611,8 @@ def main() -> int:
         extra["logits_config5"] = bench_logits(torch, K)
         log("extra: config 5 step metadata")
         extra["metadata_config5"] = bench_metadata(torch, synth)
+        log("extra: config 2 pure-decode step of the whole model")
+        extra["decode_model_config2"] = bench_decode_model(torch, synth)
         log("extra: config 5 mixed step")
         extra["mixed_config5"] = bench_mixed(torch, synth)
         log("extra: config 5 mixed step with a measured variant table")

@@ -8,6 +8,7 @@
  *   ts_decode_attention    <- ops/triton_ops.py:35-57 (_decode) and
  *                             ops/triton_decode_attention.py:169-200 (v1 / v2 / v3 launchers)
  *   ts_decode_attention_kv_write  (kv_write + decode attention of a pure-decode step, fused)
+ *   ts_decode_rope_kv_write_attention  (rope + kv_write + decode attention, fused)
  *   ts_prefill_attention   <- ops/triton_prefill_attention.py:66-79
  *   ts_prefill_attention_ws   (the same with split key ranges, + ts_prefill_workspace_bytes)
  *   ts_paged_attention     <- ops/triton_ops.py:60-71        (twin ops/reference.py:94-111)
@@ -140,6 +141,31 @@ int ts_decode_attention_kv_write(int32_t version,
                                  int32_t head_dim, float scale, int32_t max_seq_len,
                                  int32_t partition, void* workspace, size_t workspace_bytes,
                                  void* stream);
+
+/*
+ * ts_rope_kv_write followed by ts_decode_attention, as one launch: the whole attention half of a
+ * pure-decode layer step (model/qwen2.py:26-28, :89 with ops/triton_rope.py:27-31,
+ * ops/triton_kv_write.py:28-35 and ops/triton_ops.py:60-71). qkv rows as for ts_rope_kv_write
+ * ([num_seqs, (H + 2 KVH) head_dim], 16-byte aligned, one decode row per sequence); q and the
+ * new k rows are rotated at positions[i] with exactly ts_rope's arithmetic, the rotated k and the
+ * v rows land in slot_mapping[i] and the attention sees them. The output and the caches are
+ * bit-identical to the two calls; qkv itself is left unrotated when the launch is fused (the
+ * rotated q and k exist only in registers and the cache) and rotated in place otherwise.
+ * Preconditions and workspace as ts_decode_attention_kv_write; fused for v2 / v3 with at most 16
+ * query heads per KV head and head_dim a multiple of 64, else ts_rope_kv_write runs first.
+ */
+int ts_decode_rope_kv_write_attention(int32_t version, void* qkv, int64_t qkv_stride,
+                                      const int64_t* positions, const float* cos_table,
+                                      const float* sin_table, int64_t max_position,
+                                      void* out, int64_t out_stride_t,
+                                      void* k_cache, void* v_cache, int64_t num_blocks,
+                                      const int64_t* slot_mapping,
+                                      const int32_t* block_tables, int64_t bt_stride,
+                                      int32_t max_blocks_per_seq, const int32_t* seq_lens,
+                                      int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
+                                      int32_t head_dim, float scale, int32_t max_seq_len,
+                                      int32_t partition, void* workspace, size_t workspace_bytes,
+                                      void* stream);
 
 /*
  * Chunked-prefill attention for sequences num_decode .. num_seqs-1 of the flat batch.

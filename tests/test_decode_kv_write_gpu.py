@@ -137,3 +137,89 @@ def test_fused_config2_graph_replays():
         torch.cuda.synchronize()
         assert torch.isfinite(scratch)
     assert torch.equal(kc2, kc) and torch.equal(vc2, vc)
+
+
+# ------------------------------------------------------------------------------------------
+# RoPE fused as well (ts_decode_rope_kv_write_attention)
+# ------------------------------------------------------------------------------------------
+def rope_tables(D, max_len, theta=1e6):
+    inv = 1.0 / (theta ** (torch.arange(0, D, 2, dtype=torch.float64) / D))
+    ang = torch.arange(max_len, dtype=torch.float64)[:, None] * inv[None, :]
+    return torch.cos(ang).float().to(DEV), torch.sin(ang).float().to(DEV)
+
+
+@pytest.mark.parametrize("H,KVH,D,version,positions", [
+    (12, 2, 128, None, "last"),     # Qwen2.5-1.5B heads, split-K, fused
+    (12, 2, 128, "v2", "last"),
+    (14, 2, 64, None, "last"),      # Qwen2.5-0.5B heads, fused
+    (8, 8, 256, None, "last"),      # head_dim 256, fused
+    (12, 2, 128, None, "wild"),     # positions not tied to seq_lens, some out of the table
+    (12, 2, 128, "v1", "last"),     # v1: rope_kv_write's own launch first
+    (32, 1, 128, None, "last"),     # two head groups per KV head: separate launches
+    (4, 2, 32, None, "last"),       # head_dim 32: rotation pairs span lanes, separate launches
+])
+def test_rope_fused_matches_separate_calls(H, KVH, D, version, positions):
+    g = torch.Generator().manual_seed(H * 10 + D)
+    ctx = synth.log_uniform_ints(48, 2, 3000, g)
+    ctx[5] = 1
+    case = decode_step(ctx, H, KVH, D, seed=H + D + 7, pad=(9,))
+    qkv, kc, vc, qsl, sl, bt, slots = case
+    meta = meta_for(qsl, sl, bt, slots)
+    cos, sin = rope_tables(D, 3000)
+    if positions == "last":
+        pos = (sl.long() - 1).clamp(min=0)
+    else:
+        pos = torch.randint(-5, 3100, (len(ctx),), generator=g)
+    pos = pos.to(DEV)
+    scale = D ** -0.5
+    # separate calls: rope + kv_write in one pass, then attention over the rotated q
+    qkv1 = qkv.to(DEV)
+    kc1, vc1 = kc.to(DEV), vc.to(DEV)
+    assert K.rope_kv_write_(qkv1, pos, cos, sin, H, KVH, D, kc1, vc1, meta.slot_mapping)
+    q1 = qkv1[:, :H * D].view(-1, H, D)
+    ref = K.paged_attention(q1, kc1, vc1, meta, scale, decode_version=version)
+    qkv2 = qkv.to(DEV)
+    kc2, vc2 = kc.to(DEV), vc.to(DEV)
+    out = K.decode_rope_kv_write_attention(qkv2, pos, cos, sin, H, KVH, D, kc2, vc2, meta, scale,
+                                           decode_version=version)
+    torch.cuda.synchronize()
+    assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2), "caches differ"
+    assert torch.equal(out, ref), "fused output differs from rope_kv_write + paged_attention"
+    assert torch.equal(out[9], torch.zeros_like(out[9]))
+
+
+def test_rope_fused_model_decode_step():
+    """A random-init model with head_dim 128 (and 64): a pure-decode step takes the fused launch
+    in every layer and must give the hidden states and caches of the separate calls."""
+    from turingserve_amd import get_ops
+    from turingserve_amd.metadata import BatchItem, InputBuilder, SeqState
+    from turingserve_amd.qwen2 import Qwen2Config, Qwen2Model, random_weights
+
+    for cfg in (Qwen2Config(512, 1024, 2, 4, 2, 1000, max_position_embeddings=4096),
+                Qwen2Config(448, 896, 2, 7, 1, 1000, max_position_embeddings=4096)):
+        w = random_weights(cfg, DEV, seed=3)
+        fused_ops = get_ops("hip")
+        plain_ops = get_ops("hip")
+        del plain_ops.decode_rope_kv_write_attention
+        fused = Qwen2Model(cfg, w, fused_ops, DEV, max_model_len=2048)
+        plain = Qwen2Model(cfg, w, plain_ops, DEV, max_model_len=2048)
+        nb = 400
+        kv1, kv2 = fused.new_kv_cache(nb), plain.new_kv_cache(nb)
+        items, free = [], list(range(1, nb))
+        for i in range(12):
+            L = 20 + 37 * i
+            s = SeqState([(7 * i + 3 * j) % 1000 for j in range(L)])
+            s.block_table = [free.pop() for _ in range(-(-L // 16))]
+            items.append(s)
+        with torch.inference_mode():
+            pre = InputBuilder(8192, 64, 32, DEV).build(
+                [BatchItem(s, 0, s.token_ids[:-1], "none") for s in items])
+            fused.forward(pre.input_ids, pre.positions, pre.meta, kv1)
+            plain.forward(pre.input_ids, pre.positions, pre.meta, kv2)
+            assert torch.equal(kv1, kv2)
+            dec = InputBuilder(256, 64, 32, DEV).build(
+                [BatchItem(s, len(s.token_ids) - 1, [s.token_ids[-1]], "last") for s in items])
+            h1 = fused.forward(dec.input_ids, dec.positions, dec.meta, kv1)
+            h2 = plain.forward(dec.input_ids, dec.positions, dec.meta, kv2)
+        torch.cuda.synchronize()
+        assert torch.equal(h1, h2) and torch.equal(kv1, kv2)

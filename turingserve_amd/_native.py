@@ -45,6 +45,10 @@ SIGNATURES = {
                                                     _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p,
                                                     _i64, _i32, _p, _i32, _i32, _i32, _i32, _f32,
                                                     _i32, _i32, _p, _sz, _p]),
+    "ts_decode_rope_kv_write_attention": (ctypes.c_int, [_i32, _p, _i64, _p, _p, _p, _i64, _p,
+                                                         _i64, _p, _p, _i64, _p, _p, _i64, _i32,
+                                                         _p, _i32, _i32, _i32, _i32, _f32, _i32,
+                                                         _i32, _p, _sz, _p]),
     "ts_prefill_attention": (ctypes.c_int, [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _i64,
                                             _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32,
                                             _f32, _p]),

@@ -54,16 +54,25 @@ static int decode_entry(int32_t version, const void* q, int64_t q_stride_t, int6
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (nr.k) {
     // The fused write needs the MFMA kernels with one head group per KV head (so the workgroup
-    // that writes a block is the only one reading it) and 16-byte row pieces; otherwise the
-    // rows go through kv_write's own launch first.
+    // that writes a block is the only one reading it) and 16-byte row pieces, the fused RoPE
+    // also a head_dim that keeps each rotation pair in one lane; otherwise the rows go through
+    // kv_write's (or rope_kv_write's) own launch first.
+    const bool rope = nr.cos_t != nullptr;
     const bool fused = p.version != TS_DECODE_V1 && num_heads / num_kv_heads <= 16 &&
                        head_dim % 8 == 0 && nr.k_st % 8 == 0 && nr.k_sh % 8 == 0 &&
                        nr.v_st % 8 == 0 && nr.v_sh % 8 == 0 && aligned(nr.k, 16) &&
-                       aligned(nr.v, 16) && aligned(k_cache, 16) && aligned(v_cache, 16);
+                       aligned(nr.v, 16) && aligned(k_cache, 16) && aligned(v_cache, 16) &&
+                       (!rope || head_dim % 64 == 0);
     if (!fused) {
-      st = ts_kv_write(nr.k, nr.v, nr.k_st, nr.k_sh, nr.v_st, nr.v_sh, const_cast<void*>(k_cache),
-                       const_cast<void*>(v_cache), num_blocks, nr.slots, num_seqs, num_kv_heads,
-                       head_dim, stream);
+      if (rope)
+        st = ts_rope_kv_write(nr.qkv, nr.qkv_st, nr.positions, nr.cos_t, nr.sin_t, nr.max_pos,
+                              num_seqs, num_heads, num_kv_heads, head_dim,
+                              const_cast<void*>(k_cache), const_cast<void*>(v_cache), num_blocks,
+                              nr.slots, stream);
+      else
+        st = ts_kv_write(nr.k, nr.v, nr.k_st, nr.k_sh, nr.v_st, nr.v_sh,
+                         const_cast<void*>(k_cache), const_cast<void*>(v_cache), num_blocks,
+                         nr.slots, num_seqs, num_kv_heads, head_dim, stream);
       if (st != TS_OK) return st;
       return decode_entry(version, q, q_stride_t, q_stride_h, out, out_stride_t, k_cache, v_cache,
                           num_blocks, block_tables, bt_stride, max_blocks_per_seq, seq_lens,
@@ -125,8 +134,41 @@ extern "C" int ts_decode_attention_kv_write(
              TS_ERR_INVALID_ARG, "decode_attention_kv_write: negative stride");
   const NewRows nr{static_cast<const half_t*>(k), static_cast<const half_t*>(v), k_stride_t,
                    k_stride_h, v_stride_t, v_stride_h, slot_mapping,
-                   num_blocks * (int64_t)kBlockSize};
+                   num_blocks * (int64_t)kBlockSize, nullptr, nullptr, nullptr, 0, nullptr, 0};
   return decode_entry(version, q, q_stride_t, q_stride_h, out, out_stride_t, k_cache, v_cache,
+                      num_blocks, block_tables, bt_stride, max_blocks_per_seq, seq_lens, num_seqs,
+                      num_heads, num_kv_heads, head_dim, scale, max_seq_len, partition, workspace,
+                      workspace_bytes, stream, nr);
+}
+
+extern "C" int ts_decode_rope_kv_write_attention(
+    int32_t version, void* qkv, int64_t qkv_stride, const int64_t* positions,
+    const float* cos_table, const float* sin_table, int64_t max_position, void* out,
+    int64_t out_stride_t, void* k_cache, void* v_cache, int64_t num_blocks,
+    const int64_t* slot_mapping, const int32_t* block_tables, int64_t bt_stride,
+    int32_t max_blocks_per_seq, const int32_t* seq_lens, int32_t num_seqs, int32_t num_heads,
+    int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seq_len, int32_t partition,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  TS_REQUIRE(num_seqs >= 0, TS_ERR_INVALID_ARG,
+             "decode_rope_kv_write_attention: num_seqs %d < 0", num_seqs);
+  if (num_seqs == 0) return TS_OK;
+  TS_REQUIRE(qkv && positions && cos_table && sin_table && slot_mapping && max_position > 0,
+             TS_ERR_INVALID_ARG, "decode_rope_kv_write_attention: null pointer or empty table");
+  TS_REQUIRE(num_heads > 0 && num_kv_heads > 0 && head_dim > 0 && head_dim % 8 == 0,
+             TS_ERR_INVALID_ARG, "decode_rope_kv_write_attention: bad heads or head_dim %d",
+             head_dim);
+  TS_REQUIRE(qkv_stride >= (int64_t)(num_heads + 2 * num_kv_heads) * head_dim &&
+                 qkv_stride % 8 == 0 && aligned(qkv, 16) && aligned(cos_table, 16) &&
+                 aligned(sin_table, 16),
+             TS_ERR_INVALID_ARG,
+             "decode_rope_kv_write_attention: qkv rows and tables must be 16-byte aligned");
+  half_t* base = static_cast<half_t*>(qkv);
+  const int64_t kv_off = (int64_t)num_heads * head_dim;
+  const NewRows nr{base + kv_off, base + kv_off + (int64_t)num_kv_heads * head_dim, qkv_stride,
+                   head_dim, qkv_stride, head_dim, slot_mapping,
+                   num_blocks * (int64_t)kBlockSize, positions, cos_table, sin_table,
+                   max_position, qkv, qkv_stride};
+  return decode_entry(version, qkv, qkv_stride, head_dim, out, out_stride_t, k_cache, v_cache,
                       num_blocks, block_tables, bt_stride, max_blocks_per_seq, seq_lens, num_seqs,
                       num_heads, num_kv_heads, head_dim, scale, max_seq_len, partition, workspace,
                       workspace_bytes, stream, nr);

@@ -29,6 +29,7 @@
 
 #include "common.h"
 #include "paged_kv.h"
+#include "rope.h"
 namespace ts {
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -235,16 +236,25 @@ struct DecodeLds {
   static constexpr int BYTES = MAP + (NW + 5) * 4;
 };
 
-// The step's new K/V rows (one per decode row), for the launch that also performs kv_write.
+// The step's new K/V rows (one per decode row), for the launch that also performs kv_write
+// (and, with cos_t set, the RoPE of q and of the new k rows first).
 struct NewRows {
   const half_t* k;
   const half_t* v;
   int64_t k_st, k_sh, v_st, v_sh;
   const int64_t* slots;     // slot_mapping [S] (-1: padding row, not written)
   int64_t num_slots;        // NB * 16: slots at or past it are not written (as kv_write)
+  // RoPE (ops/triton_rope.py:10-31): row s of q and k rotated at positions[s] with the fp32
+  // tables [max_pos, D / 2]; qkv / qkv_st / H describe the packed rows for the host's fallback.
+  const int64_t* positions;
+  const float* cos_t;
+  const float* sin_t;
+  int64_t max_pos;
+  void* qkv;
+  int64_t qkv_st;
 };
 
-template <int D, int NW, bool WRITE = false>
+template <int D, int NW, bool WRITE = false, bool ROPE = false>
 __device__ __forceinline__ void decode_mfma_body(
     const half_t* __restrict__ q, int64_t q_st, int64_t q_sh, half_t* __restrict__ out,
     int64_t o_st, const half_t* __restrict__ kc, const half_t* __restrict__ vc, int64_t NB,
@@ -310,14 +320,34 @@ __device__ __forceinline__ void decode_mfma_body(
     // pointers are the same restrict pointers the loads use, so the compiler orders them too.
     if (split_j == nsplit - 1) {
       const int64_t slot = nr.slots[s];
-      if (slot >= 0 && slot < nr.num_slots && tid < D / 4) {
+      if (slot >= 0 && slot < nr.num_slots) {
+        const int64_t row = (((slot >> 4) * KVH + kvh) * kBlockSize + (slot & 15)) * D;
+        const half_t* ksrc = nr.k + (int64_t)s * nr.k_st + (int64_t)kvh * nr.k_sh;
+        const half_t* vsrc = nr.v + (int64_t)s * nr.v_st + (int64_t)kvh * nr.v_sh;
         constexpr int PIECES = D / 8;              // 16-byte pieces per row
-        const int j = tid / PIECES, pc = tid % PIECES;   // j: 0 = K, 1 = V
-        const half_t* src = j ? nr.v + (int64_t)s * nr.v_st + (int64_t)kvh * nr.v_sh
-                              : nr.k + (int64_t)s * nr.k_st + (int64_t)kvh * nr.k_sh;
-        half_t* dst = const_cast<half_t*>(j ? vc : kc) +
-                      (((slot >> 4) * KVH + kvh) * kBlockSize + (slot & 15)) * D;
-        st<half8_t>(dst + 8 * pc, ld<half8_t>(src + 8 * pc));
+        constexpr int PK = ROPE ? D / 16 : PIECES; // threads writing K (with RoPE: 8 frequencies)
+        if (tid < PK) {
+          if constexpr (ROPE) {
+            // frequencies 8 tid .. 8 tid + 7: dims d0.. of the first half and d0 + D/2.. of the
+            // second, rotated as rope_kv_write_kernel rotates them
+            const int d0 = 8 * tid;
+            const float* cp = nr.cos_t + rope_row(nr.positions[s], nr.max_pos) * (D / 2) + d0;
+            const float* sp = nr.sin_t + (cp - nr.cos_t);
+            const half8_t x1 = ld<half8_t>(ksrc + d0), x2 = ld<half8_t>(ksrc + D / 2 + d0);
+            half4_t o1a, o2a, o1b, o2b;
+            rope4(lo4(x1), lo4(x2), ld<float4_t>(cp), ld<float4_t>(sp), o1a, o2a);
+            rope4(hi4(x1), hi4(x2), ld<float4_t>(cp + 4), ld<float4_t>(sp + 4), o1b, o2b);
+            half_t* krow = const_cast<half_t*>(kc) + row;
+            st<half8_t>(krow + d0, half8_t{o1a[0], o1a[1], o1a[2], o1a[3], o1b[0], o1b[1], o1b[2], o1b[3]});
+            st<half8_t>(krow + D / 2 + d0,
+                        half8_t{o2a[0], o2a[1], o2a[2], o2a[3], o2b[0], o2b[1], o2b[2], o2b[3]});
+          } else {
+            st<half8_t>(const_cast<half_t*>(kc) + row + 8 * tid, ld<half8_t>(ksrc + 8 * tid));
+          }
+        } else if (tid < PK + PIECES) {
+          const int pc = tid - PK;
+          st<half8_t>(const_cast<half_t*>(vc) + row + 8 * pc, ld<half8_t>(vsrc + 8 * pc));
+        }
       }
       __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
       __syncthreads();
@@ -344,6 +374,23 @@ __device__ __forceinline__ void decode_mfma_body(
       } else {
         const half4_t t = head_ok ? ld<half4_t>(qp + 4 * g) : half4_t{0, 0, 0, 0};
         qf[kk] = {t[0], t[1], t[2], t[3], 0, 0, 0, 0};
+      }
+    }
+    if constexpr (ROPE) {
+      // q rotated in registers, as rope_kernel rotates it in memory: lane (c, g) holds dims
+      // 32 kk + 8 g .. + 7, and dims d and d + D / 2 (kk and kk + KK / 2) are a rotation pair.
+      static_assert(KK % 2 == 0, "RoPE pairs must sit in one lane (head_dim a multiple of 64)");
+      const int64_t trow = rope_row(nr.positions[s], nr.max_pos) * (D / 2);
+#pragma unroll
+      for (int kk = 0; kk < KK / 2; ++kk) {
+        const float* cp = nr.cos_t + trow + 32 * kk + 8 * g;
+        const float* sp = nr.sin_t + trow + 32 * kk + 8 * g;
+        half4_t o1a, o2a, o1b, o2b;
+        rope4(lo4(qf[kk]), lo4(qf[kk + KK / 2]), ld<float4_t>(cp), ld<float4_t>(sp), o1a, o2a);
+        rope4(hi4(qf[kk]), hi4(qf[kk + KK / 2]), ld<float4_t>(cp + 4), ld<float4_t>(sp + 4), o1b,
+              o2b);
+        qf[kk] = half8_t{o1a[0], o1a[1], o1a[2], o1a[3], o1b[0], o1b[1], o1b[2], o1b[3]};
+        qf[kk + KK / 2] = half8_t{o2a[0], o2a[1], o2a[2], o2a[3], o2b[0], o2b[1], o2b[2], o2b[3]};
       }
     }
   }
@@ -479,7 +526,7 @@ __device__ __forceinline__ void decode_mfma_body(
   }
 }
 
-template <int D, int NW, bool WRITE = false>
+template <int D, int NW, bool WRITE = false, bool ROPE = false>
 __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
     const half_t* __restrict__ q, int64_t q_st, int64_t q_sh, half_t* __restrict__ out,
     int64_t o_st, const half_t* __restrict__ kc, const half_t* __restrict__ vc, int64_t NB,
@@ -488,7 +535,7 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
     int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
     float* __restrict__ ws_l, int* __restrict__ ws_cnt, const NewRows nr) {
   __shared__ __attribute__((aligned(16))) char lds[DecodeLds<D, NW>::BYTES];
-  decode_mfma_body<D, NW, WRITE>(q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks,
+  decode_mfma_body<D, NW, WRITE, ROPE>(q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks,
                                  seq_lens, S, H, KVH, G, HG, sl2, cap_blocks, part_blocks, nx,
                                  max_splits, ws_acc, ws_m, ws_l, ws_cnt, (int)blockIdx.x,
                                  (int)blockIdx.z, lds, nr);
@@ -662,7 +709,8 @@ static WsLayout ws_layout(const SplitPlan& p, int S, int H, int D) {
 }
 
 // With nr.k set (kv_write fused into the launch; v2 / v3 with one head group per KV head only)
-// the MFMA kernel first writes the new rows, as in decode_mfma_body.
+// the MFMA kernel first writes the new rows, as in decode_mfma_body; with nr.cos_t set too
+// (head_dim a multiple of 64) it also rotates q and the new k rows first.
 template <int D>
 static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, int64_t q_st,
                           int64_t q_sh, half_t* out, int64_t o_st, const half_t* kc,
@@ -671,6 +719,7 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
                           void* ws, const NewRows& nr = NewRows{}) {
   const int G = H / KVH;
   const bool write = nr.k != nullptr;
+  const bool rope = write && nr.cos_t != nullptr;     // only for head_dim % 64 == 0
   if (p.version == TS_DECODE_V1) {
     decode_v1_kernel<D><<<dim3(S, H), 64, 0, st>>>(q, q_st, q_sh, out, o_st, kc, vc, NB, bt,
                                                    bt_st, max_blocks, sl, H, KVH, scale_log2);
@@ -678,14 +727,20 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
   }
   const int HG = (G + 15) / 16;
   if (p.version == TS_DECODE_V2) {
-#define TS_V2_LAUNCH(W)                                                                          \
-  decode_mfma_kernel<D, kDecodeWaves, W><<<dim3(S, 1, KVH * HG), kDecodeWaves * 64, 0, st>>>(    \
+#define TS_V2_LAUNCH(W, R)                                                                       \
+  decode_mfma_kernel<D, kDecodeWaves, W, R><<<dim3(S, 1, KVH * HG), kDecodeWaves * 64, 0, st>>>( \
       q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,        \
       scale_log2, 0, 0, 0, 0, nullptr, nullptr, nullptr, nullptr, nr)
+    if constexpr (D % 64 == 0) {
+      if (rope) {
+        TS_V2_LAUNCH(true, true);
+        return;
+      }
+    }
     if (write)
-      TS_V2_LAUNCH(true);
+      TS_V2_LAUNCH(true, false);
     else
-      TS_V2_LAUNCH(false);
+      TS_V2_LAUNCH(false, false);
 #undef TS_V2_LAUNCH
     return;
   }
@@ -696,15 +751,24 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
   float* ws_l = reinterpret_cast<float*>(b + w.l);
   int* ws_cnt = reinterpret_cast<int*>(b + w.cnt);
   const int cap = p.cap_blocks < max_blocks ? p.cap_blocks : max_blocks;
-#define TS_V3_LAUNCH(W)                                                                          \
-  decode_mfma_kernel<D, kDecodeWaves, W><<<dim3(p.nslots, 1, KVH * HG), kDecodeWaves * 64, 0,    \
-                                           st>>>(                                                \
+#define TS_V3_LAUNCH(W, R)                                                                       \
+  decode_mfma_kernel<D, kDecodeWaves, W, R><<<dim3(p.nslots, 1, KVH * HG), kDecodeWaves * 64, 0, \
+                                              st>>>(                                             \
       q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,        \
       scale_log2, cap, p.part_blocks, p.nx, p.max_splits, ws_acc, ws_m, ws_l, ws_cnt, nr)
-  if (write)
-    TS_V3_LAUNCH(true);
-  else
-    TS_V3_LAUNCH(false);
+  bool launched = false;
+  if constexpr (D % 64 == 0) {
+    if (rope) {
+      TS_V3_LAUNCH(true, true);
+      launched = true;
+    }
+  }
+  if (!launched) {
+    if (write)
+      TS_V3_LAUNCH(true, false);
+    else
+      TS_V3_LAUNCH(false, false);
+  }
 #undef TS_V3_LAUNCH
   decode_merge_kernel<D><<<dim3(S, KVH * HG), 256, 0, st>>>(ws_acc, ws_m, ws_l, ws_cnt, out, o_st,
                                                              sl, H, G, HG, p.max_splits);

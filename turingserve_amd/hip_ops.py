@@ -24,7 +24,8 @@ from turingserve_amd.quant import LinearWeight
 __all__ = ["kv_write", "paged_attention", "linear", "lm_head_int8", "logits_int8", "w8a16_linear",
            "decode_attention_v1", "decode_attention_v2", "decode_attention_v3",
            "prefill_attention", "rmsnorm", "rmsnorm_residual", "rope_", "silu_mul", "w8a16_glu",
-           "gate_up_silu", "rope_kv_write_"]
+           "gate_up_silu", "rope_kv_write_", "decode_kv_write_attention",
+           "decode_rope_kv_write_attention"]
 
 DEFAULT_PARTITION = 0            # v3 split size when the caller names none: 0 = balanced
 
@@ -270,6 +271,63 @@ def decode_kv_write_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         _ptr(v_cache), NB, _ptr(bt), bt.stride(0), bt.shape[1], _ptr(sl), S, H, KVH, D,
         float(scale), int(meta.max_seq_len), int(part), _ptr(ws), ws_bytes, _stream(q)),
         "decode_kv_write_attention")
+    return out
+
+
+def decode_rope_kv_write_attention(qkv: torch.Tensor, positions: torch.Tensor,
+                                   cos: torch.Tensor, sin: torch.Tensor, H: int, KVH: int, D: int,
+                                   k_cache: torch.Tensor, v_cache: torch.Tensor, meta,
+                                   scale: float, decode_version: str | None = None,
+                                   partition: int | None = None) -> torch.Tensor | None:
+    """The attention half of a pure-decode layer step in one launch: rope_(qkv, ...), kv_write
+    of its k and v heads and paged_attention over the rotated q (model/qwen2.py:26-28, :89 with
+    ops/triton_ops.py:60-71); returns the same [T, H*D] and leaves the same caches. qkv is left
+    unrotated when the launch is fused (rotated in place when the library runs the rotation as its
+    own launch), so only the returned output and the caches are defined afterwards. Returns None,
+    having done nothing, when qkv's layout does not allow it (rows not 16-byte aligned): the
+    caller then makes the separate calls. Every row must be a decode row, with slot_mapping as
+    for decode_kv_write_attention."""
+    T = qkv.shape[0]
+    if not (qkv.dim() == 2 and qkv.stride(1) == 1 and qkv.stride(0) % 8 == 0 and
+            qkv.data_ptr() % 16 == 0 and k_cache.is_contiguous() and v_cache.is_contiguous()):
+        return None
+    out = torch.empty(T, H * D, dtype=qkv.dtype, device=qkv.device)
+    if T == 0:
+        return out
+    _check_gpu(qkv, positions, cos, sin, k_cache, v_cache)
+    NB, ckvh, cd = _check_cache(k_cache, v_cache)
+    _require(qkv.dtype == torch.float16 and qkv.shape[1] >= (H + 2 * KVH) * D,
+             "decode_rope_kv_write_attention: qkv must be fp16 [T, (H + 2 KVH) D]")
+    _require(ckvh == KVH and cd == D, "decode_rope_kv_write_attention: cache shape mismatch")
+    _require(cos.dtype == torch.float32 and sin.dtype == torch.float32 and cos.is_contiguous()
+             and sin.is_contiguous() and cos.shape == sin.shape and cos.shape[-1] == D // 2,
+             "decode_rope_kv_write_attention: tables must be contiguous fp32 [max_len, D / 2]")
+    _require(decode_version in N.DECODE_VERSIONS, f"unknown decode version {decode_version!r}")
+    S = meta.num_decode
+    _require(S == T and meta.seq_lens.shape[0] == S,
+             "decode_rope_kv_write_attention: every row must be a decode row")
+    bt, sl = _i32(meta.block_tables), _i32(meta.seq_lens)
+    pos = positions if (positions.dtype == torch.int64 and positions.is_contiguous()) \
+        else positions.to(torch.int64).contiguous()
+    sm = meta.slot_mapping
+    slots = sm if (sm.dtype == torch.int64 and sm.is_contiguous()) else sm.to(torch.int64).contiguous()
+    _require(slots.shape[0] >= T and pos.shape[0] >= T,
+             "decode_rope_kv_write_attention: slot_mapping / positions shorter than qkv")
+    if decode_version is None:
+        tv, tp = tuner.decode_choice(S, int(meta.max_seq_len))
+        if tv is not None:
+            decode_version = tv
+            partition = tp if partition is None else partition
+    code = N.DECODE_VERSIONS[decode_version]
+    part = (DEFAULT_PARTITION if partition is None else partition) if code in (0, 3) else 0
+    ws_bytes = N.lib().ts_decode_workspace_bytes(code, S, H, KVH, D, int(meta.max_seq_len), part,
+                                                 N.cu_count(qkv.device.index or 0))
+    ws = _workspace(ws_bytes, qkv.device)
+    N.check(N.lib().ts_decode_rope_kv_write_attention(
+        code, _ptr(qkv), qkv.stride(0), _ptr(pos), _ptr(cos), _ptr(sin), cos.shape[0], _ptr(out),
+        out.stride(0), _ptr(k_cache), _ptr(v_cache), NB, _ptr(slots), _ptr(bt), bt.stride(0),
+        bt.shape[1], _ptr(sl), S, H, KVH, D, float(scale), int(meta.max_seq_len), int(part),
+        _ptr(ws), ws_bytes, _stream(qkv)), "decode_rope_kv_write_attention")
     return out
 
 

@@ -39,6 +39,7 @@ def _hip() -> SimpleNamespace:
     ns.silu_mul = h.silu_mul
     ns.gate_up_silu = h.gate_up_silu
     ns.rope_kv_write_ = h.rope_kv_write_
+    ns.decode_rope_kv_write_attention = h.decode_rope_kv_write_attention
     return ns
 
 

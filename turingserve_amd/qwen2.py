@@ -135,8 +135,11 @@ class Qwen2Model:
         """q, k, v views of the rotated qkv activation, with the new K / V rows already in the
         layer's cache (model/qwen2.py:26-28 and :89: rope, then kv_write). A backend with
         rope_kv_write_ rotates and writes them in one pass."""
+        return self._rotate_write(self.ops.linear(x, lw.qkv), positions, k_cache, v_cache,
+                                  slot_mapping)
+
+    def _rotate_write(self, qkv, positions, k_cache, v_cache, slot_mapping):
         c = self.cfg
-        qkv = self.ops.linear(x, lw.qkv)
         fused = getattr(self.ops, "rope_kv_write_", None)
         args = (qkv, positions, self.rotary.cos, self.rotary.sin, c.num_heads, c.num_kv_heads,
                 c.head_dim)
@@ -164,6 +167,12 @@ class Qwen2Model:
         c, ops, w = self.cfg, self.ops, self.w
         h = w.embed[input_ids]
         residual = None
+        # A pure-decode step on a backend that fuses rope, kv_write and decode attention into one
+        # launch takes that path (same outputs and caches as the three calls).
+        fused_decode = getattr(ops, "decode_rope_kv_write_attention", None)
+        if fused_decode is not None and not (meta.num_decode == input_ids.shape[0]
+                                             and meta.seq_lens.shape[0] == meta.num_decode):
+            fused_decode = None
         for layer, lw in enumerate(w.layers):
             if residual is None:
                 residual = h
@@ -171,8 +180,19 @@ class Qwen2Model:
             else:
                 x, residual = ops.rmsnorm_residual(h, residual, lw.w_in, c.rms_norm_eps)
             k_cache, v_cache = kv_cache[layer, 0], kv_cache[layer, 1]
-            q, _, _ = self._qkv(x, lw, positions, k_cache, v_cache, meta.slot_mapping)
-            a = ops.paged_attention(q, k_cache, v_cache, meta, self.scale)
+            a = None
+            if fused_decode is not None:
+                qkv = ops.linear(x, lw.qkv)
+                a = fused_decode(qkv, positions, self.rotary.cos, self.rotary.sin, c.num_heads,
+                                 c.num_kv_heads, c.head_dim, k_cache, v_cache, meta, self.scale)
+                if a is None:                   # layout the fused launch does not take
+                    fused_decode = None
+                    q, _, _ = self._rotate_write(qkv, positions, k_cache, v_cache,
+                                                 meta.slot_mapping)
+                    a = ops.paged_attention(q, k_cache, v_cache, meta, self.scale)
+            if a is None:
+                q, _, _ = self._qkv(x, lw, positions, k_cache, v_cache, meta.slot_mapping)
+                a = ops.paged_attention(q, k_cache, v_cache, meta, self.scale)
             h = ops.linear(a, lw.o)
             x, residual = ops.rmsnorm_residual(h, residual, lw.w_post, c.rms_norm_eps)
             h = self._mlp(x, lw)
