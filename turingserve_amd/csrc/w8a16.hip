@@ -746,18 +746,33 @@ static int wide64_splits(int M, int N, int K, int cus) {
 // that most of their rows would be padding); else 128 x 64 tiles, or 128 x 32 tiles (four
 // workgroups per CU) when M is past 64 but 128 x 64 tiles would cover fewer than half the CUs
 // with no K split (short K): twice the workgroups for the same weights, which measured ~13 %
-// faster on the 1536 x 1536 and 2048 x 1536 products at M = 256 and the former at M = 560.
-// 128 x 32 tiles never split K by their own rule, and GLU mode plans them as 128 x 64.
+// faster on the 1536 x 1536 and 2048 x 1536 products at M = 256 and the former at M = 560;
+// for M <= 64 (past the streaming path) 128 x 32 tiles split over K when 128 x 64 tiles would
+// cover under a quarter of the CUs. 128 x 32 tiles never split K by their own rule (splits 0),
+// and GLU mode plans them as 128 x 64.
 static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int splits) {
   if (variant == kVarAuto) {
     const int64_t n_tiles = (N + 127) / 128;
     variant = use_small_path(M, N, K)                                       ? kVarStream
               : (M > 64 && n_tiles * ((M + 127) / 128) * 2 >= cus) ? kVarWide128
                                                                         : kVarWide64;
+    splits = 0;
     if (variant == kVarWide64 && M > 64 && n_tiles * ((M + 63) / 64) * 2 < cus &&
         wide64_splits(M, N, K, cus) == 1)
       variant = kVarWide32;
-    splits = 0;
+    if (variant == kVarWide64 && M <= 64 && n_tiles * ((M + 63) / 64) * 4 < cus) {
+      // Few rows and few columns (a decode step's projections): 128 x 32 tiles split over K
+      // until about one workgroup per CU, at most 8 ways and at least 6 K steps each (the
+      // reduction of M x N x 4-byte partials is cheap at this M). Measured at M = 48 and 64:
+      // 2048 x 1536 11.1 -> 8.8 us, 1536 x 1536 11.0 -> 8.6 us, 1536 x 8960 18.6 -> 14.4 us.
+      const int64_t tiles32 = n_tiles * ((M + 31) / 32);
+      const int nk = (K + kTileBK - 1) / kTileBK;
+      int64_t sp = (cus + tiles32 - 1) / tiles32;
+      sp = sp < 8 ? sp : 8;
+      sp = sp < nk / 6 ? sp : nk / 6;
+      variant = kVarWide32;
+      splits = sp > 1 ? (int)sp : 1;
+    }
   }
   GemmPlan p{variant == kVarStream, (M + 15) / 16, 128,
              variant == kVarWide128 ? 128 : (variant == kVarWide32 ? 32 : 64), 1, K};
