@@ -392,33 +392,17 @@ def bench_mixed(torch, synth, reps: int = 5):
     a prompt whose already-cached prefix is drawn lognormal with median 200 tokens (the
     configuration's prompt-length distribution). Timed eagerly (the serving path for mixed steps)
     and as a hipGraph replay (GPU time alone)."""
-    import random as _r
-
     from turingserve_amd import get_ops
-    from turingserve_amd.metadata import BatchItem, InputBuilder, SeqState
+    from turingserve_amd.metadata import InputBuilder
     from turingserve_amd.qwen2 import QWEN25_15B, Qwen2Model, random_weights
 
     dev = torch.device("cuda", 0)
     cfg = QWEN25_15B
-    g = torch.Generator().manual_seed(0)
-    ctx = synth.log_uniform_ints(48, 256, 4096, g)
-    prefix = int(min(3000, round(float(torch.empty(1).log_normal_(math.log(200), 0.8, generator=g)))))
+    items, nb, prefix = synth.config5_batch(cfg.vocab_size, seed=0)
     w = random_weights(cfg, dev, quantization="int8", init_std=0.02, seed=0)
-    model = Qwen2Model(cfg, w, get_ops("hip"), dev, max_model_len=8192)
-    nb = sum(-(-c // 16) for c in ctx) + -(-(prefix + 512) // 16) + 8
+    model = Qwen2Model(cfg, w, get_ops("hip"), max_model_len=8192)
     kv = model.new_kv_cache(nb)
     kv.normal_(0.0, 0.5)
-    rng = _r.Random(0)
-    free = list(range(1, nb))
-    rng.shuffle(free)
-    items = []
-    for c in ctx:
-        s = SeqState([rng.randrange(cfg.vocab_size) for _ in range(c)])
-        s.block_table = [free.pop() for _ in range(-(-c // 16))]
-        items.append(BatchItem(s, c - 1, [s.token_ids[-1]], "last"))
-    s = SeqState([rng.randrange(cfg.vocab_size) for _ in range(prefix + 512)])
-    s.block_table = [free.pop() for _ in range(-(-(prefix + 512) // 16))]
-    items.append(BatchItem(s, prefix, s.token_ids[prefix:], "last"))
     inp = InputBuilder(1024, 64, 512, dev).build(items)
     T = inp.input_ids.shape[0]
 
@@ -471,8 +455,8 @@ def bench_decode_model(torch, synth, reps: int = 10):
     w = random_weights(cfg, dev, quantization="int8", init_std=0.02, seed=0)
     ops_plain = get_ops("hip")
     del ops_plain.decode_rope_kv_write_attention
-    models = {"fused": Qwen2Model(cfg, w, get_ops("hip"), dev, max_model_len=8192),
-              "separate": Qwen2Model(cfg, w, ops_plain, dev, max_model_len=8192)}
+    models = {"fused": Qwen2Model(cfg, w, get_ops("hip"), max_model_len=8192),
+              "separate": Qwen2Model(cfg, w, ops_plain, max_model_len=8192)}
     nb = sum(-(-c // 16) for c in ctx) + 8
     kv = models["fused"].new_kv_cache(nb)
     kv.normal_(0.0, 0.5)

@@ -1,0 +1,61 @@
+"""The end-to-end greedy cases: tiny Qwen2 models whose next-token choices are decisive.
+
+The reference's tiny test models have g2 (4 query / 2 KV heads) and g7 (14 / 2) attention with
+head_dim 16 (scripts/make_tiny_model.py:27-31). With random weights and the full 151936-token
+vocabulary their fp16 logits tie exactly at some steps, so a free-running token comparison would
+only test tie-breaking. These cases keep the head shapes, use a 2048-token vocabulary, and fix the
+prompt seeds for which every sampled step of the reference twins' greedy run, on the CPU, has a
+top-2 logit gap of at least MIN_GAP_ULPS units in the last place (fp16) of the top logit; the seeds
+were chosen by scanning prompt seeds on the CPU. The CPU test re-checks that margin; the GPU test
+requires the hip backend's free-running tokens to equal the reference backend's on the GPU.
+"""
+
+from __future__ import annotations
+
+import math
+import random
+from dataclasses import dataclass
+
+from turingserve_amd.qwen2 import Qwen2Config
+
+VOCAB = 2048
+DECISIVE_G2 = Qwen2Config(64, 128, 2, 4, 2, VOCAB, max_position_embeddings=4096)
+DECISIVE_G7 = Qwen2Config(224, 448, 2, 14, 2, VOCAB, max_position_embeddings=4096)
+PROMPT_LENS = (7, 40, 130, 33, 90)
+NEW_TOKENS = 8
+BUDGET = 48              # tokens per step: the 130- and 90-token prompts are prefilled in chunks
+MAX_SEQS = 8
+NUM_BLOCKS = 300
+MIN_GAP_ULPS = 12        # checked on the CPU
+MIN_GAP_ULPS_GPU = 6     # precondition of the GPU comparison (the GPU twins round differently)
+
+
+@dataclass(frozen=True)
+class Case:
+    name: str
+    cfg: Qwen2Config
+    quantization: str     # "none" (fp16 linears) or "int8" (W8A16 linears)
+    prompt_seed: int
+    device_metadata: bool = False
+
+    def prompts(self) -> list[list[int]]:
+        r = random.Random(1000 * self.prompt_seed)
+        return [[r.randrange(VOCAB) for _ in range(n)] for n in PROMPT_LENS]
+
+
+CASES = [
+    Case("g2", DECISIVE_G2, "none", 62),
+    Case("g7", DECISIVE_G7, "none", 125, device_metadata=True),
+    Case("g2-int8", DECISIVE_G2, "int8", 85),
+    Case("g7-int8", DECISIVE_G7, "int8", 82, device_metadata=True),
+]
+
+
+def fp16_ulp(x: float) -> float:
+    """Unit in the last place of an fp16 normal number of magnitude |x|."""
+    return 2.0 ** (math.floor(math.log2(abs(x))) - 10)
+
+
+def gap_ulps(trace) -> list[float]:
+    """Top-2 gap of every sampled step in units of the top logit's fp16 ulp."""
+    return [gap / fp16_ulp(top) for *_, gap, top in trace]

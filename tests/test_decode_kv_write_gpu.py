@@ -201,8 +201,8 @@ def test_rope_fused_model_decode_step():
         fused_ops = get_ops("hip")
         plain_ops = get_ops("hip")
         del plain_ops.decode_rope_kv_write_attention
-        fused = Qwen2Model(cfg, w, fused_ops, DEV, max_model_len=2048)
-        plain = Qwen2Model(cfg, w, plain_ops, DEV, max_model_len=2048)
+        fused = Qwen2Model(cfg, w, fused_ops, max_model_len=2048)
+        plain = Qwen2Model(cfg, w, plain_ops, max_model_len=2048)
         nb = 400
         kv1, kv2 = fused.new_kv_cache(nb), plain.new_kv_cache(nb)
         items, free = [], list(range(1, nb))

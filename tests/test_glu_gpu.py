@@ -105,7 +105,7 @@ def test_glu_empty_and_model_routing():
     ops = get_ops("hip")
     h = torch.randn(11, TINY_G2.hidden_size, device=DEV).half()
     for quantization in ("int8", "none"):                 # fused call / the two calls
-        lw = random_weights(TINY_G2, DEV, seed=4, quantization=quantization).layers[0].gu
+        lw = random_weights(TINY_G2, DEV, seed=4, quantization=quantization).layers[0].gate_up_proj
         assert lw.quantized == (quantization == "int8")
         got = ops.gate_up_silu(h, lw)
         assert torch.equal(got, ops.silu_mul(ops.linear(h, lw)))

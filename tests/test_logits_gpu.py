@@ -70,12 +70,12 @@ def test_model_uses_fused_logits_with_int8_head():
     from turingserve_amd.qwen2 import TINY_G2, Qwen2Model, random_weights
 
     w = random_weights(TINY_G2, DEV, seed=3, int8_lm_head=True)
-    model = Qwen2Model(TINY_G2, w, get_ops("hip"), DEV)
+    model = Qwen2Model(TINY_G2, w, get_ops("hip"))
     hidden = torch.randn(12, TINY_G2.hidden_size, device=DEV).half()
     idx = torch.tensor([11, 3, 7], device=DEV)
     got = model.compute_logits(hidden, idx)
-    assert torch.equal(got, K.lm_head_int8(hidden[idx], *w.embed_q).float())
-    wq, sc = w.embed_q
+    assert torch.equal(got, K.lm_head_int8(hidden[idx], *w.lm_head_int8).float())
+    wq, sc = w.lm_head_int8
     ref = OQ.w8a16(hidden[idx].cpu().numpy(), wq.cpu().numpy(), sc.float().cpu().numpy(), None,
                    np.float64)
     out = got.cpu().numpy()

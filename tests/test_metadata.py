@@ -1,16 +1,18 @@
-"""Host-side metadata (CPU): the vectorised builder equals the straightforward one on random plans
-(the reference's tests/correctness/test_paged_engine.py:125-152), slots follow the closed form, and
-the decode-row rule of runner/input_builder.py:41-48 holds."""
+"""Host-side metadata (CPU): the vectorised one-copy builder equals a straightforward per-token
+restatement of the contract on random plans (the reference's check of its two builders,
+tests/correctness/test_paged_engine.py:125-152), slots follow the closed form, and the decode-row
+rule of runner/input_builder.py:41-48 holds."""
 
 from __future__ import annotations
 
 import random
 
 import numpy as np
+import pytest
 import torch
 
 from oracle import paged as OP
-from turingserve_amd.metadata import BatchItem, InputBuilder, SeqState, build_simple, num_decode_rows
+from turingserve_amd.metadata import BatchItem, InputBuilder, SeqState, num_decode_rows
 
 
 class Blocks:
@@ -29,7 +31,31 @@ class Blocks:
         seq.block_table = []
 
 
-def test_vectorized_builder_equals_simple_builder():
+def per_token(items):
+    """The contract written out token by token: lists of ids, positions, slots, query_start_loc,
+    seq_lens, zero-padded tables, sample rows, and num_decode."""
+    ids, pos, slot, qsl, sl, bt, smp = [], [], [], [0], [], [], []
+    for it in items:
+        table = it.seq.block_table
+        for j, tok in enumerate(it.tokens):
+            p = it.start + j
+            ids.append(tok)
+            pos.append(p)
+            slot.append(table[p // 16] * 16 + p % 16)
+            if it.sample == "all" or (it.sample == "last" and j == len(it.tokens) - 1):
+                smp.append(len(ids) - 1)
+        qsl.append(len(ids))
+        sl.append(it.start + len(it.tokens))
+        bt.append(list(table))
+    width = max(1, max(len(t) for t in bt))
+    bt = [t + [0] * (width - len(t)) for t in bt]
+    nd = 0
+    while nd < len(items) and len(items[nd].tokens) == 1 and items[nd].sample != "all":
+        nd += 1
+    return ids, pos, slot, qsl, sl, bt, smp, nd
+
+
+def test_vectorized_builder_equals_per_token_contract():
     rng = random.Random(0)
     builder = InputBuilder(2048, 16, 128, "cpu")
     blocks = Blocks(400)
@@ -44,21 +70,21 @@ def test_vectorized_builder_equals_simple_builder():
             items.append(BatchItem(s, start, s.token_ids[start:start + n],
                                    rng.choice(["last", "none", "all"])))
         items.sort(key=lambda it: len(it.tokens) != 1)
-        a, b = build_simple(items, "cpu"), builder.build(items)
-        assert torch.equal(a.input_ids, b.input_ids) and torch.equal(a.positions, b.positions)
-        assert torch.equal(a.meta.slot_mapping, b.meta.slot_mapping)
-        assert torch.equal(a.meta.query_start_loc, b.meta.query_start_loc)
-        assert torch.equal(a.meta.seq_lens, b.meta.seq_lens)
-        w = a.meta.block_tables.shape[1]
-        assert torch.equal(a.meta.block_tables, b.meta.block_tables[:, :w])
-        assert torch.equal(a.sample_indices, b.sample_indices)
-        assert a.meta.num_decode == b.meta.num_decode
-        assert a.meta.max_query_len == b.meta.max_query_len
-        assert a.meta.max_seq_len == b.meta.max_seq_len
-        for it in items:
+        ids, pos, slot, qsl, sl, bt, smp, nd = per_token(items)
+        b = builder.build(items)
+        m = b.meta
+        assert b.input_ids.dtype == b.positions.dtype == m.slot_mapping.dtype == torch.int64
+        assert m.query_start_loc.dtype == m.seq_lens.dtype == m.block_tables.dtype == torch.int32
+        assert b.sample_indices.dtype == torch.int64
+        assert b.input_ids.tolist() == ids and b.positions.tolist() == pos
+        assert m.slot_mapping.tolist() == slot and m.query_start_loc.tolist() == qsl
+        assert m.seq_lens.tolist() == sl and m.block_tables.tolist() == bt
+        assert b.sample_indices.tolist() == smp and m.num_decode == nd
+        assert m.max_query_len == max(len(it.tokens) for it in items)
+        assert m.max_seq_len == max(sl) and m.max_prefill_seq_len == max(sl[nd:], default=0)
+        for i, it in enumerate(items):
             want = OP.slot_mapping(it.seq.block_table, np.arange(it.start, it.start + len(it.tokens)))
-            lo = int(a.meta.query_start_loc[items.index(it)])
-            assert a.meta.slot_mapping[lo:lo + len(it.tokens)].tolist() == want.tolist()
+            assert m.slot_mapping[qsl[i]:qsl[i + 1]].tolist() == want.tolist()
             blocks.release(it.seq)
 
 
@@ -105,7 +131,7 @@ def _expand(words: np.ndarray, B: int, T: int, width: int):
     return ids, pos, slot, qsl, sl, bt, smp
 
 
-def test_pack_step_upload_expands_to_the_simple_builder():
+def test_pack_step_upload_expands_to_the_per_token_contract():
     from turingserve_amd.metadata import pack_step
 
     rng = random.Random(1)
@@ -123,12 +149,27 @@ def test_pack_step_upload_expands_to_the_simple_builder():
         items.sort(key=lambda it: len(it.tokens) != 1)
         words, T, NB, S = pack_step(items)
         assert words.dtype == np.int32 and words.size == 5 * len(items) + T + NB
-        a = build_simple(items, "cpu")
-        width = a.meta.block_tables.shape[1]
-        ids, pos, slot, qsl, sl, bt, smp = _expand(words, len(items), T, width)
-        assert ids == a.input_ids.tolist() and pos == a.positions.tolist()
-        assert slot == a.meta.slot_mapping.tolist() and qsl == a.meta.query_start_loc.tolist()
-        assert sl == a.meta.seq_lens.tolist() and bt == a.meta.block_tables.tolist()
-        assert smp == a.sample_indices.tolist() and S == len(smp)
+        want = per_token(items)
+        width = len(want[5][0])
+        assert _expand(words, len(items), T, width) == want[:7] and S == len(want[6])
         for it in items:
             blocks.release(it.seq)
+
+
+def test_position_past_the_table_is_an_error():
+    b = InputBuilder(64, 4, 8, "cpu")
+    s = SeqState(list(range(40)), [7])
+    with pytest.raises(ValueError, match="past its 1-block table"):
+        b.build([BatchItem(s, 14, list(range(14, 18)), "all")])
+
+
+def test_one_upload_holds_every_array():
+    """Every tensor of the step is a view of the builder's one device arena."""
+    b = InputBuilder(64, 4, 8, "cpu")
+    s = SeqState(list(range(20)), [3, 4])
+    inp = b.build([BatchItem(s, 0, list(range(20)), "last")])
+    base = b._arena.untyped_storage().data_ptr()
+    for t in (inp.input_ids, inp.positions, inp.sample_indices, inp.meta.slot_mapping,
+              inp.meta.query_start_loc, inp.meta.seq_lens, inp.meta.block_tables):
+        assert t.untyped_storage().data_ptr() == base
+    assert inp.meta.slot_mapping.tolist() == [3 * 16 + p for p in range(16)] + [4 * 16 + p for p in range(4)]

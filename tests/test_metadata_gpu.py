@@ -1,7 +1,7 @@
 """Device-side step metadata (ts_step_metadata through DeviceInputBuilder) on the GPU: equal, row
-for row, to the host builder the reference uses (runner/input_builder.py:81-150, restated by
-InputBuilder and pinned on the CPU against build_simple), including the padding rows a captured
-decode graph expects (runner/cuda_graphs.py:62-78), and an engine driven by it generates the same
+for row, to the host builder (InputBuilder, pinned on the CPU against a per-token restatement of
+the contract of runner/input_builder.py:41-150), including the padding rows a captured decode
+graph expects (runner/cuda_graphs.py:62-78), and an engine driven by it generates the same
 tokens."""
 
 from __future__ import annotations
@@ -49,8 +49,9 @@ def test_device_builder_equals_host_builder():
                      (a.meta.seq_lens, b.meta.seq_lens), (a.meta.block_tables, b.meta.block_tables),
                      (a.sample_indices, b.sample_indices)):
             assert x.dtype == y.dtype and torch.equal(x, y)
-        assert (a.meta.num_decode, a.meta.max_query_len, a.meta.max_seq_len) == \
-            (b.meta.num_decode, b.meta.max_query_len, b.meta.max_seq_len)
+        assert (a.meta.num_decode, a.meta.max_query_len, a.meta.max_seq_len,
+                a.meta.max_prefill_seq_len) == (b.meta.num_decode, b.meta.max_query_len,
+                                                b.meta.max_seq_len, b.meta.max_prefill_seq_len)
         for it in items:
             blocks.release(it.seq)
 
@@ -92,7 +93,7 @@ def test_engine_with_device_metadata_generates_the_same_tokens():
     from turingserve_amd.qwen2 import TINY_G2, Qwen2Model, random_weights
 
     w = random_weights(TINY_G2, DEV, seed=1)
-    model = Qwen2Model(TINY_G2, w, get_ops("hip"), DEV)
+    model = Qwen2Model(TINY_G2, w, get_ops("hip"))
     rng = random.Random(3)
     prompts = [[rng.randrange(1000) for _ in range(rng.randint(3, 40))] for _ in range(6)]
     kw = dict(max_num_batched_tokens=48, max_num_seqs=8, graph_sizes=(1, 2, 4, 8))

@@ -11,7 +11,7 @@ import torch
 
 from oracle import paged as OP
 from turingserve_amd import hip_ops as K
-from turingserve_amd.qwen2 import RotaryCache
+from turingserve_amd.qwen2 import rope_tables
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -29,13 +29,13 @@ def test_rope_kv_write_equals_rope_then_kv_write(H, KVH, D, T):
     if T > 1:
         slots[1] = NB * 16 + 5                        # out of range: skipped like -1
     slots = slots.to(DEV)
-    rot = RotaryCache(D, 1e6, 4096, DEV)
+    cos, sin = rope_tables(D, 1e6, 4096, DEV)
     kc = torch.randn(NB, KVH, 16, D, generator=g).half().to(DEV)
     vc = torch.randn(NB, KVH, 16, D, generator=g).half().to(DEV)
     qkv1, kc1, vc1 = qkv.clone(), kc.clone(), vc.clone()
-    assert K.rope_kv_write_(qkv1, pos, rot.cos, rot.sin, H, KVH, D, kc1, vc1, slots)
+    assert K.rope_kv_write_(qkv1, pos, cos, sin, H, KVH, D, kc1, vc1, slots)
     qkv2, kc2, vc2 = qkv.clone(), kc.clone(), vc.clone()
-    K.rope_(qkv2, pos, rot.cos, rot.sin, H, KVH, D)
+    K.rope_(qkv2, pos, cos, sin, H, KVH, D)
     k2 = qkv2[:, H * D:(H + KVH) * D].view(T, KVH, D)
     v2 = qkv2[:, (H + KVH) * D:].view(T, KVH, D)
     K.kv_write(k2, v2, kc2, vc2, slots)
@@ -49,12 +49,12 @@ def test_rope_kv_write_equals_rope_then_kv_write(H, KVH, D, T):
 
 def test_rope_kv_write_declines_unaligned_rows():
     H, KVH, D = 4, 2, 16
-    rot = RotaryCache(D, 1e6, 64, DEV)
+    cos, sin = rope_tables(D, 1e6, 64, DEV)
     base = torch.zeros(3, (H + 2 * KVH) * D + 4, dtype=torch.float16, device=DEV)
     qkv = base[:, 4:]                                 # rows start 8 bytes past 16-byte alignment
     kc = torch.zeros(4, KVH, 16, D, dtype=torch.float16, device=DEV)
     before = qkv.clone()
-    assert not K.rope_kv_write_(qkv, torch.zeros(3, dtype=torch.int64, device=DEV), rot.cos,
-                                rot.sin, H, KVH, D, kc, kc.clone(),
+    assert not K.rope_kv_write_(qkv, torch.zeros(3, dtype=torch.int64, device=DEV), cos,
+                                sin, H, KVH, D, kc, kc.clone(),
                                 torch.zeros(3, dtype=torch.int64, device=DEV))
     assert torch.equal(qkv, before)                   # declined: nothing was done

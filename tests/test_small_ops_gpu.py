@@ -15,7 +15,7 @@ import torch
 from turingserve_amd import get_ops
 from turingserve_amd import hip_ops as H
 from turingserve_amd import reference_ops as R
-from turingserve_amd.qwen2 import RotaryCache
+from turingserve_amd.qwen2 import rope_tables
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -72,17 +72,17 @@ def test_rmsnorm_strided_rows_and_plain_entry():
                                         (3, 2, 1, 8)])
 def test_rope_matches_twin_in_place(T, Hq, KVH, D):
     g = torch.Generator(device=DEV).manual_seed(T + D)
-    rot = RotaryCache(D, 1e6, 4096, DEV)
+    cos, sin = rope_tables(D, 1e6, 4096, DEV)
     qkv = (torch.randn(T, (Hq + 2 * KVH) * D, generator=g, device=DEV)).half()
     pos = torch.randint(0, 4096, (T,), generator=g, device=DEV)
     ours, twin = qkv.clone(), qkv.clone()
-    H.rope_(ours, pos, rot.cos, rot.sin, Hq, KVH, D)
-    R.rope_(twin, pos, rot.cos, rot.sin, Hq, KVH, D)
+    H.rope_(ours, pos, cos, sin, Hq, KVH, D)
+    R.rope_(twin, pos, cos, sin, Hq, KVH, D)
     nqk = (Hq + KVH) * D
     assert torch.equal(ours[:, nqk:], qkv[:, nqk:]), "v heads must be untouched"
     # float64 restatement of the twin's fp16 arithmetic: tables, products and sums each rounded
-    c = rot.cos[pos].half().double()[:, None, :]
-    s = rot.sin[pos].half().double()[:, None, :]
+    c = cos[pos].half().double()[:, None, :]
+    s = sin[pos].half().double()[:, None, :]
     qk = qkv[:, :nqk].view(T, Hq + KVH, D).double()
     x1, x2 = qk[..., : D // 2], qk[..., D // 2:]
     # (fp16 products are exact in float64; each sum is formed in fp32, then rounded to fp16,
@@ -95,15 +95,15 @@ def test_rope_matches_twin_in_place(T, Hq, KVH, D):
 
 
 def test_rope_position_zero_is_identity_and_clamps():
-    rot = RotaryCache(128, 1e6, 64, DEV)
+    cos, sin = rope_tables(128, 1e6, 64, DEV)
     qkv = torch.randn(4, 16 * 128, device=DEV).half()
     ours = qkv.clone()
-    H.rope_(ours, torch.zeros(4, dtype=torch.int64, device=DEV), rot.cos, rot.sin, 12, 2, 128)
+    H.rope_(ours, torch.zeros(4, dtype=torch.int64, device=DEV), cos, sin, 12, 2, 128)
     assert torch.equal(ours, qkv)                        # cos 0 = 1, sin 0 = 0
     # positions past the table are clamped to its last row instead of reading past it
     a, b = qkv.clone(), qkv.clone()
-    H.rope_(a, torch.full((4,), 63, dtype=torch.int64, device=DEV), rot.cos, rot.sin, 12, 2, 128)
-    H.rope_(b, torch.full((4,), 10_000, dtype=torch.int64, device=DEV), rot.cos, rot.sin, 12, 2, 128)
+    H.rope_(a, torch.full((4,), 63, dtype=torch.int64, device=DEV), cos, sin, 12, 2, 128)
+    H.rope_(b, torch.full((4,), 10_000, dtype=torch.int64, device=DEV), cos, sin, 12, 2, 128)
     assert torch.equal(a, b)
 
 

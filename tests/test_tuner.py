@@ -1,6 +1,6 @@
-"""The variant-selection table on the CPU (the reference's tuning cache, autopilot/tuner.py:
-56-134): JSON round trip, round-up bucket lookup, the choices the ops take from it, the cache
-files, and the library's variant-aware size function."""
+"""The variant-selection table on the CPU (the role of the reference's tuning cache,
+autopilot/tuner.py:56-134): JSON round trip, round-up bucket lookup, the choices the ops take from
+it, the cache files, and the library's variant-aware size function."""
 
 from __future__ import annotations
 
@@ -25,11 +25,14 @@ def test_table_round_trip_and_round_up_lookup():
     t.set("decode", (4, 4096), {"version": "v3", "partition": 512})
     t.set("decode", (64, 1024), {"version": "v2", "partition": 0})
     u = T.VariantTable.from_json(t.to_json())
-    assert u.tables == t.tables and u.meta == {"gpu": "x"}
+    assert u.records("decode") == t.records("decode") and u.meta == {"gpu": "x"}
+    assert u.to_json() == t.to_json()
     assert u.lookup("decode", (3, 900)) == {"version": "v3", "partition": 0}
     assert u.lookup("decode", (4, 1025)) == {"version": "v3", "partition": 512}
     assert u.lookup("decode", (5, 100)) == {"version": "v2", "partition": 0}
     assert u.lookup("decode", (65, 100)) is None and u.lookup("w8a16", (1, 1, 1)) is None
+    with pytest.raises(ValueError):
+        T.VariantTable.from_json('{"tables": {}}')            # another layout
 
 
 def test_choices_follow_the_active_table():
@@ -38,26 +41,32 @@ def test_choices_follow_the_active_table():
     t = T.VariantTable()
     t.set("w8a16", (2048, 1536, 768), {"variant": 2, "splits": 2})
     t.set("w8a16", (2048, 1536, 32), {"variant": 1, "splits": 4})
+    t.set("w8a16", (2048, 1536, 64), {"variant": 1, "splits": 1})
     t.set("decode", (8, 4096), {"version": "v3", "partition": 256})
     T.set_active(t)
     assert T.w8a16_choice(2048, 1536, 560) == (2, 2)          # 560 rounds up to the 768 bucket
     assert T.w8a16_choice(2048, 1536, 20) == (1, 4)
+    assert T.w8a16_choice(2048, 1536, 32) == (1, 4)
+    assert T.w8a16_choice(2048, 1536, 40) == (0, 0)           # streaming cannot take M = 40
     assert T.w8a16_choice(2048, 1536, 1000) == (0, 0)         # bucket 1024 not recorded
     assert T.w8a16_choice(1536, 1536, 560) == (0, 0)          # other shape
     assert T.decode_choice(5, 3000) == ("v3", 256)
 
 
 def test_cache_files(tmp_path):
-    key = T.cache_key("AMD Instinct MI355X", 256, "qwen2.5-1.5b/int8", "turingserve_hip 0.1.0",
-                      "2.10.0+rocm7.0")
-    assert "/" not in key and " " not in key and key.endswith(".json")
+    name = T.cache_file_name("AMD Instinct MI355X", 256, "qwen2.5-1.5b/int8",
+                             "turingserve_hip 0.1.0", "2.10.0+rocm7.0")
+    assert "/" not in name and " " not in name and name.endswith(".json")
+    assert name != T.cache_file_name("AMD Instinct MI355X", 256, "qwen2.5-1.5b/int8",
+                                     "turingserve_hip 0.1.1", "2.10.0+rocm7.0")
     t = T.VariantTable()
     t.set("w8a16", (8, 8, 1), {"variant": 3, "splits": 1})
-    path = T.save_cache(str(tmp_path), key, t)
-    assert T.load_cache(str(tmp_path), key).tables == t.tables
+    path = T.store_table(str(tmp_path), name, t)
+    assert T.load_table(str(tmp_path), name).records("w8a16") == t.records("w8a16")
+    assert sorted(p.name for p in tmp_path.iterdir()) == [name]     # no temporary left behind
     open(path, "w").write("{not json")
-    assert T.load_cache(str(tmp_path), key) is None
-    assert T.load_cache(str(tmp_path), "missing.json") is None
+    assert T.load_table(str(tmp_path), name) is None
+    assert T.load_table(str(tmp_path), "missing.json") is None
 
 
 def test_variant_workspace_sizes_and_checks():

@@ -55,11 +55,11 @@ def test_tuned_w8a16_table_is_followed():
     table = T.tune_w8a16(torch, shapes, ms, DEV)
     for (N, Kd) in shapes:
         for M in ms:
-            c = table.tables["w8a16"][f"{N},{Kd},{M}"]
+            c = table.records("w8a16")[(N, Kd, M)]
             assert (c["variant"], c["splits"]) in T.w8a16_candidates(M) and c["us"] > 0
     T.set_active(table)
     (x, wq, sc, b), _ = _problem(560, 1536, 8960, seed=1)
-    c = table.tables["w8a16"]["1536,8960,768"]                    # M = 560 rounds up to 768
+    c = table.records("w8a16")[(1536, 8960, 768)]                 # M = 560 rounds up to 768
     assert T.w8a16_choice(1536, 8960, 560) == (c["variant"], c["splits"])
     assert torch.equal(K.w8a16_linear(x, wq, sc, b),
                        K.w8a16_linear(x, wq, sc, b, cfg=(c["variant"], c["splits"])))

@@ -3,8 +3,8 @@
 Restates the parts of the reference's engine that shape the kernels' inputs: a block allocator
 that never hands out the null block 0 (kv/block_allocator.py:16-62), continuous batching with
 decodes scheduled first and prompts prefilled in chunks under a token budget
-(scheduler/scheduler.py:65-130), the vectorised input builder (runner/input_builder.py:105-150)
-and graph replay of pure-decode steps (runner/model_runner.py:20-28). Sampling is greedy argmax.
+(scheduler/scheduler.py:65-130), an input builder per step (host or device) and graph replay of
+pure-decode steps (runner/model_runner.py:20-28). Sampling is greedy argmax.
 """
 
 from __future__ import annotations
@@ -13,7 +13,7 @@ from dataclasses import dataclass, field
 
 import torch
 
-from turingserve_amd.graphs import HipGraphRunner
+from turingserve_amd.graphs import DecodeGraphs
 from turingserve_amd.metadata import (BatchItem, DeviceInputBuilder, InputBuilder, SeqState,
                                       num_decode_rows)
 
@@ -41,7 +41,6 @@ class Request:
     prompt: list[int]
     max_tokens: int
     index: int = 0
-    force: list[int] | None = None
     seq: SeqState = field(init=False)
     computed: int = 0
     output: list[int] = field(default_factory=list)
@@ -69,11 +68,12 @@ class GreedyEngine:
         self.builder = make(max_num_batched_tokens, max_num_seqs, self.max_blocks, model.device)
         self.graphs = None
         if graph_sizes:
-            self.graphs = HipGraphRunner(model, self.kv, tuple(graph_sizes), self.max_blocks,
-                                         max_model_len, model.device)
+            self.graphs = DecodeGraphs(model, self.kv, graph_sizes, self.max_blocks, max_model_len)
             self.graphs.capture()
-        self.graph_steps = 0
-        self.trace: list[tuple[int, int, int, float]] = []   # (request, index, argmax, top-2 gap)
+        self.graph_steps = 0            # pure-decode steps replayed from a captured graph
+        self.mixed_steps = 0            # steps holding decode rows and prompt chunks together
+        # (request, output index, argmax, top-2 logit gap, top logit) per sampled token
+        self.trace: list[tuple[int, int, int, float, float]] = []
 
     def _schedule(self, running: list[Request]) -> list[tuple[Request, BatchItem]]:
         """Decodes first (one token each), then prompt chunks while the token budget lasts."""
@@ -101,38 +101,33 @@ class GreedyEngine:
     def step(self, running: list[Request]) -> None:
         sched = self._schedule(running)
         items = [it for _, it in sched]
-        pure_decode = num_decode_rows(items) == len(items) and all(it.sample == "last" for it in items)
-        if pure_decode and self.graphs is not None and self.graphs.can_replay(len(items)):
-            if self.device_metadata:
-                logits = self.graphs.replay_items(items, self.builder)
-            else:
-                logits = self.graphs.replay(self.builder.build(items), len(items))
+        nd = num_decode_rows(items)
+        pure_decode = nd == len(items) and all(it.sample == "last" for it in items)
+        self.mixed_steps += int(0 < nd < len(items))
+        if pure_decode and self.graphs is not None and self.graphs.size_for(len(items)):
+            logits = self.graphs.run(items, self.builder if self.device_metadata else None)
             self.graph_steps += 1
         else:
             inp = self.builder.build(items)
             hidden = self.model.forward(inp.input_ids, inp.positions, inp.meta, self.kv)
             logits = self.model.compute_logits(hidden, inp.sample_indices)
         top = logits.topk(2, dim=-1)
-        gaps = (top.values[:, 0] - top.values[:, 1]).tolist()
-        next_ids = top.indices[:, 0].tolist()          # the step's one device -> host sync
+        vals, next_ids = top.values.cpu(), top.indices[:, 0].tolist()   # the step waits here
+        best, gaps = vals[:, 0].tolist(), (vals[:, 0] - vals[:, 1]).tolist()
         k = 0
         for r, it in sched:
             r.computed += len(it.tokens)
             if it.sample == "last":
                 tok = int(next_ids[k])
-                self.trace.append((r.index, len(r.output), tok, float(gaps[k])))
-                if r.force is not None:                 # teacher forcing: follow a given sequence
-                    tok = r.force[len(r.output)]
+                self.trace.append((r.index, len(r.output), tok, float(gaps[k]), float(best[k])))
                 k += 1
                 r.output.append(tok)
                 r.seq.token_ids.append(tok)
 
-    def generate(self, prompts: list[list[int]], max_tokens: int,
-                 force: list[list[int]] | None = None) -> list[list[int]]:
-        """Greedy outputs; with `force`, request i appends force[i] instead of its own argmax
-        (teacher forcing) while `trace` still records every argmax and its top-2 gap."""
-        reqs = [Request(p, max_tokens, i, None if force is None else force[i])
-                for i, p in enumerate(prompts)]
+    def generate(self, prompts: list[list[int]], max_tokens: int) -> list[list[int]]:
+        """Greedy outputs of every prompt; `trace` records each sampled argmax with its top-2
+        gap and top logit."""
+        reqs = [Request(p, max_tokens, i) for i, p in enumerate(prompts)]
         running = list(reqs)
         while running:
             self.step(running)

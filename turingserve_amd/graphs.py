@@ -1,92 +1,133 @@
-"""hipGraph capture and replay of pure-decode steps (runner/cuda_graphs.py:15-78).
+"""hipGraph replay of pure-decode steps (the role of runner/cuda_graphs.py:15-78).
 
-A graph per batch size B is captured over static input buffers; replay copies the n real decode
-rows in and pads up to the captured size with padding rows (slot -1 so kv_write skips them,
-seq_len 0 so attention writes zeros, token/position 0, zeroed block tables). Inside a graph
-max_seq_len = max_model_len, which fixes the split-K grid of the decode kernel. Nothing captured
-allocates outside the graph pool or synchronises with the host; the decode kernels run with the
-library's workspace from the same pool. Graphs are captured after an eager warm-up of every
-size, largest first, sharing one memory pool.
+One static decode batch lives in a single device byte arena: typed views for the token ids,
+positions, slots, seq_lens, block tables (the rows a step changes, laid out first and contiguous)
+and for query_start_loc and the sample rows (written once: every decode row is its own sequence
+and samples itself). A graph is captured per batch size of the ladder, each over the first B rows
+of those views. A step refills the changing rows in one go, either from the host (numpy into a
+pinned mirror of the arena, then one host-to-device copy) or on the device
+(``DeviceInputBuilder.build_into``, one upload and one launch), then replays the smallest graph
+that holds it. Rows past the step's sequences are padding: slot -1 (kv_write skips it), seq_len 0
+(attention writes zeros), token and position 0, an all-zero table row.
+
+Inside a graph the decode kernels take the balanced split (its plan depends on the batch size
+and the device, not on the lengths), so one graph serves every context length up to the table
+width. Nothing captured synchronises with the host or allocates outside the graphs' shared pool.
 """
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 
-from turingserve_amd.metadata import AttentionMetadata, ModelInput
+from turingserve_amd.metadata import AttentionMetadata, BatchItem, _arena_bytes, _carve
 
 
-class HipGraphRunner:
-    def __init__(self, model, kv_cache: torch.Tensor, sizes: tuple[int, ...],
-                 max_blocks_per_seq: int, max_model_len: int, device) -> None:
-        self.model, self.kv_cache, self.device = model, kv_cache, device
-        self.sizes = sorted(set(sizes))
-        self.max_b = self.sizes[-1]
-        self.max_model_len = max_model_len
-        V = model.cfg.vocab_size
-        i32, i64 = torch.int32, torch.int64
-        self.ids = torch.zeros(self.max_b, dtype=i64, device=device)
-        self.pos = torch.zeros(self.max_b, dtype=i64, device=device)
-        self.slot = torch.full((self.max_b,), -1, dtype=i64, device=device)
-        self.seq_lens = torch.zeros(self.max_b, dtype=i32, device=device)
-        self.bt = torch.zeros(self.max_b, max_blocks_per_seq, dtype=i32, device=device)
-        self.qsl = torch.arange(self.max_b + 1, dtype=i32, device=device)
-        self.sample_idx = torch.arange(self.max_b, dtype=i64, device=device)
-        self.logits = torch.zeros(self.max_b, V, dtype=torch.float32, device=device)
-        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
+class StaticDecodeBatch:
+    """The captured graphs' inputs: views of one device arena (and its pinned host mirror)."""
 
-    def _meta(self, B: int) -> AttentionMetadata:
+    def __init__(self, rows: int, width: int, device) -> None:
+        self.rows, self.width = rows, width
+        i64, i32 = torch.int64, torch.int32
+        self._sections = [(i64, (rows,)), (i64, (rows,)), (i64, (rows,)), (i32, (rows,)),
+                          (i32, (rows, width)), (i32, (rows + 1,)), (i64, (rows,))]
+        size = _arena_bytes(self._sections)
+        self._dirty = _arena_bytes(self._sections[:5])          # ids .. tables
+        self.arena = torch.zeros(size, dtype=torch.uint8, device=device)
+        self.stage = torch.zeros(size, dtype=torch.uint8, pin_memory=True)
+        (self.ids, self.pos, self.slots, self.seq_lens, self.tables, self.qsl,
+         self.sample) = _carve(self.arena, self._sections)
+        host = _carve(self.stage, self._sections)
+        self._h = [t.numpy() for t in host]
+        self._h[2][:] = -1                                      # every row starts as padding
+        self._h[5][:] = np.arange(rows + 1)
+        self._h[6][:] = np.arange(rows)
+        self.arena.copy_(self.stage)
+
+    def meta(self, B: int, max_model_len: int) -> AttentionMetadata:
         return AttentionMetadata(
-            query_start_loc=self.qsl[:B + 1], seq_lens=self.seq_lens[:B], block_tables=self.bt[:B],
-            slot_mapping=self.slot[:B], num_decode=B, max_query_len=1,
-            max_seq_len=self.max_model_len, in_graph=True)
+            query_start_loc=self.qsl[:B + 1], seq_lens=self.seq_lens[:B],
+            block_tables=self.tables[:B], slot_mapping=self.slots[:B], num_decode=B,
+            max_query_len=1, max_seq_len=max_model_len, in_graph=True)
 
-    def _forward(self, B: int) -> None:
-        hidden = self.model.forward(self.ids[:B], self.pos[:B], self._meta(B), self.kv_cache)
-        self.logits[:B] = self.model.compute_logits(hidden, self.sample_idx[:B])
+    def fill_from_host(self, items: list[BatchItem], B: int) -> None:
+        """Rows 0 .. len(items)-1 from the items (one token each), rows up to B padding; one
+        copy of the changing part of the arena."""
+        n = len(items)
+        ids, pos, slots, sl, tables = self._h[:5]
+        start = np.fromiter((it.start for it in items), np.int64, n)
+        t_len = np.fromiter((len(it.seq.block_table) for it in items), np.int64, n)
+        if n and int(t_len.max()) > self.width:
+            raise ValueError(f"block table of {int(t_len.max())} blocks exceeds {self.width}")
+        if n and bool((start // 16 >= t_len).any()):
+            raise ValueError("a decode position lies past its block table")
+        ids[:n] = np.fromiter((it.tokens[0] for it in items), np.int64, n)
+        pos[:n] = start
+        sl[:n] = start + 1
+        tables[:B] = 0
+        for r, it in enumerate(items):
+            tables[r, :len(it.seq.block_table)] = it.seq.block_table
+        slots[:n] = tables[np.arange(n), start // 16].astype(np.int64) * 16 + start % 16
+        ids[n:B], pos[n:B], slots[n:B], sl[n:B] = 0, 0, -1, 0
+        self.arena[:self._dirty].copy_(self.stage[:self._dirty], non_blocking=True)
+
+
+class DecodeGraphs:
+    """Pure-decode steps captured once per batch size of `sizes` and replayed with the step's rows
+    written into the static batch."""
+
+    def __init__(self, model, kv_cache: torch.Tensor, sizes, max_blocks_per_seq: int,
+                 max_model_len: int) -> None:
+        self.model, self.kv_cache = model, kv_cache
+        self.ladder = sorted(set(int(s) for s in sizes))
+        if not self.ladder or self.ladder[0] < 1:
+            raise ValueError("graph sizes must be positive")
+        self.max_model_len = max_model_len
+        self.batch = StaticDecodeBatch(self.ladder[-1], max_blocks_per_seq, kv_cache.device)
+        self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self._logits: dict[int, torch.Tensor] = {}
+
+    def _step(self, B: int) -> torch.Tensor:
+        b = self.batch
+        hidden = self.model.forward(b.ids[:B], b.pos[:B], b.meta(B, self.max_model_len),
+                                    self.kv_cache)
+        return self.model.compute_logits(hidden, b.sample[:B])
 
     def capture(self) -> None:
-        for B in self.sizes:                  # eager warm-up of every size
-            for _ in range(2):
-                self._forward(B)
+        """One eager run per size (the padding rows write nothing), then the captures. The graphs
+        share one memory pool; each graph's logits stay allocated, so no later capture reuses
+        them. Capturing the largest first lets the smaller graphs fit in what it reserved."""
+        with torch.inference_mode():
+            for B in self.ladder:
+                self._step(B)
+            torch.cuda.synchronize()
+            pool = torch.cuda.graph_pool_handle()
+            for B in sorted(self.ladder, reverse=True):
+                g = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(g, pool=pool):
+                    self._logits[B] = self._step(B)
+                self._graphs[B] = g
         torch.cuda.synchronize()
-        pool = torch.cuda.graph_pool_handle()
-        for B in reversed(self.sizes):        # largest first so smaller graphs share the pool
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, pool=pool):
-                self._forward(B)
-            self.graphs[B] = g
-        torch.cuda.synchronize()
 
-    def can_replay(self, n: int) -> bool:
-        return 0 < n <= self.max_b and bool(self.graphs)
+    def size_for(self, n: int) -> int | None:
+        """The smallest captured size that holds n decode rows (None if none does)."""
+        for B in self.ladder:
+            if B >= n and B in self._graphs:
+                return B
+        return None
 
-    def replay(self, inp: ModelInput, n: int) -> torch.Tensor:
-        """Copy the n real decode rows into the static buffers, pad to the graph size, replay;
-        returns the logits rows [n, V] (valid until the next replay)."""
-        B = next(s for s in self.sizes if s >= n)
-        self.ids[:n].copy_(inp.input_ids[:n])
-        self.pos[:n].copy_(inp.positions[:n])
-        self.slot[:n].copy_(inp.meta.slot_mapping[:n])
-        self.seq_lens[:n].copy_(inp.meta.seq_lens[:n])
-        self.bt[:B].zero_()
-        w = inp.meta.block_tables.shape[1]
-        self.bt[:n, :w].copy_(inp.meta.block_tables[:n])
-        if B > n:
-            self.ids[n:B].zero_()
-            self.pos[n:B].zero_()
-            self.slot[n:B].fill_(-1)
-            self.seq_lens[n:B].zero_()
-        self.graphs[B].replay()
-        return self.logits[:n]
-
-    def replay_items(self, items, builder) -> torch.Tensor:
-        """The same with the step's metadata built on the device (DeviceInputBuilder.build_into):
-        the decode rows and the padding go straight into the static buffers, one upload and one
-        launch instead of the copies and fills above."""
+    def run(self, items: list[BatchItem], device_builder=None) -> torch.Tensor:
+        """Replay the step of `items` (pure decode, one token each); logits [len(items), V] fp32,
+        valid until the next replay of the same size. With `device_builder` (a
+        DeviceInputBuilder) the rows are written on the GPU, else from the host."""
         n = len(items)
-        B = next(s for s in self.sizes if s >= n)
-        builder.build_into(items, B, self.ids, self.pos, self.slot, self.qsl, self.seq_lens,
-                           self.bt)
-        self.graphs[B].replay()
-        return self.logits[:n]
+        B = self.size_for(n)
+        if B is None or any(len(it.tokens) != 1 for it in items):
+            raise ValueError(f"no captured decode graph for {n} single-token rows")
+        b = self.batch
+        if device_builder is not None:
+            device_builder.build_into(items, B, b.ids, b.pos, b.slots, b.qsl, b.seq_lens, b.tables)
+        else:
+            b.fill_from_host(items, B)
+        self._graphs[B].replay()
+        return self._logits[B][:n]

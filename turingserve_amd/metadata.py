@@ -1,14 +1,18 @@
-"""Attention metadata of one flat ragged batch, and the host builders that produce it.
+"""Attention metadata of one flat ragged batch, and the builders that produce it.
 
-Restates the reference's kernel input contract (runner/attention_metadata.py:10-27) and its two
-builders (runner/input_builder.py:41-150): rows [0, num_decode) are decodes with one query token
-each (q row index == sequence index), then prefill chunks; ``seq_lens`` is the context length
-after this step; ``slot_mapping[t] = table[pos // 16] * 16 + pos % 16`` (-1 = padding row);
-block-table rows are padded with block 0, the null block.
+The kernel input contract is the reference's (runner/attention_metadata.py:10-27,
+runner/input_builder.py:41-48): rows [0, num_decode) are decodes with one query token each (q row
+index == sequence index), then prefill chunks; ``seq_lens`` is the context length after this
+step; ``slot_mapping[t] = table[pos // 16] * 16 + pos % 16`` (-1 = padding row); block-table rows
+are padded with block 0, the null block. Two builders produce it: ``InputBuilder`` computes the
+arrays on the host in one vectorised pass and uploads them with a single copy, and
+``DeviceInputBuilder`` uploads compact per-sequence descriptors and expands them on the GPU
+(``ts_step_metadata``).
 """
 
 from __future__ import annotations
 
+import itertools
 from dataclasses import dataclass, field
 
 import numpy as np
@@ -71,116 +75,144 @@ def num_decode_rows(items: list[BatchItem]) -> int:
     return n
 
 
-def build_simple(items: list[BatchItem], device) -> ModelInput:
-    """Straightforward per-token builder (runner/input_builder.py:51-78)."""
-    ids, pos, slots, qsl, seq_lens, tables, sample = [], [], [], [0], [], [], []
-    for it in items:
-        n = len(it.tokens)
-        p = list(range(it.start, it.start + n))
-        bt = it.seq.block_table
-        ids += it.tokens
-        pos += p
-        slots += [bt[x // BLOCK_SIZE] * BLOCK_SIZE + x % BLOCK_SIZE for x in p]
-        qsl.append(qsl[-1] + n)
-        seq_lens.append(it.start + n)
-        tables.append(list(bt))
-        if it.sample == "last":
-            sample.append(qsl[-1] - 1)
-        elif it.sample == "all":
-            sample += list(range(qsl[-2], qsl[-1]))
-    width = max(1, max(len(t) for t in tables))
-    tables = [t + [0] * (width - len(t)) for t in tables]
-    meta = AttentionMetadata(
-        query_start_loc=torch.tensor(qsl, dtype=torch.int32, device=device),
-        seq_lens=torch.tensor(seq_lens, dtype=torch.int32, device=device),
-        block_tables=torch.tensor(tables, dtype=torch.int32, device=device),
-        slot_mapping=torch.tensor(slots, dtype=torch.int64, device=device),
-        num_decode=num_decode_rows(items), max_query_len=max(len(i.tokens) for i in items),
-        max_seq_len=max(seq_lens),
-        max_prefill_seq_len=max(seq_lens[num_decode_rows(items):], default=0))
-    return ModelInput(torch.tensor(ids, dtype=torch.int64, device=device),
-                      torch.tensor(pos, dtype=torch.int64, device=device), meta,
-                      torch.tensor(sample, dtype=torch.int64, device=device))
+SAMPLE_CODES = {"none": 0, "last": 1, "all": 2}
+
+
+@dataclass
+class StepArrays:
+    """The step's metadata as host arrays, before any upload."""
+
+    ids: np.ndarray            # int64 [T]
+    positions: np.ndarray      # int64 [T]
+    slots: np.ndarray          # int64 [T]
+    query_start_loc: np.ndarray  # int32 [B+1]
+    seq_lens: np.ndarray       # int32 [B]
+    tables: np.ndarray         # int32 [B, width], width >= 1, zero-padded
+    sample: np.ndarray         # int64 [S]
+    num_decode: int
+
+    def bounds(self) -> dict:
+        """The host ints of AttentionMetadata."""
+        B, nd = self.seq_lens.shape[0], self.num_decode
+        n_tok = np.diff(self.query_start_loc)
+        return dict(num_decode=nd, max_query_len=int(n_tok.max(initial=0)),
+                    max_seq_len=int(self.seq_lens.max(initial=0)),
+                    max_prefill_seq_len=int(self.seq_lens[nd:B].max(initial=0)))
+
+
+def step_arrays(items: list[BatchItem]) -> StepArrays:
+    """Every array of the step from per-item vectors, without a per-token Python loop: a token's
+    item comes from repeating item indices by token counts, its position from its offset inside
+    the item, its slot from a gather in the padded table. A position whose block lies past the
+    item's table raises ValueError (the kernels would have no slot for it). An item with no
+    tokens samples nothing."""
+    B = len(items)
+    if B == 0:
+        raise ValueError("a step needs at least one item")
+    n_tok = np.fromiter((len(it.tokens) for it in items), np.int64, B)
+    start = np.fromiter((it.start for it in items), np.int64, B)
+    t_len = np.fromiter((len(it.seq.block_table) for it in items), np.int64, B)
+    mode = np.fromiter((SAMPLE_CODES[it.sample] for it in items), np.int64, B)
+    ends = np.cumsum(n_tok)
+    T = int(ends[-1])
+    owner = np.repeat(np.arange(B), n_tok)
+    first = ends - n_tok                                   # flat index of each item's token 0
+    positions = np.arange(T, dtype=np.int64) - first[owner] + start[owner]
+    width = max(1, int(t_len.max()))
+    tables = np.zeros((B, width), np.int32)
+    tables[np.arange(width)[None, :] < t_len[:, None]] = np.fromiter(
+        itertools.chain.from_iterable(it.seq.block_table for it in items), np.int32,
+        int(t_len.sum()))
+    blk = positions // BLOCK_SIZE
+    if T and bool((blk >= t_len[owner]).any()):
+        t = int(np.argmax(blk >= t_len[owner]))
+        raise ValueError(f"position {int(positions[t])} of item {int(owner[t])} lies past its "
+                         f"{int(t_len[owner[t]])}-block table")
+    slots = tables[owner, blk].astype(np.int64) * BLOCK_SIZE + positions % BLOCK_SIZE
+    flat = np.arange(T)
+    sampled = (mode[owner] == 2) | ((mode[owner] == 1) & (flat == ends[owner] - 1))
+    leading = (n_tok == 1) & (mode != 2)
+    nd = B if bool(leading.all()) else int(np.argmin(leading))
+    qsl = np.zeros(B + 1, np.int32)
+    qsl[1:] = ends
+    return StepArrays(
+        ids=np.fromiter(itertools.chain.from_iterable(it.tokens for it in items), np.int64, T),
+        positions=positions, slots=slots, query_start_loc=qsl,
+        seq_lens=(start + n_tok).astype(np.int32), tables=tables,
+        sample=np.flatnonzero(sampled).astype(np.int64), num_decode=nd)
+
+
+_ALIGN = 256
+
+
+def _carve(arena: torch.Tensor, sections) -> list[torch.Tensor]:
+    """Typed views of a byte arena: one per (dtype, shape) in order, each at a 256-byte aligned
+    offset. Returns the views; the arena must be large enough (checked)."""
+    views, off = [], 0
+    for dtype, shape in sections:
+        n = int(np.prod(shape)) if shape else 1
+        size = n * torch.empty((), dtype=dtype).element_size()
+        if off + size > arena.numel():
+            raise ValueError("metadata arena too small")
+        views.append(arena[off:off + size].view(dtype).view(*shape))
+        off += -(-size // _ALIGN) * _ALIGN
+    return views
+
+
+def _arena_bytes(sections) -> int:
+    total = 0
+    for dtype, shape in sections:
+        n = int(np.prod(shape)) if shape else 1
+        total += -(-n * torch.empty((), dtype=dtype).element_size() // _ALIGN) * _ALIGN
+    return total
 
 
 class InputBuilder:
-    """Vectorised builder with persistent host (pinned on a GPU) and device buffers
-    (runner/input_builder.py:81-150). The host buffers are rewritten only after the previous
-    step's sampler synchronisation, so no in-flight copy can still be reading them."""
+    """Host builder: step_arrays() on the CPU, the arrays packed into one pinned staging arena (on
+    a GPU) and sent with ONE host-to-device copy into a device arena whose typed views are the
+    step's tensors. The layout is planned per step, so the copy covers only what the step uses.
+    The staging arena is rewritten only after the previous step's sampler synchronisation, so no
+    copy in flight can still be reading it; the returned tensors are valid until the next build.
+    The same ModelInput contract as DeviceInputBuilder (runner/input_builder.py:105-150)."""
 
     def __init__(self, max_tokens: int, max_seqs: int, max_blocks_per_seq: int, device) -> None:
         self.device = torch.device(device)
-        pin = self.device.type == "cuda"
-
-        def host(shape, dtype):
-            return torch.zeros(shape, dtype=dtype, pin_memory=pin)
-
-        def dev(shape, dtype):
-            return torch.zeros(shape, dtype=dtype, device=self.device)
-
         self.max_tokens, self.max_seqs, self.max_blocks = max_tokens, max_seqs, max_blocks_per_seq
-        i32, i64 = torch.int32, torch.int64
-        self.h_ids, self.d_ids = host(max_tokens, i64), dev(max_tokens, i64)
-        self.h_pos, self.d_pos = host(max_tokens, i64), dev(max_tokens, i64)
-        self.h_slot, self.d_slot = host(max_tokens, i64), dev(max_tokens, i64)
-        self.h_sample, self.d_sample = host(max_tokens, i64), dev(max_tokens, i64)
-        self.h_qsl, self.d_qsl = host(max_seqs + 1, i32), dev(max_seqs + 1, i32)
-        self.h_sl, self.d_sl = host(max_seqs, i32), dev(max_seqs, i32)
-        self.h_bt = host((max_seqs, max_blocks_per_seq), i32)
-        self.d_bt = dev((max_seqs, max_blocks_per_seq), i32)
+        cap = _arena_bytes(self._sections(max_tokens, max_tokens, max_seqs, max_blocks_per_seq))
+        on_gpu = self.device.type == "cuda"
+        self._stage = torch.zeros(cap, dtype=torch.uint8, pin_memory=on_gpu)
+        self._arena = torch.zeros(cap, dtype=torch.uint8, device=self.device)
+
+    @staticmethod
+    def _sections(T: int, S: int, B: int, width: int):
+        i64, i32 = torch.int64, torch.int32
+        return [(i64, (T,)), (i64, (T,)), (i64, (T,)), (i64, (S,)), (i32, (B + 1,)), (i32, (B,)),
+                (i32, (B, width))]
 
     def build(self, items: list[BatchItem]) -> ModelInput:
         B = len(items)
         if B > self.max_seqs:
             raise ValueError(f"batch of {B} sequences exceeds the builder's {self.max_seqs}")
-        n_tok = [len(it.tokens) for it in items]
-        T = int(sum(n_tok))
-        if T > self.max_tokens:
+        if sum(len(it.tokens) for it in items) > self.max_tokens:
             raise ValueError("batch exceeds max_num_batched_tokens")
-        width = max(1, max(len(it.seq.block_table) for it in items))
+        a = step_arrays(items)
+        width = a.tables.shape[1]
         if width > self.max_blocks:
             raise ValueError(f"block table of {width} blocks exceeds {self.max_blocks}")
-        ids, pos, slot = self.h_ids.numpy(), self.h_pos.numpy(), self.h_slot.numpy()
-        smp, qsl, sl, bt = self.h_sample.numpy(), self.h_qsl.numpy(), self.h_sl.numpy(), self.h_bt.numpy()
-        qsl[0] = 0
-        qsl[1:B + 1] = np.cumsum(n_tok)
-        off, ns = 0, 0
-        for i, it in enumerate(items):
-            n = n_tok[i]
-            p = np.arange(it.start, it.start + n, dtype=np.int64)
-            table = np.asarray(it.seq.block_table, dtype=np.int64)
-            ids[off:off + n] = it.tokens
-            pos[off:off + n] = p
-            slot[off:off + n] = table[p // BLOCK_SIZE] * BLOCK_SIZE + p % BLOCK_SIZE
-            sl[i] = it.start + n
-            nb = len(table)
-            bt[i, :nb] = table
-            bt[i, nb:width] = 0                   # rows are reused across steps: clear stale ids
-            if it.sample == "last":
-                smp[ns] = off + n - 1
-                ns += 1
-            elif it.sample == "all":
-                smp[ns:ns + n] = np.arange(off, off + n)
-                ns += n
-            off += n
-        nb_ = self.device.type != "cpu"
-        self.d_ids[:T].copy_(self.h_ids[:T], non_blocking=nb_)
-        self.d_pos[:T].copy_(self.h_pos[:T], non_blocking=nb_)
-        self.d_slot[:T].copy_(self.h_slot[:T], non_blocking=nb_)
-        self.d_sample[:ns].copy_(self.h_sample[:ns], non_blocking=nb_)
-        self.d_qsl[:B + 1].copy_(self.h_qsl[:B + 1], non_blocking=nb_)
-        self.d_sl[:B].copy_(self.h_sl[:B], non_blocking=nb_)
-        self.d_bt[:B, :width].copy_(self.h_bt[:B, :width], non_blocking=nb_)
-        meta = AttentionMetadata(
-            query_start_loc=self.d_qsl[:B + 1], seq_lens=self.d_sl[:B],
-            block_tables=self.d_bt[:B, :width], slot_mapping=self.d_slot[:T],
-            num_decode=num_decode_rows(items), max_query_len=max(n_tok),
-            max_seq_len=int(sl[:B].max()),
-            max_prefill_seq_len=int(sl[num_decode_rows(items):B].max(initial=0)))
-        return ModelInput(self.d_ids[:T], self.d_pos[:T], meta, self.d_sample[:ns])
+        T, S = a.ids.shape[0], a.sample.shape[0]
+        sections = self._sections(T, S, B, width)
+        used = _arena_bytes(sections)
+        host = _carve(self._stage, sections)
+        for view, arr in zip(host, (a.ids, a.positions, a.slots, a.sample, a.query_start_loc,
+                                    a.seq_lens, a.tables)):
+            view.numpy()[...] = arr
+        self._arena[:used].copy_(self._stage[:used], non_blocking=self.device.type == "cuda")
+        ids, pos, slots, sample, qsl, sl, bt = _carve(self._arena, sections)
+        meta = AttentionMetadata(query_start_loc=qsl, seq_lens=sl, block_tables=bt,
+                                 slot_mapping=slots, **a.bounds())
+        return ModelInput(ids, pos, meta, sample)
 
 
-SAMPLE_CODES = {"none": 0, "last": 1, "all": 2}
 DESC_WORDS = 5
 
 
@@ -217,8 +249,8 @@ def pack_step(items: list[BatchItem], out: np.ndarray | None = None) -> tuple[np
 
 
 class DeviceInputBuilder:
-    """Builds the step's metadata on the GPU (ts_step_metadata) from one packed upload instead of
-    the host arrays and seven copies of InputBuilder (runner/input_builder.py:81-150); the same
+    """Builds the step's metadata on the GPU (ts_step_metadata) from one packed upload of
+    per-sequence descriptors instead of the per-token host arrays of InputBuilder; the same
     ModelInput contract. The pinned upload buffer is rewritten only after the previous step's
     sampler synchronisation, as with InputBuilder. build_into() writes a pure-decode batch
     straight into a captured graph's static buffers, padded to the graph size

@@ -10,7 +10,7 @@ is available offline; the fused layouts match the loader's (model/loader.py:68-9
 
 from __future__ import annotations
 
-from dataclasses import dataclass, field
+from dataclasses import dataclass
 
 import torch
 
@@ -49,99 +49,100 @@ TINY_G7 = Qwen2Config(224, 448, 2, 14, 2, 151936, max_position_embeddings=4096)
 QWEN25_15B = Qwen2Config(1536, 8960, 28, 12, 2, 151936)
 
 
-class RotaryCache:
-    """cos / sin tables [max_len, D/2] in fp32, cast to the activation dtype at use
-    (model/layers.py:10-18)."""
-
-    def __init__(self, head_dim: int, theta: float, max_len: int, device) -> None:
-        inv_freq = 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim))
-        freqs = torch.outer(torch.arange(max_len).float(), inv_freq)
-        self.cos = freqs.cos().to(device)
-        self.sin = freqs.sin().to(device)
+def rope_tables(head_dim: int, theta: float, max_len: int, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """(cos, sin) [max_len, D/2] fp32 for rotate-half RoPE. The inverse frequencies are formed
+    exactly as Hugging Face's Qwen2 rotary embedding forms them, so the tables hold the same
+    bits as a checkpoint's own inference would use (model/layers.py:10-18 does the same)."""
+    exponent = torch.arange(0, head_dim, 2, dtype=torch.int64).float() / head_dim
+    angle = torch.outer(torch.arange(max_len).float(), 1.0 / (theta ** exponent))
+    return angle.cos().to(device), angle.sin().to(device)
 
 
 @dataclass
-class LayerWeights:
-    w_in: torch.Tensor
-    qkv: LinearWeight
-    o: LinearWeight
-    w_post: torch.Tensor
-    gu: LinearWeight
-    down: LinearWeight
+class DecoderLayer:
+    """One decoder layer's parameters in the fused layouts the ops take (model/loader.py:82-92):
+    qkv_proj = [q; k; v] rows with a bias, gate_up_proj = [gate; up] rows."""
+
+    input_norm: torch.Tensor
+    qkv_proj: LinearWeight
+    o_proj: LinearWeight
+    post_attention_norm: torch.Tensor
+    gate_up_proj: LinearWeight
+    down_proj: LinearWeight
 
 
 @dataclass
-class Weights:
-    embed: torch.Tensor                       # [V, hidden], also the tied lm head
-    layers: list[LayerWeights] = field(default_factory=list)
-    w_norm: torch.Tensor | None = None
-    embed_q: tuple[torch.Tensor, torch.Tensor] | None = None   # optional int8 lm head
+class Qwen2Weights:
+    """The model's parameters. embed_tokens [V, hidden] is also the (tied) lm head;
+    lm_head_int8 = (int8 [V, hidden], scale [V]) when the lm head runs as W8A16."""
+
+    embed_tokens: torch.Tensor
+    layers: list[DecoderLayer]
+    final_norm: torch.Tensor
+    lm_head_int8: tuple[torch.Tensor, torch.Tensor] | None = None
 
 
 def random_weights(cfg: Qwen2Config, device, dtype=torch.float16, seed: int = 0,
                    quantization: str = "none", init_std: float = 0.2,
-                   int8_lm_head: bool = False) -> Weights:
-    """Seeded random weights with the loader's fused layouts, drawn on `device` (a GPU generator
-    when it is one, so the 1.5B shapes initialise in seconds). init_std 0.2 (the tiny models'
-    initializer_range) spreads the logits so greedy ties are rare; the large configuration uses a
-    smaller std so activations stay in fp16 range."""
-    on_device = torch.device(device).type == "cuda"
-    g = torch.Generator(device=device if on_device else "cpu").manual_seed(seed)
-    gen_dev = device if on_device else "cpu"
+                   int8_lm_head: bool = False, draw_on: str = "device") -> Qwen2Weights:
+    """Seeded random weights in the loader's fused layouts. draw_on="device" draws with a
+    generator on `device` when it is a GPU (the 1.5B shapes initialise in seconds); "cpu" draws on
+    the host and moves the result, so the same seed gives the same weights on any device (the
+    end-to-end tests pick their seeds on the CPU). init_std 0.2 is the tiny models'
+    initializer_range; the 1.5B configuration uses a smaller std so activations stay in fp16
+    range. Norm weights are 1 + N(0, 0.1)."""
+    gpu_draw = draw_on == "device" and torch.device(device).type == "cuda"
+    where = device if gpu_draw else "cpu"
+    g = torch.Generator(device=where).manual_seed(seed)
 
-    def rnd(*shape, std=init_std):
-        return torch.randn(*shape, generator=g, device=gen_dev) * std
+    def normal(*shape, std=init_std):
+        return torch.randn(*shape, generator=g, device=where) * std
 
-    def lin(n, k, bias=False):
-        w = rnd(n, k).to(dtype)
-        b = rnd(n).to(dtype).to(device) if bias else None
+    def norm_weight(n):
+        return (1.0 + normal(n, std=0.1)).to(dtype).to(device)
+
+    def proj(n, k, bias=False):
+        w = normal(n, k).to(dtype)
+        b = normal(n).to(dtype).to(device) if bias else None
         if quantization == "int8":
             wq, scale = quantize(w.float())
             return LinearWeight(wq.to(device), b, scale.to(device))
         return LinearWeight(w.to(device), b)
 
-    H, D, I = cfg.hidden_size, cfg.head_dim, cfg.intermediate_size
-    layers = []
-    for _ in range(cfg.num_layers):
-        layers.append(LayerWeights(
-            w_in=(1.0 + 0.1 * rnd(H, std=1.0)).to(dtype).to(device),
-            qkv=lin(cfg.qkv_dim, H, bias=True),
-            o=lin(H, cfg.num_heads * D),
-            w_post=(1.0 + 0.1 * rnd(H, std=1.0)).to(dtype).to(device),
-            gu=lin(2 * I, H),
-            down=lin(H, I)))
-    embed = rnd(cfg.vocab_size, H).to(dtype).to(device)
-    w = Weights(embed=embed, layers=layers,
-                w_norm=(1.0 + 0.1 * rnd(H, std=1.0)).to(dtype).to(device))
+    hid, D, inter = cfg.hidden_size, cfg.head_dim, cfg.intermediate_size
+    layers = [DecoderLayer(input_norm=norm_weight(hid),
+                           qkv_proj=proj(cfg.qkv_dim, hid, bias=True),
+                           o_proj=proj(hid, cfg.num_heads * D),
+                           post_attention_norm=norm_weight(hid),
+                           gate_up_proj=proj(2 * inter, hid),
+                           down_proj=proj(hid, inter))
+              for _ in range(cfg.num_layers)]
+    embed = normal(cfg.vocab_size, hid).to(dtype).to(device)
+    head = None
     if int8_lm_head:
         wq, scale = quantize(embed.float())
-        w.embed_q = (wq, scale)
-    return w
+        head = (wq.to(device), scale.to(device))
+    return Qwen2Weights(embed, layers, norm_weight(hid), head)
 
 
 class Qwen2Model:
-    def __init__(self, cfg: Qwen2Config, weights: Weights, ops, device,
-                 dtype: torch.dtype = torch.float16, max_model_len: int | None = None) -> None:
-        self.cfg = cfg
-        self.w = weights
-        self.ops = ops
-        self.device = device
-        self.dtype = dtype
-        self.scale = cfg.head_dim ** -0.5
-        self.rotary = RotaryCache(cfg.head_dim, cfg.rope_theta,
-                                  max_model_len or cfg.max_position_embeddings, device)
+    """The forward pass over one flat ragged batch; `ops` is a get_ops() namespace. Device and
+    activation dtype are the embedding's."""
 
-    def _qkv(self, x, lw, positions, k_cache, v_cache, slot_mapping):
-        """q, k, v views of the rotated qkv activation, with the new K / V rows already in the
-        layer's cache (model/qwen2.py:26-28 and :89: rope, then kv_write). A backend with
-        rope_kv_write_ rotates and writes them in one pass."""
-        return self._rotate_write(self.ops.linear(x, lw.qkv), positions, k_cache, v_cache,
-                                  slot_mapping)
+    def __init__(self, cfg: Qwen2Config, weights: Qwen2Weights, ops,
+                 max_model_len: int | None = None) -> None:
+        self.cfg, self.w, self.ops = cfg, weights, ops
+        self.device = weights.embed_tokens.device
+        self.dtype = weights.embed_tokens.dtype
+        self.scale = cfg.head_dim ** -0.5
+        self.cos, self.sin = rope_tables(cfg.head_dim, cfg.rope_theta,
+                                         max_model_len or cfg.max_position_embeddings,
+                                         self.device)
 
     def _rotate_write(self, qkv, positions, k_cache, v_cache, slot_mapping):
         c = self.cfg
         fused = getattr(self.ops, "rope_kv_write_", None)
-        args = (qkv, positions, self.rotary.cos, self.rotary.sin, c.num_heads, c.num_kv_heads,
+        args = (qkv, positions, self.cos, self.sin, c.num_heads, c.num_kv_heads,
                 c.head_dim)
         written = fused is not None and fused(*args, k_cache, v_cache, slot_mapping)
         if not written:
@@ -156,59 +157,62 @@ class Qwen2Model:
 
     def _mlp(self, x, lw):
         gate_up_silu = getattr(self.ops, "gate_up_silu", None)       # fused on the hip backend
-        act = (gate_up_silu(x, lw.gu) if gate_up_silu is not None
-               else self.ops.silu_mul(self.ops.linear(x, lw.gu)))
-        return self.ops.linear(act, lw.down)
+        act = (gate_up_silu(x, lw.gate_up_proj) if gate_up_silu is not None
+               else self.ops.silu_mul(self.ops.linear(x, lw.gate_up_proj)))
+        return self.ops.linear(act, lw.down_proj)
+
+    def pure_decode(self, meta, num_tokens: int) -> bool:
+        """True when every row of the step is a decode row (the fused decode launch applies)."""
+        return meta.num_decode == num_tokens and meta.seq_lens.shape[0] == meta.num_decode
+
+    @torch.inference_mode()
+    def layer_forward(self, index: int, h, residual, positions, meta, kv_cache,
+                      fused_decode: bool = False):
+        """Decoder layer `index` (model/qwen2.py:84-92): (h, residual) in, (h, residual) out,
+        residual None before the first layer. The layer's new K/V rows go into kv_cache[index]
+        before its attention reads it. With fused_decode (a pure-decode step on a backend that
+        has decode_rope_kv_write_attention), RoPE, kv_write and attention run as one launch
+        (same outputs and caches as the three calls)."""
+        c, ops, lw = self.cfg, self.ops, self.w.layers[index]
+        if residual is None:
+            residual = h
+            x = ops.rmsnorm(h, lw.input_norm, c.rms_norm_eps)
+        else:
+            x, residual = ops.rmsnorm_residual(h, residual, lw.input_norm, c.rms_norm_eps)
+        k_cache, v_cache = kv_cache[index, 0], kv_cache[index, 1]
+        qkv = ops.linear(x, lw.qkv_proj)
+        a = None
+        if fused_decode and hasattr(ops, "decode_rope_kv_write_attention"):
+            a = ops.decode_rope_kv_write_attention(qkv, positions, self.cos, self.sin, c.num_heads,
+                                                   c.num_kv_heads, c.head_dim, k_cache, v_cache,
+                                                   meta, self.scale)
+        if a is None:                 # not fused, or a layout the fused launch does not take
+            q, _, _ = self._rotate_write(qkv, positions, k_cache, v_cache, meta.slot_mapping)
+            a = ops.paged_attention(q, k_cache, v_cache, meta, self.scale)
+        h = ops.linear(a, lw.o_proj)
+        x, residual = ops.rmsnorm_residual(h, residual, lw.post_attention_norm, c.rms_norm_eps)
+        return self._mlp(x, lw), residual
 
     @torch.inference_mode()
     def forward(self, input_ids, positions, meta, kv_cache):
-        """kv_cache [L, 2, num_blocks, KVH, 16, D]; per layer kv_write first, then attention
-        (model/qwen2.py:84-92)."""
-        c, ops, w = self.cfg, self.ops, self.w
-        h = w.embed[input_ids]
-        residual = None
-        # A pure-decode step on a backend that fuses rope, kv_write and decode attention into one
-        # launch takes that path (same outputs and caches as the three calls).
-        fused_decode = getattr(ops, "decode_rope_kv_write_attention", None)
-        if fused_decode is not None and not (meta.num_decode == input_ids.shape[0]
-                                             and meta.seq_lens.shape[0] == meta.num_decode):
-            fused_decode = None
-        for layer, lw in enumerate(w.layers):
-            if residual is None:
-                residual = h
-                x = ops.rmsnorm(h, lw.w_in, c.rms_norm_eps)
-            else:
-                x, residual = ops.rmsnorm_residual(h, residual, lw.w_in, c.rms_norm_eps)
-            k_cache, v_cache = kv_cache[layer, 0], kv_cache[layer, 1]
-            a = None
-            if fused_decode is not None:
-                qkv = ops.linear(x, lw.qkv)
-                a = fused_decode(qkv, positions, self.rotary.cos, self.rotary.sin, c.num_heads,
-                                 c.num_kv_heads, c.head_dim, k_cache, v_cache, meta, self.scale)
-                if a is None:                   # layout the fused launch does not take
-                    fused_decode = None
-                    q, _, _ = self._rotate_write(qkv, positions, k_cache, v_cache,
-                                                 meta.slot_mapping)
-                    a = ops.paged_attention(q, k_cache, v_cache, meta, self.scale)
-            if a is None:
-                q, _, _ = self._qkv(x, lw, positions, k_cache, v_cache, meta.slot_mapping)
-                a = ops.paged_attention(q, k_cache, v_cache, meta, self.scale)
-            h = ops.linear(a, lw.o)
-            x, residual = ops.rmsnorm_residual(h, residual, lw.w_post, c.rms_norm_eps)
-            h = self._mlp(x, lw)
-        x, _ = ops.rmsnorm_residual(h, residual, w.w_norm, c.rms_norm_eps)
-        return x
+        """kv_cache [L, 2, num_blocks, KVH, 16, D] -> final normed hidden rows [T, hidden]."""
+        fused = self.pure_decode(meta, input_ids.shape[0])
+        h, residual = self.w.embed_tokens[input_ids], None
+        for index in range(len(self.w.layers)):
+            h, residual = self.layer_forward(index, h, residual, positions, meta, kv_cache, fused)
+        return self.ops.rmsnorm_residual(h, residual, self.w.final_norm, self.cfg.rms_norm_eps)[0]
 
     def compute_logits(self, hidden: torch.Tensor, sample_indices: torch.Tensor) -> torch.Tensor:
         """Logits of the sampling rows only, [S, V] fp32 (model/qwen2.py:94-99). With the int8
         lm head, a backend that has logits_int8 gathers, multiplies and widens in one launch
         (same values as lm_head_int8 on the gathered rows followed by .float())."""
-        if self.w.embed_q is not None and hasattr(self.ops, "logits_int8"):
-            return self.ops.logits_int8(hidden, sample_indices, *self.w.embed_q)
+        head = self.w.lm_head_int8
+        if head is not None and hasattr(self.ops, "logits_int8"):
+            return self.ops.logits_int8(hidden, sample_indices, *head)
         h = hidden[sample_indices]
-        if self.w.embed_q is not None and hasattr(self.ops, "lm_head_int8"):
-            return self.ops.lm_head_int8(h, *self.w.embed_q).float()
-        return (h @ self.w.embed.T).float()
+        if head is not None and hasattr(self.ops, "lm_head_int8"):
+            return self.ops.lm_head_int8(h, *head).float()
+        return (h @ self.w.embed_tokens.T).float()
 
     def new_kv_cache(self, num_blocks: int) -> torch.Tensor:
         c = self.cfg

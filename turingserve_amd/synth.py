@@ -142,6 +142,34 @@ def config3(chunk_index: int, seed: int = 0, prompt: int = 8000, chunk: int = 20
     return make_step(12, 2, 128, nb + 16, [(prefix, n)], seed=seed)
 
 
+def config5_batch(vocab: int, seed: int = 0):
+    """The flat batch of one config-5 mixed step: 48 decode sequences with contexts log-uniform in
+    [256, 4096] (each decodes its last token) and one 512-token prefill chunk of a prompt whose
+    cached prefix is drawn lognormal with median 200 tokens (capped at 3000), the configuration's
+    prompt-length distribution. Token ids uniform over the vocabulary, block ids a shuffled
+    permutation of 1 .. num_blocks-1. Returns (items, num_blocks, chunk prefix)."""
+    import random
+
+    from turingserve_amd.metadata import BatchItem, SeqState
+
+    g = torch.Generator().manual_seed(seed)
+    ctx = log_uniform_ints(48, 256, 4096, g)
+    prefix = int(min(3000, round(float(torch.empty(1).log_normal_(math.log(200), 0.8, generator=g)))))
+    nb = sum(-(-c // BLOCK) for c in ctx) + -(-(prefix + 512) // BLOCK) + 8
+    rng = random.Random(seed)
+    free = list(range(1, nb))
+    rng.shuffle(free)
+    items = []
+    for c in ctx:
+        s = SeqState([rng.randrange(vocab) for _ in range(c)])
+        s.block_table = [free.pop() for _ in range(-(-c // BLOCK))]
+        items.append(BatchItem(s, c - 1, [s.token_ids[-1]], "last"))
+    s = SeqState([rng.randrange(vocab) for _ in range(prefix + 512)])
+    s.block_table = [free.pop() for _ in range(-(-(prefix + 512) // BLOCK))]
+    items.append(BatchItem(s, prefix, s.token_ids[prefix:], "last"))
+    return items, nb, prefix
+
+
 QWEN15_LINEAR_SHAPES = [(2048, 1536), (1536, 1536), (17920, 1536), (1536, 8960)]
 W8A16_M = [1, 16, 64, 256, 2048]
 

@@ -3,16 +3,16 @@
 20-43), for this backend's variants instead of Triton configs.
 
 Each kernel has candidate variants per shape bucket; tune() times every candidate with HIP events
-over graph-captured calls and keeps the fastest; the winners are stored in a JSON file keyed by
-GPU, CU count, model dimensions and library / torch versions. At run time the ops look their
-bucket up, rounding up to the smallest recorded bucket (as lookup_rounded does in the
-reference; for W8A16 only M rounds, N and K must match); a miss takes the library's own plan.
-tune() records the M buckets below the engine's token budget and the budget itself.
+over graph-captured calls and keeps the fastest; the winners are stored in a JSON file whose name
+follows the GPU, CU count, model and library / torch versions. At run time the ops look their
+bucket up and round up to the next measured bucket, as the reference's lookup does (for W8A16
+only M rounds; N and K must match); a miss takes the library's own plan. tune() records the M
+buckets below the engine's token budget and the budget itself.
 
-    kernel "decode": key "S,L"   (decode rows, max_seq_len)  -> {"version": "v2" | "v3",
-                                                                  "partition": 0 | 256 | ...}
-    kernel "w8a16":  key "N,K,M" (out features, in features, rows) -> {"variant": 0..4,
-                                                                  "splits": 0..}
+    kernel "decode": key (S, L)    (decode rows, max_seq_len)       -> {"version": "v2" | "v3",
+                                                                         "partition": 0 | 256 | ...}
+    kernel "w8a16":  key (N, K, M) (out features, in features, rows) -> {"variant": 0..4,
+                                                                         "splits": 0..}
 
 W8A16 variants (ts_w8a16_gemm_v): 0 the library's plan, 1 weight streaming (M <= 32),
 2 128 x 64 wide tiles, 3 128 x 128 wide tiles, 4 128 x 32 wide tiles (128 x 64 in the fused
@@ -23,70 +23,61 @@ fixed partition in tokens. Every variant computes the same result up to fp32 sum
 
 from __future__ import annotations
 
+import bisect
+import hashlib
 import json
 import os
-import re
-from dataclasses import dataclass, field
+import tempfile
 
 W8A16_M_BUCKETS = (1, 8, 16, 32, 64, 128, 256, 512, 768, 1024, 2048, 4096)
 DECODE_PARTITIONS = (0, 256, 512, 1024)
+FORMAT = 2                       # version of the JSON layout below
 
 
-def pow2_buckets(lo: int, hi: int) -> list[int]:
-    out, v = [], lo
-    while v < hi:
-        out.append(v)
-        v *= 2
-    out.append(hi)
-    return out
-
-
-def round_up_bucket(buckets, value: int) -> int:
-    for b in buckets:
-        if value <= b:
-            return b
-    return buckets[-1]
-
-
-def cache_key(gpu: str, cus: int, model: str, lib_version: str, torch_version: str) -> str:
-    safe = lambda s: re.sub(r"[^A-Za-z0-9_.+-]", "-", s)  # noqa: E731
-    return f"{safe(gpu)}__cu{cus}__{safe(model)}__{safe(lib_version)}__torch{safe(torch_version)}.json"
-
-
-@dataclass
 class VariantTable:
-    """kernel -> {bucket key "a,b,..": choice}; meta carries the cache key fields."""
+    """Measured choices: for each kernel, records (key, choice) with an integer tuple key.
 
-    tables: dict[str, dict[str, dict]] = field(default_factory=dict)
-    meta: dict = field(default_factory=dict)
+    JSON layout: {"format": 2, "meta": {...}, "records": [{"kernel": k, "key": [..],
+    "choice": {..}}, ...]} (records sorted by kernel and key, so equal tables serialise equally).
+    """
 
-    def set(self, kernel: str, key: tuple[int, ...], choice: dict) -> None:
-        self.tables.setdefault(kernel, {})[",".join(str(k) for k in key)] = choice
+    def __init__(self, meta: dict | None = None) -> None:
+        self.meta = dict(meta or {})
+        self._by_kernel: dict[str, dict[tuple[int, ...], dict]] = {}
 
-    def lookup(self, kernel: str, key: tuple[int, ...]) -> dict | None:
-        """The choice of the smallest recorded bucket that is >= key in every dimension (exact
-        match on leading dimensions that are not sizes is the caller's business: W8A16 keys put
-        N and K first, which only ever match exactly). None on a miss."""
-        table = self.tables.get(kernel)
-        if not table:
-            return None
-        best = None
-        for name, choice in table.items():
-            dims = tuple(int(x) for x in name.split(","))
-            if len(dims) == len(key) and all(d >= k for d, k in zip(dims, key)) \
-                    and (best is None or dims < best[0]):
-                best = (dims, choice)
-        return best[1] if best else None
+    def set(self, kernel: str, key, choice: dict) -> None:
+        self._by_kernel.setdefault(kernel, {})[tuple(int(k) for k in key)] = dict(choice)
+
+    def records(self, kernel: str) -> dict[tuple[int, ...], dict]:
+        return dict(self._by_kernel.get(kernel, {}))
+
+    def lookup(self, kernel: str, key) -> dict | None:
+        """The choice recorded under the smallest key (in tuple order) that is >= `key` in every
+        component, or None. A query of a bucket the table did not measure therefore takes the
+        next larger measured bucket."""
+        want = tuple(int(k) for k in key)
+        fits = [k for k in self._by_kernel.get(kernel, {})
+                if len(k) == len(want) and all(a >= b for a, b in zip(k, want))]
+        return self._by_kernel[kernel][min(fits)] if fits else None
 
     def to_json(self) -> str:
-        return json.dumps({"tables": self.tables, "meta": self.meta}, indent=1, sort_keys=True)
+        recs = [{"kernel": kern, "key": list(key), "choice": choice}
+                for kern in sorted(self._by_kernel)
+                for key, choice in sorted(self._by_kernel[kern].items())]
+        return json.dumps({"format": FORMAT, "meta": self.meta, "records": recs}, indent=1,
+                          sort_keys=True)
 
     @classmethod
     def from_json(cls, text: str) -> "VariantTable":
-        d = json.loads(text)
-        if not isinstance(d.get("tables"), dict):
-            raise ValueError("variant table without 'tables'")
-        return cls(tables=d["tables"], meta=d.get("meta", {}))
+        doc = json.loads(text)
+        if not isinstance(doc, dict) or doc.get("format") != FORMAT:
+            raise ValueError("not a variant table of this format")
+        table = cls(doc.get("meta", {}))
+        for rec in doc["records"]:
+            if not (isinstance(rec["key"], list) and isinstance(rec["choice"], dict)):
+                raise ValueError("malformed record")
+            table.set(str(rec["kernel"]), rec["key"], rec["choice"])
+        return table
 
 
 ACTIVE = VariantTable()          # consulted by hip_ops
@@ -98,21 +89,17 @@ def set_active(table: VariantTable) -> None:
 
 
 def w8a16_choice(N: int, K: int, M: int) -> tuple[int, int]:
-    """(variant, splits) for a W8A16 product: the choice recorded for this N and K at the
-    smallest recorded M >= M, or the library's own plan (0, 0)."""
-    table = ACTIVE.tables.get("w8a16")
-    if not table:
+    """(variant, splits) for a W8A16 product: N and K must match a record exactly, M takes the
+    smallest recorded M >= M (bisected over that shape's M list); else the library's own plan
+    (0, 0). A streaming choice (variant 1) recorded for a bucket whose range reaches past
+    M = 32 cannot apply and also falls back."""
+    shape = sorted((k[2], c) for k, c in ACTIVE.records("w8a16").items() if k[:2] == (N, K))
+    i = bisect.bisect_left([m for m, _ in shape], M)
+    if i == len(shape):
         return 0, 0
-    best = None
-    for name, choice in table.items():
-        n, k, m = (int(v) for v in name.split(","))
-        if n == N and k == K and m >= M and (best is None or m < best[0]):
-            best = (m, choice)
-    if best is None:
-        return 0, 0
-    c = best[1]
+    c = shape[i][1]
     variant, splits = int(c["variant"]), int(c["splits"])
-    if variant == 1 and M > 32:                     # streaming exists for M <= 32 only
+    if variant == 1 and M > 32:
         return 0, 0
     return variant, splits
 
@@ -125,24 +112,45 @@ def decode_choice(S: int, max_seq_len: int) -> tuple[str | None, int | None]:
     return c["version"], int(c["partition"])
 
 
-def load_cache(tuning_dir: str, key: str) -> VariantTable | None:
-    path = os.path.join(os.path.expanduser(tuning_dir), key)
+def cache_file_name(gpu: str, cus: int, model: str, lib_version: str, torch_version: str) -> str:
+    """A file name that changes whenever any of the fields does: a readable prefix (GPU, CU count,
+    model, with path-unsafe characters dropped) and a hash of all five fields."""
+    digest = hashlib.sha256("\x1f".join([gpu, str(cus), model, lib_version, torch_version])
+                            .encode()).hexdigest()[:16]
+    readable = "-".join("".join(ch for ch in f if ch.isalnum() or ch in "._") or "x"
+                        for f in (gpu, f"cu{cus}", model))
+    return f"{readable}-{digest}.json"
+
+
+def load_table(directory: str, name: str) -> VariantTable | None:
+    """The table stored under `name`, or None if it is missing or unreadable (then tune again)."""
     try:
-        with open(path, encoding="utf-8") as f:
+        with open(os.path.join(os.path.expanduser(directory), name), encoding="utf-8") as f:
             return VariantTable.from_json(f.read())
-    except (OSError, ValueError, KeyError, TypeError, json.JSONDecodeError):
-        return None                                 # missing or corrupt -> tune again
+    except (OSError, ValueError, KeyError, TypeError):
+        return None
 
 
-def save_cache(tuning_dir: str, key: str, table: VariantTable) -> str:
-    d = os.path.expanduser(tuning_dir)
+def store_table(directory: str, name: str, table: VariantTable) -> str:
+    """Write the table under `name`; a reader never sees a partial file (written to a temporary
+    file in the same directory, then renamed over the target)."""
+    d = os.path.expanduser(directory)
     os.makedirs(d, exist_ok=True)
-    path = os.path.join(d, key)
-    tmp = path + ".tmp"
-    with open(tmp, "w", encoding="utf-8") as f:
-        f.write(table.to_json())
-    os.replace(tmp, path)
-    return path
+    fd, tmp = tempfile.mkstemp(dir=d, prefix=".variant-", suffix=".json")
+    try:
+        with os.fdopen(fd, "w", encoding="utf-8") as f:
+            f.write(table.to_json())
+        os.replace(tmp, os.path.join(d, name))
+    except BaseException:
+        if os.path.exists(tmp):
+            os.unlink(tmp)
+        raise
+    return os.path.join(d, name)
+
+
+def _ladder(lo: int, hi: int) -> list[int]:
+    """lo, 2 lo, 4 lo, ... below hi, then hi."""
+    return [lo << i for i in range(max(0, (hi - 1) // lo).bit_length()) if lo << i < hi] + [hi]
 
 
 # ---- the measuring part (needs a GPU) -------------------------------------------------------------
@@ -238,8 +246,8 @@ def tune(torch, cfg, max_num_seqs: int, max_model_len: int, max_num_batched_toke
     table = VariantTable(meta={"gpu": torch.cuda.get_device_name(device),
                                "cus": _native.cu_count(torch.device(device).index or 0),
                                "lib": _native.version(), "torch": torch.__version__})
-    seqs = [s for s in pow2_buckets(1, 256) if s <= max_num_seqs]
-    lens = pow2_buckets(256, max(256, max_model_len))
+    seqs = [s for s in _ladder(1, 256) if s <= max_num_seqs]
+    lens = _ladder(256, max(256, max_model_len))
     tune_decode(torch, cfg.num_heads, cfg.num_kv_heads, cfg.head_dim, seqs, lens, device, table)
     if quantized:
         D = cfg.head_dim
@@ -283,9 +291,9 @@ def main(argv=None) -> int:
         tune_w8a16(torch, shapes, ms, dev, table)
     else:
         table = tune(torch, cfg, a.max_num_seqs, a.max_model_len, a.max_num_batched_tokens, dev)
-    key = cache_key(torch.cuda.get_device_name(dev), _native.cu_count(0), a.model,
-                    _native.version(), torch.__version__)
-    print(save_cache(a.out, key, table), flush=True)
+    name = cache_file_name(torch.cuda.get_device_name(dev), _native.cu_count(0), a.model,
+                           _native.version(), torch.__version__)
+    print(store_table(a.out, name, table), flush=True)
     return 0
 
 
