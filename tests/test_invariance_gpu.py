@@ -1,0 +1,146 @@
+"""Batch invariance and paged == contiguous on the HIP path (needs an MI355X); the reference pins
+the same properties on its CPU twins (tests/correctness/test_paged_engine.py:46-91).
+
+* Paged == contiguous: a model forward over a shuffled block table equals, bit for bit, the same
+  forward over blocks 1, 2, 3, ... in order (the kernels never look at block ids except to
+  address them), and both are close to the reference namespace: relative Frobenius error of the
+  logits below REF_REL_FRO, largest difference below REF_REL_MAX of the largest logit.
+* Prompts alone vs together: eight prompts of 5 ... 2047 tokens prefilled one by one and all in
+  one step (shuffled blocks), every position sampled. Prefill work is split per sequence and
+  query tile; the key-range split plan of the 128-row tile kernel (head_dim 128) depends on how
+  many tiles the step holds, so a row's fp32 merge order can change with its neighbours: the
+  largest logit difference must stay below BATCH_REL_MAX of the largest logit, the bar the
+  comparison with the reference namespace uses (a split's partial is kept as an fp16 row
+  average, so a split changes the attention output at fp16 rounding level). At head_dim 16 (no
+  key-range splits) the rows must be bit-identical.
+* Decode rows alone vs inside a 64-row batch: the balanced split schedule sizes every split from
+  the batch's total block count, so a row's splits (and its fp32 merge order) depend on the
+  batch; the output may differ in the last fp16 bit, never more (DECODE_ULPS).
+"""
+
+from __future__ import annotations
+
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from turingserve_amd import get_ops
+from turingserve_amd import hip_ops as K
+from turingserve_amd.metadata import BatchItem, InputBuilder, SeqState
+from turingserve_amd.qwen2 import TINY_G2, Qwen2Config, Qwen2Model, random_weights
+
+from .test_kernels_gpu import DEV, make_paged, meta_of
+
+pytestmark = pytest.mark.gpu
+
+D128 = Qwen2Config(768, 1536, 2, 6, 1, 4096, max_position_embeddings=4096)   # G = 6, head_dim 128
+LENGTHS = [5, 16, 17, 100, 333, 512, 1000, 2047]
+REF_REL_FRO, REF_REL_MAX = 5e-3, 1e-2
+BATCH_REL_MAX = REF_REL_MAX
+DECODE_ULPS = 2
+
+
+def _ids(n, seed, vocab):
+    r = random.Random(seed)
+    return [r.randrange(vocab) for _ in range(n)]
+
+
+def _model(cfg, ops="hip"):
+    w = random_weights(cfg, DEV, seed=0)
+    return Qwen2Model(cfg, w, get_ops(ops), max_model_len=4096)
+
+
+def _logits(model, items, kv, tokens):
+    inp = InputBuilder(tokens, len(items), 160, DEV).build(items)
+    with torch.inference_mode():
+        return model.compute_logits(model.forward(inp.input_ids, inp.positions, inp.meta, kv),
+                                    inp.sample_indices).clone()
+
+
+@pytest.mark.parametrize("cfg", [TINY_G2, D128], ids=["d16", "d128"])
+def test_paged_equals_contiguous_and_reference(cfg):
+    hip, ref = _model(cfg), _model(cfg, "reference")
+    ref.w = hip.w
+    ids = _ids(700, seed=5, vocab=cfg.vocab_size)
+    nb = -(-len(ids) // 16)
+    shuffled = list(range(1, 200))
+    random.Random(1).shuffle(shuffled)
+    out = {}
+    for name, table in (("contiguous", list(range(1, nb + 1))), ("shuffled", shuffled[:nb])):
+        s = SeqState(ids, table)
+        out[name] = _logits(hip, [BatchItem(s, 0, ids, "all")], hip.new_kv_cache(200), 1024)
+    assert torch.equal(out["contiguous"], out["shuffled"])
+    s = SeqState(ids, shuffled[:nb])
+    want = _logits(ref, [BatchItem(s, 0, ids, "all")], ref.new_kv_cache(200), 1024)
+    d = out["shuffled"] - want
+    rel_fro = float(d.norm() / want.norm())
+    rel_max = float(d.abs().max() / want.abs().max())
+    print(f"head_dim {cfg.head_dim}: hip vs reference logits rel Frobenius {rel_fro:.2e}, "
+          f"largest difference {rel_max:.2e} of the largest logit")
+    assert rel_fro <= REF_REL_FRO and rel_max <= REF_REL_MAX
+
+
+@pytest.mark.parametrize("cfg", [TINY_G2, D128], ids=["d16", "d128"])
+def test_prompts_alone_vs_together(cfg):
+    model = _model(cfg)
+    prompts = [_ids(n, seed=n, vocab=cfg.vocab_size) for n in LENGTHS]
+    free = list(range(1, 600))
+    random.Random(0).shuffle(free)
+    alone = []
+    for p in prompts:
+        s = SeqState(p, free[:-(-len(p) // 16)])
+        alone.append(_logits(model, [BatchItem(s, 0, p, "all")], model.new_kv_cache(600), 2048))
+    random.Random(1).shuffle(free)
+    items, off = [], 0
+    for p in prompts:
+        nb = -(-len(p) // 16)
+        items.append(BatchItem(SeqState(p, free[off:off + nb]), 0, p, "all"))
+        off += nb
+    together = _logits(model, items, model.new_kv_cache(600), sum(LENGTHS))
+    worst, start = 0.0, 0
+    for n, a in zip(LENGTHS, alone):
+        d = float((together[start:start + n] - a).abs().max() / a.abs().max())
+        worst = max(worst, d)
+        if cfg.head_dim < 128:
+            assert d == 0.0, f"prompt of {n} tokens: rows differ by {d}"
+        assert d <= BATCH_REL_MAX, f"prompt of {n} tokens: logits differ by {d:.2e} of the largest"
+        start += n
+    print(f"head_dim {cfg.head_dim}: largest logit difference alone vs together {worst:.2e} "
+          f"of the largest logit")
+
+
+def _head_ulps(a: np.ndarray, b: np.ndarray, D: int) -> float:
+    """Largest |a - b| in fp16 ulps of each head's largest magnitude (a, b: [H * D])."""
+    d = np.abs(a - b).reshape(-1, D)
+    scale = np.maximum(np.abs(a), np.abs(b)).reshape(-1, D).max(axis=1, keepdims=True)
+    ulp = 2.0 ** (np.floor(np.log2(np.maximum(scale, 2.0 ** -14))) - 10)
+    return float((d / ulp).max())
+
+
+def test_decode_rows_alone_vs_in_a_batch():
+    H, KVH, D = 12, 2, 128
+    g = torch.Generator().manual_seed(0)
+    from turingserve_amd import synth
+
+    ctx = synth.log_uniform_ints(64, 128, 4096, g)
+    q, kc, vc, qsl, sl, bt = make_paged(ctx, H, KVH, D, seed=3)
+    q, kc, vc, qsl, sl, bt = (x.to(DEV) for x in (q, kc, vc, qsl, sl, bt))
+    meta = meta_of(qsl, sl, bt, 64, [1] * 64, 64)
+    batch = K.paged_attention(q, kc, vc, meta, D ** -0.5).float().cpu().numpy()
+    order = list(range(64))
+    random.Random(2).shuffle(order)
+    perm = torch.tensor(order, device=DEV)
+    meta_p = meta_of(qsl, sl[perm], bt[perm], 64, [1] * 64, 64)
+    shuffled = K.paged_attention(q[perm], kc, vc, meta_p, D ** -0.5).float().cpu().numpy()
+    picks = sorted(range(64), key=lambda i: ctx[i])[::8] + [int(np.argmax(ctx))]
+    worst = 0.0
+    for i in picks:
+        m1 = meta_of(qsl[:2], sl[i:i + 1], bt[i:i + 1], 1, [1], 1)
+        one = K.paged_attention(q[i:i + 1], kc, vc, m1, D ** -0.5).float().cpu().numpy()[0]
+        for other, what in ((batch[i], "in the batch"), (shuffled[order.index(i)], "shuffled")):
+            ulps = _head_ulps(one, other, D)
+            worst = max(worst, ulps)
+            assert ulps <= DECODE_ULPS, f"context {ctx[i]}: alone vs {what} differ by {ulps:.1f} ulps"
+    print(f"decode rows alone vs in a batch: at most {worst:.1f} fp16 ulps apart")
