@@ -69,7 +69,7 @@ extern "C" {
 /* Library version string, e.g. "turingserve_hip 0.1.0 gfx950". */
 const char* ts_version(void);
 
-/* Message of the last failing call on this host thread ("" if none). */
+/* Message of the most recent call on this host thread: its error, or "" if it succeeded. */
 const char* ts_last_error(void);
 
 /* Number of compute units of `device` (the reference's num_sms, utils/gpu.py:19-24). */

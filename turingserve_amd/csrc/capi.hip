@@ -18,6 +18,8 @@ int set_error(int status, const char* fmt, ...) {
   return status;
 }
 
+void clear_error() { g_err[0] = '\0'; }
+
 int check_launch(const char* what) {
   hipError_t e = hipGetLastError();
   if (e != hipSuccess)
@@ -25,10 +27,20 @@ int check_launch(const char* what) {
   return TS_OK;
 }
 
-int device_cu_count(int* out) {
+// The device `stream` belongs to (the current device for the null stream): the one whose
+// kernels the call launches, whatever device the calling thread has current.
+int stream_device(void* stream, int* device) {
+  hipError_t e = stream ? hipStreamGetDevice(reinterpret_cast<hipStream_t>(stream), device)
+                        : hipGetDevice(device);
+  if (e != hipSuccess)
+    return set_error(TS_ERR_DEVICE, "cannot tell the stream's device: %s", hipGetErrorString(e));
+  return TS_OK;
+}
+
+int device_cu_count(void* stream, int* out) {
   int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return set_error(TS_ERR_DEVICE, "hipGetDevice failed");
-  return ts_device_cu_count(dev, out);
+  const int st = stream_device(stream, &dev);
+  return st != TS_OK ? st : ts_device_cu_count(dev, out);
 }
 
 }  // namespace ts
@@ -38,10 +50,11 @@ extern "C" const char* ts_version(void) { return "turingserve_hip 0.1.0 gfx950";
 extern "C" const char* ts_last_error(void) { return ts::g_err; }
 
 extern "C" int ts_device_cu_count(int device, int* cu_count) {
+  ts::clear_error();
   TS_REQUIRE(cu_count != nullptr, TS_ERR_INVALID_ARG, "device_cu_count: null output");
   // One cached answer per device (a startup query, like utils/gpu.py:19-24 behind lru_cache).
-  static int cache[64] = {0};
-  if (device >= 0 && device < 64 && cache[device] > 0) {
+  static int cache[ts::kMaxDevices] = {0};
+  if (device >= 0 && device < ts::kMaxDevices && cache[device] > 0) {
     *cu_count = cache[device];
     return TS_OK;
   }
@@ -50,7 +63,7 @@ extern "C" int ts_device_cu_count(int device, int* cu_count) {
   if (e != hipSuccess || n <= 0)
     return ts::set_error(TS_ERR_DEVICE, "device_cu_count: hipDeviceGetAttribute failed: %s",
                          hipGetErrorString(e));
-  if (device >= 0 && device < 64) cache[device] = n;
+  if (device >= 0 && device < ts::kMaxDevices) cache[device] = n;
   *cu_count = n;
   return TS_OK;
 }

@@ -90,9 +90,12 @@ __device__ __forceinline__ void st(void* p, T v) { *reinterpret_cast<T*>(p) = v;
 // Host side: error reporting shared by every entry point (defined in capi.hip).
 // ---------------------------------------------------------------------------------------------
 namespace ts {
+constexpr int kMaxDevices = 64;                 // per-device host caches (CU counts, scratch)
 int set_error(int status, const char* fmt, ...);
+void clear_error();
 int check_launch(const char* what);
-int device_cu_count(int* out);
+int stream_device(void* stream, int* device);
+int device_cu_count(void* stream, int* out);
 inline bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 }  // namespace ts
 

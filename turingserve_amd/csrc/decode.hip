@@ -43,7 +43,7 @@ static int decode_entry(int32_t version, const void* q, int64_t q_stride_t, int6
                  aligned(k_cache, 2 * vec) && aligned(v_cache, 2 * vec),
              TS_ERR_INVALID_ARG, "decode_attention: q / caches must be %d-byte aligned", 2 * vec);
   int cus = 0;
-  int st = device_cu_count(&cus);
+  int st = device_cu_count(stream, &cus);
   if (st != TS_OK) return st;
   const SplitPlan p = plan_decode(version, num_seqs, num_heads, num_kv_heads, head_dim,
                                   max_seq_len, partition, cus);
@@ -111,6 +111,7 @@ extern "C" int ts_decode_attention(int32_t version, const void* q, int64_t q_str
                                    int32_t head_dim, float scale, int32_t max_seq_len,
                                    int32_t partition, void* workspace, size_t workspace_bytes,
                                    void* stream) {
+  ts::clear_error();
   return decode_entry(version, q, q_stride_t, q_stride_h, out, out_stride_t, k_cache, v_cache,
                       num_blocks, block_tables, bt_stride, max_blocks_per_seq, seq_lens, num_seqs,
                       num_heads, num_kv_heads, head_dim, scale, max_seq_len, partition, workspace,
@@ -125,6 +126,7 @@ extern "C" int ts_decode_attention_kv_write(
     int64_t bt_stride, int32_t max_blocks_per_seq, const int32_t* seq_lens, int32_t num_seqs,
     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seq_len,
     int32_t partition, void* workspace, size_t workspace_bytes, void* stream) {
+  ts::clear_error();
   TS_REQUIRE(num_seqs >= 0, TS_ERR_INVALID_ARG, "decode_attention_kv_write: num_seqs %d < 0",
              num_seqs);
   if (num_seqs == 0) return TS_OK;
@@ -149,6 +151,7 @@ extern "C" int ts_decode_rope_kv_write_attention(
     int32_t max_blocks_per_seq, const int32_t* seq_lens, int32_t num_seqs, int32_t num_heads,
     int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seq_len, int32_t partition,
     void* workspace, size_t workspace_bytes, void* stream) {
+  ts::clear_error();
   TS_REQUIRE(num_seqs >= 0, TS_ERR_INVALID_ARG,
              "decode_rope_kv_write_attention: num_seqs %d < 0", num_seqs);
   if (num_seqs == 0) return TS_OK;

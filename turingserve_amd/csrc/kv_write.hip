@@ -48,6 +48,7 @@ extern "C" int ts_kv_write(const void* k, const void* v, int64_t k_stride_t, int
                            int64_t v_stride_t, int64_t v_stride_h, void* k_cache, void* v_cache,
                            int64_t num_blocks, const int64_t* slot_mapping, int64_t num_tokens,
                            int32_t num_kv_heads, int32_t head_dim, void* stream) {
+  ts::clear_error();
   TS_REQUIRE(num_tokens >= 0, TS_ERR_INVALID_ARG, "kv_write: num_tokens %lld < 0",
              (long long)num_tokens);
   if (num_tokens == 0) return TS_OK;     // ops/triton_kv_write.py:32-33

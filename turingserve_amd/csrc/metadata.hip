@@ -109,6 +109,7 @@ extern "C" int ts_step_metadata(const int32_t* packed, int32_t num_seqs, int64_t
                                 int64_t* slot_mapping, int32_t* query_start_loc,
                                 int32_t* seq_lens, int32_t* block_tables,
                                 int64_t* sample_indices, void* stream) {
+  ts::clear_error();
   TS_REQUIRE(num_seqs >= 0 && pad_seqs >= num_seqs && num_tokens >= 0 && num_block_ids >= 0,
              TS_ERR_INVALID_ARG, "step_metadata: num_seqs=%d pad_seqs=%d num_tokens=%lld",
              num_seqs, pad_seqs, (long long)num_tokens);

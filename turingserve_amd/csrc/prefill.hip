@@ -40,7 +40,7 @@ int prefill_launch(const void* q, int64_t q_stride_t, int64_t q_stride_h, void* 
   const float sl2 = scale * kLog2eP;
   if (head_dim == 128) {
     int cus = 0;
-    if (workspace != nullptr && device_cu_count(&cus) != TS_OK) return TS_ERR_DEVICE;
+    if (workspace != nullptr && device_cu_count(stream, &cus) != TS_OK) return TS_ERR_DEVICE;
     TilePlan pl = tile_plan(P, num_heads, head_dim, max_query_len, max_seq_len, cus,
                             workspace != nullptr);
     if (pl.ws_bytes > workspace_bytes || (pl.ws_bytes > 0 && !aligned(workspace, 16)))
@@ -100,6 +100,7 @@ extern "C" int ts_prefill_attention(const void* q, int64_t q_stride_t, int64_t q
                                     int32_t num_decode, int32_t max_query_len, int32_t num_heads,
                                     int32_t num_kv_heads, int32_t head_dim, float scale,
                                     void* stream) {
+  ts::clear_error();
   return prefill_launch(q, q_stride_t, q_stride_h, out, out_stride_t, num_tokens, k_cache,
                         v_cache, num_blocks, block_tables, bt_stride, max_blocks_per_seq, seq_lens,
                         query_start_loc, num_seqs, num_decode, max_query_len, max_query_len,
@@ -117,6 +118,7 @@ extern "C" int ts_prefill_attention_ws(const void* q, int64_t q_stride_t, int64_
                                        int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                                        float scale, void* workspace, size_t workspace_bytes,
                                        void* stream) {
+  ts::clear_error();
   return prefill_launch(q, q_stride_t, q_stride_h, out, out_stride_t, num_tokens, k_cache,
                         v_cache, num_blocks, block_tables, bt_stride, max_blocks_per_seq, seq_lens,
                         query_start_loc, num_seqs, num_decode, max_query_len, max_seq_len,

@@ -169,6 +169,7 @@ extern "C" int ts_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
                                   int32_t num_kv_heads, int32_t head_dim, float scale,
                                   int32_t decode_version, int32_t partition, void* workspace,
                                   size_t workspace_bytes, void* stream) {
+  ts::clear_error();
   TS_REQUIRE(num_decode >= 0 && num_decode <= num_seqs, TS_ERR_INVALID_ARG,
              "paged_attention: num_decode=%d outside [0, num_seqs=%d]", num_decode, num_seqs);
   TS_REQUIRE(num_decode <= num_tokens, TS_ERR_INVALID_ARG,
@@ -177,7 +178,7 @@ extern "C" int ts_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
   const int pf_seq = max_prefill_seq_len > 0 ? max_prefill_seq_len : max_seq_len;
   int cus = 0;
   if (num_decode > 0 && num_seqs > num_decode && head_dim == 128 && workspace != nullptr) {
-    const int st = device_cu_count(&cus);
+    const int st = device_cu_count(stream, &cus);
     if (st != TS_OK) return st;
     const RaggedPlan r = ragged_plan(num_seqs, num_decode, max_query_len, max_seq_len,
                                      max_prefill_seq_len, num_heads, num_kv_heads, head_dim,

@@ -166,6 +166,7 @@ extern "C" int ts_rmsnorm(const void* x, int64_t x_stride, const void* residual,
                           int64_t residual_stride, const void* weight, void* out,
                           int64_t out_stride, void* residual_out, int64_t residual_out_stride,
                           int64_t num_tokens, int32_t hidden, float eps, void* stream) {
+  ts::clear_error();
   TS_REQUIRE(num_tokens >= 0, TS_ERR_INVALID_ARG, "rmsnorm: num_tokens %lld < 0",
              (long long)num_tokens);
   if (num_tokens == 0) return TS_OK;
@@ -197,6 +198,7 @@ extern "C" int ts_rope(void* qkv, int64_t qkv_stride, const int64_t* positions,
                        const float* cos_table, const float* sin_table, int64_t max_position,
                        int64_t num_tokens, int32_t num_heads, int32_t num_kv_heads,
                        int32_t head_dim, void* stream) {
+  ts::clear_error();
   TS_REQUIRE(num_tokens >= 0, TS_ERR_INVALID_ARG, "rope: num_tokens %lld < 0", (long long)num_tokens);
   if (num_tokens == 0) return TS_OK;
   TS_REQUIRE(qkv && positions && cos_table && sin_table && max_position > 0, TS_ERR_INVALID_ARG,
@@ -220,6 +222,7 @@ extern "C" int ts_rope_kv_write(void* qkv, int64_t qkv_stride, const int64_t* po
                                 int32_t num_kv_heads, int32_t head_dim, void* k_cache,
                                 void* v_cache, int64_t num_blocks, const int64_t* slot_mapping,
                                 void* stream) {
+  ts::clear_error();
   TS_REQUIRE(num_tokens >= 0, TS_ERR_INVALID_ARG, "rope_kv_write: num_tokens %lld < 0",
              (long long)num_tokens);
   if (num_tokens == 0) return TS_OK;
@@ -243,6 +246,7 @@ extern "C" int ts_rope_kv_write(void* qkv, int64_t qkv_stride, const int64_t* po
 
 extern "C" int ts_silu_mul(const void* gu, int64_t gu_stride, void* out, int64_t out_stride,
                            int64_t num_tokens, int32_t intermediate, void* stream) {
+  ts::clear_error();
   TS_REQUIRE(num_tokens >= 0, TS_ERR_INVALID_ARG, "silu_mul: num_tokens %lld < 0",
              (long long)num_tokens);
   if (num_tokens == 0) return TS_OK;

@@ -829,7 +829,7 @@ static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const v
                         int32_t M, int32_t N, int32_t K, void* workspace, size_t workspace_bytes,
                         hipStream_t s, const GemmIo& io, int variant, int splits) {
   int cus = 0;
-  int st = device_cu_count(&cus);
+  int st = device_cu_count(s, &cus);
   if (st != TS_OK) return st;
   const bool glu = io.glu > 0;                    // N = 2 * io.glu, y is [M, io.glu]
   GemmPlan p = plan_gemm_v(M, N, K, cus, variant, splits);
@@ -923,6 +923,7 @@ extern "C" int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const
                              int32_t scale_is_fp16, const void* bias, void* y, int64_t ldy,
                              int32_t M, int32_t N, int32_t K, void* workspace,
                              size_t workspace_bytes, void* stream) {
+  ts::clear_error();
   return w8a16_gemm_checked(x, ldx, wq, scale, scale_is_fp16, bias, y, ldy, M, N, K, kVarAuto, 0,
                             workspace, workspace_bytes, stream);
 }
@@ -931,6 +932,7 @@ extern "C" int ts_w8a16_gemm_v(const void* x, int64_t ldx, const int8_t* wq, con
                                int32_t scale_is_fp16, const void* bias, void* y, int64_t ldy,
                                int32_t M, int32_t N, int32_t K, int32_t variant, int32_t splits,
                                void* workspace, size_t workspace_bytes, void* stream) {
+  ts::clear_error();
   return w8a16_gemm_checked(x, ldx, wq, scale, scale_is_fp16, bias, y, ldy, M, N, K, variant,
                             splits, workspace, workspace_bytes, stream);
 }
@@ -945,6 +947,7 @@ extern "C" int ts_logits_int8(const void* hidden, int64_t hidden_stride, int64_t
                               const void* scale, int32_t scale_is_fp16, float* logits,
                               int64_t logits_stride, int32_t vocab, int32_t hidden_size,
                               void* workspace, size_t workspace_bytes, void* stream) {
+  ts::clear_error();
   TS_REQUIRE(num_samples >= 0 && vocab > 0 && hidden_size > 0, TS_ERR_INVALID_ARG,
              "logits_int8: bad shape S=%d V=%d H=%d", num_samples, vocab, hidden_size);
   if (num_samples == 0) return TS_OK;
@@ -978,6 +981,7 @@ extern "C" int ts_w8a16_glu(const void* x, int64_t ldx, const int8_t* wq, const 
                             int32_t scale_is_fp16, const void* bias, void* out, int64_t ldo,
                             int32_t M, int32_t intermediate, int32_t K, int32_t variant,
                             int32_t splits, void* workspace, size_t workspace_bytes, void* stream) {
+  ts::clear_error();
   TS_REQUIRE(M >= 0 && intermediate > 0 && intermediate <= (1 << 29) && K > 0, TS_ERR_INVALID_ARG,
              "w8a16_glu: bad shape M=%d I=%d K=%d", M, intermediate, K);
   TS_REQUIRE(variant_valid(variant, splits, M < 1 ? 1 : M), TS_ERR_UNSUPPORTED,
