@@ -143,6 +143,31 @@ int ts_decode_attention_kv_write(int32_t version,
                                  void* stream);
 
 /*
+ * ts_decode_attention_kv_write without a workspace argument: the split-K scratch is a static
+ * device array of TS_NOALLOC_SCRATCH_BYTES inside the library (one per GPU, held until the
+ * process ends), so this call allocates nothing. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory (code under hipGraph capture, serving loops and
+ * harnesses that forbid hipMalloc). Same arguments, results and preconditions as
+ * ts_decode_attention_kv_write; a batch whose split scratch (ts_decode_workspace_bytes()) exceeds
+ * TS_NOALLOC_SCRATCH_BYTES is rejected with TS_ERR_WORKSPACE before anything is launched. The
+ * first call on a device looks up the array's device address (make it outside graph capture).
+ * Calls that overlap on one GPU share the array and race: serialise them (one stream).
+ */
+#define TS_NOALLOC_SCRATCH_BYTES (16u << 20)
+int ts_decode_attention_kv_write_noalloc(int32_t version,
+                                         const void* q, int64_t q_stride_t, int64_t q_stride_h,
+                                         const void* k, const void* v, int64_t k_stride_t,
+                                         int64_t k_stride_h, int64_t v_stride_t,
+                                         int64_t v_stride_h, const int64_t* slot_mapping,
+                                         void* out, int64_t out_stride_t,
+                                         void* k_cache, void* v_cache, int64_t num_blocks,
+                                         const int32_t* block_tables, int64_t bt_stride,
+                                         int32_t max_blocks_per_seq, const int32_t* seq_lens,
+                                         int32_t num_seqs, int32_t num_heads,
+                                         int32_t num_kv_heads, int32_t head_dim, float scale,
+                                         int32_t max_seq_len, int32_t partition, void* stream);
+
+/*
  * ts_rope_kv_write followed by ts_decode_attention, as one launch: the whole attention half of a
  * pure-decode layer step (model/qwen2.py:26-28, :89 with ops/triton_rope.py:27-31,
  * ops/triton_kv_write.py:28-35 and ops/triton_ops.py:60-71). qkv rows as for ts_rope_kv_write

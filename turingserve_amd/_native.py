@@ -24,6 +24,7 @@ TS_ERR_UNSUPPORTED = -2
 TS_ERR_WORKSPACE = -3
 TS_ERR_LAUNCH = -4
 TS_ERR_DEVICE = -5
+TS_NOALLOC_SCRATCH_BYTES = 16 << 20    # static split scratch of ts_decode_attention_kv_write_noalloc
 
 DECODE_VERSIONS = {None: 0, "auto": 0, "v1": 1, "v2": 2, "v3": 3}
 
@@ -45,6 +46,11 @@ SIGNATURES = {
                                                     _i64, _i64, _p, _p, _i64, _p, _p, _i64, _p,
                                                     _i64, _i32, _p, _i32, _i32, _i32, _i32, _f32,
                                                     _i32, _i32, _p, _sz, _p]),
+    "ts_decode_attention_kv_write_noalloc": (ctypes.c_int, [_i32, _p, _i64, _i64, _p, _p, _i64,
+                                                            _i64, _i64, _i64, _p, _p, _i64, _p,
+                                                            _p, _i64, _p, _i64, _i32, _p, _i32,
+                                                            _i32, _i32, _i32, _f32, _i32, _i32,
+                                                            _p]),
     "ts_decode_rope_kv_write_attention": (ctypes.c_int, [_i32, _p, _i64, _p, _p, _p, _i64, _p,
                                                          _i64, _p, _p, _i64, _p, _p, _i64, _i32,
                                                          _p, _i32, _i32, _i32, _i32, _f32, _i32,

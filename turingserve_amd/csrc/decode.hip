@@ -1,5 +1,7 @@
 // Paged decode attention for gfx950 (ops/triton_decode_attention.py, ops/triton_ops.py:35-57).
 // Host entry points; the kernels and their launch plans are in decode_kernels.h.
+#include <mutex>
+
 #include "decode_kernels.h"
 
 using namespace ts;
@@ -141,6 +143,76 @@ extern "C" int ts_decode_attention_kv_write(
                       num_blocks, block_tables, bt_stride, max_blocks_per_seq, seq_lens, num_seqs,
                       num_heads, num_kv_heads, head_dim, scale, max_seq_len, partition, workspace,
                       workspace_bytes, stream, nr);
+}
+
+// ---------------------------------------------------------------------------------------------
+// ts_decode_attention_kv_write_noalloc: the same launch with its split-K scratch in `scratch`,
+// a library-owned device array (one copy per GPU, held until the process ends), so the call
+// allocates nothing. The split kernel writes every partial row, and every split count, that the
+// merge kernel reads in the same call (rows past a sequence's split count are skipped, a padding
+// row reads none), so stale contents from an earlier call never matter and nothing is cleared.
+// Calls that overlap on one GPU (two streams, two threads) share the array and race.
+// ---------------------------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[TS_NOALLOC_SCRATCH_BYTES];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_addr[kMaxDevices];      // device address of `scratch`, per device
+
+// Device address of `scratch` on `dev`, looked up once per device with that device current (the
+// host-side name of a __device__ array is not a device address).
+static int scratch_address(int dev, void** addr) {
+  TS_REQUIRE(dev >= 0 && dev < kMaxDevices, TS_ERR_DEVICE, "noalloc: device %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_addr[dev] == nullptr) {
+    int cur = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e == hipSuccess && cur != dev) e = hipSetDevice(dev);
+    void* p = nullptr;
+    if (e == hipSuccess) e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) (void)hipSetDevice(cur);
+    if (e != hipSuccess || p == nullptr)
+      return set_error(TS_ERR_DEVICE, "noalloc: hipGetSymbolAddress of the scratch failed: %s",
+                       hipGetErrorString(e));
+    g_scratch_addr[dev] = p;
+  }
+  *addr = g_scratch_addr[dev];
+  return TS_OK;
+}
+
+extern "C" int ts_decode_attention_kv_write_noalloc(
+    int32_t version, const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k,
+    const void* v, int64_t k_stride_t, int64_t k_stride_h, int64_t v_stride_t,
+    int64_t v_stride_h, const int64_t* slot_mapping, void* out, int64_t out_stride_t,
+    void* k_cache, void* v_cache, int64_t num_blocks, const int32_t* block_tables,
+    int64_t bt_stride, int32_t max_blocks_per_seq, const int32_t* seq_lens, int32_t num_seqs,
+    int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seq_len,
+    int32_t partition, void* stream) {
+  ts::clear_error();
+  TS_REQUIRE(num_seqs >= 0, TS_ERR_INVALID_ARG,
+             "decode_attention_kv_write_noalloc: num_seqs %d < 0", num_seqs);
+  if (num_seqs == 0) return TS_OK;
+  int dev = 0, cus = 0;
+  int st = stream_device(stream, &dev);
+  if (st == TS_OK) st = ts_device_cu_count(dev, &cus);
+  if (st != TS_OK) return st;
+  const size_t need = ts_decode_workspace_bytes(version, num_seqs, num_heads, num_kv_heads,
+                                                head_dim, max_seq_len, partition, cus);
+  TS_REQUIRE(need <= TS_NOALLOC_SCRATCH_BYTES, TS_ERR_WORKSPACE,
+             "decode_attention_kv_write_noalloc: this batch (%d sequences, %d heads, head_dim %d) "
+             "needs %zu bytes of split scratch, the static scratch holds %zu; call "
+             "ts_decode_attention_kv_write with a workspace instead",
+             num_seqs, num_heads, head_dim, need, (size_t)TS_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0) {
+    st = scratch_address(dev, &ws);
+    if (st != TS_OK) return st;
+  }
+  return ts_decode_attention_kv_write(version, q, q_stride_t, q_stride_h, k, v, k_stride_t,
+                                      k_stride_h, v_stride_t, v_stride_h, slot_mapping, out,
+                                      out_stride_t, k_cache, v_cache, num_blocks, block_tables,
+                                      bt_stride, max_blocks_per_seq, seq_lens, num_seqs, num_heads,
+                                      num_kv_heads, head_dim, scale, max_seq_len, partition, ws,
+                                      need > 0 ? (size_t)TS_NOALLOC_SCRATCH_BYTES : 0, stream);
 }
 
 extern "C" int ts_decode_rope_kv_write_attention(
