@@ -12,12 +12,16 @@ other form is reported beside the headline either way). Steps rotate over
 from HBM, and every step is a hipGraph replay (pure-decode steps are graph-captured, as the
 reference's CudaGraphRunner does). Inputs are resident in HBM before timing starts.
 
-value = algorithmic bytes of one step / wall time of one step, in GB/s. The roofline entry prices
-the step's kernels (the fused launch and its merge; with --separate-kv-write the attention call
-alone), timed with HIP events around a graph of them on the stream they run on, against the
-8 TB/s HBM peak. The CPU baseline is the oracle's numpy restatement of the same step
-(ops/reference.py semantics) on the host cores. Secondary results for the other configurations go
-under "extra".
+value = algorithmic bytes of one step / wall time of one step, in GB/s; exactly --steps steps are
+timed (whole replays of the layer graph plus one graph of the remaining layers). The roofline
+entry prices the step's kernels (the fused launch and its merge; with --separate-kv-write the
+attention call alone), timed with HIP events around a graph of them on the stream they run on,
+against the 8 TB/s HBM peak, and (roofline.measured) against this device's measured copy rate and
+the gather floor of the same step's bytes. The CPU baseline is the reference backend
+(get_ops("reference"), the torch twins of ops/reference.py) doing the same step on every host
+core the process may use, with the numpy oracle's time beside it. Secondary results for the
+other configurations go under "extra"; W8A16 and logits weights are timed cold (copies cycled
+past the 256 MB Infinity Cache).
 """
 
 from __future__ import annotations
@@ -51,7 +55,7 @@ def parse_args():
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", choices=["decode", "prefill", "w8a16", "logits", "metadata", "mixed",
-                                       "decode_model"],
+                                       "decode_model", "calibration"],
                     default=None,
                     help="run one workload alone (for profiling); prints its result as JSON")
     ap.add_argument("--copy-calibration", action="store_true",
@@ -155,10 +159,19 @@ def bench_decode(args, torch, K, synth):
     with torch.cuda.graph(g_other, pool=pool):
         for l in range(L):
             (fused_step if args.separate_kv_write else two_call_step)(l)
+    # the remainder of --steps that is not a whole replay of L layers: one more graph of the
+    # first steps % L layers, so exactly --steps steps are timed
+    tail = args.steps % L
+    g_tail = None
+    if tail:
+        g_tail = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_tail, pool=pool):
+            for l in range(tail):
+                step_fn(l)
     torch.cuda.synchronize()
     for _ in range(max(1, args.warmup // L)):
         g_step.replay()
-    replays = max(1, -(-args.steps // L))
+    replays = max(1, args.steps // L) if args.steps >= L else 0
 
     def timed(graph):
         evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -171,16 +184,22 @@ def bench_decode(args, torch, K, synth):
         return [a.elapsed_time(b) / L for a, b in evs]
 
     ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(replays)]
+          for _ in range(replays + (1 if g_tail else 0))]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(replays):
         ev[i][0].record()
         g_step.replay()
         ev[i][1].record()
+    if g_tail:
+        ev[-1][0].record()
+        g_tail.replay()
+        ev[-1][1].record()
     torch.cuda.synchronize()
     t1 = time.perf_counter()
-    step_ev_ms = statistics.fmean(a.elapsed_time(b) for a, b in ev) / L
+    steps_timed = replays * L + tail
+    step_ev_ms = sum(a.elapsed_time(b) for a, b in ev) / steps_timed
+    replays = max(replays, 1)
     attn_ms = timed(g_attn)
     other_ms = statistics.fmean(timed(g_other))
     # graph == eager: the last layer's output of the step graph against an eager two-call step
@@ -188,7 +207,6 @@ def bench_decode(args, torch, K, synth):
                                 decode_version=version,
                                 partition=args.partition or K.DEFAULT_PARTITION)
     same = bool(torch.equal(ref_out, step_outs[L - 1]))
-    steps_timed = replays * L
     b = decode_step_bytes(st)
     step_s = (t1 - t0) / steps_timed
     res = {
@@ -198,21 +216,58 @@ def bench_decode(args, torch, K, synth):
         "fused": not args.separate_kv_write,
         ("step_two_launch_ms" if not args.separate_kv_write else "step_fused_ms"): other_ms,
     }
-    del kv, g_step, g_attn, g_other
+    del kv, g_step, g_attn, g_other, g_tail
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return st, res
 
 
+def cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo", encoding="utf-8"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
 def cpu_baseline(st, seconds: float):
-    """The oracle (numpy restatement of the reference twins) on the host: kv_write + paged
-    attention of the same step, repeated for about `seconds`."""
+    """The reference backend on the host CPU: get_ops("reference") (the torch twins of
+    ops/reference.py, what the reference's --kernels reference runs) doing the same step,
+    kv_write then paged_attention, on every core this process may use, repeated for about
+    `seconds`. Returns (median seconds per step, threads, runs)."""
+    import torch
+
+    from turingserve_amd import get_ops
+
+    ops = get_ops("reference")
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
+    torch.set_num_threads(cores)
+    qkv = st.qkv.clone()
+    q, k, v = st.views(qkv)
+    kc, vc = st.k_cache.clone(), st.v_cache.clone()
+    meta = st.meta("cpu")
+    times = []
+    t_end = time.perf_counter() + seconds
+    while True:
+        t0 = time.perf_counter()
+        ops.kv_write(k, v, kc, vc, meta.slot_mapping)
+        ops.paged_attention(q, kc, vc, meta, st.D ** -0.5)
+        times.append(time.perf_counter() - t0)
+        if time.perf_counter() >= t_end:
+            break
+    return statistics.median(times), cores, len(times)
+
+
+def oracle_baseline(st, seconds: float):
+    """The numpy oracle's restatement of the same step (fp32 math), for comparison."""
     import numpy as np
     from threadpoolctl import threadpool_limits
 
     from oracle import paged as OP
 
-    cores = max(1, min(16, os.cpu_count() or 1))
+    cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else os.cpu_count()
     q, k, v = (x.numpy() for x in st.views())
     kc, vc = st.k_cache.numpy().copy(), st.v_cache.numpy().copy()
     qsl, sl, bt, sm = (st.query_start_loc.numpy(), st.seq_lens.numpy(), st.block_tables.numpy(),
@@ -223,8 +278,7 @@ def cpu_baseline(st, seconds: float):
         while True:
             t0 = time.perf_counter()
             OP.kv_write(k, v, kc, vc, sm)
-            out = OP.paged_attention(q, kc, vc, qsl, sl, bt, st.D ** -0.5, np.float32)
-            out.astype(np.float16)
+            OP.paged_attention(q, kc, vc, qsl, sl, bt, st.D ** -0.5, np.float32).astype(np.float16)
             times.append(time.perf_counter() - t0)
             if time.perf_counter() >= t_end:
                 break
@@ -263,6 +317,71 @@ def time_graph(torch, fn, reps: int, inner: int = 1):
     return s.elapsed_time(e) / (reps * inner)
 
 
+def bench_calibration(torch, synth, layers: int = 8) -> dict:
+    """Measured ceilings beside the spec peaks (8 TB/s HBM, 2.5 PFLOP/s dense fp16 MFMA):
+    * copy: a 1 GiB device-to-device copy (bytes read + written per second);
+    * gather floor: ts_probe_gather over config 2's chunk list -- every cached (block, KV head) K
+      and V chunk of the step's 64 sequences once (4 KiB each, the decode step's KV bytes), no
+      arithmetic, no dependent metadata loads -- with `layers` layer caches rotated as in the
+      headline, and the same number of bytes read contiguously;
+    * MFMA: ts_probe_mfma, back-to-back independent v_mfma_f32_32x32x16_f16 on every SIMD."""
+    import numpy as np
+
+    from turingserve_amd import _native as N
+
+    dev = torch.device("cuda", 0)
+    lib = N.lib()
+    cur = lambda: torch.cuda.current_stream().cuda_stream      # noqa: E731 (the capture stream)
+    out = {}
+    a = torch.empty(2 ** 30, dtype=torch.uint8, device=dev)
+    b2 = torch.empty_like(a)
+    ms = time_graph(torch, lambda: b2.copy_(a), reps=5)
+    out["copy_GBps"] = round(2 * a.numel() / ms / 1e6, 1)
+    del a, b2
+    st = synth.config2(seed=0)
+    NB, KVH, D = st.k_cache.shape[0], st.KVH, st.D
+    chunk = 16 * D * 2
+    half = NB * KVH * chunk                        # bytes of one layer's K (then V) cache
+    offs = []
+    bt, sl = st.block_tables.numpy(), st.seq_lens.numpy()
+    for h in range(KVH):
+        for s_, L_ in enumerate(sl):
+            for i in range(-(-int(L_) // 16)):
+                k_off = (int(bt[s_, i]) * KVH + h) * chunk
+                offs += [k_off, half + k_off]
+    offs = np.asarray(offs, dtype=np.int64)
+    layer_bytes = 2 * half
+    assert offs.max() + chunk <= layer_bytes and offs.min() >= 0
+    kv = torch.empty(layers, layer_bytes, dtype=torch.uint8, device=dev)
+    kv.random_(0, 256)
+    n = offs.size
+    sink = torch.empty(-(-n // 8), dtype=torch.int32, device=dev)
+    results = {}
+    for name, o in (("gather_floor", offs), ("contiguous", np.arange(n, dtype=np.int64) * chunk)):
+        d_off = torch.from_numpy(o).to(dev)
+
+        def run(d_off=d_off):
+            for l in range(layers):
+                N.check(lib.ts_probe_gather(kv[l].data_ptr(), d_off.data_ptr(), n, chunk,
+                                            sink.data_ptr(), cur()), "probe_gather")
+
+        ms = time_graph(torch, run, reps=10) / layers
+        results[name] = {"us": round(ms * 1e3, 2), "GBps": round(n * chunk / ms / 1e6, 1)}
+    out["decode_step_kv_bytes"] = int(n * chunk)
+    out.update(results)
+    del kv
+    cus = N.cu_count(0)
+    wgs, iters = 2 * cus, 8000
+    fsink = torch.empty(wgs * 4, dtype=torch.float32, device=dev)
+    ms = time_graph(torch, lambda: N.check(lib.ts_probe_mfma(wgs, iters, fsink.data_ptr(),
+                                                             cur()), "probe_mfma"), reps=3)
+    flops = wgs * 4 * iters * 4 * 2 * 32 * 32 * 16
+    out["mfma_f16_TFLOPs"] = round(flops / ms / 1e9, 1)
+    out["spec"] = {"hbm_GBps": HBM_PEAK_GBS, "mfma_f16_TFLOPs": MFMA_FP16_PEAK_TFLOPS}
+    torch.cuda.empty_cache()
+    return out
+
+
 def bench_prefill(torch, K, synth):
     dev = torch.device("cuda", 0)
     rows = []
@@ -285,25 +404,47 @@ def bench_prefill(torch, K, synth):
             "tflops": round(tf, 2), "mfma_frac": round(tf / MFMA_FP16_PEAK_TFLOPS, 4)}
 
 
+def cold_copies(t, min_bytes: int = 512 * 2 ** 20) -> list:
+    """t and enough clones of it that cycling through them reads more than `min_bytes` (twice the
+    256 MB Infinity Cache), so each call finds its weights in HBM."""
+    n = max(2, -(-min_bytes // (t.numel() * t.element_size())))
+    return [t] + [t.clone() for _ in range(n - 1)]
+
+
 def bench_w8a16(torch, K, synth):
+    """Config 4: every (M, N, K) point, timed cold (the weight cycles through copies whose total
+    exceeds the Infinity Cache, one copy per call inside the graph) and warm (one copy, replayed
+    20 times: it stays in the 256 MB cache). Roofline fraction from the cold time."""
+    import itertools
+
     dev = torch.device("cuda", 0)
     rows = []
     for (Nn, Kd) in synth.QWEN15_LINEAR_SHAPES:
         x_all, wq, sc = synth.w8a16_problem(max(synth.W8A16_M), Nn, Kd, seed=0)
         wq, sc = wq.to(dev), sc.to(dev)
+        wqs = cold_copies(wq)
         for M in synth.W8A16_M:
             x = x_all[:M].to(dev)
-            inner = 20 if M <= 64 else 5
-            ms = time_graph(torch, lambda: K.w8a16_linear(x, wq, sc, None), reps=10, inner=inner)
+            it = itertools.cycle(wqs)
+            cold = time_graph(torch, lambda: K.w8a16_linear(x, next(it), sc, None), reps=3,
+                              inner=len(wqs))
+            warm = time_graph(torch, lambda: K.w8a16_linear(x, wq, sc, None), reps=10,
+                              inner=20 if M <= 64 else 5)
             byts = Nn * Kd + 2 * Nn + 2 * M * Kd + 2 * M * Nn
             flop = 2.0 * M * Nn * Kd
             t_hbm = byts / (HBM_PEAK_GBS * 1e9)
             t_mfma = flop / (MFMA_FP16_PEAK_TFLOPS * 1e12)
-            rows.append({"M": M, "N": Nn, "K": Kd, "us": round(ms * 1e3, 2),
-                         "GBps": round(byts / ms / 1e6, 1), "TFLOPs": round(flop / ms / 1e9, 2),
+            rows.append({"M": M, "N": Nn, "K": Kd, "us": round(cold * 1e3, 2),
+                         "us_warm": round(warm * 1e3, 2),
+                         "GBps": round(byts / cold / 1e6, 1), "TFLOPs": round(flop / cold / 1e9, 2),
                          "bound": "hbm" if t_hbm >= t_mfma else "mfma",
-                         "roofline_frac": round(max(t_hbm, t_mfma) / (ms / 1e3), 4)})
-    return rows
+                         "roofline_frac": round(max(t_hbm, t_mfma) / (cold / 1e3), 4)})
+        del wqs
+        torch.cuda.empty_cache()
+    per_layer = {}
+    for M in synth.W8A16_M:
+        per_layer[str(M)] = round(sum(r["us"] for r in rows if r["M"] == M), 2)
+    return {"rows": rows, "four_projections_us_cold": per_layer}
 
 
 def bench_logits(torch, K):
@@ -321,15 +462,23 @@ def bench_logits(torch, K):
     wq = torch.round(embed.float() / sc[:, None]).clamp(-127, 127).to(torch.int8).contiguous()
     hidden = torch.randn(T, H, generator=g, device=dev).half()
     idx = torch.sort(torch.randperm(T, generator=g, device=dev)[:S]).values
+    import itertools
+
     out = {}
-    for name, fn, wbytes in (
-            ("int8_fused", lambda: K.logits_int8(hidden, idx, wq, sc), V * H),
-            ("int8_unfused", lambda: K.lm_head_int8(hidden[idx], wq, sc).float(), V * H),
-            ("fp16_blas", lambda: (hidden[idx] @ embed.T).float(), 2 * V * H)):
-        ms = time_graph(torch, fn, reps=10, inner=5)
+    wqs, embeds = cold_copies(wq), cold_copies(embed)
+    iq, ie, iu = itertools.cycle(wqs), itertools.cycle(embeds), itertools.cycle(wqs)
+    for name, fn, wbytes, n in (
+            ("int8_fused", lambda: K.logits_int8(hidden, idx, next(iq), sc), V * H, len(wqs)),
+            ("int8_unfused", lambda: K.lm_head_int8(hidden[idx], next(iu), sc).float(), V * H,
+             len(wqs)),
+            ("fp16_blas", lambda: (hidden[idx] @ next(ie).T).float(), 2 * V * H, len(embeds))):
+        ms = time_graph(torch, fn, reps=3, inner=n)
         out[name] = {"us": round(ms * 1e3, 2), "weight_GBps": round(wbytes / ms / 1e6, 1),
                      "hbm_frac": round(wbytes / ms / 1e6 / HBM_PEAK_GBS, 4)}
-    return {"rows": S, "vocab": V, "hidden": H, **out}
+    del wqs, embeds
+    torch.cuda.empty_cache()
+    return {"rows": S, "vocab": V, "hidden": H, "weights": "cold (copies cycled past the "
+            "Infinity Cache)", **out}
 
 
 def bench_metadata(torch, synth):
@@ -523,8 +672,10 @@ def main() -> int:
                           "copy_bytes_written_per_launch": a.numel(), "launches": 8}))
         return 0
     _native.lib()
-    if args.only in ("prefill", "w8a16", "logits", "metadata", "mixed", "decode_model"):
+    if args.only in ("prefill", "w8a16", "logits", "metadata", "mixed", "decode_model",
+                     "calibration"):
         fn = {"decode_model": lambda: bench_decode_model(torch, synth),
+              "calibration": lambda: bench_calibration(torch, synth),
               "prefill": lambda: bench_prefill(torch, K, synth),
               "w8a16": lambda: bench_w8a16(torch, K, synth),
               "logits": lambda: bench_logits(torch, K),
@@ -580,15 +731,27 @@ def main() -> int:
         "graph_equals_eager": r["graph_equals_eager"],
     }
     if not args.no_cpu:
-        log(f"cpu baseline: oracle step on the host for ~{args.cpu_seconds:.0f} s")
+        log(f"cpu baseline: the reference backend's step on the host for ~{args.cpu_seconds:.0f} s")
         t_cpu, cores, n = cpu_baseline(st, args.cpu_seconds)
-        out["cpu_baseline"] = {"value": round(b["step"] / t_cpu / 1e9, 3), "unit": "GB/s",
-                               "cores": cores, "kind": "port",
-                               "sample": f"config2 full step (64 sequences), numpy oracle, "
-                                         f"median of {n} runs, {t_cpu * 1e3:.1f} ms/step"}
+        t_or, cores_or, n_or = oracle_baseline(st, max(2.0, args.cpu_seconds / 3))
+        out["cpu_baseline"] = {
+            "value": round(b["step"] / t_cpu / 1e9, 3), "unit": "GB/s", "cores": cores,
+            "kind": "port", "cpu": cpu_model(),
+            "sample": f"config2 full step (64 sequences: kv_write + paged_attention) through "
+                      f"get_ops('reference'), the torch twins, {cores} threads, median of {n} "
+                      f"runs, {t_cpu * 1e3:.1f} ms/step",
+            "oracle_numpy": {"value": round(b["step"] / t_or / 1e9, 3), "unit": "GB/s",
+                             "cores": cores_or, "ms_per_step": round(t_or * 1e3, 2),
+                             "runs": n_or}}
     if not args.no_extra:
+        log("calibration: copy, gather floor, MFMA loop")
+        cal = bench_calibration(torch, synth)
+        out["roofline"]["measured"] = {
+            "copy_GBps": cal["copy_GBps"], "gather_floor_GBps": cal["gather_floor"]["GBps"],
+            "frac_of_gather_floor": round(achieved / cal["gather_floor"]["GBps"], 4),
+            "mfma_f16_TFLOPs": cal["mfma_f16_TFLOPs"]}
         log("extra: config 3 chunked prefill")
-        extra = {"prefill_config3": bench_prefill(torch, K, synth)}
+        extra = {"calibration": cal, "prefill_config3": bench_prefill(torch, K, synth)}
         log("extra: config 4 W8A16")
         extra["w8a16_config4"] = bench_w8a16(torch, K, synth)
         log("extra: config 5 logits")
@@ -605,7 +768,7 @@ def main() -> int:
         tuner.set_active(table)
         try:
             extra["mixed_config5_tuned"] = {**bench_mixed(torch, synth),
-                                            "choices": table.tables}
+                                            "choices": json.loads(table.to_json())["records"]}
         finally:
             tuner.set_active(tuner.VariantTable())
         out["extra"] = extra

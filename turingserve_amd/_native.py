@@ -87,6 +87,8 @@ SIGNATURES = {
     "ts_rope_kv_write": (ctypes.c_int, [_p, _i64, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _p,
                                         _p, _i64, _p, _p]),
     "ts_silu_mul": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _i32, _p]),
+    "ts_probe_gather": (ctypes.c_int, [_p, _p, _i32, _i32, _p, _p]),
+    "ts_probe_mfma": (ctypes.c_int, [_i32, _i32, _p, _p]),
 }
 
 

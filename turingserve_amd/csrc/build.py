@@ -21,8 +21,7 @@ LIB_DIR = os.path.join(PKG, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libturingserve_hip.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 SOURCES = ["capi.hip", "kv_write.hip", "decode.hip", "prefill.hip", "ragged.hip", "w8a16.hip",
-           "small_ops.hip",
-           "metadata.hip"]
+           "small_ops.hip", "metadata.hip", "probes.hip"]
 ARCH = "gfx950"
 
 COMMON_FLAGS = [
