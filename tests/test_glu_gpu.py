@@ -3,8 +3,9 @@ gate_up W8A16 product (model/qwen2.py:35-36 with ops/triton_silu_mul.py:21-28).
 
 It must equal, bit for bit, the unfused pair it replaces -- the W8A16 product of the [M, 2I]
 shape with the same variant and splits, then silu_mul -- over every path the plan can take
-(weight streaming, 128 x 64 and 128 x 128 tiles, split-K), ragged shapes and bias; and that pair
-is pinned to the float64 oracle of the product (oracle/quant.py) composed with silu * up.
+(weight streaming, skinny, 128 x 64 and 128 x 128 tiles, split-K), ragged shapes and bias; and
+that pair is pinned to the float64 oracle of the product (oracle/quant.py) composed with
+silu * up.
 """
 
 from __future__ import annotations
@@ -72,11 +73,13 @@ def test_glu_intermediate_not_a_multiple_of_8(M, inter):
 
 
 @pytest.mark.parametrize("variant,splits", [(1, 0), (1, 1), (1, 3), (2, 0), (2, 1), (2, 4),
-                                            (3, 0), (3, 2), (4, 0), (4, 2)])
+                                            (3, 0), (3, 2), (4, 0), (4, 2), (5, 0)])
 @pytest.mark.parametrize("M", [9, 32, 200])
 def test_glu_every_variant_and_split(variant, splits, M):
     if variant == 1 and M > 32:
         pytest.skip("weight streaming is built for M <= 32")
+    if variant == 5 and M > 64:
+        pytest.skip("the skinny kernel is built for M <= 64")
     x, wq, scale, b, _, _, _ = _problem(M, 1000, 1024, seed=variant * 10 + splits + M, bias=True,
                                         fp16_scale=True)
     cfg = (variant, splits)

@@ -100,9 +100,20 @@ def test_glu_argument_checks_and_workspace():
     for M, v, s in ((560, 0, 0), (2048, 0, 0), (64, 2, 3), (200, 3, 1), (4, 1, 1), (4, 1, 3)):
         assert lib.ts_w8a16_glu_workspace_bytes(M, 8960, 1536, v, s, 256) == \
             lib.ts_w8a16_workspace_bytes_v(M, 17920, 1536, v, s, 256)
-    assert lib.ts_w8a16_glu_workspace_bytes(1, 8960, 1536, 0, 0, 256) == \
-        lib.ts_w8a16_workspace_bytes_v(1, 17920, 1536, 0, 0, 256) > 0
+    assert lib.ts_w8a16_glu_workspace_bytes(1, 8960, 1536, 1, 0, 256) == \
+        lib.ts_w8a16_workspace_bytes_v(1, 17920, 1536, 1, 0, 256) > 0
     assert lib.ts_w8a16_glu_workspace_bytes(4, 8960, 1536, 1, 1, 256) == 0
+    # M <= 16 (and the skinny variant up to M = 64) takes the skinny kernel, whole K per
+    # workgroup: no split-K workspace
+    for M in (1, 7, 16):
+        assert lib.ts_w8a16_glu_workspace_bytes(M, 8960, 1536, 0, 0, 256) == 0
+        assert lib.ts_w8a16_workspace_bytes(M, 1536, 8960, 256) == 0
+    for M in (1, 16, 33, 64):
+        assert lib.ts_w8a16_glu_workspace_bytes(M, 8960, 1536, 5, 0, 256) == 0
+        assert lib.ts_w8a16_workspace_bytes_v(M, 2048, 1536, 5, 0, 256) == 0
+    assert lib.ts_w8a16_workspace_bytes(64, 1536, 8960, 256) > 0     # wide 128 x 32, split K
+    assert lib.ts_w8a16_glu(p, 1536, p, p, 0, None, p, 8960, 65, 8960, 1536, 5, 0, None, 0,
+                            None) == N.TS_ERR_UNSUPPORTED                # skinny is M <= 64
 
 
 def test_zero_size_calls_are_no_ops():
@@ -146,9 +157,12 @@ def test_workspace_sizes():
     # fit and K = 1536 (24 steps) never splits
     assert lib.ts_w8a16_workspace_bytes(560, 1536, 8960, 256) == 2 * 560 * 1536 * 4
     assert lib.ts_w8a16_workspace_bytes(560, 1536, 1536, 256) == 0
-    # weight streaming at M = 1: 32 workgroups, split into 6 (K / 256) fp32 partial rows
-    assert lib.ts_w8a16_workspace_bytes(1, 2048, 1536, 256) == 6 * 2048 * 4
-    ws = lib.ts_w8a16_workspace_bytes(1, 1536, 8960, 256)
+    # M <= 16 takes the skinny kernel (whole K per workgroup): no workspace
+    assert lib.ts_w8a16_workspace_bytes(1, 2048, 1536, 256) == 0
+    assert lib.ts_w8a16_workspace_bytes(16, 1536, 8960, 256) == 0
+    # weight streaming (variant 1) at M = 1: 32 workgroups, split into 6 (K / 256) partial rows
+    assert lib.ts_w8a16_workspace_bytes_v(1, 2048, 1536, 1, 0, 256) == 6 * 2048 * 4
+    ws = lib.ts_w8a16_workspace_bytes_v(1, 1536, 8960, 1, 0, 256)
     assert ws > 0 and ws % (1536 * 4) == 0
 
 

@@ -321,6 +321,195 @@ __global__ void __launch_bounds__(256) w8a16_glu_reduce_kernel(
   }
 }
 
+// ------------------------------------------------------------------------------------------
+// Skinny products (M <= 64, a decode step's projections and the logits): no split-K launch.
+// ------------------------------------------------------------------------------------------
+// Workgroup = KW wavefronts on RT x 16 weight rows (output channels) and every row of x (MT
+// 16-row m tiles), over the whole K: wavefront w takes a contiguous slice of the 64-wide K steps,
+// so the workgroup streams each of its weight rows once, front to back, and reads x once. The
+// KW partial accumulators meet in LDS (a tree: half the wavefronts hand theirs to the other
+// half, log2 KW rounds) and wavefront 0 applies scale and bias and stores; no fp32 partials
+// leave the workgroup and no reduction kernel follows.
+//
+// Per K step, lane (c, g) loads 16 bytes of weight row c of each row tile (columns 16g .. 16g+15
+// of the step: 1 KiB per tile and instruction, every byte used once) and the same 16 columns of
+// x row c of each m tile (two 16-byte loads), and multiplies them on v_mfma_f32_16x16x32_f16 as
+// two K = 32 products (columns 16g .. 16g+7, then 16g+8 .. 16g+15; the contraction index is
+// permuted the same way in both operands). Loads run P steps ahead in a register ring.
+//
+// TAIL (K % 64 != 0): in the last step, 8-column pieces at or past K read column K - 8 instead
+// (in range) and their widened weights are zeroed. GLU mode (io.glu = I, N = 2I): row tiles
+// rt < RT/2 hold gate rows, rt >= RT/2 the matching up rows, so wavefront 0 forms
+// silu(gate) * up itself.
+constexpr int kSkStep = 64;
+
+template <int MT, int RT, int KW, int P, bool TAIL>
+__global__ void __launch_bounds__(KW * 64) w8a16_skinny_kernel(
+    const half_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ wq,
+    const void* __restrict__ scale, int scale_is_fp16, const half_t* __restrict__ bias,
+    half_t* __restrict__ y, int64_t ldy, int M, int N, int K, GemmIo io) {
+  static_assert(KW == 4 || KW == 8 || KW == 16, "4, 8 or 16 wavefronts");
+  static_assert(P >= 1 && P <= 8, "one to eight steps in flight");
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15, g = lane >> 4;
+  const int glu = io.glu;
+  // weight row of row tile rt, row j within the tile (clamped into the matrix)
+  auto weight_row = [&](int rt, int j) {
+    if (glu) {
+      constexpr int HALF = RT / 2 > 0 ? RT / 2 : 1;
+      const int i = blockIdx.x * 16 * HALF + 16 * (rt % HALF) + j;
+      return (rt >= HALF ? glu : 0) + (i < glu ? i : glu - 1);
+    }
+    const int n = blockIdx.x * 16 * RT + 16 * rt + j;
+    return n < N ? n : N - 1;
+  };
+  const int nsteps = (K + kSkStep - 1) / kSkStep;
+  const int per = (nsteps + KW - 1) / KW;
+  const int s0 = w * per;
+  const int s1 = s0 + per < nsteps ? s0 + per : nsteps;
+  const int8_t* wrow[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) wrow[rt] = wq + (int64_t)weight_row(rt, c) * K + 16 * g;
+  const half_t* xrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    const int mm = 16 * mt + c;
+    xrow[mt] = x + x_row(io, mm < M ? mm : M - 1) * ldx + 16 * g;
+  }
+  struct Step {
+    int4_t wv[RT];
+    half8_t xa[MT], xb[MT];
+  };
+  // Step s's loads (s < nsteps): column offsets of the lane's two 8-column pieces, clamped.
+  auto load = [&](int s, Step& st) {
+    const int k = s * kSkStep;
+    if constexpr (TAIL) {
+      const int ca = k + 16 * g < K ? k : K - 8 - 16 * g;
+      const int cb = k + 16 * g + 8 < K ? k + 8 : K - 8 - 16 * g;
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) {
+        const int2_t a = ld<int2_t>(wrow[rt] + ca), b = ld<int2_t>(wrow[rt] + cb);
+        st.wv[rt] = {a[0], a[1], b[0], b[1]};
+      }
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        st.xa[mt] = ld<half8_t>(xrow[mt] + ca);
+        st.xb[mt] = ld<half8_t>(xrow[mt] + cb);
+      }
+    } else {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt) st.wv[rt] = ld<int4_t>(wrow[rt] + k);
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        st.xa[mt] = ld<half8_t>(xrow[mt] + k);
+        st.xb[mt] = ld<half8_t>(xrow[mt] + k + 8);
+      }
+    }
+  };
+  float4_t acc[RT][MT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[rt][mt] = {0.f, 0.f, 0.f, 0.f};
+  const half8_t hz = {0, 0, 0, 0, 0, 0, 0, 0};
+  auto compute = [&](int s, const Step& st) {
+    const int k = s * kSkStep + 16 * g;
+    const bool oka = !TAIL || k < K, okb = !TAIL || k + 8 < K;
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
+      const half8_t fa = oka ? i8x8_to_half8(int2_t{st.wv[rt][0], st.wv[rt][1]}) : hz;
+      const half8_t fb = okb ? i8x8_to_half8(int2_t{st.wv[rt][2], st.wv[rt][3]}) : hz;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        acc[rt][mt] = mfma16x16x32(fa, st.xa[mt], acc[rt][mt]);
+        acc[rt][mt] = mfma16x16x32(fb, st.xb[mt], acc[rt][mt]);
+      }
+    }
+  };
+  // Ring of P register steps: step s lives in slot (s - s0) % P; every iteration computes one
+  // step and refills its slot with the step P ahead.
+  Step ring[P];
+#pragma unroll
+  for (int u = 0; u < P; ++u)
+    if (s0 + u < s1) load(s0 + u, ring[u]);
+  for (int s = s0; s < s1; s += P) {
+#pragma unroll
+    for (int u = 0; u < P; ++u) {
+      if (s + u < s1) {
+        compute(s + u, ring[u]);
+        if (s + u + P < s1) load(s + u + P, ring[u]);
+      }
+    }
+  }
+  // Tree reduction of the KW accumulators: in round h, wavefronts [h, 2h) publish theirs and
+  // wavefronts [0, h) add them.
+  __shared__ float4_t red[KW / 2][RT * MT][64];
+#pragma unroll
+  for (int h = KW / 2; h >= 1; h /= 2) {
+    if (w >= h && w < 2 * h) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) red[w - h][rt * MT + mt][lane] = acc[rt][mt];
+    }
+    __syncthreads();
+    if (w < h) {
+#pragma unroll
+      for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[rt][mt] += red[w][rt * MT + mt][lane];
+    }
+    __syncthreads();
+  }
+  if (w != 0) return;
+  // lane (c, g) of tile (rt, mt) holds Y[m = 16 mt + c][weight_row(rt, 4g + r)], r = 0..3; every
+  // output value is fp16(acc * scale + bias) formed by this one expression (the GLU and the
+  // plain epilogue must round identically)
+  auto value = [&](int rt, int mt, int r) {
+    const int nr = weight_row(rt, 4 * g + r);
+    return (half_t)(acc[rt][mt][r] * load_scale(scale, scale_is_fp16, nr) +
+                    (bias ? (float)bias[nr] : 0.f));
+  };
+  if (glu) {
+    constexpr int HALF = RT / 2 > 0 ? RT / 2 : 1;
+#pragma unroll
+    for (int rt = 0; rt < HALF; ++rt) {
+      const int col = blockIdx.x * 16 * HALF + 16 * rt + 4 * g;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int mm = 16 * mt + c;
+        if (mm >= M || col >= glu) continue;
+        half4_t o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = silu_mul_h(value(rt, mt, r), value(rt + HALF, mt, r));
+        half_t* dst = y + (int64_t)mm * ldy + col;
+        if (col + 3 < glu) {
+          st<half4_t>(dst, o);
+        } else {
+          for (int r = 0; r < 4; ++r)
+            if (col + r < glu) dst[r] = o[r];
+        }
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int nn = blockIdx.x * 16 * RT + 16 * rt + 4 * g;
+    if (nn >= N) continue;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int mm = 16 * mt + c;
+      if (mm >= M) continue;
+      float v[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[r] = (float)value(rt, mt, r);   // columns past N not stored
+      store_out4(io, y, ldy, mm, nn, N, v);
+    }
+  }
+}
+
 constexpr int kTileBK = 64;
 constexpr int kTileChunks = kTileBK / 8;          // 16-byte fp16 chunks per tile row
 
@@ -699,14 +888,39 @@ constexpr int kWidePrefetch = 3;                  // K steps of loads in flight 
 
 struct GemmPlan {
   bool small;
-  int mt;          // m tiles (small path)
+  int mt;          // m tiles (small and skinny paths)
   int bn, bm;      // tile shape (wide path): 128 x 128, 128 x 64 or 128 x 32
   int splits;      // K splits
   int k_per_split;
+  int rt;          // skinny path: 16-row weight tiles per workgroup (0: not skinny)
+  int kw;          // skinny path: wavefronts per workgroup (the K split inside it)
 };
 
 // Variants a caller (a tuning table) may name instead of the planner's choice.
-enum GemmVariant : int { kVarAuto = 0, kVarStream = 1, kVarWide64 = 2, kVarWide128 = 3, kVarWide32 = 4 };
+enum GemmVariant : int {
+  kVarAuto = 0, kVarStream = 1, kVarWide64 = 2, kVarWide128 = 3, kVarWide32 = 4, kVarSkinny = 5
+};
+constexpr int kSkinnyMMax = 64;
+
+// Skinny plan (measured on the 1.5B projections and the lm head, cold weights): one 16-row weight
+// tile per workgroup (a GLU product pairs a gate and an up tile); the most resident wavefronts
+// win, each issuing its whole share of the row at once: 8 wavefronts when the grid is at most
+// two workgroups per CU, else 4 (more workgroups per CU fit, and all of them in one round).
+// M = 1: 2048 x 1536 7.3 -> 4.3 us, 17920 x 1536 13.4 -> 8.9 us, 1536 x 8960 13.2 -> 9.3 us.
+static void skinny_shape(int N, int cus, bool glu, GemmPlan* p) {
+  p->rt = glu ? 2 : 1;
+  // from N alone, so a GLU product splits K exactly as the unfused [M, 2I] product does (the
+  // fused result must equal the unfused pair bit for bit)
+  p->kw = (int64_t)((N + 15) / 16) <= 2LL * cus ? 8 : 4;
+}
+
+// Auto plan: skinny for M <= 16, and up to M = 32 for short-K, narrow products (where the wide
+// tiles would need a K split and its reduction); past that the activations re-read per 16-row
+// tile cost more than the wide tiles' LDS sharing saves.
+static bool use_skinny(int M, int N, int K) {
+  return M <= 16 || (M <= 32 && K <= 2048 && N <= 4096);
+}
+
 constexpr int kMaxSplits = 256;
 
 // Weight streaming: fill the device with wavefronts (about eight per CU) by splitting K,
@@ -750,7 +964,13 @@ static int wide64_splits(int M, int N, int K, int cus) {
 // for M <= 64 (past the streaming path) 128 x 32 tiles split over K when 128 x 64 tiles would
 // cover under a quarter of the CUs. 128 x 32 tiles never split K by their own rule (splits 0),
 // and GLU mode plans them as 128 x 64.
-static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int splits) {
+static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int splits,
+                            bool glu = false) {
+  if (variant == kVarSkinny || (variant == kVarAuto && use_skinny(M, N, K))) {
+    GemmPlan p{false, M <= 16 ? 1 : (M <= 32 ? 2 : 4), 0, 0, 1, K, 0, 0};
+    skinny_shape(N, cus, glu, &p);
+    return p;
+  }
   if (variant == kVarAuto) {
     const int64_t n_tiles = (N + 127) / 128;
     variant = use_small_path(M, N, K)                                       ? kVarStream
@@ -775,7 +995,7 @@ static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int split
     }
   }
   GemmPlan p{variant == kVarStream, (M + 15) / 16, 128,
-             variant == kVarWide128 ? 128 : (variant == kVarWide32 ? 32 : 64), 1, K};
+             variant == kVarWide128 ? 128 : (variant == kVarWide32 ? 32 : 64), 1, K, 0, 0};
   if (p.small) {
     if (splits == 0) splits = stream_splits(M, N, K, cus);
     int kps = (K + splits - 1) / splits;
@@ -812,8 +1032,9 @@ extern "C" size_t ts_w8a16_workspace_bytes(int32_t M, int32_t N, int32_t K, int3
 }
 
 static bool variant_valid(int variant, int splits, int M) {
-  return variant >= kVarAuto && variant <= kVarWide32 && splits >= 0 && splits <= kMaxSplits &&
-         (variant != kVarStream || M <= kSmallMMax);
+  return variant >= kVarAuto && variant <= kVarSkinny && splits >= 0 && splits <= kMaxSplits &&
+         (variant != kVarStream || M <= kSmallMMax) &&
+         (variant != kVarSkinny || (M <= kSkinnyMMax && splits <= 1));
 }
 
 extern "C" size_t ts_w8a16_workspace_bytes_v(int32_t M, int32_t N, int32_t K, int32_t variant,
@@ -832,7 +1053,7 @@ static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const v
   int st = device_cu_count(s, &cus);
   if (st != TS_OK) return st;
   const bool glu = io.glu > 0;                    // N = 2 * io.glu, y is [M, io.glu]
-  GemmPlan p = plan_gemm_v(M, N, K, cus, variant, splits);
+  GemmPlan p = plan_gemm_v(M, N, K, cus, variant, splits, glu);
   if (glu && p.bm == 32) p.bm = 64;               // GLU tiles pair 32-row subtiles (same splits)
   const size_t need = gemm_workspace(p, M, N);
   TS_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
@@ -849,7 +1070,36 @@ static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const v
           part, p.splits, scale, scale_is_fp16, bp, yp, ldy, M, N, io);
     }
   };
-  if (p.small) {
+  if (p.rt > 0) {
+    // GLU: a workgroup covers 8 RT gate columns (its RT / 2 gate tiles and their up tiles)
+    const int cols = glu ? io.glu : N;
+    const int per_wg = glu ? 8 * p.rt : 16 * p.rt;
+    const dim3 grid((cols + per_wg - 1) / per_wg);
+    const bool tail = K % kSkStep != 0 || !aligned(wq, 16);
+#define TS_SK_LAUNCH(MTV, RTV, KWV)                                                                \
+  {                                                                                                \
+    constexpr int PV = MTV == 4 ? 2 : (MTV == 2 || KWV == 8 ? 4 : 8);                              \
+    if (tail)                                                                                      \
+      w8a16_skinny_kernel<MTV, RTV, KWV, PV, true><<<grid, KWV * 64, 0, s>>>(                      \
+          xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, io);                            \
+    else                                                                                           \
+      w8a16_skinny_kernel<MTV, RTV, KWV, PV, false><<<grid, KWV * 64, 0, s>>>(                     \
+          xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, io);                            \
+  }
+#define TS_SK_RT(MTV)                                                                              \
+  if (p.rt == 2) {                                                                                 \
+    if (p.kw == 8) TS_SK_LAUNCH(MTV, 2, 8) else TS_SK_LAUNCH(MTV, 2, 4)                            \
+  } else if (p.kw == 8) TS_SK_LAUNCH(MTV, 1, 8) else TS_SK_LAUNCH(MTV, 1, 4)
+    if (p.mt == 1) {
+      TS_SK_RT(1)
+    } else if (p.mt == 2) {
+      TS_SK_RT(2)
+    } else {
+      TS_SK_RT(4)
+    }
+#undef TS_SK_RT
+#undef TS_SK_LAUNCH
+  } else if (p.small) {
     float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const int rows_per_wg = glu ? 16 * kSmWaves / 2 : 16 * kSmWaves;   // GLU: gate columns
     const dim3 grid(((glu ? io.glu : N) + rows_per_wg - 1) / rows_per_wg, p.splits);
