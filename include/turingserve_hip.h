@@ -124,6 +124,9 @@ int ts_decode_attention(int32_t version,
  * attention then sees it. Precondition (what every input builder produces, incl. the graph
  * padding of runner/cuda_graphs.py:62-78): slot_mapping[i] is the slot of position
  * seq_lens[i] - 1, and a row with seq_lens[i] == 0 carries slot -1 (such a row is not written).
+ * A row whose in-range slot is any other one is not written and its output row is NaN (the
+ * write could not be ordered against other workgroups' reads of that block): use ts_kv_write
+ * and ts_decode_attention for such rows.
  * The write is fused for v2 / v3 with at most 16 query heads per KV head and 16-byte aligned
  * rows; otherwise it runs as ts_kv_write's own launch before the attention. Same workspace as
  * ts_decode_attention (ts_decode_workspace_bytes()).

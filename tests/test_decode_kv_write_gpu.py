@@ -223,3 +223,41 @@ def test_rope_fused_model_decode_step():
             h2 = plain.forward(dec.input_ids, dec.positions, dec.meta, kv2)
         torch.cuda.synchronize()
         assert torch.equal(h1, h2) and torch.equal(kv1, kv2)
+
+
+@pytest.mark.parametrize("version,partition,rope", [(None, None, False), ("v2", None, False),
+                                                    ("v3", 512, False), (None, None, True)])
+def test_fused_write_with_a_foreign_slot_gives_nan_not_a_race(version, partition, rope):
+    """The fusion's precondition is that slot_mapping[i] is the slot of position seq_lens[i] - 1.
+    A row whose slot points elsewhere (into another sequence's block, which another workgroup
+    may be reading) is not written; that sequence's output is NaN, every other row and the rest
+    of the cache are exactly those of the separate calls."""
+    H, KVH, D = 12, 2, 128
+    ctx = [700, 33, 1500, 64, 900]
+    qkv, kc, vc, qsl, sl, bt, slots = decode_step(ctx, H, KVH, D, seed=5)
+    bad = 2
+    slots = slots.clone()
+    slots[bad] = int(bt[0, 3]) * 16 + 5                   # a slot in sequence 0's fourth block
+    meta = meta_for(qsl, sl, bt, slots)
+    scale = D ** -0.5
+    kc2, vc2 = kc.to(DEV), vc.to(DEV)
+    if rope:
+        from turingserve_amd.qwen2 import rope_tables
+
+        cos, sin = rope_tables(D, 1e6, 4096, DEV)
+        pos = (sl.to(DEV).long() - 1).clamp_min(0)
+        out = K.decode_rope_kv_write_attention(qkv.to(DEV).contiguous(), pos, cos, sin, H, KVH,
+                                               D, kc2, vc2, meta, scale,
+                                               decode_version=version, partition=partition)
+    else:
+        q, k, v = views(qkv.to(DEV), H, KVH, D)
+        out = K.decode_kv_write_attention(q, k, v, kc2, vc2, meta, scale, decode_version=version,
+                                          partition=partition)
+    torch.cuda.synchronize()
+    o = out.float().cpu()
+    assert bool(torch.isnan(o[bad]).all())
+    assert not bool(torch.isnan(o[[i for i in range(len(ctx)) if i != bad]]).any())
+    # the foreign slot was not written
+    blk, off = int(slots[bad]) // 16, int(slots[bad]) % 16
+    assert torch.equal(kc2[blk, :, off].cpu(), kc[blk, :, off])
+    assert torch.equal(vc2[blk, :, off].cpu(), vc[blk, :, off])

@@ -122,3 +122,34 @@ def test_tiled_prefill_chunked_prompt_through_paged_attention():
         ref = oracle_attn(torch.from_numpy(qn), kc.cpu(), vc.cpu(), meta.query_start_loc.cpu(),
                           meta.seq_lens.cpu(), meta.block_tables.cpu(), st.D ** -0.5)
         assert_attn(out, ref, f"chunk {ci} (prefix {prefix}, {n} rows)")
+
+
+@pytest.mark.parametrize("D,n_decode", [(64, 0), (128, 0), (128, 4)])
+def test_understated_bounds_give_nan_rows_not_stale_memory(D, n_decode):
+    """max_query_len below a chunk's real q_len (a caller bug): the rows the plan does not cover
+    come out as NaN, the covered rows are still right; with decode rows in the batch the
+    one-launch ragged kernel takes the same rule. Tiles are launched longest first, so at
+    head_dim 128 the uncovered rows are the lowest tiles; the head_dim < 128 kernel covers rows
+    from 0 up."""
+    from turingserve_amd.metadata import AttentionMetadata
+
+    Hh, KV = 12, 2
+    seq = [300 + 97 * i for i in range(n_decode)] + [1200]
+    ql = [1] * n_decode + [600]
+    q, kc, vc, qsl, sl, bt = make_paged(seq, Hh, KV, D, ql, seed=9)
+    ref = oracle_attn(q, kc, vc, qsl, sl, bt, D ** -0.5)
+    dq, dkc, dvc, dqsl, dsl, dbt = (x.to(DEV) for x in (q, kc, vc, qsl, sl, bt))
+    T = n_decode + 600
+    meta = AttentionMetadata(dqsl, dsl, dbt, torch.zeros(T, dtype=torch.int64, device=DEV),
+                             n_decode, 300, 1200)              # max_query_len understated
+    out = K.paged_attention(dq, dkc, dvc, meta, D ** -0.5)
+    torch.cuda.synchronize()
+    o = out.float().cpu()[n_decode:]
+    nan_rows = torch.isnan(o).all(dim=1)
+    if D == 128:
+        covered = torch.arange(600) >= 256                     # tiles 2..4 of 5 (longest first)
+    else:
+        covered = torch.arange(600) < 320                      # 10 tiles of 32 rows
+    assert bool(nan_rows[~covered].all()) and not bool(torch.isnan(o[covered]).any())
+    rows = torch.cat([torch.ones(n_decode, dtype=torch.bool), covered])
+    assert_attn(out[rows.to(DEV)], ref[rows.numpy()], f"covered rows, D {D}")

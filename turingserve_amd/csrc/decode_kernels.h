@@ -310,6 +310,7 @@ __device__ __forceinline__ void decode_mfma_body(
       return;
     }
   }
+  bool poison = false;                           // fused write with a non-conforming slot
   if constexpr (WRITE) {
     // kv_write of sequence s's new row (ops/reference.py:50-57) for this KV head, by the
     // workgroup whose range ends the sequence (it holds position seq_len - 1, where every input
@@ -320,7 +321,13 @@ __device__ __forceinline__ void decode_mfma_body(
     // pointers are the same restrict pointers the loads use, so the compiler orders them too.
     if (split_j == nsplit - 1) {
       const int64_t slot = nr.slots[s];
-      if (slot >= 0 && slot < nr.num_slots) {
+      // The precondition of the fusion: the slot is that of position seq_len - 1. Any other
+      // slot would put the row in a block another workgroup may be reading; it is not written,
+      // and the sequence's output becomes NaN so the caller sees the broken precondition.
+      const int64_t want = (int64_t)clamp_block(bt[(int64_t)s * bt_st + (seq_len - 1) / kBlockSize], NB) *
+                               kBlockSize + (seq_len - 1) % kBlockSize;
+      poison = slot >= 0 && slot < nr.num_slots && slot != want;
+      if (slot >= 0 && slot < nr.num_slots && !poison) {
         const int64_t row = (((slot >> 4) * KVH + kvh) * kBlockSize + (slot & 15)) * D;
         const half_t* ksrc = nr.k + (int64_t)s * nr.k_st + (int64_t)kvh * nr.k_sh;
         const half_t* vsrc = nr.v + (int64_t)s * nr.v_st + (int64_t)kvh * nr.v_sh;
@@ -513,6 +520,7 @@ __device__ __forceinline__ void decode_mfma_body(
       L += wt * s_l[ww][hh];
       O += wt * s_o[ww][hh][d];
     }
+    if (poison) L = __builtin_nanf("");             // reaches the output through the merge too
     if (nsplit == 1) {
       out[(int64_t)s * o_st + (int64_t)(head0 + hh) * D + d] = (half_t)(O / L);
     } else {

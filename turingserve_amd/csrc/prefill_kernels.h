@@ -26,6 +26,22 @@ namespace ts {
 
 constexpr float kLog2eP = 1.4426950408889634f;
 
+// Rows [row_lo, q_len) of query head h of a sequence, filled with NaN by the whole workgroup:
+// what a tile gets whose rows the launch does not cover (host bounds below the batch's real
+// q_len / seq_len), so the caller sees the understated bound instead of stale memory.
+template <int D>
+__device__ __forceinline__ void poison_rows(half_t* __restrict__ out, int64_t o_st, int q_start,
+                                            int row_lo, int q_len, int h) {
+  const half_t nan = __builtin_bit_cast(half_t, (unsigned short)0x7e00);
+  const half4_t n4 = {nan, nan, nan, nan};
+  const int per_row = D / 4;
+  for (int e = (int)threadIdx.x; e < (q_len - row_lo) * per_row; e += (int)blockDim.x) {
+    const int row = row_lo + e / per_row, d0 = 4 * (e % per_row);
+    ts::st<half4_t>(out + (int64_t)(q_start + row) * o_st + (int64_t)h * D + d0, n4);
+  }
+}
+
+
 #ifndef TS_PREFILL_ROW_GROUPS
 #define TS_PREFILL_ROW_GROUPS 2
 #endif
@@ -60,6 +76,8 @@ __global__ void __launch_bounds__(NW * 64) prefill_stream_kernel(
   int seq_len = __builtin_amdgcn_readfirstlane(seq_lens[b]);
   seq_len = seq_len < 0 ? 0 : (seq_len > max_blocks * kBlockSize ? max_blocks * kBlockSize : seq_len);
   const int m0 = mtile * kPsRows;
+  if (mtile == (int)gridDim.x - 1 && (int64_t)gridDim.x * kPsRows < q_len)
+    poison_rows<D>(out, o_st, q_start, (int)gridDim.x * kPsRows, q_len, h);   // q_len past the bound
   if (m0 >= q_len) return;
   const int prefix = seq_len - q_len;
   const int last_row = (m0 + kPsRows < q_len ? m0 + kPsRows : q_len) - 1;
@@ -361,6 +379,25 @@ __device__ __forceinline__ void prefill_tile_body(
   const int r = lane & 31, hh = lane >> 5;
 
   const PrefillSeq sq = prefill_seq(qsl, seq_lens, b, num_tokens, max_blocks);
+  if (slot == slots - 1) {
+    // Slots number the tiles longest first, so the tiles a launch misses (host bounds below the
+    // real q_len / seq_len) are the lowest ones: every tile from the first (going down) whose
+    // splits run past the last slot. Their rows are written by no other workgroup.
+    const int tiles = (sq.q_len + kTileRows - 1) / kTileRows;
+    int base = 0, cut = -1;
+    for (int i = tiles - 1; i >= 0 && cut < 0; --i) {
+      const int last_row = ((i + 1) * kTileRows < sq.q_len ? (i + 1) * kTileRows : sq.q_len) - 1;
+      int hi = sq.prefix + last_row + 1 < sq.seq_len ? sq.prefix + last_row + 1 : sq.seq_len;
+      hi = hi < 0 ? 0 : hi;
+      const int n = (hi + kTileKeys - 1) / kTileKeys;
+      base += n <= smax ? 1 : (n + smax - 1) / smax;
+      if (base > slots) cut = i;
+    }
+    if (cut >= 0) {
+      const int m_end = (cut + 1) * kTileRows < sq.q_len ? (cut + 1) * kTileRows : sq.q_len;
+      poison_rows<D>(out, o_st, sq.q_start, 0, m_end, h);
+    }
+  }
   const TileSlot tsl = tile_slot(slot, sq.q_len, sq.prefix, sq.seq_len, smax);
   if (tsl.tile < 0) return;
   const int m0 = tsl.tile * kTileRows;
@@ -601,20 +638,13 @@ __global__ void __launch_bounds__(kTileThreads, 2) prefill_tile_kernel(
 // loads of all its rows for kMergeBatch splits are requested in one memory step, so one
 // resident round of workgroups covers the whole merge.
 template <int D>
-__device__ __forceinline__ void prefill_merge_body(
-    const float* __restrict__ ws, half_t* __restrict__ out, int64_t o_st, int64_t num_tokens,
-    int max_blocks, const int* __restrict__ seq_lens, const int* __restrict__ qsl,
-    int num_decode, int H, int smax, int slots,
-    int P, int bx, int by, int bz) {
-  constexpr int TPR = D / 4;                       // threads per row
-  constexpr int RG = kTileThreads / TPR;           // row groups per workgroup (8)
-  constexpr int NR = kMergeRows;                   // rows per thread
+__device__ __forceinline__ void prefill_merge_tile(
+    const float* __restrict__ ws, half_t* __restrict__ out, int64_t o_st, const PrefillSeq& sq,
+    int H, int smax, int slots, int P, int by, int h, int tile, int rbase) {
+  constexpr int TPR = D / 4;
+  constexpr int RG = kTileThreads / TPR;
+  constexpr int NR = kMergeRows;
   constexpr int MB = kMergeBatch;
-  static_assert(RG * NR * 4 == kTileRows, "four workgroups per tile");
-  const int tile = bx >> 2, part = bx & 3;
-  const int b = num_decode + by, h = bz;
-  const PrefillSeq sq = prefill_seq(qsl, seq_lens, b, num_tokens, max_blocks);
-  const int rbase = part * RG * NR + (int)(threadIdx.x / TPR);   // rows rbase + RG * k
   const int d0 = 4 * (int)(threadIdx.x % TPR);
   if (tile * kTileRows + rbase >= sq.q_len) return;
   const int2_t span = tile_span(tile, sq.q_len, sq.prefix, sq.seq_len, smax);
@@ -680,13 +710,34 @@ __device__ __forceinline__ void prefill_merge_body(
 }
 
 template <int D>
+__device__ __forceinline__ void prefill_merge_body(
+    const float* __restrict__ ws, half_t* __restrict__ out, int64_t o_st, int64_t num_tokens,
+    int max_blocks, const int* __restrict__ seq_lens, const int* __restrict__ qsl,
+    int num_decode, int H, int smax, int slots,
+    int P, int bx, int by, int bz, int tile_stride) {
+  constexpr int TPR = D / 4;                       // threads per row
+  constexpr int RG = kTileThreads / TPR;           // row groups per workgroup (8)
+  constexpr int NR = kMergeRows;                   // rows per thread
+  static_assert(RG * NR * 4 == kTileRows, "four workgroups per tile");
+  const int part = bx & 3;
+  const int b = num_decode + by, h = bz;
+  const PrefillSeq sq = prefill_seq(qsl, seq_lens, b, num_tokens, max_blocks);
+  const int rbase = part * RG * NR + (int)(threadIdx.x / TPR);   // rows rbase + RG * k
+  // The grid covers the tiles the host bounds foresee; a sequence with more (bounds below its
+  // real q_len) has its further tiles taken in turn, so every tile whose splits all ran is
+  // merged (the tile kernel fills the rows of the others with NaN).
+  for (int tile = bx >> 2; tile * kTileRows < sq.q_len; tile += tile_stride)
+    prefill_merge_tile<D>(ws, out, o_st, sq, H, smax, slots, P, by, h, tile, rbase);
+}
+
+template <int D>
 __global__ void __launch_bounds__(kTileThreads) prefill_merge_kernel(
     const float* __restrict__ ws, half_t* __restrict__ out, int64_t o_st, int64_t num_tokens,
     int max_blocks, const int* __restrict__ seq_lens, const int* __restrict__ qsl,
     int num_decode, int H, int smax, int slots) {
   prefill_merge_body<D>(ws, out, o_st, num_tokens, max_blocks, seq_lens, qsl, num_decode, H, smax,
                         slots, (int)gridDim.y, (int)blockIdx.x, (int)blockIdx.y,
-                        (int)blockIdx.z);
+                        (int)blockIdx.z, (int)gridDim.x / 4);
 }
 
 // Host-side plan of the tiled path: the most steps one split may take (smax) and the launch

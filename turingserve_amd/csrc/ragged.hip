@@ -91,7 +91,7 @@ __global__ void __launch_bounds__(256) ragged_merge_kernel(const RaggedArgs a) {
     const int x = p % a.pm_x, rest = p / a.pm_x;
     prefill_merge_body<128>(a.pf_ws, a.out, a.o_st, a.num_tokens, a.max_blocks, a.seq_lens,
                             a.qsl, a.num_decode, a.H, a.smax, a.slots, a.P, x, rest % a.P,
-                            rest / a.P);
+                            rest / a.P, a.pm_x / 4);
   }
 }
 

@@ -589,14 +589,17 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
   constexpr int BATCH = XPT + WN * WLD;           // vector memory loads per thread per step
   static_assert(XPT * 256 == BM * CH, "activation tile must split over 256 threads");
   static_assert(BN <= 256, "one scale per thread");
-  static_assert(S >= 2 && S <= 4, "two to four LDS stages");
+  static_assert(S >= 2 && S <= 8, "two to eight LDS stages");
   // One array per stage: the compiler's wait insertion then sees that an LDS read of one stage
   // cannot alias a DMA in flight into another and does not wait for it (stage indices are
   // constants after unrolling, so stage() folds to one array).
   __shared__ half8_t s_x0[BM * CH], s_x1[BM * CH], s_x2[S > 2 ? BM * CH : 1], s_x3[S > 3 ? BM * CH : 1];
+  __shared__ half8_t s_x4[S > 4 ? BM * CH : 1], s_x5[S > 5 ? BM * CH : 1];
+  __shared__ half8_t s_x6[S > 6 ? BM * CH : 1], s_x7[S > 7 ? BM * CH : 1];
   __shared__ float s_sc[BN], s_bs[BN];
   auto stage = [&](int st) -> half8_t* {
-    return st == 0 ? s_x0 : st == 1 ? s_x1 : st == 2 ? s_x2 : s_x3;
+    return st == 0 ? s_x0 : st == 1 ? s_x1 : st == 2 ? s_x2 : st == 3 ? s_x3
+         : st == 4 ? s_x4 : st == 5 ? s_x5 : st == 6 ? s_x6 : s_x7;
   };
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);

@@ -235,7 +235,9 @@ def decode_kv_write_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     ops/triton_ops.py:60-71), returning the same [T, H*D] and leaving the same cache. q [T, H, D],
     k, v [T, KVH, D] (strided views of the qkv rows allowed). Every row must be a decode row, and
     slot_mapping[i] the slot of position seq_lens[i] - 1 (-1 where seq_lens[i] == 0), as every
-    input builder produces."""
+    input builder produces; a row with any other in-range slot is not written and its output row
+    is NaN (its write would race with other workgroups' reads), so such rows need kv_write and
+    paged_attention instead."""
     T, H, D = q.shape
     out = torch.empty(T, H * D, dtype=q.dtype, device=q.device)
     if T == 0:
