@@ -633,10 +633,7 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(
 // ------------------------------------------------------------------------------------------
 // Host side
 // ------------------------------------------------------------------------------------------
-#ifndef TS_DECODE_WAVES
-#define TS_DECODE_WAVES 4
-#endif
-constexpr int kDecodeWaves = TS_DECODE_WAVES;               // wavefronts per workgroup
+constexpr int kDecodeWaves = 4;                              // wavefronts per workgroup
 
 // Workgroups of decode_mfma_kernel resident per CU (4 wavefronts each, one per SIMD), from the
 // kernel's VGPR use (512 per SIMD lane): 6 waves per SIMD up to D = 32, 3 at D = 64, 2 at
@@ -682,11 +679,7 @@ static SplitPlan plan_decode(int version, int S, int H, int KVH, int D, int max_
     p.nslots = S * num_splits;
     p.max_splits = num_splits;
   } else {
-#ifdef TS_DECODE_NX
-    int64_t nx = TS_DECODE_NX;                   // tuning override
-#else
     int64_t nx = wg_slots / groups - S;          // launched slots nx + S = resident workgroups
-#endif
     nx = nx < 16 ? 16 : (nx > 4096 ? 4096 : nx);
     p.nx = (int)nx;
     p.cap_blocks = 1 << 30;

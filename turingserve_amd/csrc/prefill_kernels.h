@@ -42,10 +42,7 @@ __device__ __forceinline__ void poison_rows(half_t* __restrict__ out, int64_t o_
 }
 
 
-#ifndef TS_PREFILL_ROW_GROUPS
-#define TS_PREFILL_ROW_GROUPS 2
-#endif
-constexpr int kPsRows = 16 * TS_PREFILL_ROW_GROUPS;   // query rows per workgroup and wavefront
+constexpr int kPsRows = 32;           // query rows per workgroup and wavefront (two 16-row groups)
 constexpr int kPsWaves = 4;
 
 template <int D, int NW>

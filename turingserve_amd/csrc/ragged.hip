@@ -49,16 +49,10 @@ struct RaggedArgs {
   int dm_launch, pm_x;
 };
 
-// Tuning overrides (eighths of the resident slots): the prefill plan's round, and the decode
-// splits' share (8: as many as on an idle device; otherwise the slots the prefill leaves).
-#ifndef TS_RAGGED_PF_SHARE
-#define TS_RAGGED_PF_SHARE 4
-#endif
-#ifndef TS_RAGGED_DEC_SHARE
-#define TS_RAGGED_DEC_SHARE 0
-#endif
-constexpr int kRaggedPfShare = TS_RAGGED_PF_SHARE;
-constexpr int kRaggedDecShare = TS_RAGGED_DEC_SHARE;
+// Shares of the resident workgroup slots, in eighths: the prefill tiles' plan gets a round of
+// half of them; the decode splits (share 0) take the slots the prefill leaves.
+constexpr int kRaggedPfShare = 4;
+constexpr int kRaggedDecShare = 0;
 
 constexpr int kRaggedLds = 2 * TileLayout<128>::STAGE > DecodeLds<128, kDecodeWaves>::BYTES
                                ? 2 * TileLayout<128>::STAGE
