@@ -124,13 +124,19 @@ def test_tiled_prefill_chunked_prompt_through_paged_attention():
         assert_attn(out, ref, f"chunk {ci} (prefix {prefix}, {n} rows)")
 
 
-@pytest.mark.parametrize("D,n_decode", [(64, 0), (128, 0), (128, 4)])
-def test_understated_bounds_give_nan_rows_not_stale_memory(D, n_decode):
+@pytest.mark.parametrize("D,n_decode,mql", [(64, 0, 300), (128, 0, 300), (128, 0, 128),
+                                            (128, 4, 300)])
+def test_understated_bounds_give_nan_rows_not_stale_memory(D, n_decode, mql):
     """max_query_len below a chunk's real q_len (a caller bug): the rows the plan does not cover
-    come out as NaN, the covered rows are still right; with decode rows in the batch the
-    one-launch ragged kernel takes the same rule. Tiles are launched longest first, so at
-    head_dim 128 the uncovered rows are the lowest tiles; the head_dim < 128 kernel covers rows
-    from 0 up."""
+    come out as NaN, the covered rows are still right.
+
+    * head_dim 128, prefill only: the stream-K plan shares the sequence's real steps over its
+      launch slots, so every tile is computed; a tile whose segments run past the workspace the
+      host bounds sized gets NaN rows. Tiles are numbered longest first, so those are the lowest
+      tiles: the NaN rows are a tile-aligned prefix.
+    * head_dim 128 with decode rows (one-launch ragged kernel): tiles the launch misses (the
+      lowest, launched longest first) are NaN.
+    * head_dim < 128: the kernel covers rows from 0 up."""
     from turingserve_amd.metadata import AttentionMetadata
 
     Hh, KV = 12, 2
@@ -141,15 +147,46 @@ def test_understated_bounds_give_nan_rows_not_stale_memory(D, n_decode):
     dq, dkc, dvc, dqsl, dsl, dbt = (x.to(DEV) for x in (q, kc, vc, qsl, sl, bt))
     T = n_decode + 600
     meta = AttentionMetadata(dqsl, dsl, dbt, torch.zeros(T, dtype=torch.int64, device=DEV),
-                             n_decode, 300, 1200)              # max_query_len understated
+                             n_decode, mql, 1200)              # max_query_len understated
     out = K.paged_attention(dq, dkc, dvc, meta, D ** -0.5)
     torch.cuda.synchronize()
     o = out.float().cpu()[n_decode:]
     nan_rows = torch.isnan(o).all(dim=1)
-    if D == 128:
-        covered = torch.arange(600) >= 256                     # tiles 2..4 of 5 (longest first)
+    rows_i = torch.arange(600)
+    if D == 128 and n_decode == 0:
+        covered = rows_i >= 128 * _stream_k_nan_tiles(mql, 600, 1200, Hh, N.cu_count(0))
+    elif D == 128:
+        covered = rows_i >= 256                                # tiles 2..4 of 5 (longest first)
     else:
-        covered = torch.arange(600) < 320                      # 10 tiles of 32 rows
+        covered = rows_i < 320                                 # 10 tiles of 32 rows
     assert bool(nan_rows[~covered].all()) and not bool(torch.isnan(o[covered]).any())
     rows = torch.cat([torch.ones(n_decode, dtype=torch.bool), covered])
     assert_attn(out[rows.to(DEV)], ref[rows.numpy()], f"covered rows, D {D}")
+
+
+def _stream_k_nan_tiles(mql: int, q_len: int, seq_len: int, H: int, cus: int) -> int:
+    """Lowest 128-row tiles (two heads per work item) of one prefill sequence that the stream-K
+    plan sized for max_query_len = mql leaves as NaN: tiles, longest first, share the sequence's
+    steps over `slots` launch slots; the tile at position pos with segments pos + k,
+    k = G // T .. (G + n - 1) // T, is NaN when it has more than one segment and one of them is
+    past the workspace's tiles_h + slots segments."""
+    items = H // 2
+    slots = cus // items
+    seg_cap = -(-mql // 128) + slots
+    tiles = -(-q_len // 128)
+    prefix = seq_len - q_len
+    steps = [-(-min(prefix + min((t + 1) * 128, q_len), seq_len) // 64) for t in range(tiles)]
+    per = -(-sum(steps) // slots)
+    nan, g = [], 0
+    for pos in range(tiles):
+        t = tiles - 1 - pos
+        k0, k1 = g // per, (g + steps[t] - 1) // per
+        nan.append(k0 < k1 and pos + k1 >= seg_cap)
+        g += steps[t]
+    # the NaN tiles must be the lowest ones (a row prefix)
+    flags = [nan[tiles - 1 - t] for t in range(tiles)]
+    n = 0
+    while n < tiles and flags[n]:
+        n += 1
+    assert not any(flags[n:]), flags
+    return n

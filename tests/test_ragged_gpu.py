@@ -76,7 +76,9 @@ def test_ragged_fused_and_sequential_match_oracle(n_decode, chunks):
     # the prefill tiles are not split, the sequential size already suffices for it.
     assert fused >= seq_need
     if n_decode == 48:
-        assert fused > seq_need, "the config 5 mixed step must split its prefill tiles"
+        dec = N.lib().ts_decode_workspace_bytes(0, n_decode, H, KVH, D, int(meta.max_seq_len), 0,
+                                                N.cu_count(0))
+        assert fused > dec, "the config 5 mixed step must split its prefill tiles"
     ws = torch.empty(fused, dtype=torch.uint8, device=DEV)
     assert_attn(call(q, kc, vc, meta, ws, fused, pf_bound), ref, "fused")
     assert_attn(call(q, kc, vc, meta, ws, seq_need, pf_bound), ref, "sequential")

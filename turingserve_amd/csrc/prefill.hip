@@ -1,6 +1,7 @@
 // Paged chunked-prefill attention for gfx950 (ops/triton_prefill_attention.py:17-79).
-// Host entry points; the kernels and their launch plans are in prefill_kernels.h.
-#include "prefill_kernels.h"
+// Host entry points; the kernels and their launch plans are in prefill_kernels.h (head_dim < 128)
+// and prefill_pair.h (head_dim 128).
+#include "prefill_pair.h"
 
 using namespace ts;
 
@@ -41,26 +42,26 @@ int prefill_launch(const void* q, int64_t q_stride_t, int64_t q_stride_h, void* 
   if (head_dim == 128) {
     int cus = 0;
     if (workspace != nullptr && device_cu_count(stream, &cus) != TS_OK) return TS_ERR_DEVICE;
-    TilePlan pl = tile_plan(P, num_heads, head_dim, max_query_len, max_seq_len, cus,
+    PairPlan pl = pair_plan(P, num_heads, num_kv_heads, max_query_len, max_seq_len, cus,
                             workspace != nullptr);
     if (pl.ws_bytes > workspace_bytes || (pl.ws_bytes > 0 && !aligned(workspace, 16)))
-      pl = tile_plan(P, num_heads, head_dim, max_query_len, max_seq_len, cus, false);
-    if (pl.ws_bytes == 0) pl.smax = 1 << 30;       // unsplit: no tile ever leaves partials
-    const int per_kvh = pl.slots * P * (num_heads / num_kv_heads);
+      pl = pair_plan(P, num_heads, num_kv_heads, max_query_len, max_seq_len, cus, false);
+    const bool heads = pair_heads(num_heads, num_kv_heads);
+    const int per_kvh = pl.slots * P * (num_heads / num_kv_heads / (heads ? 2 : 1));
     const int n_launch = 8 % num_kv_heads == 0 ? 8 * cdiv(per_kvh, 8 / num_kv_heads)
                                                 : per_kvh * num_kv_heads;
-    prefill_tile_kernel<128><<<n_launch, kTileThreads, 0, s>>>(
+    prefill_pair_kernel<<<n_launch, kPairThreads, 0, s>>>(
         static_cast<const half_t*>(q), q_stride_t, q_stride_h, static_cast<half_t*>(out),
         out_stride_t, num_tokens, static_cast<const half_t*>(k_cache),
         static_cast<const half_t*>(v_cache), num_blocks, block_tables, bt_stride,
         max_blocks_per_seq, seq_lens, query_start_loc, num_decode, num_heads, num_kv_heads, sl2,
-        pl.smax, pl.slots, P, static_cast<float*>(workspace));
-    if (pl.ws_bytes > 0)
-      prefill_merge_kernel<128><<<dim3(4 * cdiv(max_query_len, kTileRows), P, num_heads),
+        pl.slots, pl.seg_cap, P, static_cast<float*>(workspace));
+    if (pl.seg_cap > 0)
+      prefill_pair_merge_kernel<<<dim3(4 * cdiv(max_query_len, kTileRows), P, num_heads),
                                   kTileThreads, 0, s>>>(
           static_cast<const float*>(workspace), static_cast<half_t*>(out), out_stride_t,
           num_tokens, max_blocks_per_seq, seq_lens, query_start_loc, num_decode, num_heads,
-          pl.smax, pl.slots);
+          num_kv_heads, pl.slots, pl.seg_cap);
     return check_launch("prefill_attention");
   }
   const dim3 grid((max_query_len + kPsRows - 1) / kPsRows, P, num_heads);
@@ -87,8 +88,13 @@ extern "C" size_t ts_prefill_workspace_bytes(int32_t num_prefill, int32_t num_he
                                              int32_t head_dim, int32_t max_query_len,
                                              int32_t max_seq_len, int32_t cu_count) {
   if (num_prefill <= 0 || num_heads <= 0 || head_dim != 128 || max_query_len <= 0) return 0;
-  return tile_plan(num_prefill, num_heads, head_dim, max_query_len, max_seq_len, cu_count, true)
-      .ws_bytes;
+  // The plan depends on whether the GQA group size is even (not an argument here): enough for
+  // either form.
+  const size_t a = pair_plan(num_prefill, num_heads, 1, max_query_len, max_seq_len, cu_count,
+                             true).ws_bytes;
+  const size_t b = pair_plan(num_prefill, num_heads, num_heads, max_query_len, max_seq_len,
+                             cu_count, true).ws_bytes;
+  return a > b ? a : b;
 }
 
 extern "C" int ts_prefill_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,

@@ -243,7 +243,6 @@ constexpr int kTileRows = 128;
 constexpr int kTileKeys = 64;
 constexpr int kTileThreads = 256;
 constexpr int kPrefillMinSteps = 4;   // fewest 64-key steps a split is given
-constexpr int kMergeBatch = 8;        // splits whose partials the merge requests at once
 constexpr int kMergeRows = 4;         // rows per merge thread
 
 template <int D>
@@ -279,13 +278,15 @@ struct TileSlot {
   int tile, split, nsplit, lo, hi;   // steps [lo, hi) of tile `tile`; tile -1: idle slot
 };
 
-// Launch slot -> (tile, split) for one (sequence, head): tiles longest first, tile i with n_i
-// steps gets max(1, ceil(n_i / smax)) splits of balanced step ranges, numbered consecutively.
-__device__ __forceinline__ TileSlot tile_slot(int slot, int q_len, int prefix, int seq_len, int smax) {
-  const int tiles = (q_len + kTileRows - 1) / kTileRows;
+// Launch slot -> (tile, split) for one (sequence, head item): tiles of `tr` query rows longest
+// first, tile i with n_i steps gets max(1, ceil(n_i / smax)) splits of balanced step ranges,
+// numbered consecutively.
+__device__ __forceinline__ TileSlot tile_slot(int slot, int q_len, int prefix, int seq_len, int smax,
+                                              int tr) {
+  const int tiles = (q_len + tr - 1) / tr;
   int base = 0;
   for (int i = tiles - 1; i >= 0; --i) {
-    const int last = ((i + 1) * kTileRows < q_len ? (i + 1) * kTileRows : q_len) - 1;
+    const int last = ((i + 1) * tr < q_len ? (i + 1) * tr : q_len) - 1;
     int hi = prefix + last + 1 < seq_len ? prefix + last + 1 : seq_len;
     hi = hi < 0 ? 0 : hi;
     const int n = (hi + kTileKeys - 1) / kTileKeys;
@@ -300,11 +301,12 @@ __device__ __forceinline__ TileSlot tile_slot(int slot, int q_len, int prefix, i
 }
 
 // First launch slot and split count of tile `tile` (the inverse of tile_slot).
-__device__ __forceinline__ int2_t tile_span(int tile, int q_len, int prefix, int seq_len, int smax) {
-  const int tiles = (q_len + kTileRows - 1) / kTileRows;
+__device__ __forceinline__ int2_t tile_span(int tile, int q_len, int prefix, int seq_len, int smax,
+                                            int tr) {
+  const int tiles = (q_len + tr - 1) / tr;
   int base = 0;
   for (int i = tiles - 1; i >= tile; --i) {
-    const int last = ((i + 1) * kTileRows < q_len ? (i + 1) * kTileRows : q_len) - 1;
+    const int last = ((i + 1) * tr < q_len ? (i + 1) * tr : q_len) - 1;
     int hi = prefix + last + 1 < seq_len ? prefix + last + 1 : seq_len;
     hi = hi < 0 ? 0 : hi;
     const int n = (hi + kTileKeys - 1) / kTileKeys;
@@ -313,6 +315,24 @@ __device__ __forceinline__ int2_t tile_span(int tile, int q_len, int prefix, int
     base += ns;
   }
   return {0, 0};
+}
+
+// The lowest tile (of `tr` rows) whose splits run past a launch of `slots` slots, or -1: with
+// host bounds below the batch's real q_len / seq_len the tiles a launch misses are the lowest
+// ones (slots number the tiles longest first).
+__device__ __forceinline__ int first_cut_tile(int q_len, int prefix, int seq_len, int smax, int tr,
+                                              int slots) {
+  const int tiles = (q_len + tr - 1) / tr;
+  int base = 0;
+  for (int i = tiles - 1; i >= 0; --i) {
+    const int last_row = ((i + 1) * tr < q_len ? (i + 1) * tr : q_len) - 1;
+    int hi = prefix + last_row + 1 < seq_len ? prefix + last_row + 1 : seq_len;
+    hi = hi < 0 ? 0 : hi;
+    const int n = (hi + kTileKeys - 1) / kTileKeys;
+    base += n <= smax ? 1 : (n + smax - 1) / smax;
+    if (base > slots) return i;
+  }
+  return -1;
 }
 
 struct PrefillSeq {
@@ -377,25 +397,14 @@ __device__ __forceinline__ void prefill_tile_body(
 
   const PrefillSeq sq = prefill_seq(qsl, seq_lens, b, num_tokens, max_blocks);
   if (slot == slots - 1) {
-    // Slots number the tiles longest first, so the tiles a launch misses (host bounds below the
-    // real q_len / seq_len) are the lowest ones: every tile from the first (going down) whose
-    // splits run past the last slot. Their rows are written by no other workgroup.
-    const int tiles = (sq.q_len + kTileRows - 1) / kTileRows;
-    int base = 0, cut = -1;
-    for (int i = tiles - 1; i >= 0 && cut < 0; --i) {
-      const int last_row = ((i + 1) * kTileRows < sq.q_len ? (i + 1) * kTileRows : sq.q_len) - 1;
-      int hi = sq.prefix + last_row + 1 < sq.seq_len ? sq.prefix + last_row + 1 : sq.seq_len;
-      hi = hi < 0 ? 0 : hi;
-      const int n = (hi + kTileKeys - 1) / kTileKeys;
-      base += n <= smax ? 1 : (n + smax - 1) / smax;
-      if (base > slots) cut = i;
-    }
+    // Rows of tiles the launch misses are written by no other workgroup.
+    const int cut = first_cut_tile(sq.q_len, sq.prefix, sq.seq_len, smax, kTileRows, slots);
     if (cut >= 0) {
       const int m_end = (cut + 1) * kTileRows < sq.q_len ? (cut + 1) * kTileRows : sq.q_len;
       poison_rows<D>(out, o_st, sq.q_start, 0, m_end, h);
     }
   }
-  const TileSlot tsl = tile_slot(slot, sq.q_len, sq.prefix, sq.seq_len, smax);
+  const TileSlot tsl = tile_slot(slot, sq.q_len, sq.prefix, sq.seq_len, smax, kTileRows);
   if (tsl.tile < 0) return;
   const int m0 = tsl.tile * kTileRows;
   const int last = (m0 + kTileRows < sq.q_len ? m0 + kTileRows : sq.q_len) - 1;
@@ -628,30 +637,22 @@ __global__ void __launch_bounds__(kTileThreads, 2) prefill_tile_kernel(
                        (int)blockIdx.x, lds);
 }
 
-// Merge of a split tile's partials (each the split's own average A_j = O_j / l_j):
-// M = max m_j, w_j = 2^(m_j - M) l_j, out = sum w_j A_j / sum w_j (empty splits have
-// m = -inf and weigh 0). Grid (4 * tiles, P, H): workgroup (4 i + q) merges rows
-// 32q .. 32q+31 of tile i if it was split; a thread owns 4 dims of kMergeRows rows, and the
-// loads of all its rows for kMergeBatch splits are requested in one memory step, so one
-// resident round of workgroups covers the whole merge.
+// Merge of split partials (each the split's own average A_j = O_j / l_j with its (m_j, l_j)):
+// M = max m_j, w_j = 2^(m_j - M) l_j, out = sum w_j A_j / sum w_j (empty splits have m = -inf and
+// weigh 0). A thread owns 4 dims (d0) of kMergeRows rows; the partials sit at slot indices
+// base .. base + cnt - 1 of a workspace of total_slots slots x slot_rows rows, the thread's rows at
+// row0 + kMergeRowStride * k of each slot, and go to dst[k] (nullptr: not wanted). The partials
+// are taken two at a time, all of a pair's loads requested together.
+constexpr int kMergeRowStride = kTileThreads / 32;   // row groups of a 256-thread merge group
+
 template <int D>
-__device__ __forceinline__ void prefill_merge_tile(
-    const float* __restrict__ ws, half_t* __restrict__ out, int64_t o_st, const PrefillSeq& sq,
-    int H, int smax, int slots, int P, int by, int h, int tile, int rbase) {
-  constexpr int TPR = D / 4;
-  constexpr int RG = kTileThreads / TPR;
+__device__ __forceinline__ void merge_partials(const float* __restrict__ ws, int64_t total_slots,
+                                               int slot_rows, int64_t base, int cnt, int row0,
+                                               int d0, half_t* const (&dst)[kMergeRows]) {
   constexpr int NR = kMergeRows;
-  constexpr int MB = kMergeBatch;
-  const int d0 = 4 * (int)(threadIdx.x % TPR);
-  if (tile * kTileRows + rbase >= sq.q_len) return;
-  const int2_t span = tile_span(tile, sq.q_len, sq.prefix, sq.seq_len, smax);
-  const int slot = span[0], nsplit = span[1];
-  if (nsplit <= 1) return;
-  if (slot + nsplit > slots) return;               // splits past the launch (bad bounds)
-  const int64_t slot0 = ((int64_t)by * H + h) * slots + slot;
-  const int64_t total = (int64_t)P * H * slots;
+  constexpr int RG = kMergeRowStride;
   const half_t* wo = reinterpret_cast<const half_t*>(ws);
-  const float* wml = reinterpret_cast<const float*>(wo + total * kTileRows * D);
+  const float* wml = reinterpret_cast<const float*>(wo + total_slots * slot_rows * D);
   float M[NR], Lsum[NR];
   float4_t acc[NR];
 #pragma unroll
@@ -660,71 +661,83 @@ __device__ __forceinline__ void prefill_merge_tile(
     Lsum[k] = 0.f;
     acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
   }
-  // Splits taken kMergeBatch at a time (indices past the split count re-read the last split
-  // and are ignored); the running result is rescaled when a later batch raises the maximum.
-  for (int j0 = 0; j0 < nsplit; j0 += MB) {
-    float2_t ml[NR][MB];
-    half4_t a[NR][MB];
+  for (int j = 0; j < cnt; j += 2) {
+    const bool two = j + 1 < cnt;
+    float2_t ml[2][NR];
+    half4_t a[2][NR];
 #pragma unroll
-    for (int k = 0; k < NR; ++k)
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int u = 0; u < MB; ++u) {
-        const int64_t sl = slot0 + (j0 + u < nsplit ? j0 + u : nsplit - 1);
-        const int64_t rix = sl * kTileRows + rbase + RG * k;
-        ml[k][u] = ld<float2_t>(wml + rix * 2);
-        a[k][u] = ld<half4_t>(wo + rix * D + d0);
+      for (int k = 0; k < NR; ++k) {
+        const int64_t rix = (base + j + (two ? u : 0)) * slot_rows + row0 + RG * k;
+        ml[u][k] = ld<float2_t>(wml + rix * 2);
+        a[u][k] = ld<half4_t>(wo + rix * D + d0);
       }
 #pragma unroll
     for (int k = 0; k < NR; ++k) {
-      float cm = M[k];
-#pragma unroll
-      for (int u = 0; u < MB; ++u) cm = j0 + u < nsplit ? fmaxf(cm, ml[k][u][0]) : cm;
+      const float m1 = two ? ml[1][k][0] : -INFINITY;
+      const float cm = fmaxf(M[k], fmaxf(ml[0][k][0], m1));
       const float alpha = M[k] == -INFINITY ? 0.f : fast_exp2(M[k] - cm);
       Lsum[k] *= alpha;
       acc[k] *= alpha;
 #pragma unroll
-      for (int u = 0; u < MB; ++u) {
-        const bool use = j0 + u < nsplit && ml[k][u][0] != -INFINITY;
-        const float wt = use ? fast_exp2(ml[k][u][0] - cm) * ml[k][u][1] : 0.f;
+      for (int u = 0; u < 2; ++u) {
+        const float mu = u == 0 ? ml[0][k][0] : m1;
+        const float wt = mu == -INFINITY ? 0.f : fast_exp2(mu - cm) * ml[u][k][1];
         Lsum[k] += wt;
-        acc[k][0] += wt * (float)a[k][u][0];
-        acc[k][1] += wt * (float)a[k][u][1];
-        acc[k][2] += wt * (float)a[k][u][2];
-        acc[k][3] += wt * (float)a[k][u][3];
+        acc[k][0] += wt * (float)a[u][k][0];
+        acc[k][1] += wt * (float)a[u][k][1];
+        acc[k][2] += wt * (float)a[u][k][2];
+        acc[k][3] += wt * (float)a[u][k][3];
       }
       M[k] = cm;
     }
   }
 #pragma unroll
   for (int k = 0; k < NR; ++k) {
-    const int row = tile * kTileRows + rbase + RG * k;
-    if (row >= sq.q_len) continue;
+    if (dst[k] == nullptr) continue;
     const float inv = Lsum[k] == 0.f ? 0.f : 1.f / Lsum[k];
-    ts::st<half4_t>(out + (int64_t)(sq.q_start + row) * o_st + (int64_t)h * D + d0,
-                    half4_t{(half_t)(acc[k][0] * inv), (half_t)(acc[k][1] * inv),
-                            (half_t)(acc[k][2] * inv), (half_t)(acc[k][3] * inv)});
+    ts::st<half4_t>(dst[k], half4_t{(half_t)(acc[k][0] * inv), (half_t)(acc[k][1] * inv),
+                                    (half_t)(acc[k][2] * inv), (half_t)(acc[k][3] * inv)});
   }
 }
 
+// Merge of the 4-wavefront tile kernel's split tiles (the mixed-step kernel's prefill part).
+// Grid (4 * tiles, P, H): workgroup (4 i + q) merges rows 32q .. 32q+31 of tile i if it was split;
+// partials are slot-major per (sequence, head), kTileRows rows per slot.
 template <int D>
 __device__ __forceinline__ void prefill_merge_body(
     const float* __restrict__ ws, half_t* __restrict__ out, int64_t o_st, int64_t num_tokens,
     int max_blocks, const int* __restrict__ seq_lens, const int* __restrict__ qsl,
-    int num_decode, int H, int smax, int slots,
-    int P, int bx, int by, int bz, int tile_stride) {
+    int num_decode, int H, int smax, int slots, int P, int bx, int by, int bz, int tile_stride) {
   constexpr int TPR = D / 4;                       // threads per row
-  constexpr int RG = kTileThreads / TPR;           // row groups per workgroup (8)
+  constexpr int RG = kMergeRowStride;              // row groups per workgroup (8)
   constexpr int NR = kMergeRows;                   // rows per thread
-  static_assert(RG * NR * 4 == kTileRows, "four workgroups per tile");
+  static_assert(RG * NR * 4 == kTileRows && TPR * RG == kTileThreads, "four workgroups per tile");
   const int part = bx & 3;
   const int b = num_decode + by, h = bz;
   const PrefillSeq sq = prefill_seq(qsl, seq_lens, b, num_tokens, max_blocks);
   const int rbase = part * RG * NR + (int)(threadIdx.x / TPR);   // rows rbase + RG * k
+  const int d0 = 4 * (int)(threadIdx.x % TPR);
+  const int64_t total = (int64_t)P * H * slots;
   // The grid covers the tiles the host bounds foresee; a sequence with more (bounds below its
   // real q_len) has its further tiles taken in turn, so every tile whose splits all ran is
   // merged (the tile kernel fills the rows of the others with NaN).
-  for (int tile = bx >> 2; tile * kTileRows < sq.q_len; tile += tile_stride)
-    prefill_merge_tile<D>(ws, out, o_st, sq, H, smax, slots, P, by, h, tile, rbase);
+  for (int tile = bx >> 2; tile * kTileRows < sq.q_len; tile += tile_stride) {
+    if (tile * kTileRows + rbase >= sq.q_len) continue;
+    const int2_t span = tile_span(tile, sq.q_len, sq.prefix, sq.seq_len, smax, kTileRows);
+    const int slot = span[0], nsplit = span[1];
+    if (nsplit <= 1 || slot + nsplit > slots) continue;   // unsplit, or splits past the launch
+    half_t* dst[NR];
+#pragma unroll
+    for (int k = 0; k < NR; ++k) {
+      const int row = tile * kTileRows + rbase + RG * k;
+      dst[k] = row < sq.q_len ? out + (int64_t)(sq.q_start + row) * o_st + (int64_t)h * D + d0
+                              : nullptr;
+    }
+    merge_partials<D>(ws, total, kTileRows, ((int64_t)by * H + h) * slots + slot, nsplit, rbase,
+                      d0, dst);
+  }
 }
 
 template <int D>
@@ -737,8 +750,8 @@ __global__ void __launch_bounds__(kTileThreads) prefill_merge_kernel(
                         (int)blockIdx.z, (int)gridDim.x / 4);
 }
 
-// Host-side plan of the tiled path: the most steps one split may take (smax) and the launch
-// slots per (sequence, head), from host bounds of the batch (max_query_len, max_seq_len).
+// Host-side plan of the 4-wavefront tiled path: the most steps one split may take (smax) and the
+// launch slots per (sequence, head), from host bounds of the batch (max_query_len, max_seq_len).
 struct TilePlan {
   int smax, slots;
   size_t ws_bytes;
