@@ -5,23 +5,32 @@
 // Workgroup = 512 threads: two groups of four wavefronts, each group owning one 128-row unit.
 // With an even GQA group size the two units are the same 128 query rows of two query heads that
 // share a KV head; otherwise two consecutive 128-row tiles of one query head. Every 64-key step
-// of K and V is staged in LDS once for both units. Per step s and wavefront (32 query rows of its
-// unit), on v_mfma_f32_32x32x16_f16 (operand layouts as in the 4-wavefront tile kernel):
-//   MFMA phase M(s):  S^T(s) = K(s) . Q^T            16 MFMAs
-//                     O^T  += V^T(s-1) . P^T(s-1)    16 MFMAs (the previous step's P)
-//   VALU phase V(s):  this wavefront's share of staging step s + 1, then the causal mask and the
-//                     online softmax of S^T(s) -> P(s) in fp16
+// of K and V is staged in LDS once for both units (eight wavefronts, 256 query rows). Per step s
+// and wavefront (32 query rows of its unit), on v_mfma_f32_32x32x16_f16 (operand layouts as in the
+// 4-wavefront tile kernel):
+//   MFMA phase M(s):  S^T(s) = K(s) . Q^T (16 MFMAs) alternating with O^T += V^T(s-1) . P^T(s-1)
+//                     (16 MFMAs, the previous step's P), operands requested kPairAhead MFMAs
+//                     ahead; the wavefront's share of staging step s + 1 (4 LDS writes, 10 global
+//                     loads) is spread between the MFMAs
+//   VALU phase V(s):  causal mask and online softmax of S^T(s) -> P(s) in fp16
+// Keeping P(s) for the next MFMA phase puts 32 mutually independent MFMAs in every MFMA phase.
 // The groups run half a step apart -- group 0: M(s) | V(s), group 1: V(s-1) | M(s) -- with a
-// workgroup barrier between phases. The four SIMDs each hold one wavefront of either group, so on
-// every SIMD one wavefront's MFMAs run while the other does its softmax, and every MFMA phase
-// has 32 independent-enough MFMAs whose LDS operands are requested six MFMAs ahead.
+// workgroup barrier between phases, so on every SIMD (one wavefront of each group) one
+// wavefront's softmax runs beside the other's MFMAs. (Measured on MI355X: one wavefront's LDS
+// operand reads feed an MFMA only about every 55 cycles, which bounds each MFMA phase; running
+// both groups' MFMA phases together, one barrier per step, measured about as fast.)
+//
+// Launch: with a workspace, each work item's (sequence, head item) steps, tiles longest first,
+// are shared evenly over its launch slots (stream-K) and cut at tile boundaries into segments; a
+// tile covered by one segment is written directly, otherwise its segments' partials are combined
+// by prefill_pair_merge_kernel. Without one, each slot takes one whole tile.
 //
 // LDS: two K buffers [64 keys][256 bytes + 16 pad] and two V^T buffers laid out as
 // [16-key block u][dim d][32 bytes]: the 32 bytes are the two 8-key halves that lanes h = 0, 1
 // of the PV MFMA of block u read, swapped when bits 2 and 3 of d differ, so that operand reads
 // and staging writes fall on distinct banks. K(s) is in buffer (s - lo) % 2, V(s) in buffer
-// (s - lo) % 2; during the phases of step s the staging writes K(s + 1) and V(s) into the
-// buffers that step s - 1 released, and loads K(s + 2), V(s + 1) into registers.
+// (s - lo) % 2; during step s the staging writes K(s + 1) and V(s) into the buffers that step
+// s - 1 released, and loads K(s + 2), V(s + 1) into registers.
 #pragma once
 
 #include "prefill_kernels.h"
@@ -366,18 +375,17 @@ __device__ __forceinline__ void prefill_pair_body(
     // the softmax of step lo + j. Every wavefront runs every phase (past its own key range on
     // zero P), so the loop has no branches besides the causal mask and the rescale.
     if (g == 1) __syncthreads();                   // phase 0 belongs to group 0
-    auto step = [&](int j, int4_t (&kr)[2], uint32_t (&vr)[8]) {
+    for (int j = 0; j < n; ++j) {
       // Raised priority over the MFMA phase: of the two wavefronts on a SIMD, the one issuing
       // MFMAs is served first.
       __builtin_amdgcn_s_setprio(2);
-      staging(j, kr, vr);
+      staging(j, kra, vra);
       mphase(lo + j, Flag<true>{});
       __builtin_amdgcn_s_setprio(0);
       __syncthreads();
       vstep(lo + j);
       __syncthreads();
-    };
-    for (int j = 0; j < n; ++j) step(j, kra, vra);
+    }
     __builtin_amdgcn_s_setprio(2);
     mphase(hi, Flag<false>{});                     // O += V^T(hi - 1) . P^T(hi - 1)
     __builtin_amdgcn_s_setprio(0);
