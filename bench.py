@@ -590,7 +590,9 @@ def bench_decode_model(torch, synth, reps: int = 10):
     [128, 4096]) through a random-init Qwen2 at the Qwen2.5-1.5B dimensions (28 layers, W8A16
     linears), graph-replayed as pure-decode steps are; tokens/s = 64 / step time. Timed with each
     layer's rope + kv_write + attention as one launch and, for comparison, as the separate calls
-    (rope_kv_write, then paged_attention)."""
+    (rope_kv_write, then paged_attention); and with o_proj / down_proj taken into the norm that
+    consumes them (split-K partials reduced inside the norm launch) against the product and the
+    norm as separate calls ("separate_norm")."""
     import random as _r
 
     from turingserve_amd import get_ops
@@ -604,8 +606,11 @@ def bench_decode_model(torch, synth, reps: int = 10):
     w = random_weights(cfg, dev, quantization="int8", init_std=0.02, seed=0)
     ops_plain = get_ops("hip")
     del ops_plain.decode_rope_kv_write_attention
+    ops_norm = get_ops("hip")
+    del ops_norm.linear_rmsnorm_residual
     models = {"fused": Qwen2Model(cfg, w, get_ops("hip"), max_model_len=8192),
-              "separate": Qwen2Model(cfg, w, ops_plain, max_model_len=8192)}
+              "separate": Qwen2Model(cfg, w, ops_plain, max_model_len=8192),
+              "separate_norm": Qwen2Model(cfg, w, ops_norm, max_model_len=8192)}
     nb = sum(-(-c // 16) for c in ctx) + 8
     kv = models["fused"].new_kv_cache(nb)
     kv.normal_(0.0, 0.5)
@@ -642,7 +647,8 @@ def bench_decode_model(torch, synth, reps: int = 10):
         res[f"{name}_graph_ms"] = round(dt * 1e3, 3)
         res[f"{name}_tokens_per_s"] = round(T / dt, 1)
         del g_
-    res["fused_equals_separate"] = bool(torch.equal(outs["fused"], outs["separate"]))
+    res["fused_equals_separate"] = bool(torch.equal(outs["fused"], outs["separate"]) and
+                                       torch.equal(outs["fused"], outs["separate_norm"]))
     del models, w, kv
     torch.cuda.empty_cache()
     return res

@@ -17,6 +17,8 @@
  *   ts_w8a16_gemm_v        <- the same with the tuned per-bucket config (autopilot/tuner.py)
  *   ts_w8a16_glu           <- model/qwen2.py:35-36, silu_mul(linear(x, gate_up)) fused
  *                             (ops/triton_ops.py:74-91 + ops/triton_silu_mul.py:21-28)
+ *   ts_w8a16_add_rmsnorm   <- model/qwen2.py:84-92, rmsnorm_residual(linear(x, proj), residual)
+ *                             fused (ops/triton_ops.py:74-91 + ops/triton_rmsnorm.py:30-46)
  *   ts_logits_int8         <- model/qwen2.py:94-99 with ops/triton_ops.py:88-91 (gather, int8
  *                             lm head and .float() fused)
  *   ts_step_metadata       <- runner/input_builder.py:81-150 (host arrays + seven copies) and
@@ -314,6 +316,29 @@ int ts_w8a16_glu(const void* x, int64_t ldx, const int8_t* wq, const void* scale
                  int32_t scale_is_fp16, const void* bias, void* out, int64_t ldo,
                  int32_t M, int32_t intermediate, int32_t K, int32_t variant, int32_t splits,
                  void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * A W8A16 product consumed by the residual add and RMSNorm of a decoder layer (o_proj before
+ * post_attention_layernorm, down_proj before the next layer's input_layernorm or the final
+ * norm: model/qwen2.py:84-92's rmsnorm_residual(linear(x, proj), residual)):
+ *   y = fp16( x . (wq * scale)^T + bias ),   residual_out = y + residual,
+ *   out = rmsnorm(residual_out) * norm_weight
+ * equal, bit for bit, to ts_w8a16_gemm_v (same variant and splits) followed by ts_rmsnorm with
+ * the residual. When the plan splits K, the norm launch reduces the fp32 partials itself (in the
+ * split-K reduction's order) instead of a separate reduction launch; otherwise the product rows
+ * go through the workspace to the norm. y is not written to memory. x, wq, scale, bias, M, N, K,
+ * variant and splits as for ts_w8a16_gemm_v; residual, norm_weight, out, residual_out as for
+ * ts_rmsnorm with hidden = N (a multiple of 8, at most 8192). Workspace:
+ * ts_w8a16_add_rmsnorm_workspace_bytes() bytes (16-byte aligned; never zero for M > 0).
+ */
+size_t ts_w8a16_add_rmsnorm_workspace_bytes(int32_t M, int32_t N, int32_t K, int32_t variant,
+                                            int32_t splits, int32_t cu_count);
+int ts_w8a16_add_rmsnorm(const void* x, int64_t ldx, const int8_t* wq, const void* scale,
+                         int32_t scale_is_fp16, const void* bias, const void* residual,
+                         int64_t residual_stride, const void* norm_weight, void* out,
+                         int64_t out_stride, void* residual_out, int64_t residual_out_stride,
+                         int32_t M, int32_t N, int32_t K, float eps, int32_t variant,
+                         int32_t splits, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Logits of the sampling rows through the int8 tied lm head, in one launch (plus the split-K

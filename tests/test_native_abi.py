@@ -85,6 +85,31 @@ def test_logits_argument_checks():
             lib.ts_w8a16_workspace_bytes(S, 151936, 1536, 256)
 
 
+def test_add_rmsnorm_argument_checks_and_workspace():
+    lib = N.lib()
+    p = ctypes.c_void_p(256)            # never dereferenced: the call fails validation first
+    eps = ctypes.c_float(1e-6)
+    assert lib.ts_w8a16_add_rmsnorm(p, 1536, p, p, 0, None, p, 1536, p, p, 1536, p, 1536, 4,
+                                    1540, 1536, eps, 0, 0, p, 1 << 20, None) == \
+        N.TS_ERR_UNSUPPORTED and "multiple of 8" in N.last_error()
+    assert lib.ts_w8a16_add_rmsnorm(p, 1536, p, p, 0, None, p, 1536, p, p, 1536, p, 1536, 4,
+                                    16384, 1536, eps, 0, 0, p, 1 << 20, None) == \
+        N.TS_ERR_UNSUPPORTED and "8192" in N.last_error()
+    assert lib.ts_w8a16_add_rmsnorm(p, 1536, p, p, 0, None, None, 1536, p, p, 1536, p, 1536, 4,
+                                    1536, 1536, eps, 0, 0, p, 1 << 20, None) == N.TS_ERR_INVALID_ARG
+    assert lib.ts_w8a16_add_rmsnorm(None, 0, None, None, 0, None, None, 0, None, None, 0, None, 0,
+                                    0, 1536, 1536, eps, 0, 0, None, 0, None) == N.TS_OK
+    assert lib.ts_w8a16_add_rmsnorm(p, 1536, p, p, 0, None, p, 1536, p, p, 1536, p, 1536, 64,
+                                    1536, 1536, eps, 1, 0, p, 1 << 20, None) == N.TS_ERR_UNSUPPORTED
+    # split K: the partials (as ts_w8a16_gemm_v's); else the fp16 product rows for the norm
+    for M, v, s in ((64, 0, 0), (64, 4, 8), (560, 0, 0), (9, 2, 4), (4, 1, 3)):
+        ws = lib.ts_w8a16_add_rmsnorm_workspace_bytes(M, 1536, 8960, v, s, 256)
+        part = lib.ts_w8a16_workspace_bytes_v(M, 1536, 8960, v, s, 256)
+        assert ws == (part if part > 0 else M * 1536 * 2)
+    assert lib.ts_w8a16_add_rmsnorm_workspace_bytes(1, 1536, 1536, 5, 0, 256) == 1536 * 2
+    assert lib.ts_w8a16_add_rmsnorm_workspace_bytes(64, 1536, 1536, 1, 0, 256) == 0
+
+
 def test_glu_argument_checks_and_workspace():
     lib = N.lib()
     p = ctypes.c_void_p(256)            # never dereferenced: the call fails validation first

@@ -76,6 +76,10 @@ SIGNATURES = {
     "ts_w8a16_glu_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "ts_w8a16_glu": (ctypes.c_int, [_p, _i64, _p, _p, _i32, _p, _p, _i64, _i32, _i32, _i32, _i32,
                                     _i32, _p, _sz, _p]),
+    "ts_w8a16_add_rmsnorm_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "ts_w8a16_add_rmsnorm": (ctypes.c_int, [_p, _i64, _p, _p, _i32, _p, _p, _i64, _p, _p, _i64,
+                                            _p, _i64, _i32, _i32, _i32, _f32, _i32, _i32, _p, _sz,
+                                            _p]),
     "ts_logits_int8_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32]),
     "ts_step_metadata": (ctypes.c_int, [_p, _i32, _i64, _i64, _i32, _i32, _i64, _p, _p, _p, _p,
                                         _p, _p, _p, _p]),

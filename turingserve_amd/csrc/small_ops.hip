@@ -12,66 +12,10 @@
 #include <math.h>
 
 #include "common.h"
+#include "rmsnorm.h"
 #include "rope.h"
 
 namespace ts {
-
-constexpr int kRowThreads = 256;
-constexpr int kRowVec = 8;                 // halves per 16-byte access
-constexpr int kRmsMaxIter = 4;             // N <= 4 * 256 * 8 = 8192
-
-__device__ __forceinline__ float block_sum_256(float v, float* s_red) {
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
-  const int w = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  if (lane == 0) s_red[w] = v;
-  __syncthreads();
-  return (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-}
-
-// One workgroup per token row of N = hidden features.
-template <bool kRes>
-__global__ void __launch_bounds__(kRowThreads) rmsnorm_kernel(
-    const half_t* __restrict__ x, int64_t x_st, const half_t* __restrict__ res, int64_t res_st,
-    const half_t* __restrict__ w, half_t* __restrict__ out, int64_t out_st,
-    half_t* __restrict__ res_out, int64_t res_out_st, int N, float eps) {
-  __shared__ float s_red[kRowThreads / kWave];
-  const int64_t t = blockIdx.x;
-  const int tid = threadIdx.x;
-  half8_t v[kRmsMaxIter];
-  float ss = 0.f;
-#pragma unroll
-  for (int it = 0; it < kRmsMaxIter; ++it) {
-    const int i = (it * kRowThreads + tid) * kRowVec;
-    if (i < N) {
-      half8_t a = ld<half8_t>(x + t * x_st + i);
-      if constexpr (kRes) {
-        const half8_t b = ld<half8_t>(res + t * res_st + i);
-#pragma unroll
-        for (int e = 0; e < kRowVec; ++e) a[e] = (half_t)((float)a[e] + (float)b[e]);
-        st<half8_t>(res_out + t * res_out_st + i, a);
-      }
-      v[it] = a;
-#pragma unroll
-      for (int e = 0; e < kRowVec; ++e) ss += (float)a[e] * (float)a[e];
-    }
-  }
-  const float inv = rsqrtf(block_sum_256(ss, s_red) / (float)N + eps);
-#pragma unroll
-  for (int it = 0; it < kRmsMaxIter; ++it) {
-    const int i = (it * kRowThreads + tid) * kRowVec;
-    if (i < N) {
-      const half8_t wv = ld<half8_t>(w + i);
-      half8_t o;
-#pragma unroll
-      for (int e = 0; e < kRowVec; ++e) {
-        const half_t y = (half_t)((float)v[it][e] * inv);          // cast before the weight
-        o[e] = (half_t)((float)wv[e] * (float)y);
-      }
-      st<half8_t>(out + t * out_st + i, o);
-    }
-  }
-}
 
 // One workgroup per token; the (H + KVH) rotated heads of the row are covered by 256 threads,
 // each owning 4 consecutive frequency indices of one head (8-byte accesses of both halves).

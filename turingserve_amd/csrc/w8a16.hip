@@ -17,6 +17,7 @@
 //    into the A operands of the wavefront that owns them, activations are DMA'd into a ring of
 //    LDS stages that all four wavefronts read.
 #include "common.h"
+#include "rmsnorm.h"
 
 namespace ts {
 
@@ -277,16 +278,24 @@ __global__ void __launch_bounds__(kSmWaves * 64) w8a16_small_kernel(
   }
 }
 
-// Element i of the [M, N] product from its split-K partials: sum, scale, bias, fp16.
+// Output channel nn from its fp32 K sum: scale, bias, fp16.
+__device__ __forceinline__ half_t finish_channel(float s, const void* __restrict__ scale,
+                                                 int scale_is_fp16, const half_t* __restrict__ bias,
+                                                 int nn) {
+  float v = s * load_scale(scale, scale_is_fp16, nn);
+  if (bias) v += (float)bias[nn];
+  return (half_t)v;
+}
+
+// Element i of the [M, N] product from its split-K partials: sum (in split order), scale, bias,
+// fp16.
 __device__ __forceinline__ half_t reduce_partials(const float* __restrict__ part, int splits,
                                                   int64_t total, int64_t i,
                                                   const void* __restrict__ scale, int scale_is_fp16,
                                                   const half_t* __restrict__ bias, int nn) {
   float s = 0.f;
   for (int k = 0; k < splits; ++k) s += part[(int64_t)k * total + i];
-  float v = s * load_scale(scale, scale_is_fp16, nn);
-  if (bias) v += (float)bias[nn];
-  return (half_t)v;
+  return finish_channel(s, scale, scale_is_fp16, bias, nn);
 }
 
 // Sum of the split-K partials, then scale, bias and fp16 conversion.
@@ -319,6 +328,36 @@ __global__ void __launch_bounds__(256) w8a16_glu_reduce_kernel(
     const half_t u = reduce_partials(part, splits, total, i + I, scale, scale_is_fp16, bias, I + ii);
     y[(int64_t)mm * ldy + ii] = silu_mul_h(g, u);
   }
+}
+
+// Split-K epilogue of a product that a residual add and RMSNorm consume (o_proj and down_proj in
+// a decoder layer): row t of y is reduced as w8a16_reduce_kernel reduces it (split order, scale,
+// bias, fp16), then res_out = y + res and out = rmsnorm(res_out) * w as the standalone norm
+// computes them, so the pair of launches replaces reduce + norm with the same values.
+__global__ void __launch_bounds__(kRowThreads) w8a16_reduce_rmsnorm_kernel(
+    const float* __restrict__ part, int splits, const void* __restrict__ scale, int scale_is_fp16,
+    const half_t* __restrict__ bias, const half_t* __restrict__ res, int64_t res_st,
+    const half_t* __restrict__ w, half_t* __restrict__ out, int64_t out_st,
+    half_t* __restrict__ res_out, int64_t res_out_st, int M, int N, float eps) {
+  const int64_t t = blockIdx.x;
+  const int64_t total = (int64_t)M * N;
+  auto load_x = [&](int i) {
+    float4_t a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < splits; ++k) {
+      const float* pp = part + (int64_t)k * total + t * N + i;
+      a += ld<float4_t>(pp);
+      b += ld<float4_t>(pp + 4);
+    }
+    half8_t v;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = finish_channel(a[e], scale, scale_is_fp16, bias, i + e);
+      v[4 + e] = finish_channel(b[e], scale, scale_is_fp16, bias, i + 4 + e);
+    }
+    return v;
+  };
+  rmsnorm_row<true>(load_x, res + t * res_st, w, out + t * out_st, res_out + t * res_out_st, N,
+                    eps);
 }
 
 // ------------------------------------------------------------------------------------------
@@ -1048,10 +1087,14 @@ extern "C" size_t ts_w8a16_workspace_bytes_v(int32_t M, int32_t N, int32_t K, in
 }
 
 // Validated launch shared by the GEMM and logits entry points.
+// With splits_out, a product planned with split K leaves its fp32 partials in the workspace
+// (no reduction launch) and *splits_out says how many; otherwise *splits_out = 1 and y is
+// written.
 static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const void* scale,
                         int32_t scale_is_fp16, const half_t* bp, half_t* yp, int64_t ldy,
                         int32_t M, int32_t N, int32_t K, void* workspace, size_t workspace_bytes,
-                        hipStream_t s, const GemmIo& io, int variant, int splits) {
+                        hipStream_t s, const GemmIo& io, int variant, int splits,
+                        int* splits_out = nullptr) {
   int cus = 0;
   int st = device_cu_count(s, &cus);
   if (st != TS_OK) return st;
@@ -1062,7 +1105,9 @@ static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const v
   TS_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
              TS_ERR_WORKSPACE, "w8a16: workspace of %zu bytes needed, got %zu", need,
              workspace_bytes);
+  if (splits_out) *splits_out = p.splits;
   auto reduce = [&](float* part) {
+    if (splits_out) return;
     if (glu) {
       const int64_t want = ((int64_t)M * io.glu + 255) / 256;
       w8a16_glu_reduce_kernel<<<(int)(want < 4096 ? want : 4096), 256, 0, s>>>(
@@ -1188,6 +1233,76 @@ extern "C" int ts_w8a16_gemm_v(const void* x, int64_t ldx, const int8_t* wq, con
   ts::clear_error();
   return w8a16_gemm_checked(x, ldx, wq, scale, scale_is_fp16, bias, y, ldy, M, N, K, variant,
                             splits, workspace, workspace_bytes, stream);
+}
+
+// Workspace of the fused product + residual add + RMSNorm: the split-K partials when the plan
+// splits K, else the fp16 product rows the norm reads.
+static size_t add_rmsnorm_workspace(const GemmPlan& p, int M, int N) {
+  return p.splits > 1 ? gemm_workspace(p, M, N) : (size_t)M * N * sizeof(half_t);
+}
+
+extern "C" size_t ts_w8a16_add_rmsnorm_workspace_bytes(int32_t M, int32_t N, int32_t K,
+                                                       int32_t variant, int32_t splits,
+                                                       int32_t cu_count) {
+  if (M <= 0 || N <= 0 || K <= 0 || !variant_valid(variant, splits, M)) return 0;
+  return add_rmsnorm_workspace(plan_gemm_v(M, N, K, cu_count > 0 ? cu_count : 256, variant, splits),
+                               M, N);
+}
+
+extern "C" int ts_w8a16_add_rmsnorm(const void* x, int64_t ldx, const int8_t* wq,
+                                    const void* scale, int32_t scale_is_fp16, const void* bias,
+                                    const void* residual, int64_t residual_stride,
+                                    const void* norm_weight, void* out, int64_t out_stride,
+                                    void* residual_out, int64_t residual_out_stride, int32_t M,
+                                    int32_t N, int32_t K, float eps, int32_t variant,
+                                    int32_t splits, void* workspace, size_t workspace_bytes,
+                                    void* stream) {
+  ts::clear_error();
+  TS_REQUIRE(M >= 0 && N > 0 && K > 0, TS_ERR_INVALID_ARG,
+             "w8a16_add_rmsnorm: bad shape M=%d N=%d K=%d", M, N, K);
+  TS_REQUIRE(variant_valid(variant, splits, M < 1 ? 1 : M), TS_ERR_UNSUPPORTED,
+             "w8a16_add_rmsnorm: variant %d with %d splits is not available for M=%d", variant,
+             splits, M);
+  if (M == 0) return TS_OK;
+  TS_REQUIRE(x && wq && scale && residual && norm_weight && out && residual_out,
+             TS_ERR_INVALID_ARG, "w8a16_add_rmsnorm: null pointer argument");
+  TS_REQUIRE(K % 8 == 0, TS_ERR_UNSUPPORTED, "w8a16_add_rmsnorm: K=%d is not a multiple of 8", K);
+  TS_REQUIRE(N % kRowVec == 0 && N <= kRmsMaxIter * kRowThreads * kRowVec, TS_ERR_UNSUPPORTED,
+             "w8a16_add_rmsnorm: N=%d must be a multiple of 8 and <= 8192", N);
+  TS_REQUIRE(ldx >= K && ldx % 8 == 0 && aligned(x, 16) && aligned(wq, 8), TS_ERR_INVALID_ARG,
+             "w8a16_add_rmsnorm: x must be 16-byte aligned rows (ldx %% 8 == 0), wq 8-byte aligned");
+  TS_REQUIRE(residual_stride >= N && out_stride >= N && residual_out_stride >= N &&
+                 residual_stride % kRowVec == 0 && out_stride % kRowVec == 0 &&
+                 residual_out_stride % kRowVec == 0 && aligned(residual, 16) && aligned(out, 16) &&
+                 aligned(residual_out, 16) && aligned(norm_weight, 16),
+             TS_ERR_INVALID_ARG, "w8a16_add_rmsnorm: norm rows must be 16-byte aligned");
+  int cus = 0;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (device_cu_count(stream, &cus) != TS_OK) return TS_ERR_DEVICE;
+  const GemmPlan p = plan_gemm_v(M, N, K, cus, variant, splits);
+  const size_t need = add_rmsnorm_workspace(p, M, N);
+  TS_REQUIRE(workspace && workspace_bytes >= need && aligned(workspace, 16), TS_ERR_WORKSPACE,
+             "w8a16_add_rmsnorm: workspace of %zu bytes needed, got %zu", need, workspace_bytes);
+  const GemmIo io{nullptr, 0, nullptr, 0, 0};
+  half_t* ytmp = static_cast<half_t*>(workspace);  // used only when K is not split
+  int used_splits = 1;
+  const int st = w8a16_launch(static_cast<const half_t*>(x), ldx, wq, scale, scale_is_fp16,
+                              static_cast<const half_t*>(bias), ytmp, N, M, N, K, workspace,
+                              workspace_bytes, s, io, variant, splits, &used_splits);
+  if (st != TS_OK) return st;
+  const half_t* rp = static_cast<const half_t*>(residual);
+  const half_t* wp = static_cast<const half_t*>(norm_weight);
+  half_t* op = static_cast<half_t*>(out);
+  half_t* rop = static_cast<half_t*>(residual_out);
+  if (used_splits > 1)
+    w8a16_reduce_rmsnorm_kernel<<<dim3((unsigned)M), kRowThreads, 0, s>>>(
+        static_cast<const float*>(workspace), used_splits, scale, scale_is_fp16,
+        static_cast<const half_t*>(bias), rp, residual_stride, wp, op, out_stride, rop,
+        residual_out_stride, M, N, eps);
+  else
+    rmsnorm_kernel<true><<<dim3((unsigned)M), kRowThreads, 0, s>>>(
+        ytmp, N, rp, residual_stride, wp, op, out_stride, rop, residual_out_stride, N, eps);
+  return check_launch("w8a16_add_rmsnorm");
 }
 
 extern "C" size_t ts_logits_int8_workspace_bytes(int32_t num_samples, int32_t vocab,

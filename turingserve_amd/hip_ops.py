@@ -416,6 +416,57 @@ def w8a16_glu(x: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor,
     return out
 
 
+def w8a16_add_rmsnorm(x: torch.Tensor, wq: torch.Tensor, scale: torch.Tensor,
+                      bias: torch.Tensor | None, residual: torch.Tensor, w: torch.Tensor,
+                      eps: float, cfg=None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(out, new_residual) = rmsnorm_residual(w8a16_linear(x, wq, scale, bias, cfg), residual,
+    w, eps), bit for bit, in two launches: the product, then the norm, which reduces the
+    product's split-K partials itself when the plan splits K (no reduction launch of its own)."""
+    x = x.contiguous()
+    M, K = x.shape
+    Nn, Kw = wq.shape
+    _require(Kw == K, f"w8a16_add_rmsnorm: x has K={K}, weight has K={Kw}")
+    _require(x.dtype == torch.float16, "w8a16_add_rmsnorm: activations must be fp16")
+    _require(wq.dtype == torch.int8 and wq.is_contiguous(),
+             "w8a16_add_rmsnorm: weight must be int8 row-major")
+    _require(scale.dtype in (torch.float32, torch.float16) and scale.numel() == Nn,
+             "w8a16_add_rmsnorm: scale must be fp32 or fp16 [N]")
+    residual = _rows(residual, "w8a16_add_rmsnorm")
+    _require(residual.shape == (M, Nn), "w8a16_add_rmsnorm: residual must be [M, N]")
+    w = w.contiguous()
+    _require(w.shape == (Nn,) and w.dtype == torch.float16, "w8a16_add_rmsnorm: norm weight must be fp16 [N]")
+    out = torch.empty(M, Nn, dtype=x.dtype, device=x.device)
+    res_out = torch.empty_like(out)
+    if M == 0:
+        return out, res_out
+    _check_gpu(x, wq, scale, residual, w)
+    sc = scale.contiguous()
+    b = None
+    if bias is not None:
+        _require(bias.numel() == Nn, "w8a16_add_rmsnorm: bias must be [N]")
+        b = bias.to(torch.float16).contiguous()
+    cus = N.cu_count(x.device.index or 0)
+    variant, splits = tuner.w8a16_choice(Nn, K, M) if cfg is None else (int(cfg[0]), int(cfg[1]))
+    ws_bytes = N.lib().ts_w8a16_add_rmsnorm_workspace_bytes(M, Nn, K, variant, splits, cus)
+    ws = _workspace(ws_bytes, x.device)
+    N.check(N.lib().ts_w8a16_add_rmsnorm(
+        _ptr(x), x.stride(0), _ptr(wq), _ptr(sc), 1 if sc.dtype == torch.float16 else 0, _ptr(b),
+        _ptr(residual), residual.stride(0), _ptr(w), _ptr(out), out.stride(0), _ptr(res_out),
+        res_out.stride(0), M, Nn, K, float(eps), variant, splits, _ptr(ws), ws_bytes,
+        _stream(x)), "w8a16_add_rmsnorm")
+    return out, res_out
+
+
+def linear_rmsnorm_residual(x: torch.Tensor, lw: LinearWeight, residual: torch.Tensor,
+                            w: torch.Tensor, eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """rmsnorm_residual(linear(x, lw), residual, w, eps) (model/qwen2.py:84-92, o_proj then
+    post_attention_layernorm, down_proj then the next norm): one fused call for int8 weights,
+    the two calls otherwise."""
+    if not lw.quantized:
+        return rmsnorm_residual(linear(x, lw), residual, w, eps)
+    return w8a16_add_rmsnorm(x, lw.w, lw.scale, lw.b, residual, w, eps)
+
+
 def gate_up_silu(x: torch.Tensor, lw: LinearWeight) -> torch.Tensor:
     """silu_mul(linear(x, gate_up)) (model/qwen2.py:36): one fused call for int8 weights, the
     two calls otherwise."""

@@ -38,6 +38,7 @@ def _hip() -> SimpleNamespace:
     ns.rope_ = h.rope_
     ns.silu_mul = h.silu_mul
     ns.gate_up_silu = h.gate_up_silu
+    ns.linear_rmsnorm_residual = h.linear_rmsnorm_residual
     ns.rope_kv_write_ = h.rope_kv_write_
     ns.decode_rope_kv_write_attention = h.decode_rope_kv_write_attention
     return ns

@@ -155,30 +155,32 @@ class Qwen2Model:
             self.ops.kv_write(k, v, k_cache, v_cache, slot_mapping)
         return q, k, v
 
-    def _mlp(self, x, lw):
+    def _mlp_act(self, x, lw):
+        """silu(gate) * up, the input of down_proj."""
         gate_up_silu = getattr(self.ops, "gate_up_silu", None)       # fused on the hip backend
-        act = (gate_up_silu(x, lw.gate_up_proj) if gate_up_silu is not None
-               else self.ops.silu_mul(self.ops.linear(x, lw.gate_up_proj)))
-        return self.ops.linear(act, lw.down_proj)
+        return (gate_up_silu(x, lw.gate_up_proj) if gate_up_silu is not None
+                else self.ops.silu_mul(self.ops.linear(x, lw.gate_up_proj)))
+
+    def _project_norm(self, x, proj, residual, norm_w):
+        """rmsnorm_residual(linear(x, proj), residual, norm_w): on a backend that has
+        linear_rmsnorm_residual the product's split-K reduction runs inside the norm launch
+        (same values as the two calls)."""
+        fused = getattr(self.ops, "linear_rmsnorm_residual", None)
+        if fused is not None:
+            return fused(x, proj, residual, norm_w, self.cfg.rms_norm_eps)
+        return self.ops.rmsnorm_residual(self.ops.linear(x, proj), residual, norm_w,
+                                         self.cfg.rms_norm_eps)
 
     def pure_decode(self, meta, num_tokens: int) -> bool:
         """True when every row of the step is a decode row (the fused decode launch applies)."""
         return meta.num_decode == num_tokens and meta.seq_lens.shape[0] == meta.num_decode
 
-    @torch.inference_mode()
-    def layer_forward(self, index: int, h, residual, positions, meta, kv_cache,
-                      fused_decode: bool = False):
-        """Decoder layer `index` (model/qwen2.py:84-92): (h, residual) in, (h, residual) out,
-        residual None before the first layer. The layer's new K/V rows go into kv_cache[index]
-        before its attention reads it. With fused_decode (a pure-decode step on a backend that
-        has decode_rope_kv_write_attention), RoPE, kv_write and attention run as one launch
-        (same outputs and caches as the three calls)."""
+    def _attention_block(self, index: int, x, residual, positions, meta, kv_cache,
+                         fused_decode: bool):
+        """Decoder layer `index` from its normed input x to the MLP activation: qkv, RoPE, the
+        K/V write into kv_cache[index], attention, o_proj with post_attention_layernorm, and
+        silu(gate) * up; returns (the input of down_proj, residual)."""
         c, ops, lw = self.cfg, self.ops, self.w.layers[index]
-        if residual is None:
-            residual = h
-            x = ops.rmsnorm(h, lw.input_norm, c.rms_norm_eps)
-        else:
-            x, residual = ops.rmsnorm_residual(h, residual, lw.input_norm, c.rms_norm_eps)
         k_cache, v_cache = kv_cache[index, 0], kv_cache[index, 1]
         qkv = ops.linear(x, lw.qkv_proj)
         a = None
@@ -189,18 +191,44 @@ class Qwen2Model:
         if a is None:                 # not fused, or a layout the fused launch does not take
             q, _, _ = self._rotate_write(qkv, positions, k_cache, v_cache, meta.slot_mapping)
             a = ops.paged_attention(q, k_cache, v_cache, meta, self.scale)
-        h = ops.linear(a, lw.o_proj)
-        x, residual = ops.rmsnorm_residual(h, residual, lw.post_attention_norm, c.rms_norm_eps)
-        return self._mlp(x, lw), residual
+        x, residual = self._project_norm(a, lw.o_proj, residual, lw.post_attention_norm)
+        return self._mlp_act(x, lw), residual
+
+    @torch.inference_mode()
+    def layer_forward(self, index: int, h, residual, positions, meta, kv_cache,
+                      fused_decode: bool = False):
+        """Decoder layer `index` (model/qwen2.py:84-92): (h, residual) in, (h, residual) out,
+        residual None before the first layer. The layer's new K/V rows go into kv_cache[index]
+        before its attention reads it. With fused_decode (a pure-decode step on a backend that
+        has decode_rope_kv_write_attention), RoPE, kv_write and attention run as one launch
+        (same outputs and caches as the three calls)."""
+        c, lw = self.cfg, self.w.layers[index]
+        if residual is None:
+            residual = h
+            x = self.ops.rmsnorm(h, lw.input_norm, c.rms_norm_eps)
+        else:
+            x, residual = self.ops.rmsnorm_residual(h, residual, lw.input_norm, c.rms_norm_eps)
+        act, residual = self._attention_block(index, x, residual, positions, meta, kv_cache,
+                                              fused_decode)
+        return self.ops.linear(act, lw.down_proj), residual
 
     @torch.inference_mode()
     def forward(self, input_ids, positions, meta, kv_cache):
-        """kv_cache [L, 2, num_blocks, KVH, 16, D] -> final normed hidden rows [T, hidden]."""
+        """kv_cache [L, 2, num_blocks, KVH, 16, D] -> final normed hidden rows [T, hidden].
+        The same chain as layer_forward over every layer and the final norm, with each layer's
+        down_proj taken together with the norm that consumes it (the next input_layernorm, or
+        the final norm): the same values, without a separate split-K reduction launch."""
+        c, layers = self.cfg, self.w.layers
         fused = self.pure_decode(meta, input_ids.shape[0])
-        h, residual = self.w.embed_tokens[input_ids], None
-        for index in range(len(self.w.layers)):
-            h, residual = self.layer_forward(index, h, residual, positions, meta, kv_cache, fused)
-        return self.ops.rmsnorm_residual(h, residual, self.w.final_norm, self.cfg.rms_norm_eps)[0]
+        h = self.w.embed_tokens[input_ids]
+        residual = h
+        x = self.ops.rmsnorm(h, layers[0].input_norm, c.rms_norm_eps)
+        for index in range(len(layers)):
+            act, residual = self._attention_block(index, x, residual, positions, meta, kv_cache,
+                                                  fused)
+            norm_w = layers[index + 1].input_norm if index + 1 < len(layers) else self.w.final_norm
+            x, residual = self._project_norm(act, layers[index].down_proj, residual, norm_w)
+        return x
 
     def compute_logits(self, hidden: torch.Tensor, sample_indices: torch.Tensor) -> torch.Tensor:
         """Logits of the sampling rows only, [S, V] fp32 (model/qwen2.py:94-99). With the int8
