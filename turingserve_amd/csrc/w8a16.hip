@@ -560,22 +560,29 @@ constexpr int kTileChunks = kTileBK / 8;          // 16-byte fp16 chunks per til
 // layouts, lane l = 32h + r: A holds A[row r][k 8h .. 8h+7], B holds B[k 8h .. 8h+7][col r], and
 // result element e is D[row 8(e / 4) + 4h + e % 4][col r].
 //
-// Each wavefront owns 32 WN weight rows that no other wavefront reads, so it loads them from
-// global memory straight into its A operands: lane (h, r) takes the 32 bytes
-// W[n + r][k + 32h .. + 31] of each 32-row subtile per K step, and the step's MFMA q uses bytes
-// 8q .. 8q+7 (the MFMA reduces over its K slots in any order as long as both operands use the
-// same one). Only the fp16 activation tile goes through LDS, and every wavefront reads all of it:
-// the B operand of MFMA q for lane (h, r) is chunk 4h + q of activation row r. The activations
-// travel by global_load_lds_dwordx4 (each lane's 16 bytes land at the next 16-byte slot of LDS,
-// so they need no registers); a lane picks the chunk its slot must hold under the row swizzle
-// (chunk kc of row r at slot kc ^ (r & 7), conflict-free for the operand reads, which touch
-// rows r .. r+7 at one chunk index each).
+// Each wavefront owns 32 WN weight rows: lane (h, r) of a 32-row subtile uses the 32 bytes
+// W[n + r][k + 32h .. + 31] of each K step, MFMA q bytes 8q .. 8q+7 (the MFMA reduces over its K
+// slots in any order as long as both operands use the same one). The B operand of MFMA q for
+// lane (h, r) is chunk 4h + q of activation row r, and every wavefront reads the whole
+// activation tile from LDS. Both tiles travel by global_load_lds_dwordx4 (each lane's 16 bytes
+// land at the next 16-byte slot of LDS, so they need no registers); a lane picks the piece its
+// slot must hold under the stage's swizzle:
+//   activations: chunk kc of row r at slot kc ^ (r & 7), so one DMA instruction reads 8 rows x
+//     128 bytes and the operand reads (rows r .. r+7 at one chunk index) are conflict-free;
+//   weights (WIDE): 16-byte piece c of row n at slot c ^ ((n >> 2) & 3) of the row's four, so one
+//     DMA instruction reads 16 rows x 64 bytes, and each 16-lane group of the ds_read_b128 that
+//     fetches a lane's pieces (rows r .. r+15 at one piece index) covers the 64 banks once.
+// Measured on MI355X: loads whose wavefront instruction reads 32 rows x 32 bytes (the pattern of
+// lanes loading their own A operands straight from the weight rows) stream at most ~2.9 TB/s
+// with every CU busy and ~1.8 TB/s on 140 CUs; 16 rows x 64 bytes by DMA reach ~5 TB/s and
+// ~3.7 TB/s. Without 16-byte alignment (K % 64 != 0, or an unaligned weight pointer) the weights
+// go straight to registers in 8-byte pieces instead, one register stage per LDS stage.
 //
-// Loads are issued one step ahead of a ring of PD + 1 LDS stages and weight register stages;
-// each step waits for the batch of the next step (PD - 1 younger batches may stay in flight)
-// and then takes one barrier. The wait and the barrier are written out instead of
-// __syncthreads(), whose release fence would wait for every LDS-bound load in flight; the
-// barrier carries a memory clobber so no load or LDS read moves across it.
+// Loads are issued one step ahead of a ring of PD + 1 stages; each step waits for the batch of
+// the next step (PD - 1 younger batches may stay in flight) and then takes one barrier. The wait
+// and the barrier are written out instead of __syncthreads(), whose release fence would wait for
+// every LDS-bound load in flight; the barrier carries a memory clobber so no load or LDS read
+// moves across it.
 //
 // K tail (only the last split can end inside a K step, and only if K % 64 != 0): weight columns
 // past the split end are zeroed at conversion; activation chunks past it are read at column
@@ -623,22 +630,32 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
   constexpr int BK = kTileBK, CH = kTileChunks;
   constexpr int BN = 128 * WN, BM = 32 * WM;
   constexpr int XPT = BM * CH / 256;              // activation DMAs per thread per step
-  constexpr int S = PD + 1;                       // LDS stages = weight register stages
-  constexpr int WLD = WIDE ? 2 : 4;               // weight loads per subtile per step
-  constexpr int BATCH = XPT + WN * WLD;           // vector memory loads per thread per step
+  constexpr int S = PD + 1;                       // stages (LDS, and weight registers if !WIDE)
+  constexpr int WP = BN * BK / 16;                // 16-byte weight pieces per step
+  constexpr int WDMA = WP / 256;                  // weight DMAs per thread per step (WIDE)
+  constexpr int BATCH = XPT + (WIDE ? WDMA : 4 * WN);   // vector memory loads per thread per step
   static_assert(XPT * 256 == BM * CH, "activation tile must split over 256 threads");
+  static_assert(WDMA * 256 == WP, "weight tile must split over 256 threads");
   static_assert(BN <= 256, "one scale per thread");
   static_assert(S >= 2 && S <= 8, "two to eight LDS stages");
+  static_assert(!(WIDE && TAIL), "weight DMA needs whole 16-byte pieces");
   // One array per stage: the compiler's wait insertion then sees that an LDS read of one stage
   // cannot alias a DMA in flight into another and does not wait for it (stage indices are
   // constants after unrolling, so stage() folds to one array).
   __shared__ half8_t s_x0[BM * CH], s_x1[BM * CH], s_x2[S > 2 ? BM * CH : 1], s_x3[S > 3 ? BM * CH : 1];
   __shared__ half8_t s_x4[S > 4 ? BM * CH : 1], s_x5[S > 5 ? BM * CH : 1];
   __shared__ half8_t s_x6[S > 6 ? BM * CH : 1], s_x7[S > 7 ? BM * CH : 1];
+  constexpr int WS = WIDE ? WP : 1;
+  __shared__ int4_t s_w0[WS], s_w1[WS], s_w2[S > 2 ? WS : 1], s_w3[S > 3 ? WS : 1];
+  __shared__ int4_t s_w4[S > 4 ? WS : 1], s_w5[S > 5 ? WS : 1], s_w6[S > 6 ? WS : 1], s_w7[S > 7 ? WS : 1];
   __shared__ float s_sc[BN], s_bs[BN];
   auto stage = [&](int st) -> half8_t* {
     return st == 0 ? s_x0 : st == 1 ? s_x1 : st == 2 ? s_x2 : st == 3 ? s_x3
          : st == 4 ? s_x4 : st == 5 ? s_x5 : st == 6 ? s_x6 : s_x7;
+  };
+  auto wstage = [&](int st) -> int4_t* {
+    return st == 0 ? s_w0 : st == 1 ? s_w1 : st == 2 ? s_w2 : st == 3 ? s_w3
+         : st == 4 ? s_w4 : st == 5 ? s_w5 : st == 6 ? s_w6 : s_w7;
   };
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -659,6 +676,8 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
     return n < N ? n : N - 1;
   };
   static_assert(WN == 1, "GLU mode pairs wavefronts 0, 1 with 2, 3 (32 rows each)");
+  // Weight piece c (16 bytes) of tile row nl sits at slot 4 nl + (c ^ ((nl >> 2) & 3)) of a stage.
+  auto wslot = [](int nl, int c) { return 4 * nl + (c ^ ((nl >> 2) & 3)); };
   const int kb = blockIdx.z * k_per_split;
   const int ke = (kb + k_per_split < K) ? kb + k_per_split : K;
   const int nk = (ke - kb + BK - 1) / BK;
@@ -670,9 +689,19 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
     s_sc[tid] = part ? 1.f : load_scale(scale, scale_is_fp16, nc);
     s_bs[tid] = (part || !bias) ? 0.f : (float)bias[nc];
   }
-  const int8_t* wrow[WN];
+  const int8_t* wrow[WIDE ? WDMA : WN];
+  if constexpr (WIDE) {
+    // DMA j of thread t fills slot 256 j + t: tile row (256 j + t) / 4, which holds piece
+    // (t % 4) ^ ((row >> 2) & 3) there.
 #pragma unroll
-  for (int i = 0; i < WN; ++i) wrow[i] = wq + (int64_t)weight_row(w * 32 * WN + 32 * i + r) * K + 32 * h;
+    for (int j = 0; j < WDMA; ++j) {
+      const int nl = (256 * j + tid) / 4;
+      wrow[j] = wq + (int64_t)weight_row(nl) * K + 16 * ((tid % 4) ^ ((nl >> 2) & 3));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < WN; ++i) wrow[i] = wq + (int64_t)weight_row(w * 32 * WN + 32 * i + r) * K + 32 * h;
+  }
   // DMA i of thread t fills slot 256 i + t of a stage: row (256 i + t) / 8, position t % 8,
   // which holds chunk (t % 8) ^ (row & 7) = (t % 8) ^ ((t / 8) & 7) for every i.
   const int kcx = (tid % CH) ^ ((tid / CH) & 7);
@@ -694,13 +723,11 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
                                        (__attribute__((address_space(3))) void*)(stage(st) + 256 * i + 64 * w),
                                        16, 0, 0);
     if constexpr (WIDE) {
-      const int k0 = !TAIL || k + 32 * h < ke ? k : K - 16 - 32 * h;
-      const int k1 = !TAIL || k + 32 * h + 16 < ke ? k + 16 : K - 16 - 32 * h;
 #pragma unroll
-      for (int i = 0; i < WN; ++i) {
-        wr[i][0] = ld<int4_t>(wrow[i] + k0);
-        wr[i][1] = ld<int4_t>(wrow[i] + k1);
-      }
+      for (int j = 0; j < WDMA; ++j)
+        __builtin_amdgcn_global_load_lds((const void*)(wrow[j] + k),
+                                         (__attribute__((address_space(3))) void*)(wstage(st) + 256 * j + 64 * w),
+                                         16, 0, 0);
     } else {
       int kp[4];
 #pragma unroll
@@ -745,6 +772,16 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
       }
     }
   };
+  // WIDE: lane (h, r)'s weight pieces 2h, 2h + 1 of each subtile row of a stage.
+  auto read_a = [&](int st, int4_t (&wr)[WN][2]) {
+    const int4_t* sw = wstage(st);
+#pragma unroll
+    for (int i = 0; i < WN; ++i) {
+      const int nl = 32 * (w * WN + i) + r;
+      wr[i][0] = sw[wslot(nl, 2 * h)];
+      wr[i][1] = sw[wslot(nl, 2 * h + 1)];
+    }
+  };
   auto mma = [&](const half8_t (&a)[2][WN], const half8_t (&b)[2][WM]) {
 #pragma unroll
     for (int q = 0; q < 2; ++q)
@@ -755,37 +792,42 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[q][i], b[q][j], acc[i][j], 0, 0, 0);
   };
 
-  int4_t wreg[S][WN][2];
+  // Weight operands: WIDE reads step t's pieces from its LDS stage into `araw` (just after the
+  // barrier that publishes it); otherwise they wait in register stage t % S.
+  int4_t wreg[WIDE ? 1 : S][WN][2];
+  int4_t araw[WN][2];
+  auto wsrc = [&](int u) -> int4_t (&)[WN][2] {
+    if constexpr (WIDE) return araw; else return wreg[u];
+  };
   half8_t b0[2][WM], b1[2][WM];
-  // Step t lives in LDS stage and weight registers t % S, constants of the loops unrolled by S.
-  // The prologue issues steps 0 .. S-1 and waits for step 0; each main-loop iteration computes
-  // step kt and then issues step kt + S into the stage and registers it has just released. The
-  // main loop holds only whole groups of S steps and no branch, so the compiler's wait
-  // accounting stays exact across its back edge (the prologue leaves the same loads in flight as
-  // a group does); the last nk % S steps follow it, after waiting for everything.
+  // Step t lives in stage t % S, constants of the loops unrolled by S. The prologue issues steps
+  // 0 .. S-1 and waits for step 0; each main-loop iteration computes step kt and then issues step
+  // kt + S into the stage it has just released. The main loop holds only whole groups of S steps
+  // and no branch, so the compiler's wait accounting stays exact across its back edge (the
+  // prologue leaves the same loads in flight as a group does); the last nk % S steps follow it,
+  // after waiting for everything.
   //
   // Each step is split into two halves (MFMAs q = 0, 1 and q = 2, 3) so that LDS reads overlap
   // MFMAs instead of following the barrier in lock step on all four wavefronts: the second
   // half's B operands are read while the first half multiplies, and the next step's first-half
-  // B operands while the second half multiplies. The barrier between the halves publishes step
-  // kt + 1's activations (its batch has landed on every wavefront) and guarantees that every
-  // wavefront has finished its reads of step kt's LDS stage (the wait before it includes this
-  // wavefront's LDS reads; both halves' A operands are widened before it), so step kt + S's
-  // batch is issued right after it into that stage and those registers.
+  // B operands (and weight pieces) while the second half multiplies. The barrier between the
+  // halves publishes step kt + 1's tiles (its batch has landed on every wavefront) and guarantees
+  // that every wavefront has finished its reads of step kt's stage (the wait before it includes
+  // this wavefront's LDS reads; both halves' A operands are widened before it), so step kt + S's
+  // batch is issued right after it into that stage.
   //
   // The explicit waits count vector-memory operations, which retire in issue order on one
   // counter whatever their kind. Each batch issues its activation DMAs before its weight loads:
-  // the compiler may sink the prologue's last weight loads (registers only the main loop reads)
-  // below the first wait, and with this order that only removes operations the wait's count
-  // already allows to be outstanding, never ones between the awaited DMAs and the wait. (A
-  // weights-first order, tried for a deeper weight-only register ring, broke exactly there; the
-  // deeper ring gains nothing anyway, since the in-order counter makes every wait for step
-  // kt + 1's activations also wait for all weights issued before them.)
+  // without WIDE the compiler may sink the prologue's last weight loads (registers only the main
+  // loop reads) below the first wait, and with this order that only removes operations the
+  // wait's count already allows to be outstanding, never ones between the awaited DMAs and the
+  // wait.
 #pragma unroll
-  for (int u = 0; u < S; ++u) issue(u, u, wreg[u]);
+  for (int u = 0; u < S; ++u) issue(u, u, wsrc(u));
   wait_vmem_below_lds_done<PD * BATCH>();
   workgroup_barrier();
   read_b(0, 0, b0);
+  if constexpr (WIDE) read_a(0, araw);
   int kt0 = 0;
   for (; kt0 + S <= nk; kt0 += S) {
 #pragma unroll
@@ -793,17 +835,18 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
       const int kt = kt0 + u;
       half8_t a0[2][WN], a1[2][WN];
       read_b(u, 2, b1);
-      convert(wreg[u], kt, 0, a0);
-      convert(wreg[u], kt, 2, a1);
+      convert(wsrc(u), kt, 0, a0);
+      convert(wsrc(u), kt, 2, a1);
       mma(a0, b0);
       interleave_mfma_valu<2 * WN * WM, 40 * WN, 2 * WM>();
       __builtin_amdgcn_sched_barrier(0);
       wait_vmem_below_lds_done<(PD - 1) * BATCH>();   // step kt + 1's batch has landed
       workgroup_barrier();
-      issue(kt + S, u, wreg[u]);                      // step kt's stage and registers
+      issue(kt + S, u, wsrc(u));                      // step kt's stage (and registers)
       read_b((u + 1) % S, 0, b0);                     // past the last step: never used
+      if constexpr (WIDE) read_a((u + 1) % S, araw);
       mma(a1, b1);
-      interleave_mfma_valu<2 * WN * WM, 0, 2 * WM>();
+      interleave_mfma_valu<2 * WN * WM, 0, 2 * WM + (WIDE ? 2 * WN : 0)>();
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -811,15 +854,16 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
   for (int u = 0; u < S - 1; ++u) {
     const int kt = kt0 + u;
     if (kt < nk) {
-      half8_t a[2][WN];
+      half8_t a0[2][WN], a1[2][WN];
       read_b(u, 2, b1);
-      convert(wreg[u], kt, 0, a);
-      mma(a, b0);
+      convert(wsrc(u), kt, 0, a0);
+      convert(wsrc(u), kt, 2, a1);
+      mma(a0, b0);
       wait_vmem_below_lds_done<0>();
       workgroup_barrier();
       read_b((u + 1) % S, 0, b0);
-      convert(wreg[u], kt, 2, a);
-      mma(a, b1);
+      if constexpr (WIDE) read_a((u + 1) % S, araw);
+      mma(a1, b1);
     }
   }
   // No DMA may still be writing this workgroup's LDS when it exits.
@@ -926,7 +970,11 @@ static bool use_small_path(int M, int N, int K) {
   if (M <= 8) return true;
   return M <= kSmallMMax && (int64_t)M * N <= 65536 && K <= 2048;
 }
-constexpr int kWidePrefetch = 3;                  // K steps of loads in flight (wide kernel)
+// K steps of loads in flight (wide kernel). With weights in LDS as well, 128-column tiles take
+// one step fewer so that two workgroups (3 x 24 KB of stages each) stay resident per CU; measured
+// at M = 2048 on the gate_up product: 165 us at 2 steps, 186 us at 3 (one workgroup per CU).
+constexpr int kWidePrefetch = 3;
+constexpr int wide_prefetch(bool dma, int wm) { return dma && wm == 4 ? 2 : kWidePrefetch; }
 
 struct GemmPlan {
   bool small;
@@ -1171,13 +1219,13 @@ static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const v
     float* part = p.splits > 1 ? static_cast<float*>(workspace) : nullptr;
     const int tiles_n = glu ? (io.glu + p.bn / 2 - 1) / (p.bn / 2) : (N + p.bn - 1) / p.bn;
     const dim3 grid(tiles_n, (M + p.bm - 1) / p.bm, p.splits);
-    const bool fast = K % kTileBK == 0 && aligned(wq, 16);   // 16-byte weight loads, no K tail
+    const bool fast = K % kTileBK == 0 && aligned(wq, 16);   // weight DMA, no K tail
 #define TS_WIDE_LAUNCH(WNV, WMV)                                                                   \
   if (fast)                                                                                        \
-    w8a16_wide_kernel<WNV, WMV, kWidePrefetch, true, false><<<grid, 256, 0, s>>>(                   \
+    w8a16_wide_kernel<WNV, WMV, wide_prefetch(true, WMV), true, false><<<grid, 256, 0, s>>>(       \
         xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part, io);         \
   else                                                                                             \
-    w8a16_wide_kernel<WNV, WMV, kWidePrefetch, false, true><<<grid, 256, 0, s>>>(                   \
+    w8a16_wide_kernel<WNV, WMV, wide_prefetch(false, WMV), false, true><<<grid, 256, 0, s>>>(      \
         xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part, io)
     if (p.bm == 128) {
       TS_WIDE_LAUNCH(1, 4);
