@@ -567,8 +567,10 @@ constexpr int kTileChunks = kTileBK / 8;          // 16-byte fp16 chunks per til
 // activation tile from LDS. Both tiles travel by global_load_lds_dwordx4 (each lane's 16 bytes
 // land at the next 16-byte slot of LDS, so they need no registers); a lane picks the piece its
 // slot must hold under the stage's swizzle:
-//   activations: chunk kc of row r at slot kc ^ (r & 7), so one DMA instruction reads 8 rows x
-//     128 bytes and the operand reads (rows r .. r+7 at one chunk index) are conflict-free;
+//   activations: chunk kc of row r at slot kc ^ ((r >> 1) & 7), so one DMA instruction reads 8
+//     rows x 128 bytes and each 16-lane group of an operand read (rows r .. r+15 at one chunk
+//     index) covers the 64 banks once (an XOR with r & 7 left pairs of lanes on one bank:
+//     measured 1-9 % slower);
 //   weights (WIDE): 16-byte piece c of row n at slot c ^ ((n >> 2) & 3) of the row's four, so one
 //     DMA instruction reads 16 rows x 64 bytes, and each 16-lane group of the ds_read_b128 that
 //     fetches a lane's pieces (rows r .. r+15 at one piece index) covers the 64 banks once.
@@ -703,8 +705,8 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
     for (int i = 0; i < WN; ++i) wrow[i] = wq + (int64_t)weight_row(w * 32 * WN + 32 * i + r) * K + 32 * h;
   }
   // DMA i of thread t fills slot 256 i + t of a stage: row (256 i + t) / 8, position t % 8,
-  // which holds chunk (t % 8) ^ (row & 7) = (t % 8) ^ ((t / 8) & 7) for every i.
-  const int kcx = (tid % CH) ^ ((tid / CH) & 7);
+  // which holds chunk (t % 8) ^ ((row >> 1) & 7) = (t % 8) ^ ((t / 16) & 7) for every i.
+  const int kcx = (tid % CH) ^ ((tid / 16) & 7);
   const half_t* xrow[XPT];
 #pragma unroll
   for (int i = 0; i < XPT; ++i) {
@@ -756,7 +758,7 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
 #pragma unroll
     for (int q = 0; q < 2; ++q)
 #pragma unroll
-      for (int j = 0; j < WM; ++j) b[q][j] = sx[(32 * j + r) * CH + ((4 * h + q0 + q) ^ (r & 7))];
+      for (int j = 0; j < WM; ++j) b[q][j] = sx[(32 * j + r) * CH + ((4 * h + q0 + q) ^ ((r >> 1) & 7))];
   };
   // A operands of MFMAs q0 and q0 + 1 of step kt (K tail columns zeroed).
   auto convert = [&](const int4_t (&wr)[WN][2], int kt, int q0, half8_t (&a)[2][WN]) {
