@@ -1,11 +1,12 @@
-"""The LDS-tiled prefill path (head_dim 128) against the oracle (needs an MI355X).
+"""The LDS-tiled prefill paths (head_dim 128) against the oracle (needs an MI355X).
 
-128-row query tiles share each staged 64-key step; long key ranges are split over several
-workgroups whose fp32 partials a merge kernel combines (ts_prefill_attention_ws). Both forms
-are checked against the oracle (ops/reference.py:60-77, 94-111) with the attention criterion of
-the other kernel tests, on shapes that put the diagonal, the key tail and the split boundaries in
-every position of a step; a NaN-filled workspace and NaN cache rows past seq_len must not reach
-the output.
+128-row query tiles share each staged 64-key step: the paired kernel (two units per workgroup,
+stream-K key-range slots) or, when its slots would get few key steps, the 4-wavefront tile
+kernel with its own split plan; split partials are combined by a merge kernel
+(ts_prefill_attention_ws). Every form is checked against the oracle (ops/reference.py:60-77,
+94-111) with the attention criterion of the other kernel tests, on shapes that put the diagonal,
+the key tail and the split boundaries in every position of a step; a NaN-filled workspace and
+NaN cache rows past seq_len must not reach the output.
 """
 
 from __future__ import annotations
@@ -60,8 +61,12 @@ def ws_bytes_for(meta, P):
 @pytest.mark.parametrize("q_lens,prefixes", [
     ([1], [0]), ([63], [1]), ([128], [0]), ([129], [63]), ([200], [64]), ([512], [1037]),
     ([700], [3000]), ([2048], [0]), ([17], [4000]), ([5, 300, 128], [0, 900, 2500]),
+    ([1024], [6000]), ([640, 512], [5000, 7000]),
 ])
 def test_tiled_prefill_split_and_unsplit(q_lens, prefixes):
+    """Without a workspace the paired kernel runs unsplit; with one, short key ranges per launch
+    slot take the tile kernel's split plan and long ones (the last two cases) the paired
+    kernel's stream-K plan."""
     (q, kc, vc, qsl, sl, bt), meta, ref = setup(q_lens, prefixes)
     out1 = run_prefill(q, kc, vc, qsl, sl, bt, meta, None)
     assert_attn(out1, ref, "unsplit")
@@ -73,7 +78,8 @@ def test_tiled_prefill_split_and_unsplit(q_lens, prefixes):
 
 def test_tiled_prefill_splits_when_it_should():
     """A short chunk on a long prefix gets a split plan (the case the split path is for), and a
-    workspace one byte short runs unsplit with the same result quality."""
+    workspace one byte short of the queried size (a smaller plan, or none) gives the same
+    result quality."""
     (q, kc, vc, qsl, sl, bt), meta, ref = setup([512], [1037], seed=3)
     nb = ws_bytes_for(meta, 1)
     assert nb > 0
@@ -124,44 +130,59 @@ def test_tiled_prefill_chunked_prompt_through_paged_attention():
         assert_attn(out, ref, f"chunk {ci} (prefix {prefix}, {n} rows)")
 
 
-@pytest.mark.parametrize("D,n_decode,mql", [(64, 0, 300), (128, 0, 300), (128, 0, 128),
-                                            (128, 4, 300)])
-def test_understated_bounds_give_nan_rows_not_stale_memory(D, n_decode, mql):
+@pytest.mark.parametrize("D,n_decode,mql,q_len,prefix", [
+    (64, 0, 300, 600, 600), (128, 0, 300, 600, 600), (128, 0, 128, 600, 600),
+    (128, 4, 300, 600, 600), (128, 0, 640, 1280, 8000)])
+def test_understated_bounds_give_nan_rows_not_stale_memory(D, n_decode, mql, q_len, prefix):
     """max_query_len below a chunk's real q_len (a caller bug): the rows the plan does not cover
     come out as NaN, the covered rows are still right.
 
-    * head_dim 128, prefill only: the stream-K plan shares the sequence's real steps over its
-      launch slots, so every tile is computed; a tile whose segments run past the workspace the
-      host bounds sized gets NaN rows. Tiles are numbered longest first, so those are the lowest
-      tiles: the NaN rows are a tile-aligned prefix.
-    * head_dim 128 with decode rows (one-launch ragged kernel): tiles the launch misses (the
-      lowest, launched longest first) are NaN.
+    * head_dim 128, prefill only, few key steps per paired launch slot: the 4-wavefront tile
+      kernel; tiles the launch misses (the lowest, launched longest first) are NaN.
+    * head_dim 128, prefill only, many steps per slot: the paired kernel's stream-K plan shares
+      the sequence's real steps over its launch slots, so every tile is computed; a tile whose
+      segments run past the workspace the host bounds sized gets NaN rows. Tiles are numbered
+      longest first, so those are the lowest tiles: the NaN rows are a tile-aligned prefix.
+    * head_dim 128 with decode rows (one-launch ragged kernel): as the tile kernel.
     * head_dim < 128: the kernel covers rows from 0 up."""
     from turingserve_amd.metadata import AttentionMetadata
 
     Hh, KV = 12, 2
-    seq = [300 + 97 * i for i in range(n_decode)] + [1200]
-    ql = [1] * n_decode + [600]
+    seq_len = prefix + q_len
+    seq = [300 + 97 * i for i in range(n_decode)] + [seq_len]
+    ql = [1] * n_decode + [q_len]
     q, kc, vc, qsl, sl, bt = make_paged(seq, Hh, KV, D, ql, seed=9)
     ref = oracle_attn(q, kc, vc, qsl, sl, bt, D ** -0.5)
     dq, dkc, dvc, dqsl, dsl, dbt = (x.to(DEV) for x in (q, kc, vc, qsl, sl, bt))
-    T = n_decode + 600
+    T = n_decode + q_len
     meta = AttentionMetadata(dqsl, dsl, dbt, torch.zeros(T, dtype=torch.int64, device=DEV),
-                             n_decode, mql, 1200)              # max_query_len understated
+                             n_decode, mql, seq_len)           # max_query_len understated
     out = K.paged_attention(dq, dkc, dvc, meta, D ** -0.5)
     torch.cuda.synchronize()
     o = out.float().cpu()[n_decode:]
     nan_rows = torch.isnan(o).all(dim=1)
-    rows_i = torch.arange(600)
-    if D == 128 and n_decode == 0:
-        covered = rows_i >= 128 * _stream_k_nan_tiles(mql, 600, 1200, Hh, N.cu_count(0))
+    rows_i = torch.arange(q_len)
+    tiles = -(-q_len // 128)
+    cus = N.cu_count(0)
+    paired = D == 128 and n_decode == 0 and _paired_route(mql, seq_len, Hh, cus)
+    assert paired == (prefix == 8000), "the cases cover each route once"
+    if paired:
+        covered = rows_i >= 128 * _stream_k_nan_tiles(mql, q_len, seq_len, Hh, cus)
     elif D == 128:
-        covered = rows_i >= 256                                # tiles 2..4 of 5 (longest first)
+        covered = rows_i >= 128 * (tiles - (-(-mql // 128)))   # the longest cdiv(mql, 128) tiles
     else:
-        covered = rows_i < 320                                 # 10 tiles of 32 rows
+        covered = rows_i < 32 * (-(-mql // 32))                 # tiles of 32 rows from row 0
     assert bool(nan_rows[~covered].all()) and not bool(torch.isnan(o[covered]).any())
     rows = torch.cat([torch.ones(n_decode, dtype=torch.bool), covered])
     assert_attn(out[rows.to(DEV)], ref[rows.numpy()], f"covered rows, D {D}")
+
+
+def _paired_route(mql: int, msl: int, H: int, cus: int) -> bool:
+    """Whether a prefill-only head_dim 128 launch (even GQA group) takes the paired kernel: its
+    stream-K plan gives each of the cus // (H / 2) slots of a sequence at least 16 of the
+    cdiv(mql, 128) * cdiv(msl, 64) key steps the host bounds allow."""
+    slots = cus // (H // 2)
+    return -(-mql // 128) * -(-max(msl, mql) // 64) >= 16 * slots
 
 
 def _stream_k_nan_tiles(mql: int, q_len: int, seq_len: int, H: int, cus: int) -> int:

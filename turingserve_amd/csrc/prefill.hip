@@ -7,8 +7,27 @@ using namespace ts;
 
 namespace {
 
-// Shared body of the prefill entry points. With `workspace` the tiled path may split long key
-// ranges (tile_plan); a workspace smaller than the plan needs runs it unsplit.
+// head_dim 128 runs one of two kernels. The paired kernel (two 128-row units per 512-thread
+// workgroup, one workgroup per CU, stream-K key-range slots) wins when each launch slot has many
+// key steps; with few steps per slot its per-segment prologue, partials and merge dominate and
+// the 4-wavefront tile kernel (two workgroups per CU, split plan sized for one resident round)
+// is faster. Measured on MI355X (H 12, KVH 2; us per call, tile / paired, and the host-bound
+// steps per paired slot): 512 rows on a 1037 prefix 28.0 / 34.0 (2.4), 2048 on 0 39.6 / 43.3
+// (12.2), 1024 on 0 21.8 / 28.9 (3.0), 2048 on 2048 67.8 / 65.7 (24.4), 2048 on 4096 99.6 / 89.7
+// (36.6), 1856 on 6144 125.5 / 106.2 (44.6).
+constexpr int kPairMinSlotSteps = 16;
+
+bool pair_pays(const PairPlan& pl, int num_heads, int num_kv_heads, int max_query_len,
+               int max_seq_len) {
+  if (pl.seg_cap == 0) return true;                // no split: the paired kernel as is
+  const int tr = pair_heads(num_heads, num_kv_heads) ? kTileRows : 2 * kTileRows;
+  const int seq = max_seq_len > max_query_len ? max_seq_len : max_query_len;
+  const int64_t bound = (int64_t)cdiv(max_query_len, tr) * cdiv(seq, kTileKeys);
+  return bound >= (int64_t)kPairMinSlotSteps * pl.slots;
+}
+
+// Shared body of the prefill entry points. With `workspace` the head_dim 128 kernels may split
+// long key ranges; a workspace smaller than the plan needs runs the paired kernel unsplit.
 int prefill_launch(const void* q, int64_t q_stride_t, int64_t q_stride_h, void* out,
                    int64_t out_stride_t, int64_t num_tokens, const void* k_cache,
                    const void* v_cache, int64_t num_blocks, const int32_t* block_tables,
@@ -44,6 +63,28 @@ int prefill_launch(const void* q, int64_t q_stride_t, int64_t q_stride_h, void* 
     if (workspace != nullptr && device_cu_count(stream, &cus) != TS_OK) return TS_ERR_DEVICE;
     PairPlan pl = pair_plan(P, num_heads, num_kv_heads, max_query_len, max_seq_len, cus,
                             workspace != nullptr);
+    if (!pair_pays(pl, num_heads, num_kv_heads, max_query_len, max_seq_len)) {
+      TilePlan tp = tile_plan(P, num_heads, head_dim, max_query_len, max_seq_len, cus, true);
+      if (tp.ws_bytes <= workspace_bytes && (tp.ws_bytes == 0 || aligned(workspace, 16))) {
+        if (tp.ws_bytes == 0) tp.smax = 1 << 30;     // unsplit: no tile leaves partials
+        const int per_kvh = tp.slots * P * (num_heads / num_kv_heads);
+        const int n_launch = 8 % num_kv_heads == 0 ? 8 * cdiv(per_kvh, 8 / num_kv_heads)
+                                                    : per_kvh * num_kv_heads;
+        prefill_tile_kernel<128><<<n_launch, kTileThreads, 0, s>>>(
+            static_cast<const half_t*>(q), q_stride_t, q_stride_h, static_cast<half_t*>(out),
+            out_stride_t, num_tokens, static_cast<const half_t*>(k_cache),
+            static_cast<const half_t*>(v_cache), num_blocks, block_tables, bt_stride,
+            max_blocks_per_seq, seq_lens, query_start_loc, num_decode, num_heads, num_kv_heads,
+            sl2, tp.smax, tp.slots, P, static_cast<float*>(workspace));
+        if (tp.ws_bytes > 0)
+          prefill_merge_kernel<128><<<dim3(4 * cdiv(max_query_len, kTileRows), P, num_heads),
+                                      kTileThreads, 0, s>>>(
+              static_cast<const float*>(workspace), static_cast<half_t*>(out), out_stride_t,
+              num_tokens, max_blocks_per_seq, seq_lens, query_start_loc, num_decode, num_heads,
+              tp.smax, tp.slots);
+        return check_launch("prefill_attention");
+      }
+    }
     if (pl.ws_bytes > workspace_bytes || (pl.ws_bytes > 0 && !aligned(workspace, 16)))
       pl = pair_plan(P, num_heads, num_kv_heads, max_query_len, max_seq_len, cus, false);
     const bool heads = pair_heads(num_heads, num_kv_heads);
@@ -88,13 +129,16 @@ extern "C" size_t ts_prefill_workspace_bytes(int32_t num_prefill, int32_t num_he
                                              int32_t head_dim, int32_t max_query_len,
                                              int32_t max_seq_len, int32_t cu_count) {
   if (num_prefill <= 0 || num_heads <= 0 || head_dim != 128 || max_query_len <= 0) return 0;
-  // The plan depends on whether the GQA group size is even (not an argument here): enough for
-  // either form.
+  // The paired plan depends on whether the GQA group size is even (not an argument here), and
+  // short splits take the tile plan instead: enough for every form.
   const size_t a = pair_plan(num_prefill, num_heads, 1, max_query_len, max_seq_len, cu_count,
                              true).ws_bytes;
   const size_t b = pair_plan(num_prefill, num_heads, num_heads, max_query_len, max_seq_len,
                              cu_count, true).ws_bytes;
-  return a > b ? a : b;
+  const size_t c = tile_plan(num_prefill, num_heads, head_dim, max_query_len, max_seq_len,
+                             cu_count, true).ws_bytes;
+  const size_t ab = a > b ? a : b;
+  return ab > c ? ab : c;
 }
 
 extern "C" int ts_prefill_attention(const void* q, int64_t q_stride_t, int64_t q_stride_h,

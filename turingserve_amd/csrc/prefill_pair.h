@@ -196,11 +196,13 @@ __device__ __forceinline__ void prefill_pair_body(
   // Cache offset of this wavefront's block at step st (past the range: the range's last step,
   // past the tile's keys: its last block; those keys are masked or zeroed). The block ids come
   // from a window of 64 steps held one per lane and read with v_readlane, so the staging never
-  // waits on a scalar load (whose wait would also drain the wavefront's LDS writes).
+  // waits on a scalar load (whose wait would also drain the wavefront's LDS writes). Callers ask
+  // for non-decreasing steps, so the window moves forward once per 64 steps; a step outside it
+  // (either side) reloads it.
   int bwin = 0, win = -kWave;
   auto block_at = [&](int st) -> int64_t {
     st = st < hi1 ? st : hi1;
-    if (st - win >= kWave) {
+    if (st < win || st - win >= kWave) {
       win = st;
       int sl = win + lane;
       sl = sl < hi1 ? sl : hi1;
@@ -365,7 +367,8 @@ __device__ __forceinline__ void prefill_pair_body(
     // to LDS, then load K(lo + j + 2) and V(lo + j + 1).
     auto staging = [&](int j, int4_t (&kr)[2], uint32_t (&vr)[8]) {
       const int st = lo + j;
-      const int64_t bk = block_at(st + 2), bv = block_at(st + 1);
+      const int64_t bv = block_at(st + 1);         // steps in increasing order (see block_at)
+      const int64_t bk = block_at(st + 2);
       store_v(j & 1, st, vr);
       store_k((j + 1) & 1, kr);                    // at j = n - 1 a copy of K(hi - 1), unused
       load_k(bk, kr);
