@@ -8,9 +8,12 @@ contexts log-uniform in [128, 4096], 16384 cache blocks, fp16. One *step* is one
 kv_write of the 64 new K/V rows, then decode attention over every cached token (by default in
 one launch, ts_decode_attention_kv_write; --separate-kv-write times the two launches, and the
 other form is reported beside the headline either way). Steps rotate over
-8 layer caches (2 GiB in total, far above the 256 MB Infinity Cache) so each step reads its KV
-from HBM, and every step is a hipGraph replay (pure-decode steps are graph-captured, as the
-reference's CudaGraphRunner does). Inputs are resident in HBM before timing starts.
+28 layer caches, one per decoder layer of Qwen2.5-1.5B (7.2 GiB in total, far above the 256 MB
+Infinity Cache), so each step reads its KV from HBM, and every step is a hipGraph replay
+(pure-decode steps are graph-captured, as the reference's CudaGraphRunner does): one replay is the
+attention of one model step, and the decode split map (ts_decode_split_map) is built once at its
+start and read by its 28 layer steps, as a model step does. Inputs are resident in HBM before
+timing starts.
 
 value = algorithmic bytes of one step / wall time of one step, in GB/s; exactly --steps steps are
 timed (whole replays of the layer graph plus one graph of the remaining layers). The roofline
@@ -45,12 +48,17 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=400)
     ap.add_argument("--warmup", type=int, default=40)
-    ap.add_argument("--layers", type=int, default=8, help="layer caches rotated over")
+    ap.add_argument("--layers", type=int, default=28,
+                    help="layer caches rotated over (28: the decoder layers of Qwen2.5-1.5B, so "
+                         "one graph replay is the attention of one model step)")
     ap.add_argument("--partition", type=int, default=0, help="v3 split size (0 = library policy)")
     ap.add_argument("--decode-version", default="auto", choices=["auto", "v1", "v2", "v3"])
     ap.add_argument("--separate-kv-write", action="store_true",
                     help="time the decode step as kv_write + attention launches instead of the "
                          "fused ts_decode_attention_kv_write")
+    ap.add_argument("--no-split-map", action="store_true",
+                    help="fused decode steps without the per-step split map (each workgroup "
+                         "scans seq_lens itself)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-extra", action="store_true", help="headline workload only")
     ap.add_argument("--no-cpu", action="store_true")
@@ -128,28 +136,43 @@ def bench_decode(args, torch, K, synth):
         outs[l] = K.paged_attention(q, kv[l, 0], kv[l, 1], meta, scale, decode_version=version,
                                     partition=args.partition or K.DEFAULT_PARTITION)
 
+    part = args.partition or K.DEFAULT_PARTITION
+    smap = [None]
+
+    def build_map():                        # once per model step, shared by its layers
+        if not args.no_split_map:
+            smap[0] = K.decode_split_map(meta, H, KVH, D, NB, dev, decode_version=version,
+                                         partition=part)
+
     def fused_step(l):                      # kv_write fused into the attention launch
         outs[l] = K.decode_kv_write_attention(q, k, v, kv[l, 0], kv[l, 1], meta, scale,
-                                              decode_version=version,
-                                              partition=args.partition or K.DEFAULT_PARTITION)
+                                              decode_version=version, partition=part,
+                                              split_map=smap[0])
 
     def two_call_step(l):
         kv_step(l)
         attn_step(l)
 
+    def steps(n, fn):                       # n layers' steps of one model step
+        if fn is fused_step:
+            build_map()
+        for l in range(n):
+            fn(l)
+
     step_fn = two_call_step if args.separate_kv_write else fused_step
+    build_map()
     for l in range(L):                      # eager warm-up (library, workspace, allocator)
         two_call_step(l)
         fused_step(l)
     torch.cuda.synchronize()
     # One replay = L steps (every layer's kv_write + attention), the way a model's layer stack
-    # sits in one graph; a second graph holds the L attention calls alone for the kernel timing
-    # and a third the other form of the step (two launches or one) for comparison.
+    # sits in one graph, with the fused form's split map built once at its start (a model step
+    # builds it once for all its layers); a second graph holds the L attention calls alone for
+    # the kernel timing and a third the other form of the step (two launches or one).
     pool = torch.cuda.graph_pool_handle()
     g_step = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_step, pool=pool):
-        for l in range(L):
-            step_fn(l)
+        steps(L, step_fn)
     step_outs = list(outs)
     g_attn = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_attn, pool=pool):
@@ -157,8 +180,7 @@ def bench_decode(args, torch, K, synth):
             attn_step(l)
     g_other = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_other, pool=pool):
-        for l in range(L):
-            (fused_step if args.separate_kv_write else two_call_step)(l)
+        steps(L, fused_step if args.separate_kv_write else two_call_step)
     # the remainder of --steps that is not a whole replay of L layers: one more graph of the
     # first steps % L layers, so exactly --steps steps are timed
     tail = args.steps % L
@@ -166,8 +188,7 @@ def bench_decode(args, torch, K, synth):
     if tail:
         g_tail = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g_tail, pool=pool):
-            for l in range(tail):
-                step_fn(l)
+            steps(tail, step_fn)
     torch.cuda.synchronize()
     for _ in range(max(1, args.warmup // L)):
         g_step.replay()
@@ -213,7 +234,7 @@ def bench_decode(args, torch, K, synth):
         "step_s": step_s, "steps": steps_timed, "bytes": b, "step_ev_ms": step_ev_ms,
         "attn_ms_mean": statistics.fmean(attn_ms), "attn_ms_median": statistics.median(attn_ms),
         "graph_equals_eager": same, "mean_ctx": float(st.seq_lens.float().mean()),
-        "fused": not args.separate_kv_write,
+        "fused": not args.separate_kv_write, "split_map": not args.no_split_map,
         ("step_two_launch_ms" if not args.separate_kv_write else "step_fused_ms"): other_ms,
     }
     del kv, g_step, g_attn, g_other, g_tail
@@ -317,7 +338,7 @@ def time_graph(torch, fn, reps: int, inner: int = 1):
     return s.elapsed_time(e) / (reps * inner)
 
 
-def bench_calibration(torch, synth, layers: int = 8) -> dict:
+def bench_calibration(torch, synth, layers: int = 28) -> dict:
     """Measured ceilings beside the spec peaks (8 TB/s HBM, 2.5 PFLOP/s dense fp16 MFMA):
     * copy: a 1 GiB device-to-device copy (bytes read + written per second);
     * gather floor: ts_probe_gather over config 2's chunk list -- every cached (block, KV head) K
@@ -681,7 +702,7 @@ def main() -> int:
     if args.only in ("prefill", "w8a16", "logits", "metadata", "mixed", "decode_model",
                      "calibration"):
         fn = {"decode_model": lambda: bench_decode_model(torch, synth),
-              "calibration": lambda: bench_calibration(torch, synth),
+              "calibration": lambda: bench_calibration(torch, synth, args.layers),
               "prefill": lambda: bench_prefill(torch, K, synth),
               "w8a16": lambda: bench_w8a16(torch, K, synth),
               "logits": lambda: bench_logits(torch, K),
@@ -700,7 +721,8 @@ def main() -> int:
     # merge) priced with the step's bytes, or with the two-launch step the attention call alone.
     if r["fused"]:
         kern = ("decode attention with kv_write fused (decode_mfma_kernel<128, 4, write> + "
-                "decode_merge_kernel)")
+                "decode_merge_kernel" + (f", decode_split_map_kernel once per {args.layers} steps)"
+                                         if r["split_map"] else ")"))
         kern_ms, kern_bytes = r["step_ev_ms"], b["step"]
     else:
         kern = "decode attention (paged_attention, decode rows)"
@@ -726,6 +748,8 @@ def main() -> int:
                    "max_context": st.max_seq_len, "num_blocks": st.k_cache.shape[0],
                    "layers_rotated": args.layers, "hipgraph": True,
                    "kv_write": "fused into the attention launch" if r["fused"] else "own launch",
+                   "split_map": (f"built once per replay of {args.layers} layer steps, inside "
+                                 f"the timed region" if r["fused"] and r["split_map"] else None),
                    other_key.replace("_ms", "_us"): round(r[other_key] * 1e3, 3),
                    "bytes_per_step": b["step"], "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": kern,
@@ -761,7 +785,7 @@ def main() -> int:
                              "runs": n_or}}
     if not args.no_extra:
         log("calibration: copy, gather floor, MFMA loop")
-        cal = bench_calibration(torch, synth)
+        cal = bench_calibration(torch, synth, args.layers)
         out["roofline"]["measured"] = {
             "copy_GBps": cal["copy_GBps"], "gather_floor_GBps": cal["gather_floor"]["GBps"],
             "frac_of_gather_floor": round(achieved / cal["gather_floor"]["GBps"], 4),

@@ -103,6 +103,12 @@ int ts_kv_write(const void* k, const void* v,
  * and no split slot is idle (max_seq_len then only feeds TS_DECODE_AUTO's choice).
  * max_seq_len: a host-side upper bound of seq_lens (inside graphs: max_model_len).
  * Workspace: ts_decode_workspace_bytes() bytes, 256-byte aligned (0 bytes for v1 / v2).
+ * split_map / split_map_bytes: NULL / 0, or a map that ts_decode_split_map built from the same
+ * seq_lens, block tables and plan arguments (version, num_seqs, heads, head_dim, max_seq_len,
+ * partition, max_blocks_per_seq): the v3 split kernel then reads its split and its first block
+ * ids from the map instead of scanning seq_lens. The results are identical either way; a map
+ * built for another plan is ignored (the kernel scans), one smaller than the plan needs is an
+ * error. The map must be rebuilt whenever seq_lens or the block tables change.
  * Replaces ops/triton_ops.py:35-57 and ops/triton_decode_attention.py:169-200.
  */
 size_t ts_decode_workspace_bytes(int32_t version, int32_t num_seqs, int32_t num_heads,
@@ -116,7 +122,31 @@ int ts_decode_attention(int32_t version,
                         const int32_t* seq_lens, int32_t num_seqs,
                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim,
                         float scale, int32_t max_seq_len, int32_t partition,
-                        void* workspace, size_t workspace_bytes, void* stream);
+                        void* workspace, size_t workspace_bytes, void* stream,
+                        const void* split_map, size_t split_map_bytes);
+
+/*
+ * The per-step split map of the v3 decode schedule: for every launch slot of the plan the
+ * sequence, split and block range it covers and the first block ids its wavefronts load. Built
+ * once per step (one small launch) and passed to every layer's decode call of that step, it
+ * replaces the per-workgroup seq_lens scan and block-table load that otherwise precede a split's
+ * first K/V request. No counterpart in the reference (its split kernel needs no lookup: the
+ * fixed grid of ops/triton_decode_attention.py:187-200 maps program ids to splits directly);
+ * it belongs with the step metadata (runner/input_builder.py). ts_decode_split_map_bytes():
+ * bytes for the plan, 0 when the plan does not split (v1 / v2) or for more than 4096 sequences
+ * (then no map is built and the decode calls take NULL). The arguments mean what they mean for
+ * ts_decode_attention. Stream-ordered: the decode calls that read the map follow it on the
+ * same stream.
+ */
+size_t ts_decode_split_map_bytes(int32_t version, int32_t num_seqs, int32_t num_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t max_seq_len,
+                                 int32_t partition, int32_t cu_count);
+int ts_decode_split_map(int32_t version, const int32_t* block_tables, int64_t bt_stride,
+                        int32_t max_blocks_per_seq, int64_t num_blocks,
+                        const int32_t* seq_lens, int32_t num_seqs, int32_t num_heads,
+                        int32_t num_kv_heads, int32_t head_dim, int32_t max_seq_len,
+                        int32_t partition, void* split_map, size_t split_map_bytes,
+                        void* stream);
 
 /*
  * ts_kv_write of the step's new rows followed by ts_decode_attention, as one launch: the
@@ -130,8 +160,8 @@ int ts_decode_attention(int32_t version,
  * write could not be ordered against other workgroups' reads of that block): use ts_kv_write
  * and ts_decode_attention for such rows.
  * The write is fused for v2 / v3 with at most 16 query heads per KV head and 16-byte aligned
- * rows; otherwise it runs as ts_kv_write's own launch before the attention. Same workspace as
- * ts_decode_attention (ts_decode_workspace_bytes()).
+ * rows; otherwise it runs as ts_kv_write's own launch before the attention. Same workspace and
+ * split map as ts_decode_attention (ts_decode_workspace_bytes(), ts_decode_split_map()).
  */
 int ts_decode_attention_kv_write(int32_t version,
                                  const void* q, int64_t q_stride_t, int64_t q_stride_h,
@@ -145,7 +175,7 @@ int ts_decode_attention_kv_write(int32_t version,
                                  int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
                                  int32_t head_dim, float scale, int32_t max_seq_len,
                                  int32_t partition, void* workspace, size_t workspace_bytes,
-                                 void* stream);
+                                 void* stream, const void* split_map, size_t split_map_bytes);
 
 /*
  * ts_decode_attention_kv_write without a workspace argument: the split-K scratch is a static
@@ -181,8 +211,9 @@ int ts_decode_attention_kv_write_noalloc(int32_t version,
  * v rows land in slot_mapping[i] and the attention sees them. The output and the caches are
  * bit-identical to the two calls; qkv itself is left unrotated when the launch is fused (the
  * rotated q and k exist only in registers and the cache) and rotated in place otherwise.
- * Preconditions and workspace as ts_decode_attention_kv_write; fused for v2 / v3 with at most 16
- * query heads per KV head and head_dim a multiple of 64, else ts_rope_kv_write runs first.
+ * Preconditions, workspace and split map as ts_decode_attention_kv_write; fused for v2 / v3 with
+ * at most 16 query heads per KV head and head_dim a multiple of 64, else ts_rope_kv_write runs
+ * first.
  */
 int ts_decode_rope_kv_write_attention(int32_t version, void* qkv, int64_t qkv_stride,
                                       const int64_t* positions, const float* cos_table,
@@ -195,7 +226,8 @@ int ts_decode_rope_kv_write_attention(int32_t version, void* qkv, int64_t qkv_st
                                       int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
                                       int32_t head_dim, float scale, int32_t max_seq_len,
                                       int32_t partition, void* workspace, size_t workspace_bytes,
-                                      void* stream);
+                                      void* stream, const void* split_map,
+                                      size_t split_map_bytes);
 
 /*
  * Chunked-prefill attention for sequences num_decode .. num_seqs-1 of the flat batch.

@@ -170,7 +170,7 @@ def test_decode_v3_merge_ignores_stale_workspace():
             3, q_d.data_ptr(), q_d.stride(0), q_d.stride(1), out.data_ptr(), out.stride(0),
             kc_d.data_ptr(), vc_d.data_ptr(), kc.shape[0], bt_d.data_ptr(), bt_d.stride(0),
             bt.shape[1], sl_d.data_ptr(), n, H, KVH, D, D ** -0.5, 4096, partition,
-            ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream), "decode")
+            ws.data_ptr(), ws_bytes, torch.cuda.current_stream().cuda_stream, None, 0), "decode")
         assert_attn(out, oracle_attn(q, kc, vc, qsl, sl, bt, D ** -0.5), f"stale ws {partition}")
         assert (out[4] == 0).all()
 

@@ -41,11 +41,11 @@ def test_invalid_arguments_return_status_and_message():
     st = lib.ts_kv_write(None, None, 0, 0, 0, 0, None, None, 1, None, 4, 2, 64, None)
     assert st == N.TS_ERR_INVALID_ARG and "null pointer" in N.last_error()
     st = lib.ts_decode_attention(9, None, 0, 0, None, 0, None, None, 1, None, 1, 1, None, 1, 2, 1,
-                                 64, 1.0, 16, 0, None, 0, None)
+                                 64, 1.0, 16, 0, None, 0, None, None, 0)
     assert st == N.TS_ERR_INVALID_ARG and "unknown version" in N.last_error()
     p = ctypes.c_void_p(256)            # never dereferenced: the call fails validation first
     st = lib.ts_decode_attention(2, p, 96, 96, p, 96, p, p, 4, p, 1, 1, p, 1, 2, 1, 96, 1.0,
-                                 16, 0, None, 0, None)
+                                 16, 0, None, 0, None, None, 0)
     assert st == N.TS_ERR_UNSUPPORTED and "head_dim 96" in N.last_error()
     st = lib.ts_w8a16_gemm(p, 12, p, p, 0, None, p, 8, 3, 8, 12, None, 0, None)
     assert st == N.TS_ERR_UNSUPPORTED and "multiple of 8" in N.last_error()
@@ -145,7 +145,7 @@ def test_zero_size_calls_are_no_ops():
     lib = N.lib()
     assert lib.ts_kv_write(None, None, 0, 0, 0, 0, None, None, 0, None, 0, 2, 64, None) == N.TS_OK
     assert lib.ts_decode_attention(0, None, 0, 0, None, 0, None, None, 0, None, 0, 0, None, 0, 12,
-                                   2, 128, 1.0, 0, 0, None, 0, None) == N.TS_OK
+                                   2, 128, 1.0, 0, 0, None, 0, None, None, 0) == N.TS_OK
     assert lib.ts_w8a16_gemm(None, 0, None, None, 0, None, None, 0, 0, 16, 16, None, 0,
                              None) == N.TS_OK
 
@@ -189,6 +189,29 @@ def test_workspace_sizes():
     assert lib.ts_w8a16_workspace_bytes_v(1, 2048, 1536, 1, 0, 256) == 6 * 2048 * 4
     ws = lib.ts_w8a16_workspace_bytes_v(1, 1536, 8960, 1, 0, 256)
     assert ws > 0 and ws % (1536 * 4) == 0
+
+
+def test_split_map_sizes_and_checks():
+    lib = N.lib()
+    # one header of 8 ints and 32 ints per launch slot of the v3 plan: the balanced schedule on
+    # 256 CUs launches 2 x 256 / 2 - 64 = 192 extra slots plus one per sequence, the fixed grid
+    # 16 slots per sequence at 4096 / 256
+    assert lib.ts_decode_split_map_bytes(3, 64, 12, 2, 128, 4096, 0, 256) == (8 + 256 * 32) * 4
+    assert lib.ts_decode_split_map_bytes(3, 64, 12, 2, 128, 4096, 256, 256) == (8 + 64 * 16 * 32) * 4
+    assert lib.ts_decode_split_map_bytes(0, 64, 12, 2, 128, 1024, 0, 256) == (8 + 256 * 32) * 4
+    # no split, no map: v1 / v2, AUTO resolving to v2, more than 4096 sequences
+    assert lib.ts_decode_split_map_bytes(2, 64, 12, 2, 128, 4096, 0, 256) == 0
+    assert lib.ts_decode_split_map_bytes(1, 64, 12, 2, 128, 4096, 0, 256) == 0
+    assert lib.ts_decode_split_map_bytes(0, 256, 12, 2, 128, 4096, 0, 256) == 0
+    assert lib.ts_decode_split_map_bytes(3, 4097, 12, 2, 128, 4096, 256, 256) == 0
+    assert lib.ts_decode_split_map(3, None, 1, 1, 1, None, 0, 12, 2, 128, 4096, 0, None, 0,
+                                   None) == N.TS_OK                     # empty batch
+    st = lib.ts_decode_split_map(3, None, 1, 1, 1, None, 4097, 12, 2, 128, 4096, 0, None, 0, None)
+    assert st == N.TS_ERR_UNSUPPORTED and "4096" in N.last_error()
+    st = lib.ts_decode_split_map(7, None, 1, 1, 1, None, 4, 12, 2, 128, 4096, 0, None, 0, None)
+    assert st == N.TS_ERR_INVALID_ARG and "unknown version" in N.last_error()
+    st = lib.ts_decode_split_map(3, None, 1, 1, 1, None, 4, 12, 2, 128, 4096, 0, None, 0, None)
+    assert st == N.TS_ERR_INVALID_ARG and "null pointer" in N.last_error()
 
 
 def test_python_wrappers_reject_cpu_tensors():

@@ -47,7 +47,7 @@ def _call(st, noalloc, version=0, partition=0):
         nb = lib.ts_decode_workspace_bytes(version, S, H, KVH, D, int(m.max_seq_len), partition,
                                            N.cu_count(0))
         ws = torch.full((max(nb, 256) // 4,), float("nan"), dtype=torch.float32, device=DEV)
-        status = lib.ts_decode_attention_kv_write(*head, ws.data_ptr(), nb, stream)
+        status = lib.ts_decode_attention_kv_write(*head, ws.data_ptr(), nb, stream, None, 0)
     torch.cuda.synchronize()
     return status, out, kc, vc
 

@@ -16,14 +16,63 @@ extern "C" size_t ts_decode_workspace_bytes(int32_t version, int32_t num_seqs, i
   return ws_layout(p, num_seqs, num_heads, head_dim).total;
 }
 
-// Shared by the two entry points; nr.k set: kv_write fused into the attention launch.
+extern "C" size_t ts_decode_split_map_bytes(int32_t version, int32_t num_seqs, int32_t num_heads,
+                                            int32_t num_kv_heads, int32_t head_dim,
+                                            int32_t max_seq_len, int32_t partition,
+                                            int32_t cu_count) {
+  if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads) return 0;
+  if (num_seqs > kMapMaxSeqs) return 0;
+  const SplitPlan p = plan_decode(version, num_seqs, num_heads, num_kv_heads, head_dim,
+                                  max_seq_len, partition, cu_count > 0 ? cu_count : 256);
+  return map_bytes_of(p);
+}
+
+extern "C" int ts_decode_split_map(int32_t version, const int32_t* block_tables, int64_t bt_stride,
+                                   int32_t max_blocks_per_seq, int64_t num_blocks,
+                                   const int32_t* seq_lens, int32_t num_seqs, int32_t num_heads,
+                                   int32_t num_kv_heads, int32_t head_dim, int32_t max_seq_len,
+                                   int32_t partition, void* split_map, size_t split_map_bytes,
+                                   void* stream) {
+  ts::clear_error();
+  TS_REQUIRE(version >= TS_DECODE_AUTO && version <= TS_DECODE_V3, TS_ERR_INVALID_ARG,
+             "decode_split_map: unknown version %d", version);
+  TS_REQUIRE(num_seqs >= 0 && num_seqs <= kMapMaxSeqs, TS_ERR_UNSUPPORTED,
+             "decode_split_map: %d sequences (the map builder handles 0 .. %d; launch without a map)",
+             num_seqs, kMapMaxSeqs);
+  if (num_seqs == 0) return TS_OK;
+  TS_REQUIRE(num_heads > 0 && num_kv_heads > 0 && num_heads % num_kv_heads == 0,
+             TS_ERR_INVALID_ARG, "decode_split_map: num_heads=%d not a multiple of num_kv_heads=%d",
+             num_heads, num_kv_heads);
+  TS_REQUIRE(block_tables && seq_lens, TS_ERR_INVALID_ARG, "decode_split_map: null pointer argument");
+  TS_REQUIRE(num_blocks > 0 && max_blocks_per_seq > 0 && bt_stride >= max_blocks_per_seq,
+             TS_ERR_INVALID_ARG, "decode_split_map: bad block table (num_blocks=%lld width=%d stride=%lld)",
+             (long long)num_blocks, max_blocks_per_seq, (long long)bt_stride);
+  TS_REQUIRE(partition >= 0 && partition % kBlockSize == 0, TS_ERR_INVALID_ARG,
+             "decode_split_map: partition %d is not a multiple of 16", partition);
+  int cus = 0;
+  int st = device_cu_count(stream, &cus);
+  if (st != TS_OK) return st;
+  const SplitPlan p = plan_decode(version, num_seqs, num_heads, num_kv_heads, head_dim,
+                                  max_seq_len, partition, cus);
+  const size_t need = map_bytes_of(p);
+  if (need == 0) return TS_OK;                 // this plan does not split: no map
+  TS_REQUIRE(split_map && split_map_bytes >= need && aligned(split_map, 16), TS_ERR_WORKSPACE,
+             "decode_split_map: map of %zu bytes (16-byte aligned) needed, got %zu", need,
+             split_map_bytes);
+  launch_split_map(p, reinterpret_cast<hipStream_t>(stream), seq_lens, block_tables, bt_stride,
+                   num_blocks, max_blocks_per_seq, num_seqs, static_cast<int*>(split_map));
+  return check_launch("decode_split_map");
+}
+
+// Shared by the entry points; nr.k set: kv_write fused into the attention launch.
 static int decode_entry(int32_t version, const void* q, int64_t q_stride_t, int64_t q_stride_h,
                         void* out, int64_t out_stride_t, const void* k_cache, const void* v_cache,
                         int64_t num_blocks, const int32_t* block_tables, int64_t bt_stride,
                         int32_t max_blocks_per_seq, const int32_t* seq_lens, int32_t num_seqs,
                         int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale,
                         int32_t max_seq_len, int32_t partition, void* workspace,
-                        size_t workspace_bytes, void* stream, const NewRows& nr) {
+                        size_t workspace_bytes, void* stream, const NewRows& nr,
+                        const void* split_map, size_t split_map_bytes) {
   TS_REQUIRE(version >= TS_DECODE_AUTO && version <= TS_DECODE_V3, TS_ERR_INVALID_ARG,
              "decode_attention: unknown version %d", version);
   TS_REQUIRE(num_seqs >= 0, TS_ERR_INVALID_ARG, "decode_attention: num_seqs %d < 0", num_seqs);
@@ -53,6 +102,12 @@ static int decode_entry(int32_t version, const void* q, int64_t q_stride_t, int6
   TS_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 256)),
              TS_ERR_WORKSPACE, "decode_attention: workspace of %zu bytes (256-aligned) needed, got %zu",
              need, workspace_bytes);
+  const size_t map_need = split_map ? map_bytes_of(p) : 0;
+  TS_REQUIRE(map_need == 0 || (split_map_bytes >= map_need && aligned(split_map, 16)),
+             TS_ERR_INVALID_ARG,
+             "decode_attention: split map of %zu bytes (16-byte aligned) needed for this plan, got %zu",
+             map_need, split_map_bytes);
+  const int* smap = map_need ? static_cast<const int*>(split_map) : nullptr;
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (nr.k) {
     // The fused write needs the MFMA kernels with one head group per KV head (so the workgroup
@@ -79,7 +134,8 @@ static int decode_entry(int32_t version, const void* q, int64_t q_stride_t, int6
       return decode_entry(version, q, q_stride_t, q_stride_h, out, out_stride_t, k_cache, v_cache,
                           num_blocks, block_tables, bt_stride, max_blocks_per_seq, seq_lens,
                           num_seqs, num_heads, num_kv_heads, head_dim, scale, max_seq_len,
-                          partition, workspace, workspace_bytes, stream, NewRows{});
+                          partition, workspace, workspace_bytes, stream, NewRows{}, split_map,
+                          split_map_bytes);
     }
   }
   const float sl2 = scale * kLog2e;
@@ -91,7 +147,7 @@ static int decode_entry(int32_t version, const void* q, int64_t q_stride_t, int6
   case DD:                                                                                      \
     launch_decode<DD>(p, s, qp, q_stride_t, q_stride_h, op, out_stride_t, kp, vp, num_blocks,  \
                       block_tables, bt_stride, max_blocks_per_seq, seq_lens, num_seqs, num_heads, \
-                      num_kv_heads, sl2, workspace, nr);                                        \
+                      num_kv_heads, sl2, workspace, nr, smap);                                  \
     break;
   switch (head_dim) {
     TS_DECODE_CASE(16)
@@ -112,12 +168,12 @@ extern "C" int ts_decode_attention(int32_t version, const void* q, int64_t q_str
                                    int32_t num_seqs, int32_t num_heads, int32_t num_kv_heads,
                                    int32_t head_dim, float scale, int32_t max_seq_len,
                                    int32_t partition, void* workspace, size_t workspace_bytes,
-                                   void* stream) {
+                                   void* stream, const void* split_map, size_t split_map_bytes) {
   ts::clear_error();
   return decode_entry(version, q, q_stride_t, q_stride_h, out, out_stride_t, k_cache, v_cache,
                       num_blocks, block_tables, bt_stride, max_blocks_per_seq, seq_lens, num_seqs,
                       num_heads, num_kv_heads, head_dim, scale, max_seq_len, partition, workspace,
-                      workspace_bytes, stream, NewRows{});
+                      workspace_bytes, stream, NewRows{}, split_map, split_map_bytes);
 }
 
 extern "C" int ts_decode_attention_kv_write(
@@ -127,7 +183,8 @@ extern "C" int ts_decode_attention_kv_write(
     void* k_cache, void* v_cache, int64_t num_blocks, const int32_t* block_tables,
     int64_t bt_stride, int32_t max_blocks_per_seq, const int32_t* seq_lens, int32_t num_seqs,
     int32_t num_heads, int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seq_len,
-    int32_t partition, void* workspace, size_t workspace_bytes, void* stream) {
+    int32_t partition, void* workspace, size_t workspace_bytes, void* stream,
+    const void* split_map, size_t split_map_bytes) {
   ts::clear_error();
   TS_REQUIRE(num_seqs >= 0, TS_ERR_INVALID_ARG, "decode_attention_kv_write: num_seqs %d < 0",
              num_seqs);
@@ -142,7 +199,7 @@ extern "C" int ts_decode_attention_kv_write(
   return decode_entry(version, q, q_stride_t, q_stride_h, out, out_stride_t, k_cache, v_cache,
                       num_blocks, block_tables, bt_stride, max_blocks_per_seq, seq_lens, num_seqs,
                       num_heads, num_kv_heads, head_dim, scale, max_seq_len, partition, workspace,
-                      workspace_bytes, stream, nr);
+                      workspace_bytes, stream, nr, split_map, split_map_bytes);
 }
 
 // ---------------------------------------------------------------------------------------------
@@ -212,7 +269,8 @@ extern "C" int ts_decode_attention_kv_write_noalloc(
                                       out_stride_t, k_cache, v_cache, num_blocks, block_tables,
                                       bt_stride, max_blocks_per_seq, seq_lens, num_seqs, num_heads,
                                       num_kv_heads, head_dim, scale, max_seq_len, partition, ws,
-                                      need > 0 ? (size_t)TS_NOALLOC_SCRATCH_BYTES : 0, stream);
+                                      need > 0 ? (size_t)TS_NOALLOC_SCRATCH_BYTES : 0, stream,
+                                      nullptr, 0);
 }
 
 extern "C" int ts_decode_rope_kv_write_attention(
@@ -222,7 +280,8 @@ extern "C" int ts_decode_rope_kv_write_attention(
     const int64_t* slot_mapping, const int32_t* block_tables, int64_t bt_stride,
     int32_t max_blocks_per_seq, const int32_t* seq_lens, int32_t num_seqs, int32_t num_heads,
     int32_t num_kv_heads, int32_t head_dim, float scale, int32_t max_seq_len, int32_t partition,
-    void* workspace, size_t workspace_bytes, void* stream) {
+    void* workspace, size_t workspace_bytes, void* stream, const void* split_map,
+    size_t split_map_bytes) {
   ts::clear_error();
   TS_REQUIRE(num_seqs >= 0, TS_ERR_INVALID_ARG,
              "decode_rope_kv_write_attention: num_seqs %d < 0", num_seqs);
@@ -246,5 +305,5 @@ extern "C" int ts_decode_rope_kv_write_attention(
   return decode_entry(version, qkv, qkv_stride, head_dim, out, out_stride_t, k_cache, v_cache,
                       num_blocks, block_tables, bt_stride, max_blocks_per_seq, seq_lens, num_seqs,
                       num_heads, num_kv_heads, head_dim, scale, max_seq_len, partition, workspace,
-                      workspace_bytes, stream, nr);
+                      workspace_bytes, stream, nr, split_map, split_map_bytes);
 }

@@ -147,6 +147,20 @@ __device__ __forceinline__ int round_part(int blocks) {
   return (blocks + kMinPartBlocks - 1) / kMinPartBlocks * kMinPartBlocks;
 }
 
+// P of the balanced schedule for a batch of total_blocks blocks.
+__device__ __forceinline__ int balanced_part(int total_blocks, int nx) {
+  const int P = round_part((total_blocks + nx - 1) / nx);
+  return P > kMinPartBlocks ? P : kMinPartBlocks;
+}
+
+// P_s of a sequence of nb blocks: P itself, or (balanced) the multiple of kMinPartBlocks that
+// keeps its split count within max_splits.
+__device__ __forceinline__ int seq_part(bool balanced, int P, int nb, int max_splits) {
+  if (!balanced) return P;
+  const int q = round_part((nb + max_splits - 1) / max_splits);
+  return q > P ? q : P;
+}
+
 // Called by every thread of an NT-thread workgroup (S >= 1): finds the sequence that owns
 // launch slot `slot`. s_map holds NT / 64 + 5 ints of LDS.
 template <int NT>
@@ -169,15 +183,9 @@ __device__ SplitSlot split_lookup(const int* __restrict__ seq_lens, int S, int c
     int total = 0;
 #pragma unroll
     for (int k = 0; k < NWV; ++k) total += s_map[k];
-    P = round_part((total + nx - 1) / nx);
-    P = P > kMinPartBlocks ? P : kMinPartBlocks;
+    P = balanced_part(total, nx);
     __syncthreads();
   }
-  auto part_of = [&](int nb) {
-    if (!balanced) return P;
-    const int q = round_part((nb + max_splits - 1) / max_splits);
-    return q > P ? q : P;
-  };
   if (tid == 0) {
     s_map[NWV] = -1;
     s_map[NWV + 1] = 0;
@@ -190,7 +198,7 @@ __device__ SplitSlot split_lookup(const int* __restrict__ seq_lens, int S, int c
     const int i = c0 + tid;
     const int len = c0 == 0 ? len0 : (i < S ? clamp_len(seq_lens[i]) : 0);
     const int nb = (len + kBlockSize - 1) / kBlockSize;
-    const int ps = part_of(nb);
+    const int ps = seq_part(balanced, P, nb, max_splits);
     const int n = (nb + ps - 1) / ps;
     const int incl = wave_inclusive_sum(n, lane);
     if (lane == kWave - 1) s_map[w] = incl;
@@ -216,6 +224,131 @@ __device__ SplitSlot split_lookup(const int* __restrict__ seq_lens, int S, int c
   return {__builtin_amdgcn_readfirstlane(s_map[NWV]), __builtin_amdgcn_readfirstlane(s_map[NWV + 1]),
           __builtin_amdgcn_readfirstlane(s_map[NWV + 2]), __builtin_amdgcn_readfirstlane(s_map[NWV + 4]),
           __builtin_amdgcn_readfirstlane(s_map[NWV + 3])};
+}
+
+// Per-step split map: the result of split_lookup for every launch slot, plus the block ids its
+// wavefronts request first, built once per step by decode_split_map_kernel and read by every
+// layer's v3 launch in place of split_lookup (the layers of a step share seq_lens, the block
+// tables and the plan). A workgroup then issues its first K/V requests one scalar load after it
+// starts instead of after a seq_lens load, a block-wide scan and a block-table load. Layout
+// (int32): a header of kMapHeader ints {kMapMagic, S, slots, part_blocks, nx, max_splits,
+// cap_blocks, 0} naming the plan it was built for (a launch whose plan differs ignores the map
+// and runs split_lookup), then kMapEntry ints per slot: {seq (-1: past the last split), C_s,
+// n_s, clamped seq_len, first block, end block, block id of the sequence's last token, P_s}
+// and the block ids of pairs 0 .. kMapPairs - 1 of the split as blk_id gives them to the
+// wavefronts' first loads (a pair past the range repeats the id its wavefront falls back to).
+constexpr int kMapMagic = 0x314d5354;
+constexpr int kMapHeader = 8;
+constexpr int kMapEntry = 32;
+constexpr int kMapPairs = 8;                 // two pairs per wavefront of a 4-wavefront launch
+constexpr int kMapMaxSeqs = 4096;            // sequences per step the builder handles
+constexpr int kMapThreads = 1024;
+
+__device__ __forceinline__ int4 int4_of(int a, int b, int c, int d) { return int4{a, b, c, d}; }
+
+template <int NT>
+__global__ void __launch_bounds__(NT) decode_split_map_kernel(
+    const int* __restrict__ seq_lens, const int* __restrict__ bt, int64_t bt_st, int64_t NB,
+    int S, int cap_blocks, int part_blocks, int nx, int max_splits, int nslots,
+    int* __restrict__ map) {
+  constexpr int NWV = NT / kWave;
+  __shared__ int s_first[kMapMaxSeqs];
+  __shared__ int s_len[kMapMaxSeqs];
+  __shared__ int s_part[kMapMaxSeqs];
+  __shared__ int s_red[NWV];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
+  const int cap = cap_blocks * kBlockSize;
+  const bool balanced = part_blocks <= 0;
+  int tb = 0;
+  for (int i = tid; i < S; i += NT) {
+    int len = seq_lens[i];
+    len = len < 0 ? 0 : (len > cap ? cap : len);
+    s_len[i] = len;
+    tb += (len + kBlockSize - 1) / kBlockSize;
+  }
+  int P = part_blocks;
+  if (balanced) {
+    tb = wave_sum(tb);
+    if (lane == 0) s_red[w] = tb;
+    __syncthreads();
+    int total = 0;
+#pragma unroll
+    for (int k = 0; k < NWV; ++k) total += s_red[k];
+    P = balanced_part(total, nx);
+  }
+  __syncthreads();                             // s_len complete, s_red free
+  int base = 0;
+  for (int c0 = 0; c0 < S; c0 += NT) {         // exclusive prefix of the split counts
+    const int i = c0 + tid;
+    int n = 0;
+    if (i < S) {
+      const int nb = (s_len[i] + kBlockSize - 1) / kBlockSize;
+      const int ps = seq_part(balanced, P, nb, max_splits);
+      s_part[i] = ps;
+      n = (nb + ps - 1) / ps;
+    }
+    const int incl = wave_inclusive_sum(n, lane);
+    if (lane == kWave - 1) s_red[w] = incl;
+    __syncthreads();
+    int off = base, tot = 0;
+#pragma unroll
+    for (int k = 0; k < NWV; ++k) {
+      const int v = s_red[k];
+      off += k < w ? v : 0;
+      tot += v;
+    }
+    if (i < S) s_first[i] = off + incl - n;
+    base += tot;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    int4* h = reinterpret_cast<int4*>(map);
+    h[0] = int4_of(kMapMagic, S, nslots, part_blocks);
+    h[1] = int4_of(nx, max_splits, cap_blocks, 0);
+  }
+  constexpr int NWF = kMapPairs / 2;           // wavefronts of the consuming launch
+  for (int slot = tid; slot < nslots; slot += NT) {
+    int lo = 0, hi = S - 1;                    // last sequence whose first split is <= slot
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_first[mid] <= slot) lo = mid;
+      else hi = mid - 1;
+    }
+    const int i = lo, len = s_len[i], ps = s_part[i];
+    const int nb = (len + kBlockSize - 1) / kBlockSize;
+    const int n = (nb + ps - 1) / ps;
+    int4* dst = reinterpret_cast<int4*>(map + kMapHeader + (int64_t)slot * kMapEntry);
+    const int j = slot - s_first[i];
+    if (j >= n) {                              // past the batch's last split
+      dst[0] = int4_of(-1, 0, 0, 0);
+#pragma unroll
+      for (int k = 1; k < kMapEntry / 4; ++k) dst[k] = int4_of(0, 0, 0, 0);
+      continue;
+    }
+    const int* btrow = bt + (int64_t)i * bt_st;
+    const int blk_lo = j * ps;
+    const int blk_hi = blk_lo + ps < nb ? blk_lo + ps : nb;
+    const int npairs = (blk_hi - blk_lo + 1) >> 1;
+    int ids[2 * kMapPairs];
+#pragma unroll
+    for (int q = 0; q < kMapPairs; ++q) {
+      const int qq = q < npairs ? q : (q >= NWF ? q - NWF : q);
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int bi = blk_lo + 2 * qq + h;
+        bi = bi < blk_hi ? bi : blk_hi - 1;
+        ids[2 * q + h] = clamp_block(btrow[bi], NB);
+      }
+    }
+    const int last = clamp_block(btrow[(len - 1) / kBlockSize], NB);
+    dst[0] = int4_of(i, s_first[i], n, len);
+    dst[1] = int4_of(blk_lo, blk_hi, last, ps);
+#pragma unroll
+    for (int k = 0; k < kMapPairs / 2; ++k)
+      dst[2 + k] = int4_of(ids[4 * k], ids[4 * k + 1], ids[4 * k + 2], ids[4 * k + 3]);
+#pragma unroll
+    for (int k = 2 + kMapPairs / 2; k < kMapEntry / 4; ++k) dst[k] = int4_of(0, 0, 0, 0);
+  }
 }
 
 // One workgroup = NW wavefronts = one (split slot, KV head, head group) in v3 or one (sequence,
@@ -262,7 +395,8 @@ __device__ __forceinline__ void decode_mfma_body(
     int S, int H, int KVH, int G, int HG, float sl2, int cap_blocks, int part_blocks, int nx,
     int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
     float* __restrict__ ws_l, int* __restrict__ ws_cnt,
-    int bx, int bz, char* __restrict__ lds, const NewRows& nr = NewRows{}) {
+    int bx, int bz, char* __restrict__ lds, const NewRows& nr = NewRows{},
+    const int* __restrict__ smap = nullptr) {
   constexpr int KK = KvRegs<D>::KK;
   constexpr int VW = KvRegs<D>::VW;
   constexpr int TILES = KvRegs<D>::TILES;
@@ -284,9 +418,30 @@ __device__ __forceinline__ void decode_mfma_body(
   const bool split = ws_acc != nullptr;
 
   int s, seq_len, blk_lo, blk_hi, nsplit, split_j = 0;
+  // With a split map built for this launch's plan (header equal to the plan; smap is only
+  // passed by decode_mfma_kernel, whose grid.x is the slot count) the slot's entry replaces
+  // split_lookup, and the first two pairs' block ids of this wavefront come with it. The header
+  // and the entry are requested together (the host checked that the map holds every slot).
+  bool mapped = false;
+  int m_last = 0, m_id[4] = {0, 0, 0, 0};
+  SplitSlot sp{-1, 0, 0, 0, 0};
+  if constexpr (2 * NW == kMapPairs) {
+    if (split && smap != nullptr) {
+      const int* e = smap + kMapHeader + (int64_t)bx * kMapEntry;
+      mapped = smap[0] == kMapMagic && smap[1] == S && smap[2] == (int)gridDim.x &&
+               smap[3] == part_blocks && smap[4] == nx && smap[5] == max_splits &&
+               smap[6] == cap_blocks;
+      sp = {e[0], e[1], e[2], e[7], e[3]};
+      m_last = e[6];
+      m_id[0] = e[8 + 2 * w];
+      m_id[1] = e[9 + 2 * w];
+      m_id[2] = e[8 + 2 * (w + NW)];
+      m_id[3] = e[9 + 2 * (w + NW)];
+    }
+  }
   if (split) {
-    const SplitSlot sp = split_lookup<NW * 64>(seq_lens, S, cap_blocks, part_blocks, nx,
-                                               max_splits, bx, s_map);
+    if (!mapped)
+      sp = split_lookup<NW * 64>(seq_lens, S, cap_blocks, part_blocks, nx, max_splits, bx, s_map);
     if (sp.seq < 0) return;                      // slot past the batch's last split
     s = sp.seq;
     seq_len = sp.len;
@@ -324,8 +479,9 @@ __device__ __forceinline__ void decode_mfma_body(
       // The precondition of the fusion: the slot is that of position seq_len - 1. Any other
       // slot would put the row in a block another workgroup may be reading; it is not written,
       // and the sequence's output becomes NaN so the caller sees the broken precondition.
-      const int64_t want = (int64_t)clamp_block(bt[(int64_t)s * bt_st + (seq_len - 1) / kBlockSize], NB) *
-                               kBlockSize + (seq_len - 1) % kBlockSize;
+      const int last_blk =
+          mapped ? m_last : clamp_block(bt[(int64_t)s * bt_st + (seq_len - 1) / kBlockSize], NB);
+      const int64_t want = (int64_t)last_blk * kBlockSize + (seq_len - 1) % kBlockSize;
       poison = slot >= 0 && slot < nr.num_slots && slot != want;
       if (slot >= 0 && slot < nr.num_slots && !poison) {
         const int64_t row = (((slot >> 4) * KVH + kvh) * kBlockSize + (slot & 15)) * D;
@@ -483,8 +639,15 @@ __device__ __forceinline__ void decode_mfma_body(
   int p = w;
   if (p < npairs) {
     int id0[2], id1[2];
-    ids_of(p, id0);
-    ids_of(last_or(p + NW, p), id1);
+    if (mapped) {
+      id0[0] = m_id[0];
+      id0[1] = m_id[1];
+      id1[0] = m_id[2];
+      id1[1] = m_id[3];
+    } else {
+      ids_of(p, id0);
+      ids_of(last_or(p + NW, p), id1);
+    }
     load_k(id0, kf);
     load_v(id0, vA);
     load_v(id1, vB);
@@ -541,21 +704,23 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
     const int* __restrict__ bt, int64_t bt_st, int max_blocks, const int* __restrict__ seq_lens,
     int S, int H, int KVH, int G, int HG, float sl2, int cap_blocks, int part_blocks, int nx,
     int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
-    float* __restrict__ ws_l, int* __restrict__ ws_cnt, const NewRows nr) {
+    float* __restrict__ ws_l, int* __restrict__ ws_cnt, const NewRows nr,
+    const int* __restrict__ smap) {
   __shared__ __attribute__((aligned(16))) char lds[DecodeLds<D, NW>::BYTES];
   decode_mfma_body<D, NW, WRITE, ROPE>(q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks,
                                  seq_lens, S, H, KVH, G, HG, sl2, cap_blocks, part_blocks, nx,
                                  max_splits, ws_acc, ws_m, ws_l, ws_cnt, (int)blockIdx.x,
-                                 (int)blockIdx.z, lds, nr);
+                                 (int)blockIdx.z, lds, nr, smap);
 }
 
 // Merge of the split partials (ops/triton_decode_attention.py:144-163): M = max m_j,
 // w_j = 2^(m_j - M), out = sum w_j acc_j / sum w_j l_j. One workgroup per (sequence, KV head,
 // head group), one thread per 4 output dims of a head. A sequence's partials sit in rows
-// s * max_splits + j, so the split count written by the first kernel, seq_len and the partials
-// of the first kMergeChunk splits are all requested in one memory step (rows past the count are
-// read but ignored). Sequences with one split were finished by the first kernel; a sequence
-// with none (seq_len 0) gets zeros here.
+// s * max_splits + j; the split count written by the first kernel is read first and only the
+// rows below it are requested (a second memory step, but a few hundred KB instead of kMergeChunk
+// rows for every sequence: measured faster than requesting a fixed chunk together with the
+// count). Sequences with one split were finished by the first kernel; a sequence with none
+// (seq_len 0) gets zeros here.
 constexpr int kMaxSplits = 256;
 constexpr int kMergeChunk = 16;
 
@@ -580,23 +745,29 @@ __device__ __forceinline__ void decode_merge_body(
     const int64_t hoff = head0 + (active ? hh : 0);
     float mv[CH], lv[CH];
     float4_t av[CH];
-    auto load_chunk = [&](int j0) {
-#pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        const int j = (j0 + u) < max_splits ? (j0 + u) : (max_splits - 1);
-        const int64_t pidx = (row0 + j) * H + hoff;
-        mv[u] = ws_m[pidx];
-        lv[u] = ws_l[pidx];
-        av[u] = ld<float4_t>(ws_acc + pidx * D + d0);
-      }
-    };
-    load_chunk(0);
     if (len <= 0) {                              // padding row: zeros (ops/reference.py:99,104-105)
       if (active) st<half4_t>(out + (int64_t)s * o_st + (head0 + hh) * (int64_t)D + d0, half4_t{0, 0, 0, 0});
       continue;
     }
     const int n = cnt < 1 ? 1 : (cnt > max_splits ? max_splits : cnt);
     if (n == 1) return;                          // written by the first kernel
+    // rows past n are neither requested nor used: their stale contents may be inf or NaN
+    auto load_chunk = [&](int j0) {
+#pragma unroll
+      for (int u = 0; u < CH; ++u) {
+        if (j0 + u < n) {                        // uniform over the workgroup
+          const int64_t pidx = (row0 + j0 + u) * H + hoff;
+          mv[u] = ws_m[pidx];
+          lv[u] = ws_l[pidx];
+          av[u] = ld<float4_t>(ws_acc + pidx * D + d0);
+        } else {
+          mv[u] = -INFINITY;
+          lv[u] = 0.f;
+          av[u] = float4_t{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+    };
+    load_chunk(0);
     float M = -INFINITY, L = 0.f;
     float4_t O = {0.f, 0.f, 0.f, 0.f};
     for (int j0 = 0; j0 < n; j0 += CH) {
@@ -634,6 +805,7 @@ __global__ void __launch_bounds__(256) decode_merge_kernel(
 // Host side
 // ------------------------------------------------------------------------------------------
 constexpr int kDecodeWaves = 4;                              // wavefronts per workgroup
+static_assert(2 * kDecodeWaves == kMapPairs, "split map entries hold two pairs per wavefront");
 
 // Workgroups of decode_mfma_kernel resident per CU (4 wavefronts each, one per SIMD), from the
 // kernel's VGPR use (512 per SIMD lane): 6 waves per SIMD up to D = 32, 3 at D = 64, 2 at
@@ -709,6 +881,24 @@ static WsLayout ws_layout(const SplitPlan& p, int S, int H, int D) {
   return w;
 }
 
+// Bytes of the per-step split map of plan p (0: the plan does not split).
+static size_t map_bytes_of(const SplitPlan& p) {
+  if (p.version != TS_DECODE_V3) return 0;
+  return ((size_t)kMapHeader + (size_t)p.nslots * kMapEntry) * sizeof(int);
+}
+
+// The cap_blocks a v3 launch of plan p passes to its kernels (and the map records).
+static int launch_cap_blocks(const SplitPlan& p, int max_blocks) {
+  return p.cap_blocks < max_blocks ? p.cap_blocks : max_blocks;
+}
+
+static void launch_split_map(const SplitPlan& p, hipStream_t st, const int* sl, const int* bt,
+                             int64_t bt_st, int64_t NB, int max_blocks, int S, int* map) {
+  decode_split_map_kernel<kMapThreads><<<1, kMapThreads, 0, st>>>(
+      sl, bt, bt_st, NB, S, launch_cap_blocks(p, max_blocks), p.part_blocks, p.nx, p.max_splits,
+      p.nslots, map);
+}
+
 // With nr.k set (kv_write fused into the launch; v2 / v3 with one head group per KV head only)
 // the MFMA kernel first writes the new rows, as in decode_mfma_body; with nr.cos_t set too
 // (head_dim a multiple of 64) it also rotates q and the new k rows first.
@@ -717,7 +907,7 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
                           int64_t q_sh, half_t* out, int64_t o_st, const half_t* kc,
                           const half_t* vc, int64_t NB, const int* bt, int64_t bt_st,
                           int max_blocks, const int* sl, int S, int H, int KVH, float scale_log2,
-                          void* ws, const NewRows& nr = NewRows{}) {
+                          void* ws, const NewRows& nr = NewRows{}, const int* smap = nullptr) {
   const int G = H / KVH;
   const bool write = nr.k != nullptr;
   const bool rope = write && nr.cos_t != nullptr;     // only for head_dim % 64 == 0
@@ -731,7 +921,7 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
 #define TS_V2_LAUNCH(W, R)                                                                       \
   decode_mfma_kernel<D, kDecodeWaves, W, R><<<dim3(S, 1, KVH * HG), kDecodeWaves * 64, 0, st>>>( \
       q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,        \
-      scale_log2, 0, 0, 0, 0, nullptr, nullptr, nullptr, nullptr, nr)
+      scale_log2, 0, 0, 0, 0, nullptr, nullptr, nullptr, nullptr, nr, nullptr)
     if constexpr (D % 64 == 0) {
       if (rope) {
         TS_V2_LAUNCH(true, true);
@@ -751,12 +941,12 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
   float* ws_m = reinterpret_cast<float*>(b + w.m);
   float* ws_l = reinterpret_cast<float*>(b + w.l);
   int* ws_cnt = reinterpret_cast<int*>(b + w.cnt);
-  const int cap = p.cap_blocks < max_blocks ? p.cap_blocks : max_blocks;
+  const int cap = launch_cap_blocks(p, max_blocks);
 #define TS_V3_LAUNCH(W, R)                                                                       \
   decode_mfma_kernel<D, kDecodeWaves, W, R><<<dim3(p.nslots, 1, KVH * HG), kDecodeWaves * 64, 0, \
                                               st>>>(                                             \
       q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,        \
-      scale_log2, cap, p.part_blocks, p.nx, p.max_splits, ws_acc, ws_m, ws_l, ws_cnt, nr)
+      scale_log2, cap, p.part_blocks, p.nx, p.max_splits, ws_acc, ws_m, ws_l, ws_cnt, nr, smap)
   bool launched = false;
   if constexpr (D % 64 == 0) {
     if (rope) {

@@ -241,7 +241,8 @@ extern "C" int ts_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
                                        out_stride_t, k_cache, v_cache, num_blocks, block_tables,
                                        bt_stride, max_blocks_per_seq, seq_lens, num_decode,
                                        num_heads, num_kv_heads, head_dim, scale, max_seq_len,
-                                       partition, workspace, workspace_bytes, stream);
+                                       partition, workspace, workspace_bytes, stream,
+                                       nullptr, 0);
     if (st != TS_OK) return st;
   }
   if (num_seqs > num_decode) {

@@ -110,8 +110,51 @@ def _decode_call(version: int, q, out, k_cache, v_cache, block_tables, seq_lens,
     N.check(N.lib().ts_decode_attention(
         version, _ptr(q), q.stride(0), q.stride(1), _ptr(out), out.stride(0), _ptr(k_cache),
         _ptr(v_cache), NB, _ptr(bt), bt.stride(0), bt.shape[1], _ptr(sl), S, H, KVH, D,
-        float(scale), int(max_seq_len), int(partition), _ptr(ws), ws_bytes, _stream(q)),
+        float(scale), int(max_seq_len), int(partition), _ptr(ws), ws_bytes, _stream(q), None, 0),
         "decode_attention")
+
+
+def _decode_plan(S: int, max_seq_len: int, decode_version: str | None,
+                 partition: int | None) -> tuple[int, int]:
+    """(version code, partition) of a fused decode call: the variant table's choice for
+    (S, max_seq_len) when no version is given, the default partition for v3 / AUTO."""
+    _require(decode_version in N.DECODE_VERSIONS, f"unknown decode version {decode_version!r}")
+    if decode_version is None:
+        tv, tp = tuner.decode_choice(S, int(max_seq_len))
+        if tv is not None:
+            decode_version = tv
+            partition = tp if partition is None else partition
+    code = N.DECODE_VERSIONS[decode_version]
+    part = (DEFAULT_PARTITION if partition is None else partition) if code in (0, 3) else 0
+    return code, part
+
+
+def _map_args(split_map) -> tuple:
+    return (None, 0) if split_map is None else (_ptr(split_map[0]), split_map[1])
+
+
+def decode_split_map(meta, H: int, KVH: int, D: int, num_blocks: int, device,
+                     decode_version: str | None = None, partition: int | None = None):
+    """The step's split map (ts_decode_split_map) for the fused decode calls of a pure-decode
+    step with this attention shape: built once, passed as split_map= to every layer's
+    decode_kv_write_attention / decode_rope_kv_write_attention of the same step (same meta,
+    decode_version and partition). Returns (int32 device tensor, bytes), or None when the plan
+    does not split (nothing to build; the calls then take split_map=None)."""
+    S = meta.num_decode
+    if S == 0:
+        return None
+    code, part = _decode_plan(S, int(meta.max_seq_len), decode_version, partition)
+    nb = N.lib().ts_decode_split_map_bytes(code, S, H, KVH, D, int(meta.max_seq_len), part,
+                                          N.cu_count(device.index or 0))
+    if nb == 0:
+        return None
+    bt, sl = _i32(meta.block_tables), _i32(meta.seq_lens)
+    _check_gpu(bt, sl)
+    buf = torch.empty(nb // 4, dtype=torch.int32, device=device)
+    N.check(N.lib().ts_decode_split_map(code, _ptr(bt), bt.stride(0), bt.shape[1], int(num_blocks),
+                                        _ptr(sl), S, H, KVH, D, int(meta.max_seq_len), part,
+                                        _ptr(buf), nb, _stream(buf)), "decode_split_map")
+    return buf, nb
 
 
 def decode_attention_v1(q, out, k_cache, v_cache, block_tables, seq_lens, scale, S: int):
@@ -229,7 +272,7 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
 def decode_kv_write_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                               k_cache: torch.Tensor, v_cache: torch.Tensor, meta, scale: float,
                               decode_version: str | None = None,
-                              partition: int | None = None) -> torch.Tensor:
+                              partition: int | None = None, split_map=None) -> torch.Tensor:
     """A pure-decode layer step in one launch: kv_write(k, v, caches, meta.slot_mapping) and
     then paged_attention(q, caches, meta, scale) (model/qwen2.py:26-28 with
     ops/triton_ops.py:60-71), returning the same [T, H*D] and leaving the same cache. q [T, H, D],
@@ -237,7 +280,8 @@ def decode_kv_write_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     slot_mapping[i] the slot of position seq_lens[i] - 1 (-1 where seq_lens[i] == 0), as every
     input builder produces; a row with any other in-range slot is not written and its output row
     is NaN (its write would race with other workgroups' reads), so such rows need kv_write and
-    paged_attention instead."""
+    paged_attention instead. split_map: decode_split_map()'s result for this step (same meta,
+    decode_version and partition) or None; the output is the same either way."""
     T, H, D = q.shape
     out = torch.empty(T, H * D, dtype=q.dtype, device=q.device)
     if T == 0:
@@ -257,13 +301,7 @@ def decode_kv_write_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
     sm = meta.slot_mapping
     slots = sm if (sm.dtype == torch.int64 and sm.is_contiguous()) else sm.to(torch.int64).contiguous()
     _require(slots.shape[0] >= T, "decode_kv_write_attention: slot_mapping shorter than q")
-    if decode_version is None:
-        tv, tp = tuner.decode_choice(S, int(meta.max_seq_len))
-        if tv is not None:
-            decode_version = tv
-            partition = tp if partition is None else partition
-    code = N.DECODE_VERSIONS[decode_version]
-    part = (DEFAULT_PARTITION if partition is None else partition) if code in (0, 3) else 0
+    code, part = _decode_plan(S, int(meta.max_seq_len), decode_version, partition)
     ws_bytes = N.lib().ts_decode_workspace_bytes(code, S, H, KVH, D, int(meta.max_seq_len), part,
                                                  N.cu_count(q.device.index or 0))
     ws = _workspace(ws_bytes, q.device)
@@ -271,8 +309,8 @@ def decode_kv_write_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
         code, _ptr(q), q.stride(0), q.stride(1), _ptr(k), _ptr(v), k.stride(0), k.stride(1),
         v.stride(0), v.stride(1), _ptr(slots), _ptr(out), out.stride(0), _ptr(k_cache),
         _ptr(v_cache), NB, _ptr(bt), bt.stride(0), bt.shape[1], _ptr(sl), S, H, KVH, D,
-        float(scale), int(meta.max_seq_len), int(part), _ptr(ws), ws_bytes, _stream(q)),
-        "decode_kv_write_attention")
+        float(scale), int(meta.max_seq_len), int(part), _ptr(ws), ws_bytes, _stream(q),
+        *_map_args(split_map)), "decode_kv_write_attention")
     return out
 
 
@@ -280,15 +318,16 @@ def decode_rope_kv_write_attention(qkv: torch.Tensor, positions: torch.Tensor,
                                    cos: torch.Tensor, sin: torch.Tensor, H: int, KVH: int, D: int,
                                    k_cache: torch.Tensor, v_cache: torch.Tensor, meta,
                                    scale: float, decode_version: str | None = None,
-                                   partition: int | None = None) -> torch.Tensor | None:
+                                   partition: int | None = None,
+                                   split_map=None) -> torch.Tensor | None:
     """The attention half of a pure-decode layer step in one launch: rope_(qkv, ...), kv_write
     of its k and v heads and paged_attention over the rotated q (model/qwen2.py:26-28, :89 with
     ops/triton_ops.py:60-71); returns the same [T, H*D] and leaves the same caches. qkv is left
     unrotated when the launch is fused (rotated in place when the library runs the rotation as its
     own launch), so only the returned output and the caches are defined afterwards. Returns None,
     having done nothing, when qkv's layout does not allow it (rows not 16-byte aligned): the
-    caller then makes the separate calls. Every row must be a decode row, with slot_mapping as
-    for decode_kv_write_attention."""
+    caller then makes the separate calls. Every row must be a decode row, with slot_mapping and
+    split_map as for decode_kv_write_attention."""
     T = qkv.shape[0]
     if not (qkv.dim() == 2 and qkv.stride(1) == 1 and qkv.stride(0) % 8 == 0 and
             qkv.data_ptr() % 16 == 0 and k_cache.is_contiguous() and v_cache.is_contiguous()):
@@ -315,13 +354,7 @@ def decode_rope_kv_write_attention(qkv: torch.Tensor, positions: torch.Tensor,
     slots = sm if (sm.dtype == torch.int64 and sm.is_contiguous()) else sm.to(torch.int64).contiguous()
     _require(slots.shape[0] >= T and pos.shape[0] >= T,
              "decode_rope_kv_write_attention: slot_mapping / positions shorter than qkv")
-    if decode_version is None:
-        tv, tp = tuner.decode_choice(S, int(meta.max_seq_len))
-        if tv is not None:
-            decode_version = tv
-            partition = tp if partition is None else partition
-    code = N.DECODE_VERSIONS[decode_version]
-    part = (DEFAULT_PARTITION if partition is None else partition) if code in (0, 3) else 0
+    code, part = _decode_plan(S, int(meta.max_seq_len), decode_version, partition)
     ws_bytes = N.lib().ts_decode_workspace_bytes(code, S, H, KVH, D, int(meta.max_seq_len), part,
                                                  N.cu_count(qkv.device.index or 0))
     ws = _workspace(ws_bytes, qkv.device)
@@ -329,7 +362,7 @@ def decode_rope_kv_write_attention(qkv: torch.Tensor, positions: torch.Tensor,
         code, _ptr(qkv), qkv.stride(0), _ptr(pos), _ptr(cos), _ptr(sin), cos.shape[0], _ptr(out),
         out.stride(0), _ptr(k_cache), _ptr(v_cache), NB, _ptr(slots), _ptr(bt), bt.stride(0),
         bt.shape[1], _ptr(sl), S, H, KVH, D, float(scale), int(meta.max_seq_len), int(part),
-        _ptr(ws), ws_bytes, _stream(qkv)), "decode_rope_kv_write_attention")
+        _ptr(ws), ws_bytes, _stream(qkv), *_map_args(split_map)), "decode_rope_kv_write_attention")
     return out
 
 

@@ -41,6 +41,7 @@ def _hip() -> SimpleNamespace:
     ns.linear_rmsnorm_residual = h.linear_rmsnorm_residual
     ns.rope_kv_write_ = h.rope_kv_write_
     ns.decode_rope_kv_write_attention = h.decode_rope_kv_write_attention
+    ns.decode_split_map = h.decode_split_map
     return ns
 
 

@@ -176,10 +176,11 @@ class Qwen2Model:
         return meta.num_decode == num_tokens and meta.seq_lens.shape[0] == meta.num_decode
 
     def _attention_block(self, index: int, x, residual, positions, meta, kv_cache,
-                         fused_decode: bool):
+                         fused_decode: bool, split_map=None):
         """Decoder layer `index` from its normed input x to the MLP activation: qkv, RoPE, the
         K/V write into kv_cache[index], attention, o_proj with post_attention_layernorm, and
-        silu(gate) * up; returns (the input of down_proj, residual)."""
+        silu(gate) * up; returns (the input of down_proj, residual). split_map: the step's
+        decode split map (fused decode only), shared by every layer."""
         c, ops, lw = self.cfg, self.ops, self.w.layers[index]
         k_cache, v_cache = kv_cache[index, 0], kv_cache[index, 1]
         qkv = ops.linear(x, lw.qkv_proj)
@@ -187,7 +188,7 @@ class Qwen2Model:
         if fused_decode and hasattr(ops, "decode_rope_kv_write_attention"):
             a = ops.decode_rope_kv_write_attention(qkv, positions, self.cos, self.sin, c.num_heads,
                                                    c.num_kv_heads, c.head_dim, k_cache, v_cache,
-                                                   meta, self.scale)
+                                                   meta, self.scale, split_map=split_map)
         if a is None:                 # not fused, or a layout the fused launch does not take
             q, _, _ = self._rotate_write(qkv, positions, k_cache, v_cache, meta.slot_mapping)
             a = ops.paged_attention(q, k_cache, v_cache, meta, self.scale)
@@ -220,12 +221,16 @@ class Qwen2Model:
         the final norm): the same values, without a separate split-K reduction launch."""
         c, layers = self.cfg, self.w.layers
         fused = self.pure_decode(meta, input_ids.shape[0])
+        # one decode split map per step, read by every layer's fused decode launch
+        build_map = getattr(self.ops, "decode_split_map", None) if fused else None
+        split_map = (build_map(meta, c.num_heads, c.num_kv_heads, c.head_dim, kv_cache.shape[2],
+                               kv_cache.device) if build_map is not None else None)
         h = self.w.embed_tokens[input_ids]
         residual = h
         x = self.ops.rmsnorm(h, layers[0].input_norm, c.rms_norm_eps)
         for index in range(len(layers)):
             act, residual = self._attention_block(index, x, residual, positions, meta, kv_cache,
-                                                  fused)
+                                                  fused, split_map)
             norm_w = layers[index + 1].input_norm if index + 1 < len(layers) else self.w.final_norm
             x, residual = self._project_norm(act, layers[index].down_proj, residual, norm_w)
         return x
