@@ -243,7 +243,7 @@ constexpr int kTileRows = 128;
 constexpr int kTileKeys = 64;
 constexpr int kTileThreads = 256;
 constexpr int kPrefillMinSteps = 4;   // fewest 64-key steps a split is given
-constexpr int kMergeRows = 4;         // rows per merge thread
+constexpr int kMergeRows = 2;         // rows per merge thread (8 dims each)
 
 template <int D>
 struct TileLayout {
@@ -639,11 +639,13 @@ __global__ void __launch_bounds__(kTileThreads, 2) prefill_tile_kernel(
 
 // Merge of split partials (each the split's own average A_j = O_j / l_j with its (m_j, l_j)):
 // M = max m_j, w_j = 2^(m_j - M) l_j, out = sum w_j A_j / sum w_j (empty splits have m = -inf and
-// weigh 0). A thread owns 4 dims (d0) of kMergeRows rows; the partials sit at slot indices
-// base .. base + cnt - 1 of a workspace of total_slots slots x slot_rows rows, the thread's rows at
-// row0 + kMergeRowStride * k of each slot, and go to dst[k] (nullptr: not wanted). The partials
-// are taken two at a time, all of a pair's loads requested together.
-constexpr int kMergeRowStride = kTileThreads / 32;   // row groups of a 256-thread merge group
+// weigh 0). A thread owns 8 dims (d0, one 16-byte load per partial row) of kMergeRows rows; the
+// partials sit at slot indices base .. base + cnt - 1 of a workspace of total_slots slots x
+// slot_rows rows, the thread's rows at row0 + kMergeRowStride * k of each slot, and go to dst[k]
+// (nullptr: not wanted). The partials are taken kMergeBatch at a time, all of a batch's loads
+// requested together (cnt is uniform over the workgroup, so the unused ones are not issued).
+constexpr int kMergeRowStride = kTileThreads / 16;   // 16 rows per pass of a 256-thread group
+constexpr int kMergeBatch = 4;
 
 template <int D>
 __device__ __forceinline__ void merge_partials(const float* __restrict__ ws, int64_t total_slots,
@@ -651,44 +653,49 @@ __device__ __forceinline__ void merge_partials(const float* __restrict__ ws, int
                                                int d0, half_t* const (&dst)[kMergeRows]) {
   constexpr int NR = kMergeRows;
   constexpr int RG = kMergeRowStride;
+  constexpr int B = kMergeBatch;
   const half_t* wo = reinterpret_cast<const half_t*>(ws);
   const float* wml = reinterpret_cast<const float*>(wo + total_slots * slot_rows * D);
-  float M[NR], Lsum[NR];
-  float4_t acc[NR];
+  float M[NR], Lsum[NR], acc[NR][8];
 #pragma unroll
   for (int k = 0; k < NR; ++k) {
     M[k] = -INFINITY;
     Lsum[k] = 0.f;
-    acc[k] = float4_t{0.f, 0.f, 0.f, 0.f};
-  }
-  for (int j = 0; j < cnt; j += 2) {
-    const bool two = j + 1 < cnt;
-    float2_t ml[2][NR];
-    half4_t a[2][NR];
 #pragma unroll
-    for (int u = 0; u < 2; ++u)
+    for (int e = 0; e < 8; ++e) acc[k][e] = 0.f;
+  }
+  for (int j = 0; j < cnt; j += B) {
+    float2_t ml[B][NR];
+    half8_t a[B][NR];
+#pragma unroll
+    for (int u = 0; u < B; ++u)
 #pragma unroll
       for (int k = 0; k < NR; ++k) {
-        const int64_t rix = (base + j + (two ? u : 0)) * slot_rows + row0 + RG * k;
-        ml[u][k] = ld<float2_t>(wml + rix * 2);
-        a[u][k] = ld<half4_t>(wo + rix * D + d0);
+        if (j + u < cnt) {
+          const int64_t rix = (base + j + u) * slot_rows + row0 + RG * k;
+          ml[u][k] = ld<float2_t>(wml + rix * 2);
+          a[u][k] = ld<half8_t>(wo + rix * D + d0);
+        } else {
+          ml[u][k] = float2_t{-INFINITY, 0.f};
+          a[u][k] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+        }
       }
 #pragma unroll
     for (int k = 0; k < NR; ++k) {
-      const float m1 = two ? ml[1][k][0] : -INFINITY;
-      const float cm = fmaxf(M[k], fmaxf(ml[0][k][0], m1));
+      float cm = M[k];
+#pragma unroll
+      for (int u = 0; u < B; ++u) cm = fmaxf(cm, ml[u][k][0]);
       const float alpha = M[k] == -INFINITY ? 0.f : fast_exp2(M[k] - cm);
       Lsum[k] *= alpha;
-      acc[k] *= alpha;
 #pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const float mu = u == 0 ? ml[0][k][0] : m1;
+      for (int e = 0; e < 8; ++e) acc[k][e] *= alpha;
+#pragma unroll
+      for (int u = 0; u < B; ++u) {
+        const float mu = ml[u][k][0];
         const float wt = mu == -INFINITY ? 0.f : fast_exp2(mu - cm) * ml[u][k][1];
         Lsum[k] += wt;
-        acc[k][0] += wt * (float)a[u][k][0];
-        acc[k][1] += wt * (float)a[u][k][1];
-        acc[k][2] += wt * (float)a[u][k][2];
-        acc[k][3] += wt * (float)a[u][k][3];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[k][e] += wt * (float)a[u][k][e];
       }
       M[k] = cm;
     }
@@ -697,8 +704,14 @@ __device__ __forceinline__ void merge_partials(const float* __restrict__ ws, int
   for (int k = 0; k < NR; ++k) {
     if (dst[k] == nullptr) continue;
     const float inv = Lsum[k] == 0.f ? 0.f : 1.f / Lsum[k];
-    ts::st<half4_t>(dst[k], half4_t{(half_t)(acc[k][0] * inv), (half_t)(acc[k][1] * inv),
-                                    (half_t)(acc[k][2] * inv), (half_t)(acc[k][3] * inv)});
+    half4_t o0, o1;                              // two 8-byte stores: out rows are 8-byte aligned
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o0[e] = (half_t)(acc[k][e] * inv);
+      o1[e] = (half_t)(acc[k][e + 4] * inv);
+    }
+    ts::st<half4_t>(dst[k], o0);
+    ts::st<half4_t>(dst[k] + 4, o1);
   }
 }
 
@@ -710,15 +723,15 @@ __device__ __forceinline__ void prefill_merge_body(
     const float* __restrict__ ws, half_t* __restrict__ out, int64_t o_st, int64_t num_tokens,
     int max_blocks, const int* __restrict__ seq_lens, const int* __restrict__ qsl,
     int num_decode, int H, int smax, int slots, int P, int bx, int by, int bz, int tile_stride) {
-  constexpr int TPR = D / 4;                       // threads per row
-  constexpr int RG = kMergeRowStride;              // row groups per workgroup (8)
+  constexpr int TPR = D / 8;                       // threads per row
+  constexpr int RG = kMergeRowStride;              // row groups per workgroup (16)
   constexpr int NR = kMergeRows;                   // rows per thread
   static_assert(RG * NR * 4 == kTileRows && TPR * RG == kTileThreads, "four workgroups per tile");
   const int part = bx & 3;
   const int b = num_decode + by, h = bz;
   const PrefillSeq sq = prefill_seq(qsl, seq_lens, b, num_tokens, max_blocks);
   const int rbase = part * RG * NR + (int)(threadIdx.x / TPR);   // rows rbase + RG * k
-  const int d0 = 4 * (int)(threadIdx.x % TPR);
+  const int d0 = 8 * (int)(threadIdx.x % TPR);
   const int64_t total = (int64_t)P * H * slots;
   // The grid covers the tiles the host bounds foresee; a sequence with more (bounds below its
   // real q_len) has its further tiles taken in turn, so every tile whose splits all ran is

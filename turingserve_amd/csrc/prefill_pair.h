@@ -480,9 +480,10 @@ __global__ void __launch_bounds__(kTileThreads) prefill_pair_merge_kernel(
     int max_blocks, const int* __restrict__ seq_lens, const int* __restrict__ qsl,
     int num_decode, int H, int KVH, int slots, int seg_cap) {
   constexpr int D = PairLayout::D;
-  constexpr int TPR = D / 4;
+  constexpr int TPR = D / 8;
   constexpr int RG = kMergeRowStride;
   constexpr int NR = kMergeRows;
+  static_assert(RG * NR * 4 == kTileRows && TPR * RG == kTileThreads, "four workgroups per block");
   const int bx = (int)blockIdx.x, by = (int)blockIdx.y, h = (int)blockIdx.z;
   const int part = bx & 3;
   const PrefillSeq sq = prefill_seq(qsl, seq_lens, num_decode + by, num_tokens, max_blocks);
@@ -500,7 +501,7 @@ __global__ void __launch_bounds__(kTileThreads) prefill_pair_merge_kernel(
   for (int t = 0; t < tiles; ++t) total_steps += tile_steps(t);
   const int per = (total_steps + slots - 1) / slots;
   const int rbase = part * RG * NR + (int)(threadIdx.x / TPR);
-  const int d0 = 4 * (int)(threadIdx.x % TPR);
+  const int d0 = 8 * (int)(threadIdx.x % TPR);
   const int64_t total = (int64_t)gridDim.y * (H / hp) * seg_cap;
   const half_t nan = __builtin_bit_cast(half_t, (unsigned short)0x7e00);
   // The grid covers the blocks the host bounds foresee; a longer sequence has its further blocks
@@ -526,7 +527,10 @@ __global__ void __launch_bounds__(kTileThreads) prefill_pair_merge_kernel(
     if (pos + k1 >= seg_cap) {
 #pragma unroll
       for (int k = 0; k < NR; ++k)
-        if (dst[k] != nullptr) ts::st<half4_t>(dst[k], half4_t{nan, nan, nan, nan});
+        if (dst[k] != nullptr) {
+          ts::st<half4_t>(dst[k], half4_t{nan, nan, nan, nan});
+          ts::st<half4_t>(dst[k] + 4, half4_t{nan, nan, nan, nan});
+        }
       continue;
     }
     merge_partials<D>(ws, total, kPairSlotRows, ((int64_t)by * (H / hp) + h / hp) * seg_cap + pos + k0,
