@@ -414,7 +414,10 @@ def bench_prefill(torch, K, synth):
         q, k, v = st.views(qkv)
         meta = st.meta(dev)
         K.kv_write(k, v, kc, vc, meta.slot_mapping)
-        ms = time_graph(torch, lambda: K.paged_attention(q, kc, vc, meta, st.D ** -0.5), reps=10)
+        # eight calls per graph: each call's kernels follow the previous call's as a model step's
+        # layers follow each other, instead of paying a graph launch per call
+        ms = time_graph(torch, lambda: K.paged_attention(q, kc, vc, meta, st.D ** -0.5), reps=10,
+                        inner=8)
         fl = prefill_flops(st.H, st.D, prefix, n)
         rows.append({"prefix": prefix, "q_len": n, "ms": round(ms, 4),
                      "tflops": round(fl / ms / 1e9, 2)})

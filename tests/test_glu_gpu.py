@@ -73,7 +73,8 @@ def test_glu_intermediate_not_a_multiple_of_8(M, inter):
 
 
 @pytest.mark.parametrize("variant,splits", [(1, 0), (1, 1), (1, 3), (2, 0), (2, 1), (2, 4),
-                                            (3, 0), (3, 2), (4, 0), (4, 2), (5, 0)])
+                                            (3, 0), (3, 2), (4, 0), (4, 2), (5, 0), (6, 0),
+                                            (6, 2)])
 @pytest.mark.parametrize("M", [9, 32, 200])
 def test_glu_every_variant_and_split(variant, splits, M):
     if variant == 1 and M > 32:

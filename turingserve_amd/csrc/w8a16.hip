@@ -975,13 +975,16 @@ static bool use_small_path(int M, int N, int K) {
 // K steps of loads in flight (wide kernel). With weights in LDS as well, 128-column tiles take
 // one step fewer so that two workgroups (3 x 24 KB of stages each) stay resident per CU; measured
 // at M = 2048 on the gate_up product: 165 us at 2 steps, 186 us at 3 (one workgroup per CU).
+// 192-column tiles keep one step in flight (2 x 32 KB of stages, two workgroups per CU).
 constexpr int kWidePrefetch = 3;
-constexpr int wide_prefetch(bool dma, int wm) { return dma && wm == 4 ? 2 : kWidePrefetch; }
+constexpr int wide_prefetch(bool dma, int wm) {
+  return wm == 6 ? 1 : (dma && wm == 4 ? 2 : kWidePrefetch);
+}
 
 struct GemmPlan {
   bool small;
   int mt;          // m tiles (small and skinny paths)
-  int bn, bm;      // tile shape (wide path): 128 x 128, 128 x 64 or 128 x 32
+  int bn, bm;      // tile shape (wide path): 128 x 192, 128 x 128, 128 x 64 or 128 x 32
   int splits;      // K splits
   int k_per_split;
   int rt;          // skinny path: 16-row weight tiles per workgroup (0: not skinny)
@@ -990,7 +993,8 @@ struct GemmPlan {
 
 // Variants a caller (a tuning table) may name instead of the planner's choice.
 enum GemmVariant : int {
-  kVarAuto = 0, kVarStream = 1, kVarWide64 = 2, kVarWide128 = 3, kVarWide32 = 4, kVarSkinny = 5
+  kVarAuto = 0, kVarStream = 1, kVarWide64 = 2, kVarWide128 = 3, kVarWide32 = 4, kVarSkinny = 5,
+  kVarWide192 = 6
 };
 constexpr int kSkinnyMMax = 64;
 
@@ -1049,7 +1053,8 @@ static int wide64_splits(int M, int N, int K, int cus) {
 // The plan of a variant with `splits` K splits (0: the variant's own rule). kVarAuto: weight
 // streaming when use_small_path says so; else 128 x 128 tiles (two workgroups per CU; the most
 // work per CU of the shapes measured) once they cover half the CUs and M is past 64 (below
-// that most of their rows would be padding); else 128 x 64 tiles, or 128 x 32 tiles (four
+// that most of their rows would be padding), or 128 x 192 tiles where those fit one resident
+// round and 128 x 128 tiles would not; else 128 x 64 tiles, or 128 x 32 tiles (four
 // workgroups per CU) when M is past 64 but 128 x 64 tiles would cover fewer than half the CUs
 // with no K split (short K): twice the workgroups for the same weights, which measured ~13 %
 // faster on the 1536 x 1536 and 2048 x 1536 products at M = 256 and the former at M = 560;
@@ -1072,6 +1077,14 @@ static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int split
     if (variant == kVarWide64 && M > 64 && n_tiles * ((M + 63) / 64) * 2 < cus &&
         wide64_splits(M, N, K, cus) == 1)
       variant = kVarWide32;
+    // 128 x 192 tiles when their grid fits one round of resident workgroups (two per CU) and the
+    // 128 x 128 grid does not: the leftover partial round of 128-row tiles costs more than the
+    // larger tiles. Measured on the gate_up product (17920 x 1536, cold weights) at M = 560:
+    // 59.5 -> 48.3 us fused with SiLU.up, 56.3 -> 44.0 us plain; at M = 1024 and 2048, where
+    // neither grid fits one round, 192-column tiles were no faster.
+    if (variant == kVarWide128 && n_tiles * ((M + 191) / 192) <= 2LL * cus &&
+        n_tiles * ((M + 127) / 128) > 2LL * cus)
+      variant = kVarWide192;
     if (variant == kVarWide64 && M <= 64 && n_tiles * ((M + 63) / 64) * 4 < cus) {
       // Few rows and few columns (a decode step's projections): 128 x 32 tiles split over K
       // until about one workgroup per CU, at most 8 ways and at least 6 K steps each (the
@@ -1087,7 +1100,9 @@ static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int split
     }
   }
   GemmPlan p{variant == kVarStream, (M + 15) / 16, 128,
-             variant == kVarWide128 ? 128 : (variant == kVarWide32 ? 32 : 64), 1, K, 0, 0};
+             variant == kVarWide192 ? 192
+                                    : (variant == kVarWide128 ? 128 : (variant == kVarWide32 ? 32 : 64)),
+             1, K, 0, 0};
   if (p.small) {
     if (splits == 0) splits = stream_splits(M, N, K, cus);
     int kps = (K + splits - 1) / splits;
@@ -1124,7 +1139,7 @@ extern "C" size_t ts_w8a16_workspace_bytes(int32_t M, int32_t N, int32_t K, int3
 }
 
 static bool variant_valid(int variant, int splits, int M) {
-  return variant >= kVarAuto && variant <= kVarSkinny && splits >= 0 && splits <= kMaxSplits &&
+  return variant >= kVarAuto && variant <= kVarWide192 && splits >= 0 && splits <= kMaxSplits &&
          (variant != kVarStream || M <= kSmallMMax) &&
          (variant != kVarSkinny || (M <= kSkinnyMMax && splits <= 1));
 }
@@ -1229,7 +1244,9 @@ static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const v
   else                                                                                             \
     w8a16_wide_kernel<WNV, WMV, wide_prefetch(false, WMV), false, true><<<grid, 256, 0, s>>>(      \
         xp, ldx, wq, scale, scale_is_fp16, bp, yp, ldy, M, N, K, p.k_per_split, part, io)
-    if (p.bm == 128) {
+    if (p.bm == 192) {
+      TS_WIDE_LAUNCH(1, 6);
+    } else if (p.bm == 128) {
       TS_WIDE_LAUNCH(1, 4);
     } else if (p.bm == 64) {
       TS_WIDE_LAUNCH(1, 2);

@@ -11,13 +11,13 @@ buckets below the engine's token budget and the budget itself.
 
     kernel "decode": key (S, L)    (decode rows, max_seq_len)       -> {"version": "v2" | "v3",
                                                                          "partition": 0 | 256 | ...}
-    kernel "w8a16":  key (N, K, M) (out features, in features, rows) -> {"variant": 0..5,
+    kernel "w8a16":  key (N, K, M) (out features, in features, rows) -> {"variant": 0..6,
                                                                          "splits": 0..}
 
 W8A16 variants (ts_w8a16_gemm_v): 0 the library's plan, 1 weight streaming (M <= 32),
 2 128 x 64 wide tiles, 3 128 x 128 wide tiles, 4 128 x 32 wide tiles (128 x 64 in the fused
-gated-MLP product), 5 skinny (M <= 64: whole K per workgroup, no split-K); splits 0 = the
-variant's own rule. Decode:
+gated-MLP product), 5 skinny (M <= 64: whole K per workgroup, no split-K), 6 128 x 192 wide
+tiles; splits 0 = the variant's own rule. Decode:
 v2 (one workgroup per sequence and KV head group) or v3 with partition 0 (balanced split) or a
 fixed partition in tokens. Every variant computes the same result up to fp32 summation order.
 """
@@ -176,7 +176,7 @@ def time_call(torch, fn, inner: int = 10, reps: int = 5) -> float:
 
 
 def w8a16_candidates(M: int) -> list[tuple[int, int]]:
-    cands = [(0, 0), (2, 0), (2, 1), (2, 2), (2, 4), (3, 0), (3, 2), (4, 0), (4, 2)]
+    cands = [(0, 0), (2, 0), (2, 1), (2, 2), (2, 4), (3, 0), (3, 2), (4, 0), (4, 2), (6, 0), (6, 2)]
     if M <= 32:
         cands += [(1, 0), (1, 1), (1, 2), (1, 4)]
     if M <= 64:
