@@ -154,9 +154,9 @@ def test_workspace_sizes():
     lib = N.lib()
 
     def v3_bytes(rows_per_seq, S=64, H=12, D=128):
-        n = S * rows_per_seq * H                 # partial rows x heads, each D + 2 fp32
+        n = S * rows_per_seq * H                 # partial rows x heads: D fp16, 2 fp32
         a256 = lambda x: (x + 255) // 256 * 256
-        return a256(n * D * 4) + 2 * a256(n * 4) + a256(S * 4)
+        return a256(n * D * 2) + 2 * a256(n * 4) + a256(S * 4)
 
     # fixed grid: 4096 / 256 = 16 split rows per sequence
     want = v3_bytes(16)

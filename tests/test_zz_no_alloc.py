@@ -64,7 +64,7 @@ def test_noalloc_equals_workspace_entry_on_two_calls(version, partition):
 
 
 def test_noalloc_rejects_a_batch_beyond_its_scratch():
-    st = _batch(96, 64, 256, seed=2)                            # v3: 96 x 32 split rows
+    st = _batch(192, 64, 256, seed=2)                           # v3: 192 x 32 split rows
     need = N.lib().ts_decode_workspace_bytes(3, st.T, H, KVH, D, int(st.max_seq_len), 0,
                                              N.cu_count(0))
     assert need > N.TS_NOALLOC_SCRATCH_BYTES

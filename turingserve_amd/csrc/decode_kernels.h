@@ -393,7 +393,7 @@ __device__ __forceinline__ void decode_mfma_body(
     int64_t o_st, const half_t* __restrict__ kc, const half_t* __restrict__ vc, int64_t NB,
     const int* __restrict__ bt, int64_t bt_st, int max_blocks, const int* __restrict__ seq_lens,
     int S, int H, int KVH, int G, int HG, float sl2, int cap_blocks, int part_blocks, int nx,
-    int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
+    int max_splits, half_t* __restrict__ ws_acc, float* __restrict__ ws_m,
     float* __restrict__ ws_l, int* __restrict__ ws_cnt,
     int bx, int bz, char* __restrict__ lds, const NewRows& nr = NewRows{},
     const int* __restrict__ smap = nullptr) {
@@ -688,7 +688,7 @@ __device__ __forceinline__ void decode_mfma_body(
       out[(int64_t)s * o_st + (int64_t)(head0 + hh) * D + d] = (half_t)(O / L);
     } else {
       const int64_t pidx = ((int64_t)s * max_splits + split_j) * H + head0 + hh;
-      ws_acc[pidx * D + d] = O;
+      ws_acc[pidx * D + d] = (half_t)(O / L);    // the split's own average, with its (m, l)
       if (d == 0) {
         ws_m[pidx] = M;
         ws_l[pidx] = L;
@@ -703,7 +703,7 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
     int64_t o_st, const half_t* __restrict__ kc, const half_t* __restrict__ vc, int64_t NB,
     const int* __restrict__ bt, int64_t bt_st, int max_blocks, const int* __restrict__ seq_lens,
     int S, int H, int KVH, int G, int HG, float sl2, int cap_blocks, int part_blocks, int nx,
-    int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
+    int max_splits, half_t* __restrict__ ws_acc, float* __restrict__ ws_m,
     float* __restrict__ ws_l, int* __restrict__ ws_cnt, const NewRows nr,
     const int* __restrict__ smap) {
   __shared__ __attribute__((aligned(16))) char lds[DecodeLds<D, NW>::BYTES];
@@ -713,8 +713,9 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
                                  (int)blockIdx.z, lds, nr, smap);
 }
 
-// Merge of the split partials (ops/triton_decode_attention.py:144-163): M = max m_j,
-// w_j = 2^(m_j - M), out = sum w_j acc_j / sum w_j l_j. One workgroup per (sequence, KV head,
+// Merge of the split partials (ops/triton_decode_attention.py:144-163): each split leaves its own
+// average A_j = acc_j / l_j (fp16) with its (m_j, l_j); M = max m_j, w_j = 2^(m_j - M) l_j,
+// out = sum w_j A_j / sum w_j. One workgroup per (sequence, KV head,
 // head group), one thread per 4 output dims of a head. A sequence's partials sit in rows
 // s * max_splits + j; the split count written by the first kernel is read first and only the
 // rows below it are requested (a second memory step, but a few hundred KB instead of kMergeChunk
@@ -726,7 +727,7 @@ constexpr int kMergeChunk = 16;
 
 template <int D>
 __device__ __forceinline__ void decode_merge_body(
-    const float* __restrict__ ws_acc, const float* __restrict__ ws_m,
+    const half_t* __restrict__ ws_acc, const float* __restrict__ ws_m,
     const float* __restrict__ ws_l, const int* __restrict__ ws_cnt, half_t* __restrict__ out,
     int64_t o_st, const int* __restrict__ seq_lens, int H, int G, int HG, int max_splits, int bx, int by) {
   constexpr int TPH = D / 4;                     // threads per head (4 dims each)
@@ -744,7 +745,7 @@ __device__ __forceinline__ void decode_merge_body(
     const bool active = hh < nh;
     const int64_t hoff = head0 + (active ? hh : 0);
     float mv[CH], lv[CH];
-    float4_t av[CH];
+    half4_t av[CH];                              // converted where used: the loads stay in flight
     if (len <= 0) {                              // padding row: zeros (ops/reference.py:99,104-105)
       if (active) st<half4_t>(out + (int64_t)s * o_st + (head0 + hh) * (int64_t)D + d0, half4_t{0, 0, 0, 0});
       continue;
@@ -759,11 +760,11 @@ __device__ __forceinline__ void decode_merge_body(
           const int64_t pidx = (row0 + j0 + u) * H + hoff;
           mv[u] = ws_m[pidx];
           lv[u] = ws_l[pidx];
-          av[u] = ld<float4_t>(ws_acc + pidx * D + d0);
+          av[u] = ld<half4_t>(ws_acc + pidx * D + d0);
         } else {
           mv[u] = -INFINITY;
           lv[u] = 0.f;
-          av[u] = float4_t{0.f, 0.f, 0.f, 0.f};
+          av[u] = half4_t{0, 0, 0, 0};
         }
       }
     };
@@ -781,9 +782,10 @@ __device__ __forceinline__ void decode_merge_body(
 #pragma unroll
       for (int u = 0; u < CH; ++u) {
         // rows past n are skipped, not weighted by 0: their stale contents may be inf or NaN
-        const float wt = fast_exp2(mv[u] - cm);
-        L = (j0 + u < n) ? L + wt * lv[u] : L;
-        const float4_t o2 = O + wt * av[u];
+        const float wt = fast_exp2(mv[u] - cm) * lv[u];
+        L = (j0 + u < n) ? L + wt : L;
+        const float4_t a = {(float)av[u][0], (float)av[u][1], (float)av[u][2], (float)av[u][3]};
+        const float4_t o2 = O + wt * a;
         O = (j0 + u < n) ? o2 : O;
       }
       M = cm;
@@ -794,7 +796,7 @@ __device__ __forceinline__ void decode_merge_body(
 
 template <int D>
 __global__ void __launch_bounds__(256) decode_merge_kernel(
-    const float* __restrict__ ws_acc, const float* __restrict__ ws_m,
+    const half_t* __restrict__ ws_acc, const float* __restrict__ ws_m,
     const float* __restrict__ ws_l, const int* __restrict__ ws_cnt, half_t* __restrict__ out,
     int64_t o_st, const int* __restrict__ seq_lens, int H, int G, int HG, int max_splits) {
   decode_merge_body<D>(ws_acc, ws_m, ws_l, ws_cnt, out, o_st, seq_lens, H, G, HG, max_splits,
@@ -867,14 +869,15 @@ struct WsLayout {
   size_t acc, m, l, cnt, total;
 };
 
-// [acc: rows * H * D fp32][m: rows * H][l: rows * H][count: S int32] with rows = S * max_splits:
-// split j of sequence s keeps query head h's partial in row s * max_splits + j, column h.
+// [avg: rows * H * D fp16][m: rows * H fp32][l: rows * H fp32][count: S int32] with
+// rows = S * max_splits: split j of sequence s keeps query head h's partial in row
+// s * max_splits + j, column h.
 static WsLayout ws_layout(const SplitPlan& p, int S, int H, int D) {
   WsLayout w{0, 0, 0, 0, 0};
   if (p.version != TS_DECODE_V3) return w;
   const size_t n = (size_t)S * p.max_splits * H;
   w.acc = 0;
-  w.m = align256(n * D * sizeof(float));
+  w.m = align256(n * D * sizeof(half_t));
   w.l = w.m + align256(n * sizeof(float));
   w.cnt = w.l + align256(n * sizeof(float));
   w.total = w.cnt + align256((size_t)S * sizeof(int));
@@ -937,7 +940,7 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
   }
   const WsLayout w = ws_layout(p, S, H, D);
   char* b = static_cast<char*>(ws);
-  float* ws_acc = reinterpret_cast<float*>(b + w.acc);
+  half_t* ws_acc = reinterpret_cast<half_t*>(b + w.acc);
   float* ws_m = reinterpret_cast<float*>(b + w.m);
   float* ws_l = reinterpret_cast<float*>(b + w.l);
   int* ws_cnt = reinterpret_cast<int*>(b + w.cnt);

@@ -40,7 +40,7 @@ struct RaggedArgs {
   float* pf_ws;
   // decode splits: launch ids [pf_launch, pf_launch + nslots * KVH * HG)
   int nslots, cap_blocks, nx, max_splits;
-  float* ws_acc;
+  half_t* ws_acc;
   float* ws_m;
   float* ws_l;
   int* ws_cnt;
@@ -219,7 +219,7 @@ extern "C" int ts_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
       char* ws = static_cast<char*>(workspace);
       a.pf_ws = reinterpret_cast<float*>(ws + r.dec_bytes);
       const WsLayout w = ws_layout(r.dec, num_decode, num_heads, head_dim);
-      a.ws_acc = reinterpret_cast<float*>(ws + w.acc);
+      a.ws_acc = reinterpret_cast<half_t*>(ws + w.acc);
       a.ws_m = reinterpret_cast<float*>(ws + w.m);
       a.ws_l = reinterpret_cast<float*>(ws + w.l);
       a.ws_cnt = reinterpret_cast<int*>(ws + w.cnt);
