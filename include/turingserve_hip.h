@@ -374,6 +374,28 @@ int ts_w8a16_add_rmsnorm(const void* x, int64_t ldx, const int8_t* wq, const voi
                          int32_t splits, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * The qkv product of a layer step followed by RoPE and the K/V cache write (model/qwen2.py:26-28,
+ * :89: linear(x, qkv_proj), then rope_ and kv_write, as ts_w8a16_gemm_v then ts_rope_kv_write):
+ *   qkv = fp16( x . (wq * scale)^T + bias )  [M, (H + 2 KVH) head_dim] at row stride ld_qkv,
+ * then q and k heads rotated in place at positions[m] and the rotated k and the v rows written to
+ * slot_mapping[m] (slot -1 or past the cache: not written), bit for bit what the two calls leave.
+ * With head_dim 128, a plan of wide tiles with one K split, K % 64 == 0, a 16-byte aligned
+ * weight and 16-byte aligned qkv rows, tables and caches, the rotation and the cache rows happen
+ * in the product's epilogue (one launch, the unrotated rows never reach memory); otherwise the two
+ * launches run. x, wq, scale, bias, M, K, variant, splits and the workspace as for
+ * ts_w8a16_gemm_v with N = (H + 2 KVH) head_dim; positions, tables and caches as for
+ * ts_rope_kv_write. No separate counterpart in the reference (its layer makes the three calls).
+ */
+int ts_w8a16_qkv_rope_kv_write(const void* x, int64_t ldx, const int8_t* wq, const void* scale,
+                               int32_t scale_is_fp16, const void* bias, void* qkv, int64_t ld_qkv,
+                               int32_t M, int32_t K, int32_t num_heads, int32_t num_kv_heads,
+                               int32_t head_dim, const int64_t* positions, const float* cos_table,
+                               const float* sin_table, int64_t max_position, void* k_cache,
+                               void* v_cache, int64_t num_blocks, const int64_t* slot_mapping,
+                               int32_t variant, int32_t splits, void* workspace,
+                               size_t workspace_bytes, void* stream);
+
+/*
  * Logits of the sampling rows through the int8 tied lm head, in one launch (plus the split-K
  * reduction when num_samples is small): for s < num_samples,
  *   logits[s][v] = (float) fp16( sum_k hidden[sample_indices[s]][k] * wq[v][k] * scale[v] )

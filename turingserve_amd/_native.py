@@ -42,6 +42,9 @@ SIGNATURES = {
     "ts_decode_attention": (ctypes.c_int, [_i32, _p, _i64, _i64, _p, _i64, _p, _p, _i64, _p, _i64,
                                            _i32, _p, _i32, _i32, _i32, _i32, _f32, _i32, _i32,
                                            _p, _sz, _p, _p, _sz]),
+    "ts_w8a16_qkv_rope_kv_write": (ctypes.c_int, [_p, _i64, _p, _p, _i32, _p, _p, _i64, _i32, _i32,
+                                                  _i32, _i32, _i32, _p, _p, _p, _i64, _p, _p,
+                                                  _i64, _p, _i32, _i32, _p, _sz, _p]),
     "ts_decode_split_map_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32, _i32, _i32]),
     "ts_decode_split_map": (ctypes.c_int, [_i32, _p, _i64, _i32, _i64, _p, _i32, _i32, _i32, _i32,
                                            _i32, _i32, _p, _sz, _p]),

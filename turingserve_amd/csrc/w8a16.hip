@@ -18,6 +18,7 @@
 //    LDS stages that all four wavefronts read.
 #include "common.h"
 #include "rmsnorm.h"
+#include "rope.h"
 
 namespace ts {
 
@@ -58,6 +59,19 @@ struct GemmIo {
   float* yf;
   int64_t ldyf;
   int glu;
+  // The qkv product with RoPE and the K/V cache write in its epilogue (rope_cos set): each
+  // 128-column tile is one head of 128 dims (q heads [0, rope_heads), then rope_kv_heads k and
+  // rope_kv_heads v heads); rows at positions[m], K / V rows to slots[m] (as rope_kv_write).
+  const int64_t* positions;
+  const float* rope_cos;
+  const float* rope_sin;
+  int64_t rope_max_pos;
+  int rope_heads;
+  int rope_kv_heads;
+  half_t* kc;
+  half_t* vc;
+  const int64_t* slots;
+  int64_t num_slots;
 };
 
 // silu(gate) * up from the fp16 GEMM outputs, with the rounding points of the unfused pair
@@ -872,6 +886,67 @@ __global__ void __launch_bounds__(256) w8a16_wide_kernel(
   wait_vmem_below<0>();
   // lane (h, r) of subtile (i, j), element e = 4a + c: Y[m][n] with m = m_base + 32 j + r and
   // n = weight_row(32 WN w + 32 i + 8a + 4h + c); the four c are one 8-byte store.
+  if constexpr (WN == 1 && WIDE) {   // the host fuses only products on the weight-DMA path
+    if (io.rope_cos != nullptr && !part) {
+      // RoPE + K/V cache write (the qkv product of a layer step, rope_kv_write_kernel's work):
+      // the tile is head hd, dims 0..127. Every wavefront puts its fp16 results in LDS, dims
+      // [0, 64) in stage 0 and [64, 128) in stage 1 (both idle now), rows in place; then each
+      // thread takes 8 rotation pairs of a row, rotates them with rope4 (q and k heads) exactly
+      // as rope_kv_write_kernel does from the same fp16 values, stores the row's 16-byte pieces
+      // and, for k and v heads, the cache row of its slot.
+      __syncthreads();                                  // every wavefront is done with the stages
+      half_t* x1s = reinterpret_cast<half_t*>(s_x0);    // [BM][64]
+      half_t* x2s = reinterpret_cast<half_t*>(s_x1);
+      static_assert(sizeof(s_x0) == (size_t)BM * 64 * sizeof(half_t), "a stage holds half a head");
+#pragma unroll
+      for (int j = 0; j < WM; ++j)
+#pragma unroll
+        for (int a4 = 0; a4 < 4; ++a4) {
+          const int nl = w * 32 + 8 * a4 + 4 * h;
+          const float4_t sc = *reinterpret_cast<const float4_t*>(&s_sc[nl]);
+          const float4_t bs = *reinterpret_cast<const float4_t*>(&s_bs[nl]);
+          const float o[4] = {acc[0][j][4 * a4] * sc[0] + bs[0], acc[0][j][4 * a4 + 1] * sc[1] + bs[1],
+                              acc[0][j][4 * a4 + 2] * sc[2] + bs[2], acc[0][j][4 * a4 + 3] * sc[3] + bs[3]};
+          const half4_t hv = {(half_t)o[0], (half_t)o[1], (half_t)o[2], (half_t)o[3]};
+          *reinterpret_cast<half4_t*>((nl < 64 ? x1s : x2s) + (32 * j + r) * 64 + (nl & 63)) = hv;
+        }
+      __syncthreads();
+      const int hd = blockIdx.x;
+      const int H = io.rope_heads, KVH = io.rope_kv_heads;
+      const bool rotate = hd < H + KVH;
+      const int kvh = hd < H + KVH ? hd - H : hd - H - KVH;   // cache head of k / v tiles
+      half_t* cache = hd < H ? nullptr : (hd < H + KVH ? io.kc : io.vc);
+      for (int it = tid; it < BM * 8; it += 256) {
+        const int m = it >> 3, g = it & 7;
+        const int mm = m_base + m;
+        if (mm >= M) continue;
+        half8_t y1 = *reinterpret_cast<const half8_t*>(x1s + m * 64 + 8 * g);
+        half8_t y2 = *reinterpret_cast<const half8_t*>(x2s + m * 64 + 8 * g);
+        if (rotate) {
+          const int64_t prow = rope_row(io.positions[mm], io.rope_max_pos) * 64 + 8 * g;
+          half4_t a1, a2, b1, b2;
+          rope4(lo4(y1), lo4(y2), ld<float4_t>(io.rope_cos + prow), ld<float4_t>(io.rope_sin + prow),
+                a1, a2);
+          rope4(hi4(y1), hi4(y2), ld<float4_t>(io.rope_cos + prow + 4),
+                ld<float4_t>(io.rope_sin + prow + 4), b1, b2);
+          y1 = half8_t{a1[0], a1[1], a1[2], a1[3], b1[0], b1[1], b1[2], b1[3]};
+          y2 = half8_t{a2[0], a2[1], a2[2], a2[3], b2[0], b2[1], b2[2], b2[3]};
+        }
+        half_t* dst = y + (int64_t)mm * ldy + n_tile + 8 * g;
+        st<half8_t>(dst, y1);
+        st<half8_t>(dst + 64, y2);
+        if (cache != nullptr) {
+          const int64_t slot = io.slots[mm];
+          if (slot >= 0 && slot < io.num_slots) {             // -1 = padding row
+            half_t* crow = cache + (((slot >> 4) * KVH + kvh) * kBlockSize + (slot & 15)) * 128 + 8 * g;
+            st<half8_t>(crow, y1);
+            st<half8_t>(crow + 64, y2);
+          }
+        }
+      }
+      return;
+    }
+  }
   if constexpr (WM % 2 == 0) {         // GLU tiles pair subtiles (no 32-row GLU tiles)
     if (glu && !part) {
       // Every wavefront puts its fp16 results in LDS (gate values in stage 0, up values in stage
@@ -1300,6 +1375,71 @@ extern "C" int ts_w8a16_gemm_v(const void* x, int64_t ldx, const int8_t* wq, con
   ts::clear_error();
   return w8a16_gemm_checked(x, ldx, wq, scale, scale_is_fp16, bias, y, ldy, M, N, K, variant,
                             splits, workspace, workspace_bytes, stream);
+}
+
+// The qkv product of a layer step with RoPE and the K/V cache write in the product's epilogue
+// (linear, then rope_kv_write: model/qwen2.py:26-28, :89). Fused when each 128-column tile is
+// one head (head_dim 128), the plan has one K split and the rows and tables are 16-byte
+// aligned; otherwise the product and ts_rope_kv_write run as two launches. Same results either
+// way: the epilogue rotates the product's own fp16 values with rope_kv_write's arithmetic.
+extern "C" int ts_w8a16_qkv_rope_kv_write(
+    const void* x, int64_t ldx, const int8_t* wq, const void* scale, int32_t scale_is_fp16,
+    const void* bias, void* qkv, int64_t ld_qkv, int32_t M, int32_t K, int32_t num_heads,
+    int32_t num_kv_heads, int32_t head_dim, const int64_t* positions, const float* cos_table,
+    const float* sin_table, int64_t max_position, void* k_cache, void* v_cache,
+    int64_t num_blocks, const int64_t* slot_mapping, int32_t variant, int32_t splits,
+    void* workspace, size_t workspace_bytes, void* stream) {
+  ts::clear_error();
+  TS_REQUIRE(num_heads > 0 && num_kv_heads > 0 && head_dim > 0, TS_ERR_INVALID_ARG,
+             "w8a16_qkv_rope_kv_write: bad head counts");
+  const int N = (num_heads + 2 * num_kv_heads) * head_dim;
+  if (M == 0) return TS_OK;
+  TS_REQUIRE(M > 0, TS_ERR_INVALID_ARG, "w8a16_qkv_rope_kv_write: M=%d < 0", M);
+  TS_REQUIRE(positions && cos_table && sin_table && max_position > 0 && k_cache && v_cache &&
+                 slot_mapping && num_blocks > 0,
+             TS_ERR_INVALID_ARG, "w8a16_qkv_rope_kv_write: null pointer, empty table or empty cache");
+  int cus = 0;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  int st = device_cu_count(s, &cus);
+  if (st != TS_OK) return st;
+  bool fuse = head_dim == 128 && variant_valid(variant, splits, M) && ld_qkv % 8 == 0 &&
+              aligned(qkv, 16) && aligned(cos_table, 16) && aligned(sin_table, 16) &&
+              aligned(k_cache, 16) && aligned(v_cache, 16);
+  if (fuse) {
+    const GemmPlan p = plan_gemm_v(M, N, K, cus, variant, splits);
+    fuse = !p.small && p.rt == 0 && p.splits == 1 && p.bn == 128 && K % kTileBK == 0 &&
+           aligned(wq, 16);                         // the weight-DMA wide kernel
+  }
+  if (!fuse) {
+    st = w8a16_gemm_checked(x, ldx, wq, scale, scale_is_fp16, bias, qkv, ld_qkv, M, N, K, variant,
+                            splits, workspace, workspace_bytes, stream);
+    if (st != TS_OK) return st;
+    return ts_rope_kv_write(qkv, ld_qkv, positions, cos_table, sin_table, max_position, M,
+                            num_heads, num_kv_heads, head_dim, k_cache, v_cache, num_blocks,
+                            slot_mapping, stream);
+  }
+  TS_REQUIRE(x && wq && scale, TS_ERR_INVALID_ARG, "w8a16_qkv_rope_kv_write: null pointer argument");
+  TS_REQUIRE(K > 0 && K % 8 == 0, TS_ERR_UNSUPPORTED,
+             "w8a16_qkv_rope_kv_write: K=%d is not a multiple of 8", K);
+  TS_REQUIRE(ldx >= K && ldx % 8 == 0 && ld_qkv >= N && aligned(x, 16) && aligned(wq, 8),
+             TS_ERR_INVALID_ARG,
+             "w8a16_qkv_rope_kv_write: x must be 16-byte aligned rows (ldx %% 8 == 0), wq 8-byte aligned");
+  GemmIo io{nullptr, 0, nullptr, 0, 0};
+  io.positions = positions;
+  io.rope_cos = cos_table;
+  io.rope_sin = sin_table;
+  io.rope_max_pos = max_position;
+  io.rope_heads = num_heads;
+  io.rope_kv_heads = num_kv_heads;
+  io.kc = static_cast<half_t*>(k_cache);
+  io.vc = static_cast<half_t*>(v_cache);
+  io.slots = slot_mapping;
+  io.num_slots = num_blocks * kBlockSize;
+  st = w8a16_launch(static_cast<const half_t*>(x), ldx, wq, scale, scale_is_fp16,
+                    static_cast<const half_t*>(bias), static_cast<half_t*>(qkv), ld_qkv, M, N, K,
+                    workspace, workspace_bytes, s, io, variant, splits);
+  if (st != TS_OK) return st;
+  return check_launch("w8a16_qkv_rope_kv_write");
 }
 
 // Workspace of the fused product + residual add + RMSNorm: the split-K partials when the plan

@@ -639,6 +639,59 @@ def rope_kv_write_(qkv: torch.Tensor, positions: torch.Tensor, cos: torch.Tensor
     return True
 
 
+def linear_rope_kv_write(x: torch.Tensor, lw: LinearWeight, positions: torch.Tensor,
+                         cos: torch.Tensor, sin: torch.Tensor, H: int, KVH: int, D: int,
+                         k_cache: torch.Tensor, v_cache: torch.Tensor,
+                         slot_mapping: torch.Tensor) -> torch.Tensor:
+    """qkv = linear(x, lw), then rope_kv_write_(qkv, ...) (model/qwen2.py:26-28, :89); returns
+    qkv with q and k rotated, the rotated k and the v rows in the caches, the same bits as the
+    calls it replaces. For int8 weights one call (ts_w8a16_qkv_rope_kv_write: the rotation and
+    the cache rows in the product's epilogue where the plan allows, else its two launches)."""
+    if not lw.quantized:
+        qkv = linear(x, lw)
+        if not rope_kv_write_(qkv, positions, cos, sin, H, KVH, D, k_cache, v_cache, slot_mapping):
+            rope_(qkv, positions, cos, sin, H, KVH, D)
+            T = qkv.shape[0]
+            kv_write(qkv[:, H * D:(H + KVH) * D].view(T, KVH, D), qkv[:, (H + KVH) * D:].view(T, KVH, D),
+                     k_cache, v_cache, slot_mapping)
+        return qkv
+    x = x.contiguous()
+    M, K = x.shape
+    wq, scale = lw.w, lw.scale
+    Nn = (H + 2 * KVH) * D
+    _require(x.dtype == torch.float16 and wq.dtype == torch.int8 and wq.is_contiguous() and
+             tuple(wq.shape) == (Nn, K), "linear_rope_kv_write: int8 [(H + 2 KVH) D, K] weight")
+    _require(scale.dtype in (torch.float32, torch.float16) and scale.numel() == Nn,
+             "linear_rope_kv_write: scale must be fp32 or fp16 [N]")
+    qkv = torch.empty(M, Nn, dtype=x.dtype, device=x.device)
+    if M == 0:
+        return qkv
+    _check_gpu(x, wq, scale, positions, cos, sin, k_cache, v_cache, slot_mapping)
+    NB, ckvh, cd = _check_cache(k_cache, v_cache)
+    _require(ckvh == KVH and cd == D, "linear_rope_kv_write: cache shape mismatch")
+    _require(cos.dtype == torch.float32 and sin.dtype == torch.float32 and cos.is_contiguous()
+             and sin.is_contiguous() and cos.shape == sin.shape and cos.shape[-1] == D // 2,
+             "linear_rope_kv_write: tables must be contiguous fp32 [max_len, D / 2]")
+    _require(slot_mapping.shape[0] >= M and positions.shape[0] >= M,
+             "linear_rope_kv_write: slot_mapping / positions shorter than x")
+    pos = positions if (positions.dtype == torch.int64 and positions.is_contiguous()) \
+        else positions.to(torch.int64).contiguous()
+    slots = slot_mapping if (slot_mapping.dtype == torch.int64 and slot_mapping.is_contiguous()) \
+        else slot_mapping.to(torch.int64).contiguous()
+    sc = scale.contiguous()
+    b = None if lw.b is None else lw.b.to(torch.float16).contiguous()
+    cus = N.cu_count(x.device.index or 0)
+    variant, splits = tuner.w8a16_choice(Nn, K, M)
+    ws_bytes = N.lib().ts_w8a16_workspace_bytes_v(M, Nn, K, variant, splits, cus)
+    ws = _workspace(ws_bytes, x.device)
+    N.check(N.lib().ts_w8a16_qkv_rope_kv_write(
+        _ptr(x), x.stride(0), _ptr(wq), _ptr(sc), 1 if sc.dtype == torch.float16 else 0, _ptr(b),
+        _ptr(qkv), qkv.stride(0), M, K, H, KVH, D, _ptr(pos), _ptr(cos), _ptr(sin), cos.shape[0],
+        _ptr(k_cache), _ptr(v_cache), NB, _ptr(slots), variant, splits, _ptr(ws), ws_bytes,
+        _stream(x)), "w8a16_qkv_rope_kv_write")
+    return qkv
+
+
 def silu_mul(gu: torch.Tensor) -> torch.Tensor:
     """silu(gate) * up for gu = [gate | up] rows (ops/triton_silu_mul.py:21-28)."""
     gu = _rows(gu, "silu_mul")

@@ -42,6 +42,7 @@ def _hip() -> SimpleNamespace:
     ns.rope_kv_write_ = h.rope_kv_write_
     ns.decode_rope_kv_write_attention = h.decode_rope_kv_write_attention
     ns.decode_split_map = h.decode_split_map
+    ns.linear_rope_kv_write = h.linear_rope_kv_write
     return ns
 
 

@@ -183,14 +183,24 @@ class Qwen2Model:
         decode split map (fused decode only), shared by every layer."""
         c, ops, lw = self.cfg, self.ops, self.w.layers[index]
         k_cache, v_cache = kv_cache[index, 0], kv_cache[index, 1]
-        qkv = ops.linear(x, lw.qkv_proj)
+        H, KVH, D = c.num_heads, c.num_kv_heads, c.head_dim
         a = None
+        qkv_rope = getattr(ops, "linear_rope_kv_write", None)
         if fused_decode and hasattr(ops, "decode_rope_kv_write_attention"):
-            a = ops.decode_rope_kv_write_attention(qkv, positions, self.cos, self.sin, c.num_heads,
-                                                   c.num_kv_heads, c.head_dim, k_cache, v_cache,
-                                                   meta, self.scale, split_map=split_map)
-        if a is None:                 # not fused, or a layout the fused launch does not take
-            q, _, _ = self._rotate_write(qkv, positions, k_cache, v_cache, meta.slot_mapping)
+            qkv = ops.linear(x, lw.qkv_proj)
+            a = ops.decode_rope_kv_write_attention(qkv, positions, self.cos, self.sin, H, KVH, D,
+                                                   k_cache, v_cache, meta, self.scale,
+                                                   split_map=split_map)
+            if a is None:             # a layout the fused launch does not take
+                q, _, _ = self._rotate_write(qkv, positions, k_cache, v_cache, meta.slot_mapping)
+        elif qkv_rope is not None:    # the product, RoPE and the cache write in one call
+            qkv = qkv_rope(x, lw.qkv_proj, positions, self.cos, self.sin, H, KVH, D, k_cache,
+                           v_cache, meta.slot_mapping)
+            q = qkv[:, :H * D].view(qkv.shape[0], H, D)
+        else:
+            q, _, _ = self._rotate_write(ops.linear(x, lw.qkv_proj), positions, k_cache, v_cache,
+                                         meta.slot_mapping)
+        if a is None:
             a = ops.paged_attention(q, k_cache, v_cache, meta, self.scale)
         x, residual = self._project_norm(a, lw.o_proj, residual, lw.post_attention_norm)
         return self._mlp_act(x, lw), residual
