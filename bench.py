@@ -223,6 +223,15 @@ def bench_decode(args, torch, K, synth):
     replays = max(replays, 1)
     attn_ms = timed(g_attn)
     other_ms = statistics.fmean(timed(g_other))
+    # warm: the same L steps all on layer 0's cache (74.9 MB of KV, inside the 256 MB Infinity
+    # Cache), for comparison with the cold headline
+    g_warm = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_warm, pool=pool):
+        if step_fn is fused_step:
+            build_map()
+        for _ in range(L):
+            step_fn(0)
+    warm_ms = statistics.median(timed(g_warm))
     # graph == eager: the last layer's output of the step graph against an eager two-call step
     ref_out = K.paged_attention(q, kv[L - 1, 0], kv[L - 1, 1], meta, scale,
                                 decode_version=version,
@@ -236,8 +245,9 @@ def bench_decode(args, torch, K, synth):
         "graph_equals_eager": same, "mean_ctx": float(st.seq_lens.float().mean()),
         "fused": not args.separate_kv_write, "split_map": not args.no_split_map,
         ("step_two_launch_ms" if not args.separate_kv_write else "step_fused_ms"): other_ms,
+        "warm_step_ms": warm_ms,
     }
-    del kv, g_step, g_attn, g_other, g_tail
+    del kv, g_step, g_attn, g_other, g_tail, g_warm
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return st, res
@@ -736,6 +746,7 @@ def main() -> int:
     log(f"step {r['step_s'] * 1e6:.2f} us (events {r['step_ev_ms'] * 1e3:.2f} us, "
         f"{'fused' if r['fused'] else 'two launches'}; {other_key} {r[other_key] * 1e3:.2f} us)  "
         f"attention alone {r['attn_ms_mean'] * 1e3:.2f} us ({attn_gbs:.0f} GB/s)  "
+        f"warm {r['warm_step_ms'] * 1e3:.2f} us  "
         f"graph==eager {r['graph_equals_eager']}")
     traffic = traffic_from_profiles("decode_c2_traffic" if r["fused"] else
                                     "decode_c2_traffic_two_launch")
@@ -754,6 +765,7 @@ def main() -> int:
                    "split_map": (f"built once per replay of {args.layers} layer steps, inside "
                                  f"the timed region" if r["fused"] and r["split_map"] else None),
                    other_key.replace("_ms", "_us"): round(r[other_key] * 1e3, 3),
+                   "warm_step_us": round(r["warm_step_ms"] * 1e3, 3),
                    "bytes_per_step": b["step"], "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": kern,
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
