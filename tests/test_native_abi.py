@@ -214,6 +214,20 @@ def test_split_map_sizes_and_checks():
     assert st == N.TS_ERR_INVALID_ARG and "null pointer" in N.last_error()
 
 
+def test_qkv_rope_kv_write_argument_checks():
+    lib = N.lib()
+    p = ctypes.c_void_p(256)            # never dereferenced: the call fails validation first
+    assert lib.ts_w8a16_qkv_rope_kv_write(None, 0, None, None, 0, None, None, 0, 0, 1536, 12, 2,
+                                          128, p, p, p, 16, p, p, 4, p, 0, 0, None, 0,
+                                          None) == N.TS_OK                  # no rows
+    st = lib.ts_w8a16_qkv_rope_kv_write(p, 1536, p, p, 0, None, p, 2048, 4, 1536, 12, 2, 128,
+                                        None, p, p, 16, p, p, 4, p, 0, 0, None, 0, None)
+    assert st == N.TS_ERR_INVALID_ARG and "null pointer" in N.last_error()
+    st = lib.ts_w8a16_qkv_rope_kv_write(p, 1536, p, p, 0, None, p, 2048, 4, 1536, 0, 2, 128,
+                                        p, p, p, 16, p, p, 4, p, 0, 0, None, 0, None)
+    assert st == N.TS_ERR_INVALID_ARG and "head counts" in N.last_error()
+
+
 def test_python_wrappers_reject_cpu_tensors():
     from turingserve_amd import hip_ops as K
 
