@@ -103,14 +103,16 @@ def test_map_entries_follow_the_schedule(name, version, partition):
         assert got[s] == want[s], f"slot {s}: {got[s]} != {want[s]}"
 
 
-@pytest.mark.parametrize("name", ["config2", "mixed", "long_one"])
+@pytest.mark.parametrize("name", ["config2", "mixed", "long_one", "long_one_capped"])
 @pytest.mark.parametrize("version,partition", [(None, None), ("v3", 256)])
 def test_decode_with_map_equals_without(name, version, partition):
     H, KVH, D = 12, 2, 128
-    lens = cases()[name]
+    lens = cases()[name.replace("_capped", "")]
     case = decode_step(lens, H, KVH, D, seed=7, pad=(1,))
     qkv, kc, vc, qsl, sl, bt, slots = case
     meta = meta_for(qsl, sl, bt, slots)
+    if name.endswith("_capped"):
+        meta.max_seq_len = 4096            # the fixed grid then covers 4096 of the 32768 tokens
     NB = kc.shape[0]
     q, k, v = views(qkv.to(DEV), H, KVH, D)
     scale = D ** -0.5
