@@ -30,6 +30,7 @@ past the 256 MB Infinity Cache).
 from __future__ import annotations
 
 import argparse
+import dataclasses
 import json
 import math
 import os
@@ -626,11 +627,14 @@ def bench_decode_model(torch, synth, reps: int = 10):
     layer's rope + kv_write + attention as one launch and, for comparison, as the separate calls
     (rope_kv_write, then paged_attention); and with o_proj / down_proj taken into the norm that
     consumes them (split-K partials reduced inside the norm launch) against the product and the
-    norm as separate calls ("separate_norm")."""
+    norm as separate calls ("separate_norm"). The tied lm head stays fp16 (the reference's default,
+    int8_lm_head=False); "fused_int8_head" times the fused step with the opt-in int8 head on the
+    fused logits launch, and its argmax agreement with the fp16 head is reported beside it."""
     import random as _r
 
     from turingserve_amd import get_ops
     from turingserve_amd.metadata import BatchItem, InputBuilder, SeqState
+    from turingserve_amd.quant import quantize
     from turingserve_amd.qwen2 import QWEN25_15B, Qwen2Model, random_weights
 
     dev = torch.device("cuda", 0)
@@ -642,9 +646,11 @@ def bench_decode_model(torch, synth, reps: int = 10):
     del ops_plain.decode_rope_kv_write_attention
     ops_norm = get_ops("hip")
     del ops_norm.linear_rmsnorm_residual
+    w_head = dataclasses.replace(w, lm_head_int8=quantize(w.embed_tokens.float()))
     models = {"fused": Qwen2Model(cfg, w, get_ops("hip"), max_model_len=8192),
               "separate": Qwen2Model(cfg, w, ops_plain, max_model_len=8192),
-              "separate_norm": Qwen2Model(cfg, w, ops_norm, max_model_len=8192)}
+              "separate_norm": Qwen2Model(cfg, w, ops_norm, max_model_len=8192),
+              "fused_int8_head": Qwen2Model(cfg, w_head, get_ops("hip"), max_model_len=8192)}
     nb = sum(-(-c // 16) for c in ctx) + 8
     kv = models["fused"].new_kv_cache(nb)
     kv.normal_(0.0, 0.5)
@@ -683,7 +689,9 @@ def bench_decode_model(torch, synth, reps: int = 10):
         del g_
     res["fused_equals_separate"] = bool(torch.equal(outs["fused"], outs["separate"]) and
                                        torch.equal(outs["fused"], outs["separate_norm"]))
-    del models, w, kv
+    res["int8_head_argmax_agreement"] = round(float(
+        (outs["fused_int8_head"].argmax(-1) == outs["fused"].argmax(-1)).float().mean()), 4)
+    del models, w, w_head, kv
     torch.cuda.empty_cache()
     return res
 
