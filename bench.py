@@ -67,6 +67,9 @@ def parse_args():
                                        "decode_model", "calibration"],
                     default=None,
                     help="run one workload alone (for profiling); prints its result as JSON")
+    ap.add_argument("--w8a16-m", default=None,
+                    help="comma-separated M values for --only w8a16 (default: every config 4 M; "
+                         "one M at a time keeps a counter run to one plan per shape)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="copy a 256 MiB buffer 8 times (the known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -446,19 +449,21 @@ def cold_copies(t, min_bytes: int = 512 * 2 ** 20) -> list:
     return [t] + [t.clone() for _ in range(n - 1)]
 
 
-def bench_w8a16(torch, K, synth):
-    """Config 4: every (M, N, K) point, timed cold (the weight cycles through copies whose total
-    exceeds the Infinity Cache, one copy per call inside the graph) and warm (one copy, replayed
-    20 times: it stays in the 256 MB cache). Roofline fraction from the cold time."""
+def bench_w8a16(torch, K, synth, ms=None):
+    """Config 4: every (M, N, K) point (or the M values in `ms`), timed cold (the weight cycles
+    through copies whose total exceeds the Infinity Cache, one copy per call inside the graph) and
+    warm (one copy, replayed 20 times: it stays in the 256 MB cache). Roofline fraction from the
+    cold time."""
     import itertools
 
     dev = torch.device("cuda", 0)
+    ms = list(ms or synth.W8A16_M)
     rows = []
     for (Nn, Kd) in synth.QWEN15_LINEAR_SHAPES:
         x_all, wq, sc = synth.w8a16_problem(max(synth.W8A16_M), Nn, Kd, seed=0)
         wq, sc = wq.to(dev), sc.to(dev)
         wqs = cold_copies(wq)
-        for M in synth.W8A16_M:
+        for M in ms:
             x = x_all[:M].to(dev)
             it = itertools.cycle(wqs)
             cold = time_graph(torch, lambda: K.w8a16_linear(x, next(it), sc, None), reps=3,
@@ -477,7 +482,7 @@ def bench_w8a16(torch, K, synth):
         del wqs
         torch.cuda.empty_cache()
     per_layer = {}
-    for M in synth.W8A16_M:
+    for M in ms:
         per_layer[str(M)] = round(sum(r["us"] for r in rows if r["M"] == M), 2)
     return {"rows": rows, "four_projections_us_cold": per_layer}
 
@@ -725,7 +730,9 @@ def main() -> int:
         fn = {"decode_model": lambda: bench_decode_model(torch, synth),
               "calibration": lambda: bench_calibration(torch, synth, args.layers),
               "prefill": lambda: bench_prefill(torch, K, synth),
-              "w8a16": lambda: bench_w8a16(torch, K, synth),
+              "w8a16": lambda: bench_w8a16(
+                  torch, K, synth,
+                  [int(m) for m in args.w8a16_m.split(",")] if args.w8a16_m else None),
               "logits": lambda: bench_logits(torch, K),
               "metadata": lambda: bench_metadata(torch, synth),
               "mixed": lambda: bench_mixed(torch, synth)}[args.only]
