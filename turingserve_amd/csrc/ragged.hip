@@ -49,10 +49,10 @@ struct RaggedArgs {
   int dm_launch, pm_x;
 };
 
-// Shares of the resident workgroup slots, in eighths: the prefill tiles' plan gets a round of
-// half of them; the decode splits (share 0) take the slots the prefill leaves.
+// Share of the resident workgroup slots, in eighths, that the prefill tiles' plan gets as one
+// round (half: measured best on the config 5 attention shape among 2-5 eighths); the decode
+// splits take the slots the prefill leaves.
 constexpr int kRaggedPfShare = 4;
-constexpr int kRaggedDecShare = 0;
 
 constexpr int kRaggedLds = 2 * TileLayout<128>::STAGE > DecodeLds<128, kDecodeWaves>::BYTES
                                ? 2 * TileLayout<128>::STAGE
@@ -114,7 +114,7 @@ static RaggedPlan ragged_plan(int num_seqs, int num_decode, int max_query_len, i
   if (r.dec.version != TS_DECODE_V3) return r;
   const int G = H / KVH, HG = (G + 15) / 16;
   const int64_t groups = (int64_t)KVH * HG;
-  const int64_t dec_slots = kRaggedDecShare == 0 ? slots - r.pf.est_wg : slots * kRaggedDecShare / 8;
+  const int64_t dec_slots = slots - r.pf.est_wg;
   int64_t nx = dec_slots / groups - num_decode;
   nx = nx < 16 ? 16 : (nx > 4096 ? 4096 : nx);
   r.dec.nx = (int)nx;
