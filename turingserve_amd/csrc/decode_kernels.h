@@ -716,7 +716,7 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
 // Merge of the split partials (ops/triton_decode_attention.py:144-163): each split leaves its own
 // average A_j = acc_j / l_j (fp16) with its (m_j, l_j); M = max m_j, w_j = 2^(m_j - M) l_j,
 // out = sum w_j A_j / sum w_j. One workgroup per (sequence, KV head,
-// head group), one thread per 4 output dims of a head. A sequence's partials sit in rows
+// head group), one thread per 8 output dims of a head (16-byte partial loads). A sequence's partials sit in rows
 // s * max_splits + j; the split count written by the first kernel is read first and only the
 // rows below it are requested (a second memory step, but a few hundred KB instead of kMergeChunk
 // rows for every sequence: measured faster than requesting a fixed chunk together with the
@@ -730,7 +730,7 @@ __device__ __forceinline__ void decode_merge_body(
     const half_t* __restrict__ ws_acc, const float* __restrict__ ws_m,
     const float* __restrict__ ws_l, const int* __restrict__ ws_cnt, half_t* __restrict__ out,
     int64_t o_st, const int* __restrict__ seq_lens, int H, int G, int HG, int max_splits, int bx, int by) {
-  constexpr int TPH = D / 4;                     // threads per head (4 dims each)
+  constexpr int TPH = D / 8;                     // threads per head (8 dims each)
   constexpr int HPP = 256 / TPH;                 // heads per pass
   constexpr int CH = kMergeChunk;
   const int s = bx, kvh = by / HG, hg = by % HG;
@@ -741,13 +741,17 @@ __device__ __forceinline__ void decode_merge_body(
   const int cnt = __builtin_amdgcn_readfirstlane(ws_cnt[s]);
   const int64_t row0 = (int64_t)s * max_splits;
   for (int hp = 0; hp < nh; hp += HPP) {
-    const int hh = hp + tid / TPH, d0 = (tid % TPH) * 4;
+    const int hh = hp + tid / TPH, d0 = (tid % TPH) * 8;
     const bool active = hh < nh;
     const int64_t hoff = head0 + (active ? hh : 0);
+    half_t* dst = out + (int64_t)s * o_st + (head0 + (active ? hh : 0)) * (int64_t)D + d0;
     float mv[CH], lv[CH];
-    half4_t av[CH];                              // converted where used: the loads stay in flight
+    half8_t av[CH];                              // converted where used: the loads stay in flight
     if (len <= 0) {                              // padding row: zeros (ops/reference.py:99,104-105)
-      if (active) st<half4_t>(out + (int64_t)s * o_st + (head0 + hh) * (int64_t)D + d0, half4_t{0, 0, 0, 0});
+      if (active) {                              // output rows are 8-byte aligned: two stores
+        st<half4_t>(dst, half4_t{0, 0, 0, 0});
+        st<half4_t>(dst + 4, half4_t{0, 0, 0, 0});
+      }
       continue;
     }
     const int n = cnt < 1 ? 1 : (cnt > max_splits ? max_splits : cnt);
@@ -760,17 +764,17 @@ __device__ __forceinline__ void decode_merge_body(
           const int64_t pidx = (row0 + j0 + u) * H + hoff;
           mv[u] = ws_m[pidx];
           lv[u] = ws_l[pidx];
-          av[u] = ld<half4_t>(ws_acc + pidx * D + d0);
+          av[u] = ld<half8_t>(ws_acc + pidx * D + d0);
         } else {
           mv[u] = -INFINITY;
           lv[u] = 0.f;
-          av[u] = half4_t{0, 0, 0, 0};
+          av[u] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
         }
       }
     };
     load_chunk(0);
     float M = -INFINITY, L = 0.f;
-    float4_t O = {0.f, 0.f, 0.f, 0.f};
+    float4_t O0 = {0.f, 0.f, 0.f, 0.f}, O1 = {0.f, 0.f, 0.f, 0.f};
     for (int j0 = 0; j0 < n; j0 += CH) {
       if (j0 > 0) load_chunk(j0);
       float cm = M;
@@ -778,19 +782,25 @@ __device__ __forceinline__ void decode_merge_body(
       for (int u = 0; u < CH; ++u) cm = (j0 + u < n) ? fmaxf(cm, mv[u]) : cm;
       const float alpha = fast_exp2(M - cm);     // M = -inf on the first chunk -> 0
       L *= alpha;
-      O *= alpha;
+      O0 *= alpha;
+      O1 *= alpha;
 #pragma unroll
       for (int u = 0; u < CH; ++u) {
         // rows past n are skipped, not weighted by 0: their stale contents may be inf or NaN
         const float wt = fast_exp2(mv[u] - cm) * lv[u];
         L = (j0 + u < n) ? L + wt : L;
-        const float4_t a = {(float)av[u][0], (float)av[u][1], (float)av[u][2], (float)av[u][3]};
-        const float4_t o2 = O + wt * a;
-        O = (j0 + u < n) ? o2 : O;
+        const float4_t a0 = {(float)av[u][0], (float)av[u][1], (float)av[u][2], (float)av[u][3]};
+        const float4_t a1 = {(float)av[u][4], (float)av[u][5], (float)av[u][6], (float)av[u][7]};
+        const float4_t o0 = O0 + wt * a0, o1 = O1 + wt * a1;
+        O0 = (j0 + u < n) ? o0 : O0;
+        O1 = (j0 + u < n) ? o1 : O1;
       }
       M = cm;
     }
-    if (active) st<half4_t>(out + (int64_t)s * o_st + (head0 + hh) * (int64_t)D + d0, to_half4(O / L));
+    if (active) {
+      st<half4_t>(dst, to_half4(O0 / L));
+      st<half4_t>(dst + 4, to_half4(O1 / L));
+    }
   }
 }
 
