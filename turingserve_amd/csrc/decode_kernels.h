@@ -742,16 +742,14 @@ __device__ __forceinline__ void decode_merge_body(
   const int64_t row0 = (int64_t)s * max_splits;
   for (int hp = 0; hp < nh; hp += HPP) {
     const int hh = hp + tid / TPH, d0 = (tid % TPH) * 8;
-    const bool active = hh < nh;
-    const int64_t hoff = head0 + (active ? hh : 0);
-    half_t* dst = out + (int64_t)s * o_st + (head0 + (active ? hh : 0)) * (int64_t)D + d0;
+    if (hh >= nh) continue;                      // no head for this thread (no barrier below)
+    const int64_t hoff = head0 + hh;
+    half_t* dst = out + (int64_t)s * o_st + (head0 + hh) * (int64_t)D + d0;
     float mv[CH], lv[CH];
     half8_t av[CH];                              // converted where used: the loads stay in flight
     if (len <= 0) {                              // padding row: zeros (ops/reference.py:99,104-105)
-      if (active) {                              // output rows are 8-byte aligned: two stores
-        st<half4_t>(dst, half4_t{0, 0, 0, 0});
-        st<half4_t>(dst + 4, half4_t{0, 0, 0, 0});
-      }
+      st<half4_t>(dst, half4_t{0, 0, 0, 0});     // output rows are 8-byte aligned: two stores
+      st<half4_t>(dst + 4, half4_t{0, 0, 0, 0});
       continue;
     }
     const int n = cnt < 1 ? 1 : (cnt > max_splits ? max_splits : cnt);
@@ -797,10 +795,8 @@ __device__ __forceinline__ void decode_merge_body(
       }
       M = cm;
     }
-    if (active) {
-      st<half4_t>(dst, to_half4(O0 / L));
-      st<half4_t>(dst + 4, to_half4(O1 / L));
-    }
+    st<half4_t>(dst, to_half4(O0 / L));
+    st<half4_t>(dst + 4, to_half4(O1 / L));
   }
 }
 
