@@ -307,8 +307,19 @@ __device__ __forceinline__ half_t reduce_partials(const float* __restrict__ part
                                                   int64_t total, int64_t i,
                                                   const void* __restrict__ scale, int scale_is_fp16,
                                                   const half_t* __restrict__ bias, int nn) {
+  // Up to 8 partials requested before any is summed (a plain loop waits for each load in turn),
+  // then summed in split order; rows past `splits` are skipped, not added as zeros (which would
+  // turn a -0 sum into +0).
+  constexpr int U = 8;
   float s = 0.f;
-  for (int k = 0; k < splits; ++k) s += part[(int64_t)k * total + i];
+  for (int k0 = 0; k0 < splits; k0 += U) {
+    float v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = k0 + u < splits ? part[(int64_t)(k0 + u) * total + i] : 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      if (k0 + u < splits) s += v[u];
+  }
   return finish_channel(s, scale, scale_is_fp16, bias, nn);
 }
 
@@ -357,10 +368,25 @@ __global__ void __launch_bounds__(kRowThreads) w8a16_reduce_rmsnorm_kernel(
   const int64_t total = (int64_t)M * N;
   auto load_x = [&](int i) {
     float4_t a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
-    for (int k = 0; k < splits; ++k) {
-      const float* pp = part + (int64_t)k * total + t * N + i;
-      a += ld<float4_t>(pp);
-      b += ld<float4_t>(pp + 4);
+    constexpr int U = 4;                         // partials requested before any is summed
+    for (int k0 = 0; k0 < splits; k0 += U) {
+      float4_t va[U], vb[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        if (k0 + u < splits) {                   // uniform over the workgroup
+          const float* pp = part + (int64_t)(k0 + u) * total + t * N + i;
+          va[u] = ld<float4_t>(pp);
+          vb[u] = ld<float4_t>(pp + 4);
+        } else {
+          va[u] = vb[u] = float4_t{0.f, 0.f, 0.f, 0.f};
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        if (k0 + u < splits) {                   // split order, as the plain reduction
+          a += va[u];
+          b += vb[u];
+        }
     }
     half8_t v;
 #pragma unroll
