@@ -98,9 +98,10 @@ int ts_kv_write(const void* k, const void* v,
  * version: TS_DECODE_*. partition: tokens per split for v3 (multiple of 16). partition > 0
  * gives the reference's fixed split grid: ceil(max_seq_len / partition) splits per sequence
  * (ops/triton_ops.py:50-51), tokens past max_seq_len are not attended. partition = 0 gives the
- * balanced schedule: the kernel numbers the splits of the whole batch densely and sizes them
- * from the batch's total block count, so every launched workgroup gets about the same work
- * and no split slot is idle (max_seq_len then only feeds TS_DECODE_AUTO's choice).
+ * own-length schedule: sequence s of nb_s blocks is cut into min(R, ceil(nb_s / 24)) splits of
+ * near-equal size, R = min(32, ceil(max_seq_len / 384)) (a longer sequence than max_seq_len gets
+ * R longer splits and is still attended in full), so a row's result does not depend on the rest
+ * of the batch; the splits of the batch are numbered densely, busy workgroups first.
  * max_seq_len: a host-side upper bound of seq_lens (inside graphs: max_model_len).
  * Workspace: ts_decode_workspace_bytes() bytes, 256-byte aligned (0 bytes for v1 / v2).
  * split_map / split_map_bytes: NULL / 0, or a map that ts_decode_split_map built from the same

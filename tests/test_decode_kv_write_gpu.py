@@ -73,7 +73,7 @@ def run_both(case, H, KVH, D, version, partition):
 
 
 @pytest.mark.parametrize("H,KVH,D,version,partition", [
-    (12, 2, 128, None, None),       # config 2 heads: balanced split-K, fused
+    (12, 2, 128, None, None),       # config 2 heads: own-length split-K, fused
     (12, 2, 128, "v2", None),       # one workgroup per (sequence, KV head), fused
     (12, 2, 128, "v3", 512),        # the reference's fixed partition grid, fused
     (12, 2, 128, "v1", None),       # no MFMA kernel: kv_write's own launch first

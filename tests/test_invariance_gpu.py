@@ -8,14 +8,16 @@ the same properties on its CPU twins (tests/correctness/test_paged_engine.py:46-
 * Prompts alone vs together: eight prompts of 5 ... 2047 tokens prefilled one by one and all in
   one step (shuffled blocks), every position sampled. Prefill work is split per sequence and
   query tile; the key-range split plan of the 128-row tile kernel (head_dim 128) depends on how
-  many tiles the step holds, so a row's fp32 merge order can change with its neighbours: the
-  largest logit difference must stay below BATCH_REL_MAX of the largest logit, the bar the
-  comparison with the reference namespace uses (a split's partial is kept as an fp16 row
-  average, so a split changes the attention output at fp16 rounding level). At head_dim 16 (no
-  key-range splits) the rows must be bit-identical.
-* Decode rows alone vs inside a 64-row batch: the balanced split schedule sizes every split from
-  the batch's total block count, so a row's splits (and its fp32 merge order) depend on the
-  batch; the output may differ in the last fp16 bit, never more (DECODE_ULPS).
+  many tiles the step holds, so a row's split boundaries can change with its neighbours (and
+  with them the lazy softmax's reference point, hence P's fp16 rounding), and the W8A16 products
+  pick their variant, and so their K summation order, from the step's row count. Split partials
+  are fp32 (O, m, l), as in the reference, but those two sources remain: the largest logit
+  difference must stay below BATCH_REL_MAX of the largest logit, the bar the comparison with the
+  reference namespace uses (measured up to 3.8e-3). At head_dim 16 (no key-range splits, and
+  products that take one plan at every row count here) the rows must be bit-identical.
+* Decode rows alone vs inside a 64-row batch (and shuffled): the decode split schedule cuts each
+  sequence from its own length only, so a row's splits and merge order do not depend on the
+  batch: the rows must be bit-identical.
 """
 
 from __future__ import annotations
@@ -39,7 +41,6 @@ D128 = Qwen2Config(768, 1536, 2, 6, 1, 4096, max_position_embeddings=4096)   # G
 LENGTHS = [5, 16, 17, 100, 333, 512, 1000, 2047]
 REF_REL_FRO, REF_REL_MAX = 5e-3, 1e-2
 BATCH_REL_MAX = REF_REL_MAX
-DECODE_ULPS = 2
 
 
 def _ids(n, seed, vocab):
@@ -111,14 +112,6 @@ def test_prompts_alone_vs_together(cfg):
           f"of the largest logit")
 
 
-def _head_ulps(a: np.ndarray, b: np.ndarray, D: int) -> float:
-    """Largest |a - b| in fp16 ulps of each head's largest magnitude (a, b: [H * D])."""
-    d = np.abs(a - b).reshape(-1, D)
-    scale = np.maximum(np.abs(a), np.abs(b)).reshape(-1, D).max(axis=1, keepdims=True)
-    ulp = 2.0 ** (np.floor(np.log2(np.maximum(scale, 2.0 ** -14))) - 10)
-    return float((d / ulp).max())
-
-
 def test_decode_rows_alone_vs_in_a_batch():
     H, KVH, D = 12, 2, 128
     g = torch.Generator().manual_seed(0)
@@ -135,12 +128,11 @@ def test_decode_rows_alone_vs_in_a_batch():
     meta_p = meta_of(qsl, sl[perm], bt[perm], 64, [1] * 64, 64)
     shuffled = K.paged_attention(q[perm], kc, vc, meta_p, D ** -0.5).float().cpu().numpy()
     picks = sorted(range(64), key=lambda i: ctx[i])[::8] + [int(np.argmax(ctx))]
-    worst = 0.0
     for i in picks:
         m1 = meta_of(qsl[:2], sl[i:i + 1], bt[i:i + 1], 1, [1], 1)
         one = K.paged_attention(q[i:i + 1], kc, vc, m1, D ** -0.5).float().cpu().numpy()[0]
         for other, what in ((batch[i], "in the batch"), (shuffled[order.index(i)], "shuffled")):
-            ulps = _head_ulps(one, other, D)
-            worst = max(worst, ulps)
-            assert ulps <= DECODE_ULPS, f"context {ctx[i]}: alone vs {what} differ by {ulps:.1f} ulps"
-    print(f"decode rows alone vs in a batch: at most {worst:.1f} fp16 ulps apart")
+            diff = int((one != other).sum())
+            assert diff == 0, f"context {ctx[i]}: alone vs {what}: {diff} values differ"
+    for i in range(64):
+        assert np.array_equal(batch[i], shuffled[order.index(i)]), f"row {i}: batch vs shuffled"

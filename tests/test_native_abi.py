@@ -154,23 +154,22 @@ def test_workspace_sizes():
     lib = N.lib()
 
     def v3_bytes(rows_per_seq, S=64, H=12, D=128):
-        n = S * rows_per_seq * H                 # partial rows x heads: D fp16, 2 fp32
+        n = S * rows_per_seq * H                 # partial rows x heads: D fp32 (acc), 2 fp32
         a256 = lambda x: (x + 255) // 256 * 256
-        return a256(n * D * 2) + 2 * a256(n * 4) + a256(S * 4)
+        return a256(n * D * 4) + 2 * a256(n * 4) + a256(S * 4)
 
     # fixed grid: 4096 / 256 = 16 split rows per sequence
     want = v3_bytes(16)
     assert lib.ts_decode_workspace_bytes(3, 64, 12, 2, 128, 4096, 256, 256) == want
     assert lib.ts_decode_workspace_bytes(2, 64, 12, 2, 128, 4096, 0, 256) == 0
     assert lib.ts_decode_workspace_bytes(1, 64, 12, 2, 128, 4096, 0, 256) == 0
-    # balanced v3 (partition 0): at most 32 split rows per sequence, whatever max_seq_len is
-    balanced = v3_bytes(32)
-    assert lib.ts_decode_workspace_bytes(3, 64, 12, 2, 128, 4096, 0, 256) == balanced
-    assert lib.ts_decode_workspace_bytes(3, 64, 12, 2, 128, 32768, 0, 256) == balanced
+    # own-length v3 (partition 0): ceil(max blocks / 24) split rows per sequence, at most 32
+    assert lib.ts_decode_workspace_bytes(3, 64, 12, 2, 128, 4096, 0, 256) == v3_bytes(11)
+    assert lib.ts_decode_workspace_bytes(3, 64, 12, 2, 128, 32768, 0, 256) == v3_bytes(32)
     # the automatic policy splits 64 x 2 (seq, KV head) workgroups < 512 resident ones, with the
-    # fixed grid when a partition is named and the balanced schedule otherwise ...
+    # fixed grid when a partition is named and the own-length schedule otherwise ...
     assert lib.ts_decode_workspace_bytes(0, 64, 12, 2, 128, 4096, 256, 256) == want
-    assert lib.ts_decode_workspace_bytes(0, 64, 12, 2, 128, 1024, 0, 256) == balanced
+    assert lib.ts_decode_workspace_bytes(0, 64, 12, 2, 128, 1024, 0, 256) == v3_bytes(3)
     # ... but not contexts of at most two minimum splits or a batch that fills the device
     assert lib.ts_decode_workspace_bytes(0, 64, 12, 2, 128, 256, 0, 256) == 0
     assert lib.ts_decode_workspace_bytes(0, 256, 12, 2, 128, 4096, 0, 256) == 0
@@ -193,12 +192,12 @@ def test_workspace_sizes():
 
 def test_split_map_sizes_and_checks():
     lib = N.lib()
-    # one header of 8 ints and 32 ints per launch slot of the v3 plan: the balanced schedule on
-    # 256 CUs launches 2 x 256 / 2 - 64 = 192 extra slots plus one per sequence, the fixed grid
-    # 16 slots per sequence at 4096 / 256
-    assert lib.ts_decode_split_map_bytes(3, 64, 12, 2, 128, 4096, 0, 256) == (8 + 256 * 32) * 4
+    # one header of 8 ints and 32 ints per launch slot of the v3 plan: the own-length schedule
+    # launches ceil(max blocks / 24) slots per sequence (11 at 4096 tokens, 3 at 1024), the
+    # fixed grid 16 slots per sequence at 4096 / 256
+    assert lib.ts_decode_split_map_bytes(3, 64, 12, 2, 128, 4096, 0, 256) == (8 + 64 * 11 * 32) * 4
     assert lib.ts_decode_split_map_bytes(3, 64, 12, 2, 128, 4096, 256, 256) == (8 + 64 * 16 * 32) * 4
-    assert lib.ts_decode_split_map_bytes(0, 64, 12, 2, 128, 1024, 0, 256) == (8 + 256 * 32) * 4
+    assert lib.ts_decode_split_map_bytes(0, 64, 12, 2, 128, 1024, 0, 256) == (8 + 64 * 3 * 32) * 4
     # no split, no map: v1 / v2, AUTO resolving to v2, more than 4096 sequences
     assert lib.ts_decode_split_map_bytes(2, 64, 12, 2, 128, 4096, 0, 256) == 0
     assert lib.ts_decode_split_map_bytes(1, 64, 12, 2, 128, 4096, 0, 256) == 0

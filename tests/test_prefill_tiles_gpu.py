@@ -6,7 +6,9 @@ kernel with its own split plan; split partials are combined by a merge kernel
 (ts_prefill_attention_ws). Every form is checked against the oracle (ops/reference.py:60-77,
 94-111) with the attention criterion of the other kernel tests, on shapes that put the diagonal,
 the key tail and the split boundaries in every position of a step; a NaN-filled workspace and
-NaN cache rows past seq_len must not reach the output.
+NaN cache rows past seq_len must not reach the output. An odd GQA group (14 / 2, 28 / 4, as in
+Qwen2-7B) puts the paired kernel in its two-tiles mode (256-row work items, 128-row units): the
+same checks run there, unsplit, split and with understated bounds.
 """
 
 from __future__ import annotations
@@ -27,7 +29,9 @@ pytestmark = pytest.mark.gpu
 H, KVH, D = 12, 2, 128
 
 
-def run_prefill(q, kc, vc, qsl, sl, bt, meta, ws: torch.Tensor | None, ws_bytes: int | None = None):
+def run_prefill(q, kc, vc, qsl, sl, bt, meta, ws: torch.Tensor | None, ws_bytes: int | None = None,
+                heads=(H, KVH)):
+    H, KVH = heads
     out = torch.full((q.shape[0], H * D), float("nan"), dtype=torch.float16, device=DEV)
     B = sl.shape[0]
     common = (q.data_ptr(), q.stride(0), q.stride(1), out.data_ptr(), out.stride(0), q.shape[0],
@@ -44,17 +48,17 @@ def run_prefill(q, kc, vc, qsl, sl, bt, meta, ws: torch.Tensor | None, ws_bytes:
     return out
 
 
-def setup(q_lens, prefixes, seed=0):
+def setup(q_lens, prefixes, seed=0, heads=(H, KVH)):
     seq = [p + n for p, n in zip(prefixes, q_lens)]
-    q, kc, vc, qsl, sl, bt = make_paged(seq, H, KVH, D, list(q_lens), seed=seed)
+    q, kc, vc, qsl, sl, bt = make_paged(seq, heads[0], heads[1], D, list(q_lens), seed=seed)
     meta = meta_of(qsl, sl, bt, 0, list(q_lens), q.shape[0])
     dev = [x.to(DEV) for x in (q, kc, vc, qsl, sl, bt)]
     ref = oracle_attn(q, kc, vc, qsl, sl, bt, D ** -0.5)
     return dev, meta, ref
 
 
-def ws_bytes_for(meta, P):
-    return N.lib().ts_prefill_workspace_bytes(P, H, D, int(meta.max_query_len),
+def ws_bytes_for(meta, P, heads=(H, KVH)):
+    return N.lib().ts_prefill_workspace_bytes(P, heads[0], D, int(meta.max_query_len),
                                               int(meta.max_seq_len), N.cu_count(0))
 
 
@@ -74,6 +78,37 @@ def test_tiled_prefill_split_and_unsplit(q_lens, prefixes):
     ws = torch.empty(max(nb, 16), dtype=torch.uint8, device=DEV)
     out2 = run_prefill(q, kc, vc, qsl, sl, bt, meta, ws)
     assert_attn(out2, ref, "split")
+
+
+@pytest.mark.parametrize("heads", [(14, 2), (28, 4)], ids=["14-2", "28-4"])
+@pytest.mark.parametrize("q_lens,prefixes", [
+    ([129], [63]), ([512], [1037]), ([700], [3000]), ([1024], [6000]),
+    ([640, 512], [5000, 7000]),
+])
+def test_odd_group_prefill_split_and_unsplit(heads, q_lens, prefixes):
+    """Odd GQA groups: the paired kernel's two-tiles mode unsplit (no workspace), and with a
+    workspace the tile kernel's split plan (short key ranges per slot) or the paired kernel's
+    stream-K plan merged by prefill_pair_merge_kernel (the long ones; the cases cover both
+    routes for each group, test_odd_group_cases_cover_both_routes)."""
+    (q, kc, vc, qsl, sl, bt), meta, ref = setup(q_lens, prefixes, seed=sum(q_lens), heads=heads)
+    out1 = run_prefill(q, kc, vc, qsl, sl, bt, meta, None, heads=heads)
+    assert_attn(out1, ref, f"unsplit {heads}")
+    nb = ws_bytes_for(meta, len(q_lens), heads)
+    assert nb > 0
+    paired = _paired_route(int(meta.max_query_len), int(meta.max_seq_len), *heads, N.cu_count(0),
+                           P=len(q_lens))
+    ws = torch.empty(nb, dtype=torch.uint8, device=DEV)
+    out2 = run_prefill(q, kc, vc, qsl, sl, bt, meta, ws, heads=heads)
+    assert_attn(out2, ref, f"split {heads} ({'stream-K' if paired else 'tile'})")
+
+
+def test_odd_group_cases_cover_both_routes():
+    cases = [([129], [63]), ([512], [1037]), ([700], [3000]), ([1024], [6000]),
+             ([640, 512], [5000, 7000])]
+    for heads in ((14, 2), (28, 4)):
+        routes = {_paired_route(max(ql), max(p + n for p, n in zip(pf, ql)), *heads,
+                                N.cu_count(0), P=len(ql)) for ql, pf in cases}
+        assert routes == {True, False}, heads
 
 
 def test_tiled_prefill_splits_when_it_should():
@@ -130,10 +165,12 @@ def test_tiled_prefill_chunked_prompt_through_paged_attention():
         assert_attn(out, ref, f"chunk {ci} (prefix {prefix}, {n} rows)")
 
 
-@pytest.mark.parametrize("D,n_decode,mql,q_len,prefix", [
-    (64, 0, 300, 600, 600), (128, 0, 300, 600, 600), (128, 0, 128, 600, 600),
-    (128, 4, 300, 600, 600), (128, 0, 640, 1280, 8000)])
-def test_understated_bounds_give_nan_rows_not_stale_memory(D, n_decode, mql, q_len, prefix):
+@pytest.mark.parametrize("D,n_decode,mql,q_len,prefix,heads", [
+    (64, 0, 300, 600, 600, (12, 2)), (128, 0, 300, 600, 600, (12, 2)),
+    (128, 0, 128, 600, 600, (12, 2)), (128, 4, 300, 600, 600, (12, 2)),
+    (128, 0, 640, 1280, 8000, (12, 2)), (128, 0, 300, 600, 600, (14, 2)),
+    (128, 0, 640, 1280, 8000, (14, 2))])
+def test_understated_bounds_give_nan_rows_not_stale_memory(D, n_decode, mql, q_len, prefix, heads):
     """max_query_len below a chunk's real q_len (a caller bug): the rows the plan does not cover
     come out as NaN, the covered rows are still right.
 
@@ -142,12 +179,13 @@ def test_understated_bounds_give_nan_rows_not_stale_memory(D, n_decode, mql, q_l
     * head_dim 128, prefill only, many steps per slot: the paired kernel's stream-K plan shares
       the sequence's real steps over its launch slots, so every tile is computed; a tile whose
       segments run past the workspace the host bounds sized gets NaN rows. Tiles are numbered
-      longest first, so those are the lowest tiles: the NaN rows are a tile-aligned prefix.
+      longest first, so those are the lowest tiles: the NaN rows are a tile-aligned prefix
+      (128-row tiles with an even GQA group, 256-row ones with an odd group).
     * head_dim 128 with decode rows (one-launch ragged kernel): as the tile kernel.
     * head_dim < 128: the kernel covers rows from 0 up."""
     from turingserve_amd.metadata import AttentionMetadata
 
-    Hh, KV = 12, 2
+    Hh, KV = heads
     seq_len = prefix + q_len
     seq = [300 + 97 * i for i in range(n_decode)] + [seq_len]
     ql = [1] * n_decode + [q_len]
@@ -164,10 +202,11 @@ def test_understated_bounds_give_nan_rows_not_stale_memory(D, n_decode, mql, q_l
     rows_i = torch.arange(q_len)
     tiles = -(-q_len // 128)
     cus = N.cu_count(0)
-    paired = D == 128 and n_decode == 0 and _paired_route(mql, seq_len, Hh, cus)
+    paired = D == 128 and n_decode == 0 and _paired_route(mql, seq_len, Hh, KV, cus)
     assert paired == (prefix == 8000), "the cases cover each route once"
     if paired:
-        covered = rows_i >= 128 * _stream_k_nan_tiles(mql, q_len, seq_len, Hh, cus)
+        tr = 128 if (Hh // KV) % 2 == 0 else 256
+        covered = rows_i >= tr * _stream_k_nan_tiles(mql, q_len, seq_len, Hh, KV, cus)
     elif D == 128:
         covered = rows_i >= 128 * (tiles - (-(-mql // 128)))   # the longest cdiv(mql, 128) tiles
     else:
@@ -177,26 +216,33 @@ def test_understated_bounds_give_nan_rows_not_stale_memory(D, n_decode, mql, q_l
     assert_attn(out[rows.to(DEV)], ref[rows.numpy()], f"covered rows, D {D}")
 
 
-def _paired_route(mql: int, msl: int, H: int, cus: int) -> bool:
-    """Whether a prefill-only head_dim 128 launch (even GQA group) takes the paired kernel: its
-    stream-K plan gives each of the cus // (H / 2) slots of a sequence at least 16 of the
-    cdiv(mql, 128) * cdiv(msl, 64) key steps the host bounds allow."""
-    slots = cus // (H // 2)
-    return -(-mql // 128) * -(-max(msl, mql) // 64) >= 16 * slots
+def _pair_shape(H: int, KVH: int) -> tuple[int, int]:
+    """(rows per work item, work items per sequence) of the paired kernel: two query heads of
+    128 rows with an even GQA group, two 128-row tiles of one head with an odd group."""
+    return (128, H // 2) if (H // KVH) % 2 == 0 else (256, H)
 
 
-def _stream_k_nan_tiles(mql: int, q_len: int, seq_len: int, H: int, cus: int) -> int:
+def _paired_route(mql: int, msl: int, H: int, KVH: int, cus: int, P: int = 1) -> bool:
+    """Whether a prefill-only head_dim 128 launch with a workspace takes the paired kernel: its
+    stream-K plan gives each of the cus // items slots of a work item at least 16 of the
+    cdiv(mql, tr) * cdiv(msl, 64) key steps the host bounds allow."""
+    tr, items = _pair_shape(H, KVH)
+    slots = cus // (items * P)
+    return -(-mql // tr) * -(-max(msl, mql) // 64) >= 16 * slots
+
+
+def _stream_k_nan_tiles(mql: int, q_len: int, seq_len: int, H: int, KVH: int, cus: int) -> int:
     """Lowest 128-row tiles (two heads per work item) of one prefill sequence that the stream-K
     plan sized for max_query_len = mql leaves as NaN: tiles, longest first, share the sequence's
     steps over `slots` launch slots; the tile at position pos with segments pos + k,
     k = G // T .. (G + n - 1) // T, is NaN when it has more than one segment and one of them is
     past the workspace's tiles_h + slots segments."""
-    items = H // 2
+    tr, items = _pair_shape(H, KVH)
     slots = cus // items
-    seg_cap = -(-mql // 128) + slots
-    tiles = -(-q_len // 128)
+    seg_cap = -(-mql // tr) + slots
+    tiles = -(-q_len // tr)
     prefix = seq_len - q_len
-    steps = [-(-min(prefix + min((t + 1) * 128, q_len), seq_len) // 64) for t in range(tiles)]
+    steps = [-(-min(prefix + min((t + 1) * tr, q_len), seq_len) // 64) for t in range(tiles)]
     per = -(-sum(steps) // slots)
     nan, g = [], 0
     for pos in range(tiles):

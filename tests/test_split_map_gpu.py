@@ -3,12 +3,13 @@
 The map is this library's own schedule table (the reference's fixed split grid needs no lookup,
 ops/triton_decode_attention.py:187-200), so it is pinned two ways: its entries against a
 restatement of the split schedule written from the rule the kernel documents (dense split
-numbering in sequence order, balanced P = ceil(total blocks / nx) rounded up to 8 blocks, a
-sequence longer than max_splits * P cut into max_splits splits of a multiple of 8 blocks, fixed
-partitions capped at the launched grid), and every decode call that reads it against the same
-call without it, bit for bit: outputs and caches (the attention arithmetic is unchanged, only
-where a workgroup learns its split from). A map built for another plan must be ignored, a map too
-small for the plan rejected.
+numbering in sequence order; by default a sequence of nb blocks cut into
+n = min(max_splits, ceil(nb / 24)) splits of P = ceil(nb / n) rounded up to 8 blocks, its own
+length alone deciding; fixed partitions capped at the launched grid), and every decode call that
+reads it against the same call without it, bit for bit: outputs and caches (the attention
+arithmetic is unchanged, only where a workgroup learns its split from). A map built for another
+plan must be ignored, a map too small for the plan rejected, and a map built for another step
+(other lengths, same plan) must poison the rows it would attend wrongly.
 """
 
 from __future__ import annotations
@@ -28,18 +29,24 @@ pytestmark = pytest.mark.gpu
 HEADER, ENTRY, MAGIC = 8, 32, 0x314D5354
 
 
-def expected_entries(lens, bt, NB, nslots, part_blocks, nx, max_splits, cap_blocks):
+OWN_PART = 24                                   # the own-length schedule's longest split
+
+
+def own_part(nb, max_splits):
+    """P_s of the own-length schedule for a sequence of nb blocks."""
+    n = min(max(-(-nb // OWN_PART), 1), max_splits)
+    return max(8, (-(-nb // n) + 7) // 8 * 8)
+
+
+def expected_entries(lens, bt, NB, nslots, part_blocks, max_splits, cap_blocks):
     """The map entries of the schedule, one list of 32 ints per launch slot."""
     cap = cap_blocks * 16
     L = [min(max(int(x), 0), cap) for x in lens]
     nb = [(x + 15) // 16 for x in L]
-    r8 = lambda b: (b + 7) // 8 * 8
-    balanced = part_blocks <= 0
-    P = max(8, r8(-(-sum(nb) // nx))) if balanced else part_blocks
     clamp = lambda b: b if 0 <= b < NB else 0
     ent, first = [], 0
     for i, nbi in enumerate(nb):
-        ps = max(r8(-(-nbi // max_splits)), P) if balanced else P
+        ps = own_part(nbi, max_splits) if part_blocks <= 0 else part_blocks
         n = -(-nbi // ps)
         for j in range(n):
             lo, hi = j * ps, min(j * ps + ps, nbi)
@@ -55,6 +62,24 @@ def expected_entries(lens, bt, NB, nslots, part_blocks, nx, max_splits, cap_bloc
     return ent + [[-1] + [0] * 31] * (nslots - len(ent))
 
 
+def abi_decode(q, kc, vc, meta, H, KVH, D, scale, smap, version="v3", partition=0):
+    """ts_decode_attention on the step's caches, with the split map smap (or none)."""
+    bt_d, sl_d = meta.block_tables.to(torch.int32), meta.seq_lens.to(torch.int32)
+    S = sl_d.shape[0]
+    code, part = K._decode_plan(S, int(meta.max_seq_len), version, partition)
+    wsb = N.lib().ts_decode_workspace_bytes(code, S, H, KVH, D, int(meta.max_seq_len), part,
+                                            N.cu_count(0))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=DEV)
+    o = torch.empty(S, H * D, dtype=torch.float16, device=DEV)
+    ptr, nb = (None, 0) if smap is None else (smap[0].data_ptr(), smap[1])
+    N.check(N.lib().ts_decode_attention(
+        code, q.data_ptr(), q.stride(0), q.stride(1), o.data_ptr(), o.stride(0),
+        kc.data_ptr(), vc.data_ptr(), kc.shape[0], bt_d.data_ptr(), bt_d.stride(0),
+        bt_d.shape[1], sl_d.data_ptr(), S, H, KVH, D, scale, int(meta.max_seq_len), part,
+        ws.data_ptr(), wsb, torch.cuda.current_stream().cuda_stream, ptr, nb), "decode")
+    return o
+
+
 def build(meta, H, KVH, D, NB, version=None, partition=None):
     return K.decode_split_map(meta, H, KVH, D, NB, torch.device(DEV), decode_version=version,
                               partition=partition)
@@ -68,7 +93,7 @@ def cases():
     return {
         "config2": [int(x) for x in c2.seq_lens],
         "mixed": mixed,
-        "long_one": [32768, 40, 700, 5],        # 2048 blocks > 32 x P: P_s grows to 64 blocks
+        "long_one": [32768, 40, 700, 5],        # 2048 blocks over 32 splits: P_s grows to 64
         "few": [4000, 2500],
     }
 
@@ -91,13 +116,14 @@ def test_map_entries_follow_the_schedule(name, version, partition):
     m = buf.cpu().tolist()
     nslots = (nbytes // 4 - HEADER) // ENTRY
     assert m[0] == MAGIC and m[1] == len(lens) and m[2] == nslots
-    part_blocks, nx, max_splits, cap = m[3], m[4], m[5], m[6]
+    part_blocks, max_splits, cap = m[3], m[5], m[6]
+    assert m[4] == 0 and m[7] == 0
     if part_blocks > 0:                      # the fixed grid covers ceil(max_seq_len / partition)
         max_blk = -(-int(meta.max_seq_len) // 16)
         assert cap == min(-(-max_blk // part_blocks) * part_blocks, bt.shape[1])
     else:
         assert cap == bt.shape[1]
-    want = expected_entries(lens, bt, NB, nslots, part_blocks, nx, max_splits, cap)
+    want = expected_entries(lens, bt, NB, nslots, part_blocks, max_splits, cap)
     got = [m[HEADER + s * ENTRY: HEADER + (s + 1) * ENTRY] for s in range(nslots)]
     for s in range(nslots):
         assert got[s] == want[s], f"slot {s}: {got[s]} != {want[s]}"
@@ -183,8 +209,8 @@ def test_map_of_another_plan_is_ignored_and_a_short_map_rejected():
     q, k, v = views(qkv.to(DEV), H, KVH, D)
     scale = D ** -0.5
     fixed = build(meta, H, KVH, D, NB, "v3", 256)       # 64 x 16 slots
-    balanced = build(meta, H, KVH, D, NB, "v3", 0)      # 256 slots
-    assert fixed[1] > balanced[1]
+    own = build(meta, H, KVH, D, NB, "v3", 0)           # 64 x ceil(max blocks / 24) slots
+    assert fixed[1] > own[1]
     kc1, vc1 = kc.to(DEV), vc.to(DEV)
     ref = K.decode_kv_write_attention(q, k, v, kc1, vc1, meta, scale, decode_version="v3",
                                       partition=0)
@@ -195,7 +221,48 @@ def test_map_of_another_plan_is_ignored_and_a_short_map_rejected():
     assert torch.equal(out, ref) and torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
     with pytest.raises(ValueError, match="split map"):
         K.decode_kv_write_attention(q, k, v, kc.to(DEV), vc.to(DEV), meta, scale,
-                                    decode_version="v3", partition=256, split_map=balanced)
+                                    decode_version="v3", partition=256, split_map=own)
+
+
+@pytest.mark.parametrize("fused", [False, True])
+def test_map_of_the_previous_step_poisons_the_rows_it_would_misread(fused):
+    """A map is built from one step's seq_lens and block tables. Passed to a later step of the
+    same batch size (same plan, so the header matches), every row whose length moved on comes
+    out NaN instead of being attended with the old split ranges; rows whose length did not move
+    are unaffected and equal the map-free call."""
+    H, KVH, D = 12, 2, 128
+    lens = cases()["config2"]
+    qkv, kc, vc, qsl, sl, bt, slots = decode_step(lens, H, KVH, D, seed=5)
+    meta = meta_for(qsl, sl, bt, slots)
+    NB = kc.shape[0]
+    q, k, v = views(qkv.to(DEV), H, KVH, D)
+    scale = D ** -0.5
+    moved = [i % 3 != 0 for i in range(len(lens))]      # two rows in three advanced one token
+    prev = [x - 1 if m else x for x, m in zip(lens, moved)]
+    meta_prev = meta_for(qsl, torch.tensor(prev, dtype=sl.dtype), bt, slots)
+    meta_prev.max_seq_len = meta.max_seq_len                 # the same plan as this step's
+    stale = build(meta_prev, H, KVH, D, NB, "v3", 0)
+    fresh = build(meta, H, KVH, D, NB, "v3", 0)
+    assert stale is not None and stale[1] == fresh[1]
+    res = {}
+    for name, smap in (("none", None), ("fresh", fresh), ("stale", stale)):
+        kc1, vc1 = kc.to(DEV), vc.to(DEV)
+        if fused:
+            res[name] = K.decode_kv_write_attention(q, k, v, kc1, vc1, meta, scale,
+                                                    decode_version="v3", partition=0,
+                                                    split_map=smap)
+        else:                                    # the attention call alone, through the C ABI
+            K.kv_write(k, v, kc1, vc1, meta.slot_mapping)
+            res[name] = abi_decode(q, kc1, vc1, meta, H, KVH, D, scale, smap)
+    torch.cuda.synchronize()
+    assert torch.equal(res["fresh"], res["none"])
+    assert torch.isfinite(res["none"]).all()
+    for i, m in enumerate(moved):
+        row = res["stale"][i]
+        if m:
+            assert torch.isnan(row).all(), f"row {i} (moved) attended with a stale map"
+        else:
+            assert torch.equal(row, res["none"][i]), f"row {i} (unmoved) changed"
 
 
 def test_map_built_inside_graph_replays():

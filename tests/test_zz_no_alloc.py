@@ -26,7 +26,7 @@ def _batch(num_seqs, lo, hi, seed):
     return st
 
 
-def _call(st, noalloc, version=0, partition=0):
+def _call(st, noalloc, version=0, partition=0, max_seq_len=None):
     kc, vc = st.k_cache.to(DEV), st.v_cache.to(DEV)
     qkv = st.qkv.to(DEV)
     q, k, v = st.views(qkv)
@@ -39,7 +39,7 @@ def _call(st, noalloc, version=0, partition=0):
             k.stride(0), k.stride(1), v.stride(0), v.stride(1), slots.data_ptr(),
             out.data_ptr(), out.stride(0), kc.data_ptr(), vc.data_ptr(), kc.shape[0],
             bt.data_ptr(), bt.stride(0), bt.shape[1], sl.data_ptr(), S, H, KVH, D, D ** -0.5,
-            int(m.max_seq_len), partition)
+            int(m.max_seq_len if max_seq_len is None else max_seq_len), partition)
     lib = N.lib()
     if noalloc:
         status = lib.ts_decode_attention_kv_write_noalloc(*head, stream)
@@ -64,11 +64,12 @@ def test_noalloc_equals_workspace_entry_on_two_calls(version, partition):
 
 
 def test_noalloc_rejects_a_batch_beyond_its_scratch():
-    st = _batch(192, 64, 256, seed=2)                           # v3: 192 x 32 split rows
-    need = N.lib().ts_decode_workspace_bytes(3, st.T, H, KVH, D, int(st.max_seq_len), 0,
-                                             N.cu_count(0))
+    # a host bound of 32768 tokens: the own-length plan reserves 32 split rows per sequence,
+    # 192 x 32 rows of 12 heads, more than the scratch holds
+    st = _batch(192, 64, 256, seed=2)
+    need = N.lib().ts_decode_workspace_bytes(3, st.T, H, KVH, D, 32768, 0, N.cu_count(0))
     assert need > N.TS_NOALLOC_SCRATCH_BYTES
-    status, out, kc, vc = _call(st, True, version=3)
+    status, out, kc, vc = _call(st, True, version=3, max_seq_len=32768)
     assert status == N.TS_ERR_WORKSPACE
     assert "static scratch" in N.last_error()
     assert torch.isnan(out).all()                              # nothing was launched

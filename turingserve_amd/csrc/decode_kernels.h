@@ -109,16 +109,18 @@ __global__ void __launch_bounds__(64) decode_v1_kernel(
 // Dense split map of v3. Sequence s has nb_s = ceil(len_s / 16) blocks (len_s clamped to
 // cap_blocks * 16) cut into n_s = ceil(nb_s / P_s) splits of P_s blocks; the splits of the batch
 // are numbered densely in sequence order (split j of sequence s is launch slot C_s + j with
-// C_s = sum_{t<s} n_t), so the launch carries no idle workgroups. With a caller partition,
-// P_s = partition. With part_blocks == 0 (the balanced schedule) P = ceil(TB / nx) for the
-// batch's total TB blocks, rounded up to a multiple of kMinPartBlocks (one pair per wavefront,
-// so every wavefront of a full split gets the same number of pairs), and a sequence longer than
-// max_splits * P uses P_s = the multiple of kMinPartBlocks that keeps n_s <= max_splits. Either
-// way sum_s n_s <= nx + S and n_s <= max_splits, and every workgroup gets about the same work.
+// C_s = sum_{t<s} n_t), so the busy workgroups come first in the launch. With a caller
+// partition, P_s = partition. With part_blocks == 0 (the default, own-length schedule) a
+// sequence is cut into n = min(max_splits, ceil(nb_s / kOwnPartBlocks)) splits of equal size,
+// P_s = ceil(nb_s / n) rounded up to a multiple of kMinPartBlocks (one pair per wavefront, so
+// every wavefront of a full split gets the same number of pairs). Either way a sequence's split
+// boundaries depend on its own length only, as in the reference's fixed grid
+// (ops/triton_ops.py:47-53), so a row's result does not depend on the rest of the batch.
 // Split j of sequence s leaves its partial in workspace row s * max_splits + j, so the merge
 // can request a sequence's partials without knowing the other sequences' lengths.
 constexpr int kMinPartBlocks = 8;
-constexpr int kBalancedMaxSplits = 32;
+constexpr int kOwnPartBlocks = 24;           // the own-length schedule's longest split (blocks)
+constexpr int kOwnMaxSplits = 32;
 
 struct SplitSlot {
   int seq;     // sequence owning the slot (-1: the slot is past the batch's last split)
@@ -147,58 +149,39 @@ __device__ __forceinline__ int round_part(int blocks) {
   return (blocks + kMinPartBlocks - 1) / kMinPartBlocks * kMinPartBlocks;
 }
 
-// P of the balanced schedule for a batch of total_blocks blocks.
-__device__ __forceinline__ int balanced_part(int total_blocks, int nx) {
-  const int P = round_part((total_blocks + nx - 1) / nx);
-  return P > kMinPartBlocks ? P : kMinPartBlocks;
-}
-
-// P_s of a sequence of nb blocks: P itself, or (balanced) the multiple of kMinPartBlocks that
-// keeps its split count within max_splits.
-__device__ __forceinline__ int seq_part(bool balanced, int P, int nb, int max_splits) {
-  if (!balanced) return P;
-  const int q = round_part((nb + max_splits - 1) / max_splits);
-  return q > P ? q : P;
+// P_s of a sequence of nb blocks: the caller's partition P, or (P <= 0, the own-length
+// schedule) nb cut into min(max_splits, ceil(nb / kOwnPartBlocks)) near-equal splits.
+__device__ __forceinline__ int seq_part(int P, int nb, int max_splits) {
+  if (P > 0) return P;
+  int n = (nb + kOwnPartBlocks - 1) / kOwnPartBlocks;
+  n = n < 1 ? 1 : (n > max_splits ? max_splits : n);
+  const int ps = round_part((nb + n - 1) / n);
+  return ps > kMinPartBlocks ? ps : kMinPartBlocks;
 }
 
 // Called by every thread of an NT-thread workgroup (S >= 1): finds the sequence that owns
 // launch slot `slot`. s_map holds NT / 64 + 5 ints of LDS.
 template <int NT>
 __device__ SplitSlot split_lookup(const int* __restrict__ seq_lens, int S, int cap_blocks,
-                                  int part_blocks, int nx, int max_splits, int slot,
-                                  int* s_map) {
+                                  int part_blocks, int max_splits, int slot, int* s_map) {
   constexpr int NWV = NT / kWave;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int cap = cap_blocks * kBlockSize;
   auto clamp_len = [&](int len) { return len < 0 ? 0 : (len > cap ? cap : len); };
   const int len0 = tid < S ? clamp_len(seq_lens[tid]) : 0;
-  const bool balanced = part_blocks <= 0;
-  int P = part_blocks;
-  if (balanced) {
-    int tb = (len0 + kBlockSize - 1) / kBlockSize;
-    for (int i = tid + NT; i < S; i += NT) tb += (clamp_len(seq_lens[i]) + kBlockSize - 1) / kBlockSize;
-    tb = wave_sum(tb);
-    if (lane == 0) s_map[w] = tb;
-    __syncthreads();
-    int total = 0;
-#pragma unroll
-    for (int k = 0; k < NWV; ++k) total += s_map[k];
-    P = balanced_part(total, nx);
-    __syncthreads();
-  }
   if (tid == 0) {
     s_map[NWV] = -1;
     s_map[NWV + 1] = 0;
     s_map[NWV + 2] = 0;
     s_map[NWV + 3] = 0;
-    s_map[NWV + 4] = P;
+    s_map[NWV + 4] = part_blocks;
   }
   int base = 0;
   for (int c0 = 0; c0 < S; c0 += NT) {
     const int i = c0 + tid;
     const int len = c0 == 0 ? len0 : (i < S ? clamp_len(seq_lens[i]) : 0);
     const int nb = (len + kBlockSize - 1) / kBlockSize;
-    const int ps = seq_part(balanced, P, nb, max_splits);
+    const int ps = seq_part(part_blocks, nb, max_splits);
     const int n = (nb + ps - 1) / ps;
     const int incl = wave_inclusive_sum(n, lane);
     if (lane == kWave - 1) s_map[w] = incl;
@@ -231,7 +214,7 @@ __device__ SplitSlot split_lookup(const int* __restrict__ seq_lens, int S, int c
 // layer's v3 launch in place of split_lookup (the layers of a step share seq_lens, the block
 // tables and the plan). A workgroup then issues its first K/V requests one scalar load after it
 // starts instead of after a seq_lens load, a block-wide scan and a block-table load. Layout
-// (int32): a header of kMapHeader ints {kMapMagic, S, slots, part_blocks, nx, max_splits,
+// (int32): a header of kMapHeader ints {kMapMagic, S, slots, part_blocks, 0, max_splits,
 // cap_blocks, 0} naming the plan it was built for (a launch whose plan differs ignores the map
 // and runs split_lookup), then kMapEntry ints per slot: {seq (-1: past the last split), C_s,
 // n_s, clamped seq_len, first block, end block, block id of the sequence's last token, P_s}
@@ -249,8 +232,7 @@ __device__ __forceinline__ int4 int4_of(int a, int b, int c, int d) { return int
 template <int NT>
 __global__ void __launch_bounds__(NT) decode_split_map_kernel(
     const int* __restrict__ seq_lens, const int* __restrict__ bt, int64_t bt_st, int64_t NB,
-    int S, int cap_blocks, int part_blocks, int nx, int max_splits, int nslots,
-    int* __restrict__ map) {
+    int S, int cap_blocks, int part_blocks, int max_splits, int nslots, int* __restrict__ map) {
   constexpr int NWV = NT / kWave;
   __shared__ int s_first[kMapMaxSeqs];
   __shared__ int s_len[kMapMaxSeqs];
@@ -258,32 +240,19 @@ __global__ void __launch_bounds__(NT) decode_split_map_kernel(
   __shared__ int s_red[NWV];
   const int tid = threadIdx.x, lane = tid & (kWave - 1), w = tid / kWave;
   const int cap = cap_blocks * kBlockSize;
-  const bool balanced = part_blocks <= 0;
-  int tb = 0;
   for (int i = tid; i < S; i += NT) {
     int len = seq_lens[i];
     len = len < 0 ? 0 : (len > cap ? cap : len);
     s_len[i] = len;
-    tb += (len + kBlockSize - 1) / kBlockSize;
   }
-  int P = part_blocks;
-  if (balanced) {
-    tb = wave_sum(tb);
-    if (lane == 0) s_red[w] = tb;
-    __syncthreads();
-    int total = 0;
-#pragma unroll
-    for (int k = 0; k < NWV; ++k) total += s_red[k];
-    P = balanced_part(total, nx);
-  }
-  __syncthreads();                             // s_len complete, s_red free
+  __syncthreads();                             // s_len complete
   int base = 0;
   for (int c0 = 0; c0 < S; c0 += NT) {         // exclusive prefix of the split counts
     const int i = c0 + tid;
     int n = 0;
     if (i < S) {
       const int nb = (s_len[i] + kBlockSize - 1) / kBlockSize;
-      const int ps = seq_part(balanced, P, nb, max_splits);
+      const int ps = seq_part(part_blocks, nb, max_splits);
       s_part[i] = ps;
       n = (nb + ps - 1) / ps;
     }
@@ -304,7 +273,7 @@ __global__ void __launch_bounds__(NT) decode_split_map_kernel(
   if (tid == 0) {
     int4* h = reinterpret_cast<int4*>(map);
     h[0] = int4_of(kMapMagic, S, nslots, part_blocks);
-    h[1] = int4_of(nx, max_splits, cap_blocks, 0);
+    h[1] = int4_of(0, max_splits, cap_blocks, 0);
   }
   constexpr int NWF = kMapPairs / 2;           // wavefronts of the consuming launch
   for (int slot = tid; slot < nslots; slot += NT) {
@@ -392,8 +361,8 @@ __device__ __forceinline__ void decode_mfma_body(
     const half_t* __restrict__ q, int64_t q_st, int64_t q_sh, half_t* __restrict__ out,
     int64_t o_st, const half_t* __restrict__ kc, const half_t* __restrict__ vc, int64_t NB,
     const int* __restrict__ bt, int64_t bt_st, int max_blocks, const int* __restrict__ seq_lens,
-    int S, int H, int KVH, int G, int HG, float sl2, int cap_blocks, int part_blocks, int nx,
-    int max_splits, half_t* __restrict__ ws_acc, float* __restrict__ ws_m,
+    int S, int H, int KVH, int G, int HG, float sl2, int cap_blocks, int part_blocks,
+    int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
     float* __restrict__ ws_l, int* __restrict__ ws_cnt,
     int bx, int bz, char* __restrict__ lds, const NewRows& nr = NewRows{},
     const int* __restrict__ smap = nullptr) {
@@ -429,7 +398,7 @@ __device__ __forceinline__ void decode_mfma_body(
     if (split && smap != nullptr) {
       const int* e = smap + kMapHeader + (int64_t)bx * kMapEntry;
       mapped = smap[0] == kMapMagic && smap[1] == S && smap[2] == (int)gridDim.x &&
-               smap[3] == part_blocks && smap[4] == nx && smap[5] == max_splits &&
+               smap[3] == part_blocks && smap[5] == max_splits &&
                smap[6] == cap_blocks;
       sp = {e[0], e[1], e[2], e[7], e[3]};
       m_last = e[6];
@@ -441,7 +410,7 @@ __device__ __forceinline__ void decode_mfma_body(
   }
   if (split) {
     if (!mapped)
-      sp = split_lookup<NW * 64>(seq_lens, S, cap_blocks, part_blocks, nx, max_splits, bx, s_map);
+      sp = split_lookup<NW * 64>(seq_lens, S, cap_blocks, part_blocks, max_splits, bx, s_map);
     if (sp.seq < 0) return;                      // slot past the batch's last split
     s = sp.seq;
     seq_len = sp.len;
@@ -654,6 +623,16 @@ __device__ __forceinline__ void decode_mfma_body(
     ids_of(last_or(p + NW, p), idk);
     ids_of(last_or(p + 2 * NW, last_or(p + NW, p)), idv);
   }
+  if (mapped) {
+    // A map built for another step (other lengths or block tables, same plan) poisons the rows
+    // it would attend wrongly: the entry's clamped length and last block must be this step's.
+    // These loads follow the first K/V requests, off their critical path.
+    const int cap = cap_blocks * kBlockSize;
+    int cur = seq_lens[s];
+    cur = cur < 0 ? 0 : (cur > cap ? cap : cur);
+    const int cur_last = clamp_block(btrow[(seq_len - 1) / kBlockSize], NB);
+    poison = poison || cur != seq_len || cur_last != m_last;
+  }
   for (; p < npairs; p += 2 * NW) {
     step(p, vA);
     if (p + NW >= npairs) break;
@@ -688,7 +667,7 @@ __device__ __forceinline__ void decode_mfma_body(
       out[(int64_t)s * o_st + (int64_t)(head0 + hh) * D + d] = (half_t)(O / L);
     } else {
       const int64_t pidx = ((int64_t)s * max_splits + split_j) * H + head0 + hh;
-      ws_acc[pidx * D + d] = (half_t)(O / L);    // the split's own average, with its (m, l)
+      ws_acc[pidx * D + d] = O;                  // fp32 (acc, m, l), as the reference keeps them
       if (d == 0) {
         ws_m[pidx] = M;
         ws_l[pidx] = L;
@@ -702,21 +681,21 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
     const half_t* __restrict__ q, int64_t q_st, int64_t q_sh, half_t* __restrict__ out,
     int64_t o_st, const half_t* __restrict__ kc, const half_t* __restrict__ vc, int64_t NB,
     const int* __restrict__ bt, int64_t bt_st, int max_blocks, const int* __restrict__ seq_lens,
-    int S, int H, int KVH, int G, int HG, float sl2, int cap_blocks, int part_blocks, int nx,
-    int max_splits, half_t* __restrict__ ws_acc, float* __restrict__ ws_m,
+    int S, int H, int KVH, int G, int HG, float sl2, int cap_blocks, int part_blocks,
+    int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
     float* __restrict__ ws_l, int* __restrict__ ws_cnt, const NewRows nr,
     const int* __restrict__ smap) {
   __shared__ __attribute__((aligned(16))) char lds[DecodeLds<D, NW>::BYTES];
   decode_mfma_body<D, NW, WRITE, ROPE>(q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks,
-                                 seq_lens, S, H, KVH, G, HG, sl2, cap_blocks, part_blocks, nx,
+                                 seq_lens, S, H, KVH, G, HG, sl2, cap_blocks, part_blocks,
                                  max_splits, ws_acc, ws_m, ws_l, ws_cnt, (int)blockIdx.x,
                                  (int)blockIdx.z, lds, nr, smap);
 }
 
-// Merge of the split partials (ops/triton_decode_attention.py:144-163): each split leaves its own
-// average A_j = acc_j / l_j (fp16) with its (m_j, l_j); M = max m_j, w_j = 2^(m_j - M) l_j,
-// out = sum w_j A_j / sum w_j. One workgroup per (sequence, KV head,
-// head group), one thread per 8 output dims of a head (16-byte partial loads). A sequence's partials sit in rows
+// Merge of the split partials (ops/triton_decode_attention.py:144-163): each split leaves its
+// fp32 (acc_j, m_j, l_j), acc_j unnormalised; M = max m_j, w_j = 2^(m_j - M),
+// out = sum w_j acc_j / sum w_j l_j. One workgroup per (sequence, KV head, head group), one
+// thread per 8 output dims of a head (two 16-byte partial loads per split). A sequence's partials sit in rows
 // s * max_splits + j; the split count written by the first kernel is read first and only the
 // rows below it are requested (a second memory step, but a few hundred KB instead of kMergeChunk
 // rows for every sequence: measured faster than requesting a fixed chunk together with the
@@ -727,7 +706,7 @@ constexpr int kMergeChunk = 16;
 
 template <int D>
 __device__ __forceinline__ void decode_merge_body(
-    const half_t* __restrict__ ws_acc, const float* __restrict__ ws_m,
+    const float* __restrict__ ws_acc, const float* __restrict__ ws_m,
     const float* __restrict__ ws_l, const int* __restrict__ ws_cnt, half_t* __restrict__ out,
     int64_t o_st, const int* __restrict__ seq_lens, int H, int G, int HG, int max_splits, int bx, int by) {
   constexpr int TPH = D / 8;                     // threads per head (8 dims each)
@@ -746,7 +725,7 @@ __device__ __forceinline__ void decode_merge_body(
     const int64_t hoff = head0 + hh;
     half_t* dst = out + (int64_t)s * o_st + (head0 + hh) * (int64_t)D + d0;
     float mv[CH], lv[CH];
-    half8_t av[CH];                              // converted where used: the loads stay in flight
+    float4_t av[CH][2];
     if (len <= 0) {                              // padding row: zeros (ops/reference.py:99,104-105)
       st<half4_t>(dst, half4_t{0, 0, 0, 0});     // output rows are 8-byte aligned: two stores
       st<half4_t>(dst + 4, half4_t{0, 0, 0, 0});
@@ -762,11 +741,13 @@ __device__ __forceinline__ void decode_merge_body(
           const int64_t pidx = (row0 + j0 + u) * H + hoff;
           mv[u] = ws_m[pidx];
           lv[u] = ws_l[pidx];
-          av[u] = ld<half8_t>(ws_acc + pidx * D + d0);
+          av[u][0] = ld<float4_t>(ws_acc + pidx * D + d0);
+          av[u][1] = ld<float4_t>(ws_acc + pidx * D + d0 + 4);
         } else {
           mv[u] = -INFINITY;
           lv[u] = 0.f;
-          av[u] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+          av[u][0] = float4_t{0.f, 0.f, 0.f, 0.f};
+          av[u][1] = float4_t{0.f, 0.f, 0.f, 0.f};
         }
       }
     };
@@ -785,11 +766,9 @@ __device__ __forceinline__ void decode_merge_body(
 #pragma unroll
       for (int u = 0; u < CH; ++u) {
         // rows past n are skipped, not weighted by 0: their stale contents may be inf or NaN
-        const float wt = fast_exp2(mv[u] - cm) * lv[u];
-        L = (j0 + u < n) ? L + wt : L;
-        const float4_t a0 = {(float)av[u][0], (float)av[u][1], (float)av[u][2], (float)av[u][3]};
-        const float4_t a1 = {(float)av[u][4], (float)av[u][5], (float)av[u][6], (float)av[u][7]};
-        const float4_t o0 = O0 + wt * a0, o1 = O1 + wt * a1;
+        const float wt = fast_exp2(mv[u] - cm);
+        L = (j0 + u < n) ? L + wt * lv[u] : L;
+        const float4_t o0 = O0 + wt * av[u][0], o1 = O1 + wt * av[u][1];
         O0 = (j0 + u < n) ? o0 : O0;
         O1 = (j0 + u < n) ? o1 : O1;
       }
@@ -802,7 +781,7 @@ __device__ __forceinline__ void decode_merge_body(
 
 template <int D>
 __global__ void __launch_bounds__(256) decode_merge_kernel(
-    const half_t* __restrict__ ws_acc, const float* __restrict__ ws_m,
+    const float* __restrict__ ws_acc, const float* __restrict__ ws_m,
     const float* __restrict__ ws_l, const int* __restrict__ ws_cnt, half_t* __restrict__ out,
     int64_t o_st, const int* __restrict__ seq_lens, int H, int G, int HG, int max_splits) {
   decode_merge_body<D>(ws_acc, ws_m, ws_l, ws_cnt, out, o_st, seq_lens, H, G, HG, max_splits,
@@ -822,21 +801,21 @@ static int decode_wgs_per_cu(int D) { return D <= 32 ? 6 : (D == 64 ? 3 : (D == 
 
 struct SplitPlan {
   int version;        // 1, 2 or 3 after resolving AUTO
-  int part_blocks;    // v3: blocks per split, 0 = balanced
-  int nx;             // v3 balanced: target split count per (KV head, head group)
+  int part_blocks;    // v3: blocks per split, 0 = the own-length schedule
   int nslots;         // v3: launched split slots per (KV head, head group)
-  int cap_blocks;     // v3 fixed partition: blocks of a sequence covered by the launched splits
+  int cap_blocks;     // v3: blocks of a sequence covered by the launched splits
   int max_splits;     // v3: workspace rows per sequence (bound on its split count)
 };
 
 // Explicit v3 partition (ops/triton_ops.py:50-51): num_splits = ceil(max_seq_len / partition)
-// splits per sequence at most; partition = 0 selects the balanced schedule. AUTO splits whenever
-// one workgroup per (sequence, KV head, head group) cannot fill the device and contexts are
-// longer than two minimum splits (the reference's rule, ops/triton_ops.py:44-45, with the CU
-// count and this kernel's residency), and uses the balanced schedule unless a partition is given.
+// splits per sequence at most; partition = 0 selects the own-length schedule (seq_part). AUTO
+// splits whenever one workgroup per (sequence, KV head, head group) cannot fill the device and
+// contexts are longer than two minimum splits (the reference's rule, ops/triton_ops.py:44-45,
+// with the CU count and this kernel's residency). With a fixed partition a sequence longer than
+// max_seq_len is attended over the launched grid's tokens, as in the reference's grid.
 static SplitPlan plan_decode(int version, int S, int H, int KVH, int D, int max_seq_len,
                              int partition, int cu_count) {
-  SplitPlan p{version, 0, 0, 0, 0, 0};
+  SplitPlan p{version, 0, 0, 0, 0};
   const int G = H / KVH;
   const int HG = (G + 15) / 16;
   const int64_t groups = (int64_t)KVH * HG;
@@ -859,12 +838,17 @@ static SplitPlan plan_decode(int version, int S, int H, int KVH, int D, int max_
     p.nslots = S * num_splits;
     p.max_splits = num_splits;
   } else {
-    int64_t nx = wg_slots / groups - S;          // launched slots nx + S = resident workgroups
-    nx = nx < 16 ? 16 : (nx > 4096 ? 4096 : nx);
-    p.nx = (int)nx;
+    // The own-length schedule: a sequence of nb <= max_blk blocks has at most
+    // per_seq = min(kOwnMaxSplits, ceil(max_blk / kOwnPartBlocks)) splits, and seq_part caps
+    // every sequence at max_splits = per_seq splits (only a sequence longer than max_seq_len,
+    // which the caller promises not to pass, gets longer splits than its own length implies;
+    // it is still attended in full). So S * per_seq slots cover every batch; the slots past
+    // the batch's last split exit at once.
+    int per_seq = (max_blk + kOwnPartBlocks - 1) / kOwnPartBlocks;
+    per_seq = per_seq < 1 ? 1 : (per_seq > kOwnMaxSplits ? kOwnMaxSplits : per_seq);
     p.cap_blocks = 1 << 30;
-    p.nslots = p.nx + S;
-    p.max_splits = kBalancedMaxSplits;
+    p.nslots = S * per_seq;
+    p.max_splits = per_seq;
   }
   return p;
 }
@@ -875,7 +859,7 @@ struct WsLayout {
   size_t acc, m, l, cnt, total;
 };
 
-// [avg: rows * H * D fp16][m: rows * H fp32][l: rows * H fp32][count: S int32] with
+// [acc: rows * H * D fp32][m: rows * H fp32][l: rows * H fp32][count: S int32] with
 // rows = S * max_splits: split j of sequence s keeps query head h's partial in row
 // s * max_splits + j, column h.
 static WsLayout ws_layout(const SplitPlan& p, int S, int H, int D) {
@@ -883,7 +867,7 @@ static WsLayout ws_layout(const SplitPlan& p, int S, int H, int D) {
   if (p.version != TS_DECODE_V3) return w;
   const size_t n = (size_t)S * p.max_splits * H;
   w.acc = 0;
-  w.m = align256(n * D * sizeof(half_t));
+  w.m = align256(n * D * sizeof(float));
   w.l = w.m + align256(n * sizeof(float));
   w.cnt = w.l + align256(n * sizeof(float));
   w.total = w.cnt + align256((size_t)S * sizeof(int));
@@ -904,7 +888,7 @@ static int launch_cap_blocks(const SplitPlan& p, int max_blocks) {
 static void launch_split_map(const SplitPlan& p, hipStream_t st, const int* sl, const int* bt,
                              int64_t bt_st, int64_t NB, int max_blocks, int S, int* map) {
   decode_split_map_kernel<kMapThreads><<<1, kMapThreads, 0, st>>>(
-      sl, bt, bt_st, NB, S, launch_cap_blocks(p, max_blocks), p.part_blocks, p.nx, p.max_splits,
+      sl, bt, bt_st, NB, S, launch_cap_blocks(p, max_blocks), p.part_blocks, p.max_splits,
       p.nslots, map);
 }
 
@@ -930,7 +914,7 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
 #define TS_V2_LAUNCH(W, R)                                                                       \
   decode_mfma_kernel<D, kDecodeWaves, W, R><<<dim3(S, 1, KVH * HG), kDecodeWaves * 64, 0, st>>>( \
       q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,        \
-      scale_log2, 0, 0, 0, 0, nullptr, nullptr, nullptr, nullptr, nr, nullptr)
+      scale_log2, 0, 0, 0, nullptr, nullptr, nullptr, nullptr, nr, nullptr)
     if constexpr (D % 64 == 0) {
       if (rope) {
         TS_V2_LAUNCH(true, true);
@@ -946,7 +930,7 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
   }
   const WsLayout w = ws_layout(p, S, H, D);
   char* b = static_cast<char*>(ws);
-  half_t* ws_acc = reinterpret_cast<half_t*>(b + w.acc);
+  float* ws_acc = reinterpret_cast<float*>(b + w.acc);
   float* ws_m = reinterpret_cast<float*>(b + w.m);
   float* ws_l = reinterpret_cast<float*>(b + w.l);
   int* ws_cnt = reinterpret_cast<int*>(b + w.cnt);
@@ -955,7 +939,7 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
   decode_mfma_kernel<D, kDecodeWaves, W, R><<<dim3(p.nslots, 1, KVH * HG), kDecodeWaves * 64, 0, \
                                               st>>>(                                             \
       q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,        \
-      scale_log2, cap, p.part_blocks, p.nx, p.max_splits, ws_acc, ws_m, ws_l, ws_cnt, nr, smap)
+      scale_log2, cap, p.part_blocks, p.max_splits, ws_acc, ws_m, ws_l, ws_cnt, nr, smap)
   bool launched = false;
   if constexpr (D % 64 == 0) {
     if (rope) {

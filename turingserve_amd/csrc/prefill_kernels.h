@@ -352,8 +352,8 @@ __device__ __forceinline__ PrefillSeq prefill_seq(const int* __restrict__ qsl,
   return p;
 }
 
-// Workspace of the split path: per-split row averages [slots_total][128][D] fp16, then (m, l)
-// pairs [slots_total][128][2] fp32, slots_total = P * H * slots.
+// Workspace of the split path: per-split rows O (unnormalised) [slots_total][128][D] fp32, then
+// (m, l) pairs [slots_total][128][2] fp32, slots_total = P * H * slots.
 template <int D>
 __device__ __forceinline__ void prefill_tile_body(
     const half_t* __restrict__ q, int64_t q_st, int64_t q_sh, half_t* __restrict__ out,
@@ -600,23 +600,19 @@ __device__ __forceinline__ void prefill_tile_body(
         ts::st<half4_t>(op + 32 * t + 8 * j, v4);
       }
   } else {
-    // Partial of this split: the row's own average O / l (a convex combination of V rows, so
-    // fp16 holds it to 2^-11 relative) and its (m, l) in fp32.
+    // Partial of this split: the row's O and (m, l), all fp32, as the reference keeps a
+    // split's state (ops/triton_decode_attention.py:190-192).
     const int64_t wslot = ((int64_t)pi * H + h) * slots + slot;
     const int64_t total = (int64_t)P * H * slots;
-    const float inv = lt == 0.f ? 0.f : 1.f / lt;
-    half_t* wo = reinterpret_cast<half_t*>(ws) + (wslot * kTileRows + 32 * w + r) * D + 4 * hh;
+    float* wo = ws + (wslot * kTileRows + 32 * w + r) * D + 4 * hh;
 #pragma unroll
     for (int t = 0; t < DT; ++t)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const half4_t v4 = {(half_t)(o[t][4 * j] * inv), (half_t)(o[t][4 * j + 1] * inv),
-                            (half_t)(o[t][4 * j + 2] * inv), (half_t)(o[t][4 * j + 3] * inv)};
-        ts::st<half4_t>(wo + 32 * t + 8 * j, v4);
-      }
+      for (int j = 0; j < 4; ++j)
+        ts::st<float4_t>(wo + 32 * t + 8 * j,
+                         float4_t{o[t][4 * j], o[t][4 * j + 1], o[t][4 * j + 2], o[t][4 * j + 3]});
     if (hh == 0) {
-      float* wml = reinterpret_cast<float*>(reinterpret_cast<half_t*>(ws) + total * kTileRows * D) +
-                   (wslot * kTileRows + 32 * w + r) * 2;
+      float* wml = ws + total * kTileRows * D + (wslot * kTileRows + 32 * w + r) * 2;
       wml[0] = m;
       wml[1] = lt;
     }
@@ -637,9 +633,9 @@ __global__ void __launch_bounds__(kTileThreads, 2) prefill_tile_kernel(
                        (int)blockIdx.x, lds);
 }
 
-// Merge of split partials (each the split's own average A_j = O_j / l_j with its (m_j, l_j)):
-// M = max m_j, w_j = 2^(m_j - M) l_j, out = sum w_j A_j / sum w_j (empty splits have m = -inf and
-// weigh 0). A thread owns 8 dims (d0, one 16-byte load per partial row) of kMergeRows rows; the
+// Merge of split partials (each the split's fp32 (O_j, m_j, l_j), O_j unnormalised):
+// M = max m_j, w_j = 2^(m_j - M), out = sum w_j O_j / sum w_j l_j (empty splits have m = -inf and
+// weigh 0). A thread owns 8 dims (d0, two 16-byte loads per partial row) of kMergeRows rows; the
 // partials sit at slot indices base .. base + cnt - 1 of a workspace of total_slots slots x
 // slot_rows rows, the thread's rows at row0 + kMergeRowStride * k of each slot, and go to dst[k]
 // (nullptr: not wanted). The partials are taken kMergeBatch at a time, all of a batch's loads
@@ -654,8 +650,8 @@ __device__ __forceinline__ void merge_partials(const float* __restrict__ ws, int
   constexpr int NR = kMergeRows;
   constexpr int RG = kMergeRowStride;
   constexpr int B = kMergeBatch;
-  const half_t* wo = reinterpret_cast<const half_t*>(ws);
-  const float* wml = reinterpret_cast<const float*>(wo + total_slots * slot_rows * D);
+  const float* wo = ws;
+  const float* wml = ws + total_slots * slot_rows * D;
   float M[NR], Lsum[NR], acc[NR][8];
 #pragma unroll
   for (int k = 0; k < NR; ++k) {
@@ -666,7 +662,7 @@ __device__ __forceinline__ void merge_partials(const float* __restrict__ ws, int
   }
   for (int j = 0; j < cnt; j += B) {
     float2_t ml[B][NR];
-    half8_t a[B][NR];
+    float4_t a[B][NR][2];
 #pragma unroll
     for (int u = 0; u < B; ++u)
 #pragma unroll
@@ -674,10 +670,12 @@ __device__ __forceinline__ void merge_partials(const float* __restrict__ ws, int
         if (j + u < cnt) {
           const int64_t rix = (base + j + u) * slot_rows + row0 + RG * k;
           ml[u][k] = ld<float2_t>(wml + rix * 2);
-          a[u][k] = ld<half8_t>(wo + rix * D + d0);
+          a[u][k][0] = ld<float4_t>(wo + rix * D + d0);
+          a[u][k][1] = ld<float4_t>(wo + rix * D + d0 + 4);
         } else {
           ml[u][k] = float2_t{-INFINITY, 0.f};
-          a[u][k] = half8_t{0, 0, 0, 0, 0, 0, 0, 0};
+          a[u][k][0] = float4_t{0.f, 0.f, 0.f, 0.f};
+          a[u][k][1] = float4_t{0.f, 0.f, 0.f, 0.f};
         }
       }
 #pragma unroll
@@ -692,10 +690,13 @@ __device__ __forceinline__ void merge_partials(const float* __restrict__ ws, int
 #pragma unroll
       for (int u = 0; u < B; ++u) {
         const float mu = ml[u][k][0];
-        const float wt = mu == -INFINITY ? 0.f : fast_exp2(mu - cm) * ml[u][k][1];
-        Lsum[k] += wt;
+        const float wt = mu == -INFINITY ? 0.f : fast_exp2(mu - cm);
+        Lsum[k] += wt * ml[u][k][1];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) acc[k][e] += wt * (float)a[u][k][e];
+        for (int e = 0; e < 4; ++e) {
+          acc[k][e] += wt * a[u][k][0][e];
+          acc[k][e + 4] += wt * a[u][k][1][e];
+        }
       }
       M[k] = cm;
     }
@@ -804,7 +805,7 @@ inline TilePlan tile_plan(int P, int H, int D, int max_query_len, int max_seq_le
   pl.smax = smax;
   pl.est_wg = workgroups(smax);
   pl.slots = tiles * cdiv(nmax, smax);
-  pl.ws_bytes = (size_t)P * H * pl.slots * kTileRows * (D * sizeof(half_t) + 2 * sizeof(float));
+  pl.ws_bytes = (size_t)P * H * pl.slots * kTileRows * (D + 2) * sizeof(float);
   return pl;
 }
 

@@ -80,7 +80,7 @@ inline PairPlan pair_plan(int P, int H, int KVH, int max_query_len, int max_seq_
   if (!split || cdiv(seq, kTileKeys) <= 1 || 2 * items > cus) return pl;
   pl.slots = cus / items;
   pl.seg_cap = tiles + pl.slots;
-  pl.ws_bytes = (size_t)items * pl.seg_cap * kPairSlotRows * (PairLayout::D * sizeof(half_t) + 2 * sizeof(float));
+  pl.ws_bytes = (size_t)items * pl.seg_cap * kPairSlotRows * (PairLayout::D + 2) * sizeof(float);
   return pl;
 }
 
@@ -397,32 +397,36 @@ __device__ __forceinline__ void prefill_pair_body(
 
   const float lt = pair_sum(l);
   if (!row_ok || (!whole && seg >= seg_cap)) return;
-  const float inv = lt == 0.f ? 0.f : 1.f / lt;
-  half_t* op;
   if (whole) {
-    op = out + (int64_t)(sq.q_start + row) * o_st + (int64_t)h * D + 4 * hh;
+    const float inv = lt == 0.f ? 0.f : 1.f / lt;
+    half_t* op = out + (int64_t)(sq.q_start + row) * o_st + (int64_t)h * D + 4 * hh;
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const half4_t v4 = {(half_t)(o[t][4 * j] * inv), (half_t)(o[t][4 * j + 1] * inv),
+                            (half_t)(o[t][4 * j + 2] * inv), (half_t)(o[t][4 * j + 3] * inv)};
+        ts::st<half4_t>(op + 32 * t + 8 * j, v4);
+      }
   } else {
-    // Partial of this segment: the row's own average O / l (a convex combination of V rows, so
-    // fp16 holds it to 2^-11 relative) and its (m, l) in fp32, at row 32 w + r of the segment.
+    // Partial of this segment: the row's O and (m, l), all fp32, as the reference keeps a
+    // split's state (ops/triton_decode_attention.py:190-192), at row 32 w + r of the segment.
     const int64_t wseg = ((int64_t)pi * (H / hp) + item) * seg_cap + seg;
     const int64_t total = (int64_t)P * (H / hp) * seg_cap;
     const int64_t prow = wseg * kPairSlotRows + 32 * w + r;
-    op = reinterpret_cast<half_t*>(ws) + prow * D + 4 * hh;
+    float* op = ws + prow * D + 4 * hh;
     if (hh == 0) {
-      float* wml = reinterpret_cast<float*>(reinterpret_cast<half_t*>(ws) + total * kPairSlotRows * D) +
-                   prow * 2;
+      float* wml = ws + total * kPairSlotRows * D + prow * 2;
       wml[0] = m;
       wml[1] = lt;
     }
+#pragma unroll
+    for (int t = 0; t < DT; ++t)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        ts::st<float4_t>(op + 32 * t + 8 * j,
+                         float4_t{o[t][4 * j], o[t][4 * j + 1], o[t][4 * j + 2], o[t][4 * j + 3]});
   }
-#pragma unroll
-  for (int t = 0; t < DT; ++t)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const half4_t v4 = {(half_t)(o[t][4 * j] * inv), (half_t)(o[t][4 * j + 1] * inv),
-                          (half_t)(o[t][4 * j + 2] * inv), (half_t)(o[t][4 * j + 3] * inv)};
-      ts::st<half4_t>(op + 32 * t + 8 * j, v4);
-    }
   };
 
   if (seg_cap == 0) {

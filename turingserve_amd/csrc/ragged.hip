@@ -6,13 +6,13 @@
 // kernel is bound by HBM bandwidth and the prefill tiles by MFMA and LDS latency. Here both run
 // in one launch: the workgroups of the prefill tile plan come first, the decode split slots take
 // the remaining resident slots (two workgroups per CU), and one merge launch then combines the
-// split partials of both. The decode part uses the balanced split schedule sized for the slots
-// the prefill leaves, the prefill part a split plan sized for half the device. Each workgroup
+// split partials of both. The decode part uses the own-length split schedule of
+// ts_decode_attention, the prefill part a split plan sized for half the device. Each workgroup
 // runs exactly the code of its standalone kernel (decode_mfma_body / prefill_tile_body), so the
 // results equal the standalone launches with the same plans.
 //
 // The fused path needs head_dim 128, the automatic decode policy resolving to v3 with the
-// balanced schedule (partition 0), at least one decode row and one prefill sequence, and a
+// own-length schedule (partition 0), at least one decode row and one prefill sequence, and a
 // workspace of ts_paged_attention_workspace_bytes(); otherwise the two kernels run one after
 // the other on the stream, sharing the workspace.
 #include "decode_kernels.h"
@@ -39,8 +39,8 @@ struct RaggedArgs {
   int pf_launch, smax, slots, P;
   float* pf_ws;
   // decode splits: launch ids [pf_launch, pf_launch + nslots * KVH * HG)
-  int nslots, cap_blocks, nx, max_splits;
-  half_t* ws_acc;
+  int nslots, cap_blocks, max_splits;
+  float* ws_acc;
   float* ws_m;
   float* ws_l;
   int* ws_cnt;
@@ -69,7 +69,7 @@ __global__ void __launch_bounds__(256, 2) ragged_split_kernel(const RaggedArgs a
     const int d = bx - a.pf_launch;
     decode_mfma_body<128, kDecodeWaves>(a.q, a.q_st, a.q_sh, a.out, a.o_st, a.kc, a.vc, a.NB,
                                         a.bt, a.bt_st, a.max_blocks, a.seq_lens, a.num_decode,
-                                        a.H, a.KVH, a.G, a.HG, a.sl2, a.cap_blocks, 0, a.nx,
+                                        a.H, a.KVH, a.G, a.HG, a.sl2, a.cap_blocks, 0,
                                         a.max_splits, a.ws_acc, a.ws_m, a.ws_l, a.ws_cnt,
                                         d % a.nslots, d / a.nslots, lds);
   }
@@ -90,7 +90,8 @@ __global__ void __launch_bounds__(256) ragged_merge_kernel(const RaggedArgs a) {
 }
 
 // The fused plan: the prefill tiles get one round of half the resident slots, the decode
-// splits the rest (balanced schedule). ok = false when the batch does not qualify.
+// splits follow (the own-length schedule, as in ts_decode_attention, so a decode row's result
+// does not depend on the prefill beside it). ok = false when the batch does not qualify.
 struct RaggedPlan {
   bool ok;
   TilePlan pf;
@@ -112,13 +113,6 @@ static RaggedPlan ragged_plan(int num_seqs, int num_decode, int max_query_len, i
   r.pf = tile_plan(P, H, D, max_query_len, pf_seq, cus, true, slots * kRaggedPfShare / 8);
   r.dec = plan_decode(decode_version, num_decode, H, KVH, D, max_seq_len, 0, cus);
   if (r.dec.version != TS_DECODE_V3) return r;
-  const int G = H / KVH, HG = (G + 15) / 16;
-  const int64_t groups = (int64_t)KVH * HG;
-  const int64_t dec_slots = slots - r.pf.est_wg;
-  int64_t nx = dec_slots / groups - num_decode;
-  nx = nx < 16 ? 16 : (nx > 4096 ? 4096 : nx);
-  r.dec.nx = (int)nx;
-  r.dec.nslots = r.dec.nx + num_decode;
   r.dec_bytes = align256(ws_layout(r.dec, num_decode, H, D).total);
   r.total_bytes = r.dec_bytes + r.pf.ws_bytes;
   r.ok = true;
@@ -219,13 +213,12 @@ extern "C" int ts_paged_attention(const void* q, int64_t q_stride_t, int64_t q_s
       char* ws = static_cast<char*>(workspace);
       a.pf_ws = reinterpret_cast<float*>(ws + r.dec_bytes);
       const WsLayout w = ws_layout(r.dec, num_decode, num_heads, head_dim);
-      a.ws_acc = reinterpret_cast<half_t*>(ws + w.acc);
+      a.ws_acc = reinterpret_cast<float*>(ws + w.acc);
       a.ws_m = reinterpret_cast<float*>(ws + w.m);
       a.ws_l = reinterpret_cast<float*>(ws + w.l);
       a.ws_cnt = reinterpret_cast<int*>(ws + w.cnt);
       a.nslots = r.dec.nslots;
       a.cap_blocks = r.dec.cap_blocks < max_blocks_per_seq ? r.dec.cap_blocks : max_blocks_per_seq;
-      a.nx = r.dec.nx;
       a.max_splits = r.dec.max_splits;
       a.dm_launch = num_decode * num_kv_heads * a.HG;
       a.pm_x = 4 * cdiv(max_query_len, kTileRows);

@@ -10,9 +10,9 @@ pinned mirror of the arena, then one host-to-device copy) or on the device
 that holds it. Rows past the step's sequences are padding: slot -1 (kv_write skips it), seq_len 0
 (attention writes zeros), token and position 0, an all-zero table row.
 
-Inside a graph the decode kernels take the balanced split (its plan depends on the batch size
-and the device, not on the lengths), so one graph serves every context length up to the table
-width. Nothing captured synchronises with the host or allocates outside the graphs' shared pool.
+Inside a graph the decode kernels take the own-length split schedule with max_seq_len =
+max_model_len (its plan depends on the batch size and that bound, not on the lengths), so one
+graph serves every context length up to the table width. Nothing captured synchronises with the host or allocates outside the graphs' shared pool.
 """
 
 from __future__ import annotations

@@ -27,7 +27,7 @@ __all__ = ["kv_write", "paged_attention", "linear", "lm_head_int8", "logits_int8
            "gate_up_silu", "rope_kv_write_", "decode_kv_write_attention",
            "decode_rope_kv_write_attention"]
 
-DEFAULT_PARTITION = 0            # v3 split size when the caller names none: 0 = balanced
+DEFAULT_PARTITION = 0            # v3 split size when the caller names none: 0 = own-length
 
 
 def _ptr(t: torch.Tensor | None) -> int | None:
@@ -179,7 +179,7 @@ def decode_attention_v3(q, out, k_cache, v_cache, block_tables, seq_lens, scale,
 
 def _decode(q, out, k_cache, v_cache, meta, scale, version: str | None = None):
     """Decode rows [0, num_decode) of the batch (ops/triton_ops.py:35-57). version None lets the
-    library choose: balanced split-K when one workgroup per (sequence, KV head) would leave CUs
+    library choose: own-length split-K when one workgroup per (sequence, KV head) would leave CUs
     idle and contexts exceed 256 tokens, else one workgroup per (sequence, KV head)."""
     _require(version in N.DECODE_VERSIONS, f"unknown decode version {version!r}")
     S = meta.num_decode
@@ -236,7 +236,7 @@ def paged_attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tenso
     """q [T, H, D] -> [T, H*D]: decode kernel on rows [0, num_decode), prefill kernel on the
     remaining sequences, one library call. Unless the caller names a decode version, the active
     variant table's choice for (num_decode, max_seq_len) applies, then the library's own
-    policy with the balanced split (partition 0)."""
+    policy with the own-length split (partition 0)."""
     T, H, D = q.shape
     out = torch.empty(T, H * D, dtype=q.dtype, device=q.device)
     if T == 0:

@@ -18,7 +18,7 @@ W8A16 variants (ts_w8a16_gemm_v): 0 the library's plan, 1 weight streaming (M <=
 2 128 x 64 wide tiles, 3 128 x 128 wide tiles, 4 128 x 32 wide tiles (128 x 64 in the fused
 gated-MLP product), 5 skinny (M <= 64: whole K per workgroup, no split-K), 6 128 x 192 wide
 tiles; splits 0 = the variant's own rule. Decode:
-v2 (one workgroup per sequence and KV head group) or v3 with partition 0 (balanced split) or a
+v2 (one workgroup per sequence and KV head group) or v3 with partition 0 (own-length split) or a
 fixed partition in tokens. Every variant computes the same result up to fp32 summation order.
 """
 
@@ -216,7 +216,7 @@ def tune_w8a16(torch, shapes, ms, device="cuda", table: VariantTable | None = No
 
 def tune_decode(torch, H: int, KVH: int, D: int, seqs, lens, device="cuda",
                 table: VariantTable | None = None, timer=time_call) -> VariantTable:
-    """Time v2 and v3 (balanced and fixed partitions) for S decode rows of length L each."""
+    """Time v2 and v3 (own-length and fixed partitions) for S decode rows of length L each."""
     from turingserve_amd import hip_ops as K_
     from turingserve_amd.metadata import AttentionMetadata
 
