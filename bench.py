@@ -196,6 +196,8 @@ def bench_decode(args, torch, K, synth):
     torch.cuda.synchronize()
     for _ in range(max(1, args.warmup // L)):
         g_step.replay()
+    if g_tail:
+        g_tail.replay()                     # the timed region is never a graph's first replay
     replays = max(1, args.steps // L) if args.steps >= L else 0
 
     def timed(graph):
@@ -224,6 +226,17 @@ def bench_decode(args, torch, K, synth):
     t1 = time.perf_counter()
     steps_timed = replays * L + tail
     step_ev_ms = sum(a.elapsed_time(b) for a, b in ev) / steps_timed
+    # the spread of the same measurement, outside the timed region: 7 more replays of the graph
+    # the timed region used last (the tail graph when --steps is not a multiple of L)
+    rep_graph, rep_n = (g_tail, tail) if g_tail else (g_step, L)
+    rep_ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(7)]
+    for a, b2 in rep_ev:
+        a.record()
+        rep_graph.replay()
+        b2.record()
+    torch.cuda.synchronize()
+    rep_ms = sorted(a.elapsed_time(b2) / rep_n for a, b2 in rep_ev)
     replays = max(replays, 1)
     attn_ms = timed(g_attn)
     other_ms = statistics.fmean(timed(g_other))
@@ -250,6 +263,9 @@ def bench_decode(args, torch, K, synth):
         "fused": not args.separate_kv_write, "split_map": not args.no_split_map,
         ("step_two_launch_ms" if not args.separate_kv_write else "step_fused_ms"): other_ms,
         "warm_step_ms": warm_ms,
+        "step_ev_ms_repeats": {"graph_steps": rep_n, "n": len(rep_ms),
+                               "median": statistics.median(rep_ms), "min": rep_ms[0],
+                               "max": rep_ms[-1]},
     }
     del kv, g_step, g_attn, g_other, g_tail, g_warm
     torch.cuda.synchronize()
@@ -365,7 +381,7 @@ def bench_calibration(torch, synth, layers: int = 28) -> dict:
     from turingserve_amd import _native as N
 
     dev = torch.device("cuda", 0)
-    lib = N.lib()
+    lib = N.probes_lib()                      # measurement-only library
     cur = lambda: torch.cuda.current_stream().cuda_stream      # noqa: E731 (the capture stream)
     out = {}
     a = torch.empty(2 ** 30, dtype=torch.uint8, device=dev)
@@ -781,6 +797,8 @@ def main() -> int:
                                  f"the timed region" if r["fused"] and r["split_map"] else None),
                    other_key.replace("_ms", "_us"): round(r[other_key] * 1e3, 3),
                    "warm_step_us": round(r["warm_step_ms"] * 1e3, 3),
+                   "step_event_us_repeats": {k: (round(v * 1e3, 3) if isinstance(v, float) else v)
+                                             for k, v in r["step_ev_ms_repeats"].items()},
                    "bytes_per_step": b["step"], "parallelism": "single GPU"},
         "roofline": {"bound": "hbm", "kernel": kern,
                      "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

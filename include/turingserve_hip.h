@@ -490,19 +490,6 @@ int ts_rope_kv_write(void* qkv, int64_t qkv_stride, const int64_t* positions,
 int ts_silu_mul(const void* gu, int64_t gu_stride, void* out, int64_t out_stride,
                 int64_t num_tokens, int32_t intermediate, void* stream);
 
-/*
- * Measurement probes (no counterpart in the reference; used by bench.py to measure the ceilings
- * its roofline fractions are read against).
- * ts_probe_gather: reads n_chunks chunks of chunk_bytes (2048 or 4096) at base + chunk_offsets[i]
- * (bytes, 16-byte aligned) with no arithmetic; writes one word per 8 chunks to sink
- * (ceil(n_chunks / 8) words). ts_probe_mfma: `workgroups` workgroups of 4 wavefronts, each
- * wavefront runs `iters` rounds of four independent v_mfma_f32_32x32x16_f16 (4 * 32768 flops);
- * writes one float per wavefront to sink.
- */
-int ts_probe_gather(const void* base, const int64_t* chunk_offsets, int32_t n_chunks,
-                    int32_t chunk_bytes, uint32_t* sink, void* stream);
-int ts_probe_mfma(int32_t workgroups, int32_t iters, float* sink, void* stream);
-
 #ifdef __cplusplus
 }
 #endif

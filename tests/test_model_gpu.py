@@ -112,3 +112,42 @@ def test_graph_equals_eager(n):
             assert torch.equal(eager, graph)
             hip.forward(inp.input_ids, inp.positions, inp.meta, kv)
             torch.cuda.synchronize()
+
+
+def test_back_to_back_graph_steps_without_a_sync():
+    """Two host-filled replays in a row with no synchronisation between them (the second fill
+    rewrites the pinned stage the first copy reads): each must still equal its eager step."""
+    hip, _ = model_pair(TINY_G2)
+    nb = 600
+    kv = hip.new_kv_cache(nb)
+    graphs = DecodeGraphs(hip, kv, (1, 2, 4, 8), 32, 512)
+    graphs.capture()
+    free = list(range(1, nb))
+    random.Random(7).shuffle(free)
+
+    def make(n, seed):
+        out = []
+        for i in range(n):
+            L = 9 + 23 * i + seed
+            s = SeqState(rand_ids(L, seed=100 * seed + i))
+            s.block_table = [free.pop() for _ in range(-(-L // 16))]
+            out.append(BatchItem(s, L - 1, [s.token_ids[-1]], "last"))
+        return out
+
+    sets = [make(4, 1), make(3, 2)]
+    eager = []
+    with torch.inference_mode():
+        for items in sets:
+            pre = InputBuilder(8192, 64, 32, DEV).build(
+                [BatchItem(it.seq, 0, it.seq.token_ids[:-1], "none") for it in items])
+            hip.forward(pre.input_ids, pre.positions, pre.meta, kv)
+            inp = InputBuilder(256, 64, 32, DEV).build(items)
+            eager.append(hip.compute_logits(hip.forward(inp.input_ids, inp.positions, inp.meta, kv),
+                                            inp.sample_indices).clone())
+        torch.cuda.synchronize()
+        for _ in range(3):
+            got = [graphs.run(items).clone() for items in sets]     # no synchronisation between
+            torch.cuda.synchronize()
+            for e, g in zip(eager, got):
+                assert torch.equal(e, g)
+

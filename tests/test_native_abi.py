@@ -14,10 +14,11 @@ from turingserve_amd import _native as N
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "turingserve_hip.h")
+PROBES_HEADER = os.path.join(ROOT, "include", "turingserve_probes.h")
 
 
-def declared_functions() -> list[str]:
-    text = open(HEADER, encoding="utf-8").read()
+def declared_functions(header: str = HEADER) -> list[str]:
+    text = open(header, encoding="utf-8").read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     return sorted(set(re.findall(r"\b(ts_[a-z0-9_]+)\s*\(", text)))
 
@@ -30,6 +31,20 @@ def test_every_declared_symbol_is_exported_and_bound():
         assert hasattr(lib, name), f"{name} declared but not exported"
         assert name in N.SIGNATURES, f"{name} has no ctypes signature"
     assert set(N.SIGNATURES) == set(names)
+
+
+def test_probes_are_a_separate_measurement_library():
+    """The measurement probes are not part of the product ABI: declared in their own header,
+    exported by libturingserve_probes.so only."""
+    names = declared_functions(PROBES_HEADER)
+    assert names == ["ts_probe_gather", "ts_probe_mfma"]
+    assert not set(names) & set(declared_functions())
+    for name in names:
+        assert not hasattr(N.lib(), name), f"{name} exported by the product library"
+        assert hasattr(N.probes_lib(), name)
+    assert set(N.PROBE_SIGNATURES) == set(names)
+    st = N.probes_lib().ts_probe_mfma(0, 1, None, None)
+    assert st == N.TS_ERR_INVALID_ARG and N.last_error() != ""
 
 
 def test_version_and_empty_error():

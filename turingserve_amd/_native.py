@@ -97,6 +97,10 @@ SIGNATURES = {
     "ts_rope_kv_write": (ctypes.c_int, [_p, _i64, _p, _p, _p, _i64, _i64, _i32, _i32, _i32, _p,
                                         _p, _i64, _p, _p]),
     "ts_silu_mul": (ctypes.c_int, [_p, _i64, _p, _i64, _i64, _i32, _p]),
+}
+
+# The measurement-only probes library (include/turingserve_probes.h): not part of the product ABI.
+PROBE_SIGNATURES = {
     "ts_probe_gather": (ctypes.c_int, [_p, _p, _i32, _i32, _p, _p]),
     "ts_probe_mfma": (ctypes.c_int, [_i32, _i32, _p, _p]),
 }
@@ -117,6 +121,22 @@ def lib() -> ctypes.CDLL:
     except OSError as e:
         raise NativeLibraryError(f"cannot load {LIB_PATH}: {e}") from e
     for name, (res, args) in SIGNATURES.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    return L
+
+
+@functools.lru_cache(maxsize=1)
+def probes_lib() -> ctypes.CDLL:
+    """libturingserve_probes.so (measurement only, bench.py's calibration); loads the product
+    library first, whose status codes and ts_last_error it shares."""
+    lib()
+    path = os.path.join(os.path.dirname(LIB_PATH), "libturingserve_probes.so")
+    if not os.path.exists(path):
+        raise NativeLibraryError(f"{path} not found: build it with `python -m turingserve_amd.csrc.build`")
+    L = ctypes.CDLL(path)
+    for name, (res, args) in PROBE_SIGNATURES.items():
         fn = getattr(L, name)
         fn.restype = res
         fn.argtypes = args

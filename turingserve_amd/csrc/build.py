@@ -1,10 +1,12 @@
 """Build libturingserve_hip.so (gfx950 only) from the .hip sources next to this file.
 
-    python -m turingserve_amd.csrc.build           # compile every source, link the library
+    python -m turingserve_amd.csrc.build           # compile every source, link the libraries
 
 Each source is compiled on its own (in parallel) into ``_build/`` and linked into
-``turingserve_amd/lib/libturingserve_hip.so``. Packed-FP32 instructions are disabled for every
-kernel (``-Xclang -target-feature -Xclang -packed-fp32-ops``).
+``turingserve_amd/lib/libturingserve_hip.so``; the measurement probes (probes.hip, declared in
+include/turingserve_probes.h, not part of the product ABI) go into their own
+``libturingserve_probes.so``, linked against the product library. Packed-FP32 instructions are
+disabled for every kernel (``-Xclang -target-feature -Xclang -packed-fp32-ops``).
 """
 
 from __future__ import annotations
@@ -19,9 +21,11 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 PKG = os.path.dirname(HERE)
 LIB_DIR = os.path.join(PKG, "lib")
 LIB_PATH = os.path.join(LIB_DIR, "libturingserve_hip.so")
+PROBES_PATH = os.path.join(LIB_DIR, "libturingserve_probes.so")
 BUILD_DIR = os.path.join(HERE, "_build")
 SOURCES = ["capi.hip", "kv_write.hip", "decode.hip", "prefill.hip", "ragged.hip", "w8a16.hip",
-           "small_ops.hip", "metadata.hip", "probes.hip"]
+           "small_ops.hip", "metadata.hip"]
+PROBE_SOURCES = ["probes.hip"]
 ARCH = "gfx950"
 
 COMMON_FLAGS = [
@@ -58,21 +62,29 @@ def _compile(src: str, extra: list[str]) -> str:
     return obj
 
 
+def _link(path: str, objs: list[str], libs: list[str]) -> None:
+    tmp = path + ".tmp"
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs, *libs]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
+    os.replace(tmp, path)
+
+
 def build(verbose: bool = False, extra: list[str] | None = None) -> str:
-    """Compile every source and link the shared library; returns its path."""
+    """Compile every source, link the product library and the probes library; returns the
+    product library's path."""
     os.makedirs(BUILD_DIR, exist_ok=True)
     os.makedirs(LIB_DIR, exist_ok=True)
     extra = list(extra or [])
     if verbose:
         extra.append("-Rpass-analysis=kernel-resource-usage")
-    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(SOURCES))) as ex:
-        objs = list(ex.map(lambda s: _compile(s, extra), SOURCES))
-    tmp = LIB_PATH + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
-    r = subprocess.run(cmd, capture_output=True, text=True)
-    if r.returncode != 0:
-        raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
-    os.replace(tmp, LIB_PATH)
+    srcs = SOURCES + PROBE_SOURCES
+    with concurrent.futures.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = dict(zip(srcs, ex.map(lambda s: _compile(s, extra), srcs)))
+    _link(LIB_PATH, [objs[s] for s in SOURCES], [])
+    _link(PROBES_PATH, [objs[s] for s in PROBE_SOURCES],
+          [f"-L{LIB_DIR}", "-lturingserve_hip", "-Wl,-rpath,$ORIGIN"])
     return LIB_PATH
 
 

@@ -502,10 +502,6 @@ __device__ __forceinline__ void prefill_tile_body(
     const char* kr0 = kb + r * L::KROW + 16 * hh;
     const char* kr1 = kr0 + 32 * L::KROW;
     half8_t ka[2][2];
-    // Raised priority over the MFMA blocks: of the wavefronts sharing a SIMD, the one entering
-    // its MFMAs is served first, which moves co-resident wavefronts into alternating MFMA and
-    // softmax phases instead of lockstep.
-    __builtin_amdgcn_s_setprio(1);
     ka[0][0] = ld<half8_t>(kr0);
     ka[1][0] = ld<half8_t>(kr1);
 #pragma unroll
@@ -519,7 +515,6 @@ __device__ __forceinline__ void prefill_tile_body(
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);   // the two reads ...
       __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);   // ... then the two MFMAs
     }
-    __builtin_amdgcn_s_setprio(0);
     if (k0 + kTileKeys - 1 > sq.prefix + r0) {     // diagonal or tail step: per-key mask
 #pragma unroll
       for (int x = 0; x < 2; ++x)
@@ -553,7 +548,6 @@ __device__ __forceinline__ void prefill_tile_body(
         p[u][i] = (half_t)pv;
       }
     l += ls;
-    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
@@ -561,7 +555,6 @@ __device__ __forceinline__ void prefill_tile_body(
         o[t] = mfma32x32x16(
             ld<half8_t>(vb + (32 * t + r) * L::VROW + 16 * ((2 * u + hh) ^ vt_swz(32 * t + r))),
             p[u], o[t]);
-    __builtin_amdgcn_s_setprio(0);
   };
 
   // Step s sits in LDS buffer (s - lo) % 2 while the registers hold step s + 1 (loaded one

@@ -43,6 +43,7 @@ class StaticDecodeBatch:
         self._h[5][:] = np.arange(rows + 1)
         self._h[6][:] = np.arange(rows)
         self.arena.copy_(self.stage)
+        self._copied: torch.cuda.Event | None = None    # the last stage -> arena copy
 
     def meta(self, B: int, max_model_len: int) -> AttentionMetadata:
         return AttentionMetadata(
@@ -52,7 +53,11 @@ class StaticDecodeBatch:
 
     def fill_from_host(self, items: list[BatchItem], B: int) -> None:
         """Rows 0 .. len(items)-1 from the items (one token each), rows up to B padding; one
-        copy of the changing part of the arena."""
+        copy of the changing part of the arena. The copy reads the pinned stage asynchronously:
+        before the stage is written again, the previous call's copy is waited for (an event
+        recorded after it), so two calls in a row without a synchronisation cannot race."""
+        if self._copied is not None:
+            self._copied.synchronize()
         n = len(items)
         ids, pos, slots, sl, tables = self._h[:5]
         start = np.fromiter((it.start for it in items), np.int64, n)
@@ -70,6 +75,9 @@ class StaticDecodeBatch:
         slots[:n] = tables[np.arange(n), start // 16].astype(np.int64) * 16 + start % 16
         ids[n:B], pos[n:B], slots[n:B], sl[n:B] = 0, 0, -1, 0
         self.arena[:self._dirty].copy_(self.stage[:self._dirty], non_blocking=True)
+        if self._copied is None:
+            self._copied = torch.cuda.Event()
+        self._copied.record()
 
 
 class DecodeGraphs:
