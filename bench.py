@@ -469,8 +469,14 @@ def bench_w8a16(torch, K, synth, ms=None):
     """Config 4: every (M, N, K) point (or the M values in `ms`), timed cold (the weight cycles
     through copies whose total exceeds the Infinity Cache, one copy per call inside the graph) and
     warm (one copy, replayed 20 times: it stays in the 256 MB cache). Roofline fraction from the
-    cold time."""
+    cold time. At M >= 256 the reference's own route for those rows (ops/triton_ops.py:84-85:
+    dequantise the int8 weight to fp16, then F.linear on the vendor BLAS) is timed beside the
+    kernel, cold, as `ref_route_us`."""
     import itertools
+
+    import torch.nn.functional as F
+
+    from turingserve_amd.quant import dequantize
 
     dev = torch.device("cuda", 0)
     ms = list(ms or synth.W8A16_M)
@@ -490,11 +496,18 @@ def bench_w8a16(torch, K, synth, ms=None):
             flop = 2.0 * M * Nn * Kd
             t_hbm = byts / (HBM_PEAK_GBS * 1e9)
             t_mfma = flop / (MFMA_FP16_PEAK_TFLOPS * 1e12)
-            rows.append({"M": M, "N": Nn, "K": Kd, "us": round(cold * 1e3, 2),
-                         "us_warm": round(warm * 1e3, 2),
-                         "GBps": round(byts / cold / 1e6, 1), "TFLOPs": round(flop / cold / 1e9, 2),
-                         "bound": "hbm" if t_hbm >= t_mfma else "mfma",
-                         "roofline_frac": round(max(t_hbm, t_mfma) / (cold / 1e3), 4)})
+            row = {"M": M, "N": Nn, "K": Kd, "us": round(cold * 1e3, 2),
+                   "us_warm": round(warm * 1e3, 2),
+                   "GBps": round(byts / cold / 1e6, 1), "TFLOPs": round(flop / cold / 1e9, 2),
+                   "bound": "hbm" if t_hbm >= t_mfma else "mfma",
+                   "roofline_frac": round(max(t_hbm, t_mfma) / (cold / 1e3), 4)}
+            if M >= 256:
+                it2 = itertools.cycle(wqs)
+                ref = time_graph(torch, lambda: F.linear(x, dequantize(next(it2), sc, x.dtype)),
+                                 reps=3, inner=len(wqs))
+                row["ref_route_us"] = round(ref * 1e3, 2)
+                row["kernel_faster_than_ref_route"] = bool(cold < ref)
+            rows.append(row)
         del wqs
         torch.cuda.empty_cache()
     per_layer = {}

@@ -107,9 +107,13 @@ int ts_kv_write(const void* k, const void* v,
  * split_map / split_map_bytes: NULL / 0, or a map that ts_decode_split_map built from the same
  * seq_lens, block tables and plan arguments (version, num_seqs, heads, head_dim, max_seq_len,
  * partition, max_blocks_per_seq): the v3 split kernel then reads its split and its first block
- * ids from the map instead of scanning seq_lens. The results are identical either way; a map
- * built for another plan is ignored (the kernel scans), one smaller than the plan needs is an
- * error. The map must be rebuilt whenever seq_lens or the block tables change.
+ * ids from the map instead of scanning seq_lens, and merges its splits in the same launch (the
+ * last split workgroup of each sequence and head group merges them, counted in the map; no
+ * merge launch follows). The results are identical either way. A map built for another plan
+ * poisons the rows (NaN); one smaller than the plan needs is an error; one built from other
+ * seq_lens or block tables (an earlier step) poisons the rows whose length or last block moved.
+ * The map must be rebuilt whenever seq_lens or the block tables change, and calls that share a
+ * map must not overlap in time (its counters are shared; one stream orders them).
  * Replaces ops/triton_ops.py:35-57 and ops/triton_decode_attention.py:169-200.
  */
 size_t ts_decode_workspace_bytes(int32_t version, int32_t num_seqs, int32_t num_heads,

@@ -207,12 +207,13 @@ def test_workspace_sizes():
 
 def test_split_map_sizes_and_checks():
     lib = N.lib()
-    # one header of 8 ints and 32 ints per launch slot of the v3 plan: the own-length schedule
-    # launches ceil(max blocks / 24) slots per sequence (11 at 4096 tokens, 3 at 1024), the
-    # fixed grid 16 slots per sequence at 4096 / 256
-    assert lib.ts_decode_split_map_bytes(3, 64, 12, 2, 128, 4096, 0, 256) == (8 + 64 * 11 * 32) * 4
-    assert lib.ts_decode_split_map_bytes(3, 64, 12, 2, 128, 4096, 256, 256) == (8 + 64 * 16 * 32) * 4
-    assert lib.ts_decode_split_map_bytes(0, 64, 12, 2, 128, 1024, 0, 256) == (8 + 64 * 3 * 32) * 4
+    # one header of 8 ints, 32 ints per launch slot of the v3 plan and one arrival counter per
+    # (sequence, KV head, head group): the own-length schedule launches ceil(max blocks / 24)
+    # slots per sequence (11 at 4096 tokens, 3 at 1024), the fixed grid 16 slots per sequence at
+    # 4096 / 256; 64 sequences x 2 KV heads x 1 head group of counters
+    assert lib.ts_decode_split_map_bytes(3, 64, 12, 2, 128, 4096, 0, 256) == (8 + 64 * 11 * 32 + 128) * 4
+    assert lib.ts_decode_split_map_bytes(3, 64, 12, 2, 128, 4096, 256, 256) == (8 + 64 * 16 * 32 + 128) * 4
+    assert lib.ts_decode_split_map_bytes(0, 64, 12, 2, 128, 1024, 0, 256) == (8 + 64 * 3 * 32 + 128) * 4
     # no split, no map: v1 / v2, AUTO resolving to v2, more than 4096 sequences
     assert lib.ts_decode_split_map_bytes(2, 64, 12, 2, 128, 4096, 0, 256) == 0
     assert lib.ts_decode_split_map_bytes(1, 64, 12, 2, 128, 4096, 0, 256) == 0

@@ -44,6 +44,26 @@ __device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t 
 __device__ __forceinline__ half4_t lo4(half8_t v) { return {v[0], v[1], v[2], v[3]}; }
 __device__ __forceinline__ half4_t hi4(half8_t v) { return {v[4], v[5], v[6], v[7]}; }
 
+// Device-coherent (sc1) buffer accesses: data one workgroup stores and another, on any XCD,
+// loads in the same launch after an agent-scope atomic has ordered them (the stores are waited
+// for, vmcnt 0, before the atomic). The resource is built from a wave-uniform base, the lane's
+// byte offset (below 2 GiB) travels in a VGPR; the raw buffer builtins move 32-bit words, so
+// floats travel as their bits.
+constexpr int kCoherentPolicy = 16;            // buffer cache policy bits: sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t coherent_rsrc(const void* uniform_base) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(uniform_base), (short)0, 0x7fffffff,
+                                           0x00020000);
+}
+__device__ __forceinline__ void coherent_store(__amdgpu_buffer_rsrc_t r, int off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(uint32_t, v), r, off, 0, kCoherentPolicy);
+}
+__device__ __forceinline__ float coherent_load(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, kCoherentPolicy));
+}
+__device__ __forceinline__ float4_t coherent_load4(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(float4_t, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCoherentPolicy));
+}
+
 __device__ __forceinline__ half4_t to_half4(float4_t v) {
   return {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
 }

@@ -24,7 +24,7 @@ extern "C" size_t ts_decode_split_map_bytes(int32_t version, int32_t num_seqs, i
   if (num_seqs > kMapMaxSeqs) return 0;
   const SplitPlan p = plan_decode(version, num_seqs, num_heads, num_kv_heads, head_dim,
                                   max_seq_len, partition, cu_count > 0 ? cu_count : 256);
-  return map_bytes_of(p);
+  return map_bytes_of(p, num_seqs, num_kv_heads * ((num_heads / num_kv_heads + 15) / 16));
 }
 
 extern "C" int ts_decode_split_map(int32_t version, const int32_t* block_tables, int64_t bt_stride,
@@ -54,13 +54,14 @@ extern "C" int ts_decode_split_map(int32_t version, const int32_t* block_tables,
   if (st != TS_OK) return st;
   const SplitPlan p = plan_decode(version, num_seqs, num_heads, num_kv_heads, head_dim,
                                   max_seq_len, partition, cus);
-  const size_t need = map_bytes_of(p);
+  const int groups = num_kv_heads * ((num_heads / num_kv_heads + 15) / 16);
+  const size_t need = map_bytes_of(p, num_seqs, groups);
   if (need == 0) return TS_OK;                 // this plan does not split: no map
   TS_REQUIRE(split_map && split_map_bytes >= need && aligned(split_map, 16), TS_ERR_WORKSPACE,
              "decode_split_map: map of %zu bytes (16-byte aligned) needed, got %zu", need,
              split_map_bytes);
   launch_split_map(p, reinterpret_cast<hipStream_t>(stream), seq_lens, block_tables, bt_stride,
-                   num_blocks, max_blocks_per_seq, num_seqs, static_cast<int*>(split_map));
+                   num_blocks, max_blocks_per_seq, num_seqs, groups, static_cast<int*>(split_map));
   return check_launch("decode_split_map");
 }
 
@@ -102,12 +103,14 @@ static int decode_entry(int32_t version, const void* q, int64_t q_stride_t, int6
   TS_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 256)),
              TS_ERR_WORKSPACE, "decode_attention: workspace of %zu bytes (256-aligned) needed, got %zu",
              need, workspace_bytes);
-  const size_t map_need = split_map ? map_bytes_of(p) : 0;
+  const size_t map_need =
+      split_map ? map_bytes_of(p, num_seqs, num_kv_heads * ((num_heads / num_kv_heads + 15) / 16)) : 0;
   TS_REQUIRE(map_need == 0 || (split_map_bytes >= map_need && aligned(split_map, 16)),
              TS_ERR_INVALID_ARG,
              "decode_attention: split map of %zu bytes (16-byte aligned) needed for this plan, got %zu",
              map_need, split_map_bytes);
-  const int* smap = map_need ? static_cast<const int*>(split_map) : nullptr;
+  // the map's arrival counters are written in place (and left at zero) by the in-launch merge
+  int* smap = map_need ? static_cast<int*>(const_cast<void*>(split_map)) : nullptr;
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   if (nr.k) {
     // The fused write needs the MFMA kernels with one head group per KV head (so the workgroup

@@ -149,6 +149,10 @@ __device__ __forceinline__ int round_part(int blocks) {
   return (blocks + kMinPartBlocks - 1) / kMinPartBlocks * kMinPartBlocks;
 }
 
+// Splits of a sequence of nb blocks cut into ps-block pieces: a sequence with no blocks (a
+// padding row, seq_len 0) still gets one split, whose workgroup writes the row's zeros.
+__device__ __forceinline__ int split_count(int nb, int ps) { return nb > 0 ? (nb + ps - 1) / ps : 1; }
+
 // P_s of a sequence of nb blocks: the caller's partition P, or (P <= 0, the own-length
 // schedule) nb cut into min(max_splits, ceil(nb / kOwnPartBlocks)) near-equal splits.
 __device__ __forceinline__ int seq_part(int P, int nb, int max_splits) {
@@ -182,7 +186,7 @@ __device__ SplitSlot split_lookup(const int* __restrict__ seq_lens, int S, int c
     const int len = c0 == 0 ? len0 : (i < S ? clamp_len(seq_lens[i]) : 0);
     const int nb = (len + kBlockSize - 1) / kBlockSize;
     const int ps = seq_part(part_blocks, nb, max_splits);
-    const int n = (nb + ps - 1) / ps;
+    const int n = i < S ? split_count(nb, ps) : 0;
     const int incl = wave_inclusive_sum(n, lane);
     if (lane == kWave - 1) s_map[w] = incl;
     __syncthreads();
@@ -194,7 +198,7 @@ __device__ SplitSlot split_lookup(const int* __restrict__ seq_lens, int S, int c
       tot += v;
     }
     const int excl = off + incl - n;
-    if (i < S && n > 0 && slot >= excl && slot < excl + n) {
+    if (i < S && slot >= excl && slot < excl + n) {
       s_map[NWV] = i;
       s_map[NWV + 1] = excl;
       s_map[NWV + 2] = n;
@@ -232,7 +236,8 @@ __device__ __forceinline__ int4 int4_of(int a, int b, int c, int d) { return int
 template <int NT>
 __global__ void __launch_bounds__(NT) decode_split_map_kernel(
     const int* __restrict__ seq_lens, const int* __restrict__ bt, int64_t bt_st, int64_t NB,
-    int S, int cap_blocks, int part_blocks, int max_splits, int nslots, int* __restrict__ map) {
+    int S, int cap_blocks, int part_blocks, int max_splits, int nslots, int n_counters,
+    int* __restrict__ map) {
   constexpr int NWV = NT / kWave;
   __shared__ int s_first[kMapMaxSeqs];
   __shared__ int s_len[kMapMaxSeqs];
@@ -254,7 +259,7 @@ __global__ void __launch_bounds__(NT) decode_split_map_kernel(
       const int nb = (s_len[i] + kBlockSize - 1) / kBlockSize;
       const int ps = seq_part(part_blocks, nb, max_splits);
       s_part[i] = ps;
-      n = (nb + ps - 1) / ps;
+      n = split_count(nb, ps);
     }
     const int incl = wave_inclusive_sum(n, lane);
     if (lane == kWave - 1) s_red[w] = incl;
@@ -270,6 +275,10 @@ __global__ void __launch_bounds__(NT) decode_split_map_kernel(
     base += tot;
     __syncthreads();
   }
+  // the arrival counters of the split kernel's in-launch merge start at zero (each merge resets
+  // its counter, so the map stays valid for every layer of the step)
+  int* counters = map + kMapHeader + (int64_t)nslots * kMapEntry;
+  for (int i = tid; i < n_counters; i += NT) counters[i] = 0;
   if (tid == 0) {
     int4* h = reinterpret_cast<int4*>(map);
     h[0] = int4_of(kMapMagic, S, nslots, part_blocks);
@@ -285,7 +294,7 @@ __global__ void __launch_bounds__(NT) decode_split_map_kernel(
     }
     const int i = lo, len = s_len[i], ps = s_part[i];
     const int nb = (len + kBlockSize - 1) / kBlockSize;
-    const int n = (nb + ps - 1) / ps;
+    const int n = split_count(nb, ps);
     int4* dst = reinterpret_cast<int4*>(map + kMapHeader + (int64_t)slot * kMapEntry);
     const int j = slot - s_first[i];
     if (j >= n) {                              // past the batch's last split
@@ -306,10 +315,10 @@ __global__ void __launch_bounds__(NT) decode_split_map_kernel(
       for (int h = 0; h < 2; ++h) {
         int bi = blk_lo + 2 * qq + h;
         bi = bi < blk_hi ? bi : blk_hi - 1;
-        ids[2 * q + h] = clamp_block(btrow[bi], NB);
+        ids[2 * q + h] = nb > 0 ? clamp_block(btrow[bi], NB) : 0;   // no blocks: nothing read
       }
     }
-    const int last = clamp_block(btrow[(len - 1) / kBlockSize], NB);
+    const int last = len > 0 ? clamp_block(btrow[(len - 1) / kBlockSize], NB) : 0;
     dst[0] = int4_of(i, s_first[i], n, len);
     dst[1] = int4_of(blk_lo, blk_hi, last, ps);
 #pragma unroll
@@ -365,7 +374,7 @@ __device__ __forceinline__ void decode_mfma_body(
     int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
     float* __restrict__ ws_l, int* __restrict__ ws_cnt,
     int bx, int bz, char* __restrict__ lds, const NewRows& nr = NewRows{},
-    const int* __restrict__ smap = nullptr) {
+    int* __restrict__ smap = nullptr) {
   constexpr int KK = KvRegs<D>::KK;
   constexpr int VW = KvRegs<D>::VW;
   constexpr int TILES = KvRegs<D>::TILES;
@@ -416,7 +425,20 @@ __device__ __forceinline__ void decode_mfma_body(
     seq_len = sp.len;
     nsplit = sp.count;
     split_j = bx - sp.first;
+    if (smap != nullptr && !mapped) {
+      // A map whose header names another plan: the launch has no merge kernel after it (the
+      // map's workgroups merge in-launch), so the rows are poisoned, loudly, not attended.
+      if (split_j == 0)
+        for (int e = tid; e < nh * D; e += NW * 64)
+          out[(int64_t)s * o_st + (int64_t)(head0 + e / D) * D + e % D] = (half_t)__builtin_nanf("");
+      return;
+    }
     if (split_j == 0 && tid == 0) ws_cnt[s] = nsplit;   // read by the merge kernel
+    if (seq_len == 0) {                          // padding row: zeros (ops/reference.py:99,104-105)
+      for (int e = tid; e < nh * D; e += NW * 64)
+        out[(int64_t)s * o_st + (int64_t)(head0 + e / D) * D + e % D] = (half_t)0.f;
+      return;
+    }
     const int nblk = (seq_len + kBlockSize - 1) / kBlockSize;
     blk_lo = split_j * sp.part;
     blk_hi = (blk_lo + sp.part) < nblk ? (blk_lo + sp.part) : nblk;
@@ -665,15 +687,60 @@ __device__ __forceinline__ void decode_mfma_body(
     if (poison) L = __builtin_nanf("");             // reaches the output through the merge too
     if (nsplit == 1) {
       out[(int64_t)s * o_st + (int64_t)(head0 + hh) * D + d] = (half_t)(O / L);
-    } else {
+    } else if (!mapped) {
       const int64_t pidx = ((int64_t)s * max_splits + split_j) * H + head0 + hh;
       ws_acc[pidx * D + d] = O;                  // fp32 (acc, m, l), as the reference keeps them
       if (d == 0) {
         ws_m[pidx] = M;
         ws_l[pidx] = L;
       }
+    } else {                                     // for the in-launch merge: device-coherent stores
+      // (offsets within sequence s's rows of the workspace: resources from its first row)
+      const int pj = split_j * H + head0 + hh;
+      coherent_store(coherent_rsrc(ws_acc + (int64_t)s * max_splits * H * D), (pj * D + d) * 4, O);
+      if (d == 0) {
+        coherent_store(coherent_rsrc(ws_m + (int64_t)s * max_splits * H), pj * 4, M);
+        coherent_store(coherent_rsrc(ws_l + (int64_t)s * max_splits * H), pj * 4, L);
+      }
     }
   }
+  if (!mapped || nsplit == 1) return;
+  // In-launch merge (a launch with the step's map): the last split of (sequence, KV head, head
+  // group) to finish merges all of them, as decode_merge_kernel would, and resets the counter.
+  // Its partial reaches the coherence point (vmcnt 0) before its arrival counts; the others are
+  // read from there.
+  __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
+  __syncthreads();
+  int* counter = smap + kMapHeader + (int64_t)gridDim.x * kMapEntry + (int64_t)s * (KVH * HG) + bz;
+  if (tid == 0)
+    s_map[0] = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+               nsplit - 1;
+  __syncthreads();
+  if (!s_map[0]) return;
+  constexpr int TPH = D / 8;                     // threads per head (8 dims each), as the merge
+  constexpr int HPP = NW * 64 / TPH;             // kernel's workgroup
+  static_assert(NW * 64 == 256, "the merge layout is that of decode_merge_kernel");
+  const auto r_acc = coherent_rsrc(ws_acc + (int64_t)s * max_splits * H * D);
+  const auto r_m = coherent_rsrc(ws_m + (int64_t)s * max_splits * H);
+  const auto r_l = coherent_rsrc(ws_l + (int64_t)s * max_splits * H);
+  for (int hp = 0; hp < nh; hp += HPP) {
+    const int hh = hp + tid / TPH, d0 = (tid % TPH) * 8;
+    if (hh >= nh) continue;
+    const int64_t hoff = head0 + hh;
+    float4_t O0, O1;
+    float L;
+    merge_dims8(nsplit, [&](int j, float& mj, float& lj, float4_t& a0, float4_t& a1) {
+      const int pj = j * H + (int)hoff;
+      mj = coherent_load(r_m, pj * 4);
+      lj = coherent_load(r_l, pj * 4);
+      a0 = coherent_load4(r_acc, (pj * D + d0) * 4);
+      a1 = coherent_load4(r_acc, (pj * D + d0 + 4) * 4);
+    }, O0, O1, L);
+    half_t* dst = out + (int64_t)s * o_st + hoff * D + d0;
+    st<half4_t>(dst, to_half4(O0 / L));
+    st<half4_t>(dst + 4, to_half4(O1 / L));
+  }
+  if (tid == 0) __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <int D, int NW, bool WRITE = false, bool ROPE = false>
@@ -684,7 +751,7 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
     int S, int H, int KVH, int G, int HG, float sl2, int cap_blocks, int part_blocks,
     int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
     float* __restrict__ ws_l, int* __restrict__ ws_cnt, const NewRows nr,
-    const int* __restrict__ smap) {
+    int* __restrict__ smap) {
   __shared__ __attribute__((aligned(16))) char lds[DecodeLds<D, NW>::BYTES];
   decode_mfma_body<D, NW, WRITE, ROPE>(q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks,
                                  seq_lens, S, H, KVH, G, HG, sl2, cap_blocks, part_blocks,
@@ -704,6 +771,57 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
 constexpr int kMaxSplits = 256;
 constexpr int kMergeChunk = 16;
 
+// One thread's share of a merge: dims d0 .. d0 + 7 of one query head over the n split partials
+// that load(j, m, l, a0, a1) returns (split j's m, l and acc[d0 .. d0 + 7]), taken CH at a time,
+// all of a chunk's loads requested together. O0 / O1 / L come back unnormalised. The merge
+// kernel and the split kernel's last workgroup both merge through this function, so a row merged
+// either way has the same value.
+template <class Load>
+__device__ __forceinline__ void merge_dims8(int n, Load load, float4_t& O0, float4_t& O1,
+                                            float& L) {
+  constexpr int CH = kMergeChunk;
+  float mv[CH], lv[CH];
+  float4_t av[CH][2];
+  auto load_chunk = [&](int j0) {
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      if (j0 + u < n) {                          // uniform over the workgroup
+        load(j0 + u, mv[u], lv[u], av[u][0], av[u][1]);
+      } else {
+        mv[u] = -INFINITY;
+        lv[u] = 0.f;
+        av[u][0] = float4_t{0.f, 0.f, 0.f, 0.f};
+        av[u][1] = float4_t{0.f, 0.f, 0.f, 0.f};
+      }
+    }
+  };
+  load_chunk(0);
+  float M = -INFINITY;
+  L = 0.f;
+  O0 = float4_t{0.f, 0.f, 0.f, 0.f};
+  O1 = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < n; j0 += CH) {
+    if (j0 > 0) load_chunk(j0);
+    float cm = M;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) cm = (j0 + u < n) ? fmaxf(cm, mv[u]) : cm;
+    const float alpha = fast_exp2(M - cm);       // M = -inf on the first chunk -> 0
+    L *= alpha;
+    O0 *= alpha;
+    O1 *= alpha;
+#pragma unroll
+    for (int u = 0; u < CH; ++u) {
+      // rows past n are skipped, not weighted by 0: their stale contents may be inf or NaN
+      const float wt = fast_exp2(mv[u] - cm);
+      L = (j0 + u < n) ? L + wt * lv[u] : L;
+      const float4_t o0 = O0 + wt * av[u][0], o1 = O1 + wt * av[u][1];
+      O0 = (j0 + u < n) ? o0 : O0;
+      O1 = (j0 + u < n) ? o1 : O1;
+    }
+    M = cm;
+  }
+}
+
 template <int D>
 __device__ __forceinline__ void decode_merge_body(
     const float* __restrict__ ws_acc, const float* __restrict__ ws_m,
@@ -711,7 +829,6 @@ __device__ __forceinline__ void decode_merge_body(
     int64_t o_st, const int* __restrict__ seq_lens, int H, int G, int HG, int max_splits, int bx, int by) {
   constexpr int TPH = D / 8;                     // threads per head (8 dims each)
   constexpr int HPP = 256 / TPH;                 // heads per pass
-  constexpr int CH = kMergeChunk;
   const int s = bx, kvh = by / HG, hg = by % HG;
   const int tid = threadIdx.x;
   const int nh = (G - hg * 16) < 16 ? (G - hg * 16) : 16;
@@ -724,8 +841,6 @@ __device__ __forceinline__ void decode_merge_body(
     if (hh >= nh) continue;                      // no head for this thread (no barrier below)
     const int64_t hoff = head0 + hh;
     half_t* dst = out + (int64_t)s * o_st + (head0 + hh) * (int64_t)D + d0;
-    float mv[CH], lv[CH];
-    float4_t av[CH][2];
     if (len <= 0) {                              // padding row: zeros (ops/reference.py:99,104-105)
       st<half4_t>(dst, half4_t{0, 0, 0, 0});     // output rows are 8-byte aligned: two stores
       st<half4_t>(dst + 4, half4_t{0, 0, 0, 0});
@@ -734,46 +849,15 @@ __device__ __forceinline__ void decode_merge_body(
     const int n = cnt < 1 ? 1 : (cnt > max_splits ? max_splits : cnt);
     if (n == 1) return;                          // written by the first kernel
     // rows past n are neither requested nor used: their stale contents may be inf or NaN
-    auto load_chunk = [&](int j0) {
-#pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        if (j0 + u < n) {                        // uniform over the workgroup
-          const int64_t pidx = (row0 + j0 + u) * H + hoff;
-          mv[u] = ws_m[pidx];
-          lv[u] = ws_l[pidx];
-          av[u][0] = ld<float4_t>(ws_acc + pidx * D + d0);
-          av[u][1] = ld<float4_t>(ws_acc + pidx * D + d0 + 4);
-        } else {
-          mv[u] = -INFINITY;
-          lv[u] = 0.f;
-          av[u][0] = float4_t{0.f, 0.f, 0.f, 0.f};
-          av[u][1] = float4_t{0.f, 0.f, 0.f, 0.f};
-        }
-      }
-    };
-    load_chunk(0);
-    float M = -INFINITY, L = 0.f;
-    float4_t O0 = {0.f, 0.f, 0.f, 0.f}, O1 = {0.f, 0.f, 0.f, 0.f};
-    for (int j0 = 0; j0 < n; j0 += CH) {
-      if (j0 > 0) load_chunk(j0);
-      float cm = M;
-#pragma unroll
-      for (int u = 0; u < CH; ++u) cm = (j0 + u < n) ? fmaxf(cm, mv[u]) : cm;
-      const float alpha = fast_exp2(M - cm);     // M = -inf on the first chunk -> 0
-      L *= alpha;
-      O0 *= alpha;
-      O1 *= alpha;
-#pragma unroll
-      for (int u = 0; u < CH; ++u) {
-        // rows past n are skipped, not weighted by 0: their stale contents may be inf or NaN
-        const float wt = fast_exp2(mv[u] - cm);
-        L = (j0 + u < n) ? L + wt * lv[u] : L;
-        const float4_t o0 = O0 + wt * av[u][0], o1 = O1 + wt * av[u][1];
-        O0 = (j0 + u < n) ? o0 : O0;
-        O1 = (j0 + u < n) ? o1 : O1;
-      }
-      M = cm;
-    }
+    float4_t O0, O1;
+    float L;
+    merge_dims8(n, [&](int j, float& mj, float& lj, float4_t& a0, float4_t& a1) {
+      const int64_t pidx = (row0 + j) * H + hoff;
+      mj = ws_m[pidx];
+      lj = ws_l[pidx];
+      a0 = ld<float4_t>(ws_acc + pidx * D + d0);
+      a1 = ld<float4_t>(ws_acc + pidx * D + d0 + 4);
+    }, O0, O1, L);
     st<half4_t>(dst, to_half4(O0 / L));
     st<half4_t>(dst + 4, to_half4(O1 / L));
   }
@@ -874,10 +958,11 @@ static WsLayout ws_layout(const SplitPlan& p, int S, int H, int D) {
   return w;
 }
 
-// Bytes of the per-step split map of plan p (0: the plan does not split).
-static size_t map_bytes_of(const SplitPlan& p) {
+// Bytes of the per-step split map of plan p (0: the plan does not split): header, entries and
+// one arrival counter per (sequence, KV head, head group).
+static size_t map_bytes_of(const SplitPlan& p, int S, int groups) {
   if (p.version != TS_DECODE_V3) return 0;
-  return ((size_t)kMapHeader + (size_t)p.nslots * kMapEntry) * sizeof(int);
+  return ((size_t)kMapHeader + (size_t)p.nslots * kMapEntry + (size_t)S * groups) * sizeof(int);
 }
 
 // The cap_blocks a v3 launch of plan p passes to its kernels (and the map records).
@@ -886,10 +971,11 @@ static int launch_cap_blocks(const SplitPlan& p, int max_blocks) {
 }
 
 static void launch_split_map(const SplitPlan& p, hipStream_t st, const int* sl, const int* bt,
-                             int64_t bt_st, int64_t NB, int max_blocks, int S, int* map) {
+                             int64_t bt_st, int64_t NB, int max_blocks, int S, int groups,
+                             int* map) {
   decode_split_map_kernel<kMapThreads><<<1, kMapThreads, 0, st>>>(
       sl, bt, bt_st, NB, S, launch_cap_blocks(p, max_blocks), p.part_blocks, p.max_splits,
-      p.nslots, map);
+      p.nslots, S * groups, map);
 }
 
 // With nr.k set (kv_write fused into the launch; v2 / v3 with one head group per KV head only)
@@ -900,7 +986,7 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
                           int64_t q_sh, half_t* out, int64_t o_st, const half_t* kc,
                           const half_t* vc, int64_t NB, const int* bt, int64_t bt_st,
                           int max_blocks, const int* sl, int S, int H, int KVH, float scale_log2,
-                          void* ws, const NewRows& nr = NewRows{}, const int* smap = nullptr) {
+                          void* ws, const NewRows& nr = NewRows{}, int* smap = nullptr) {
   const int G = H / KVH;
   const bool write = nr.k != nullptr;
   const bool rope = write && nr.cos_t != nullptr;     // only for head_dim % 64 == 0
@@ -954,6 +1040,7 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
       TS_V3_LAUNCH(false, false);
   }
 #undef TS_V3_LAUNCH
+  if (smap != nullptr) return;                 // the split kernel merged in-launch
   decode_merge_kernel<D><<<dim3(S, KVH * HG), 256, 0, st>>>(ws_acc, ws_m, ws_l, ws_cnt, out, o_st,
                                                              sl, H, G, HG, p.max_splits);
 }
