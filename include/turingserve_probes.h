@@ -25,6 +25,17 @@ int ts_probe_gather(const void* base, const int64_t* chunk_offsets, int32_t n_ch
                     int32_t chunk_bytes, uint32_t* sink, void* stream);
 int ts_probe_mfma(int32_t workgroups, int32_t iters, float* sink, void* stream);
 
+/*
+ * ts_probe_gather_persistent: the same chunk list read by `workgroups` workgroups of 4
+ * wavefronts, each wavefront streaming an equal contiguous range of the list's 1 KiB pieces with
+ * `depth` (4 or 8) whole-piece loads in flight; use_lds != 0 issues them as LDS DMA into a ring.
+ * A wavefront's range must span at most 62 chunks (else TS_ERR_INVALID_ARG: more workgroups).
+ * sink: at least 4 * workgroups words.
+ */
+int ts_probe_gather_persistent(const void* base, const int64_t* chunk_offsets, int32_t n_chunks,
+                               int32_t chunk_bytes, int32_t workgroups, int32_t depth,
+                               int32_t use_lds, uint32_t* sink, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -37,7 +37,7 @@ def test_probes_are_a_separate_measurement_library():
     """The measurement probes are not part of the product ABI: declared in their own header,
     exported by libturingserve_probes.so only."""
     names = declared_functions(PROBES_HEADER)
-    assert names == ["ts_probe_gather", "ts_probe_mfma"]
+    assert sorted(names) == ["ts_probe_gather", "ts_probe_gather_persistent", "ts_probe_mfma"]
     assert not set(names) & set(declared_functions())
     for name in names:
         assert not hasattr(N.lib(), name), f"{name} exported by the product library"
@@ -45,6 +45,12 @@ def test_probes_are_a_separate_measurement_library():
     assert set(N.PROBE_SIGNATURES) == set(names)
     st = N.probes_lib().ts_probe_mfma(0, 1, None, None)
     assert st == N.TS_ERR_INVALID_ARG and N.last_error() != ""
+    # a persistent grid too small for the chunk list is refused before any launch
+    buf = ctypes.c_uint32()
+    st = N.probes_lib().ts_probe_gather_persistent(ctypes.addressof(buf), ctypes.addressof(buf),
+                                                   100000, 4096, 1, 8, 0, ctypes.addressof(buf),
+                                                   None)
+    assert st == N.TS_ERR_INVALID_ARG and "more workgroups" in N.last_error()
 
 
 def test_version_and_empty_error():
