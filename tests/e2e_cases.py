@@ -22,11 +22,11 @@ VOCAB = 2048
 DECISIVE_G2 = Qwen2Config(64, 128, 2, 4, 2, VOCAB, max_position_embeddings=4096)
 DECISIVE_G7 = Qwen2Config(224, 448, 2, 14, 2, VOCAB, max_position_embeddings=4096)
 PROMPT_LENS = (7, 40, 130, 33, 90)
-NEW_TOKENS = 8
+NEW_TOKENS = 24           # the reference's own greedy test length (tests/correctness/test_paged_engine.py:94-101)
 BUDGET = 48              # tokens per step: the 130- and 90-token prompts are prefilled in chunks
 MAX_SEQS = 8
 NUM_BLOCKS = 300
-MIN_GAP_ULPS = 12        # checked on the CPU
+MIN_GAP_ULPS = 9         # checked on the CPU (the best of 40000 seeds per case at 24 tokens: 9-11)
 MIN_GAP_ULPS_GPU = 6     # precondition of the GPU comparison (the GPU twins round differently)
 
 
@@ -44,10 +44,10 @@ class Case:
 
 
 CASES = [
-    Case("g2", DECISIVE_G2, "none", 62),
-    Case("g7", DECISIVE_G7, "none", 125, device_metadata=True),
-    Case("g2-int8", DECISIVE_G2, "int8", 85),
-    Case("g7-int8", DECISIVE_G7, "int8", 82, device_metadata=True),
+    Case("g2", DECISIVE_G2, "none", 14408),
+    Case("g7", DECISIVE_G7, "none", 7257, device_metadata=True),
+    Case("g2-int8", DECISIVE_G2, "int8", 2693),
+    Case("g7-int8", DECISIVE_G7, "int8", 34228, device_metadata=True),
 ]
 
 

@@ -374,7 +374,7 @@ __device__ __forceinline__ void decode_mfma_body(
     int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
     float* __restrict__ ws_l, int* __restrict__ ws_cnt,
     int bx, int bz, char* __restrict__ lds, const NewRows& nr = NewRows{},
-    int* __restrict__ smap = nullptr) {
+    int* __restrict__ smap = nullptr, int nslots = 0) {
   constexpr int KK = KvRegs<D>::KK;
   constexpr int VW = KvRegs<D>::VW;
   constexpr int TILES = KvRegs<D>::TILES;
@@ -397,7 +397,7 @@ __device__ __forceinline__ void decode_mfma_body(
 
   int s, seq_len, blk_lo, blk_hi, nsplit, split_j = 0;
   // With a split map built for this launch's plan (header equal to the plan; smap is only
-  // passed by decode_mfma_kernel, whose grid.x is the slot count) the slot's entry replaces
+  // passed by decode_mfma_kernel, with its slot count nslots) the slot's entry replaces
   // split_lookup, and the first two pairs' block ids of this wavefront come with it. The header
   // and the entry are requested together (the host checked that the map holds every slot).
   bool mapped = false;
@@ -406,7 +406,7 @@ __device__ __forceinline__ void decode_mfma_body(
   if constexpr (2 * NW == kMapPairs) {
     if (split && smap != nullptr) {
       const int* e = smap + kMapHeader + (int64_t)bx * kMapEntry;
-      mapped = smap[0] == kMapMagic && smap[1] == S && smap[2] == (int)gridDim.x &&
+      mapped = smap[0] == kMapMagic && smap[1] == S && smap[2] == nslots &&
                smap[3] == part_blocks && smap[5] == max_splits &&
                smap[6] == cap_blocks;
       sp = {e[0], e[1], e[2], e[7], e[3]};
@@ -711,7 +711,7 @@ __device__ __forceinline__ void decode_mfma_body(
   // read from there.
   __builtin_amdgcn_s_waitcnt(kWaitVmcntZero);
   __syncthreads();
-  int* counter = smap + kMapHeader + (int64_t)gridDim.x * kMapEntry + (int64_t)s * (KVH * HG) + bz;
+  int* counter = smap + kMapHeader + (int64_t)nslots * kMapEntry + (int64_t)s * (KVH * HG) + bz;
   if (tid == 0)
     s_map[0] = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
                nsplit - 1;
@@ -753,10 +753,16 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
     float* __restrict__ ws_l, int* __restrict__ ws_cnt, const NewRows nr,
     int* __restrict__ smap) {
   __shared__ __attribute__((aligned(16))) char lds[DecodeLds<D, NW>::BYTES];
+  // One-dimensional grid of slots x (KV head, head group), the latter fastest: the launch
+  // bounds the slot count from max_seq_len (S times the longest sequence's split count), so
+  // most slots past the batch's last split exit at once; numbered last, they no longer hold
+  // resident slots ahead of the second KV head's splits.
+  const int zh = KVH * HG;
+  const int bx = (int)blockIdx.x / zh, bz = (int)blockIdx.x - bx * zh;
   decode_mfma_body<D, NW, WRITE, ROPE>(q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks,
                                  seq_lens, S, H, KVH, G, HG, sl2, cap_blocks, part_blocks,
-                                 max_splits, ws_acc, ws_m, ws_l, ws_cnt, (int)blockIdx.x,
-                                 (int)blockIdx.z, lds, nr, smap);
+                                 max_splits, ws_acc, ws_m, ws_l, ws_cnt, bx, bz, lds, nr, smap,
+                                 (int)gridDim.x / zh);
 }
 
 // Merge of the split partials (ops/triton_decode_attention.py:144-163): each split leaves its
@@ -998,7 +1004,7 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
   const int HG = (G + 15) / 16;
   if (p.version == TS_DECODE_V2) {
 #define TS_V2_LAUNCH(W, R)                                                                       \
-  decode_mfma_kernel<D, kDecodeWaves, W, R><<<dim3(S, 1, KVH * HG), kDecodeWaves * 64, 0, st>>>( \
+  decode_mfma_kernel<D, kDecodeWaves, W, R><<<dim3(S * KVH * HG), kDecodeWaves * 64, 0, st>>>(  \
       q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,        \
       scale_log2, 0, 0, 0, nullptr, nullptr, nullptr, nullptr, nr, nullptr)
     if constexpr (D % 64 == 0) {
@@ -1022,7 +1028,7 @@ static void launch_decode(const SplitPlan& p, hipStream_t st, const half_t* q, i
   int* ws_cnt = reinterpret_cast<int*>(b + w.cnt);
   const int cap = launch_cap_blocks(p, max_blocks);
 #define TS_V3_LAUNCH(W, R)                                                                       \
-  decode_mfma_kernel<D, kDecodeWaves, W, R><<<dim3(p.nslots, 1, KVH * HG), kDecodeWaves * 64, 0, \
+  decode_mfma_kernel<D, kDecodeWaves, W, R><<<dim3(p.nslots * KVH * HG), kDecodeWaves * 64, 0,  \
                                               st>>>(                                             \
       q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks, sl, S, H, KVH, G, HG,        \
       scale_log2, cap, p.part_blocks, p.max_splits, ws_acc, ws_m, ws_l, ws_cnt, nr, smap)

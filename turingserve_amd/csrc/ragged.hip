@@ -38,7 +38,8 @@ struct RaggedArgs {
   // prefill tiles: launch ids [0, pf_launch)
   int pf_launch, smax, slots, P;
   float* pf_ws;
-  // decode splits: launch ids [pf_launch, pf_launch + nslots * KVH * HG)
+  // decode splits: launch ids [pf_launch, pf_launch + nslots * KVH * HG), slot-major (the slots
+  // past the batch's last split, which exit at once, come last)
   int nslots, cap_blocks, max_splits;
   float* ws_acc;
   float* ws_m;
@@ -71,7 +72,7 @@ __global__ void __launch_bounds__(256, 2) ragged_split_kernel(const RaggedArgs a
                                         a.bt, a.bt_st, a.max_blocks, a.seq_lens, a.num_decode,
                                         a.H, a.KVH, a.G, a.HG, a.sl2, a.cap_blocks, 0,
                                         a.max_splits, a.ws_acc, a.ws_m, a.ws_l, a.ws_cnt,
-                                        d % a.nslots, d / a.nslots, lds);
+                                        d / (a.KVH * a.HG), d % (a.KVH * a.HG), lds);
   }
 }
 
