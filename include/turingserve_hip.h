@@ -322,7 +322,9 @@ int ts_w8a16_gemm(const void* x, int64_t ldx, const int8_t* wq, const void* scal
  * ops/triton_ops.py:74-86): variant 0 = the library's own plan (as ts_w8a16_gemm), 1 = weight
  * streaming (M <= 32 only), 2 = 128 x 64 wide tiles, 3 = 128 x 128 wide tiles, 4 = 128 x 32
  * wide tiles (planned as 128 x 64 by ts_w8a16_glu), 5 = skinny (M <= 64, whole K per workgroup),
- * 6 = 128 x 192 wide tiles (128 weight rows x 192 activation rows); splits = the
+ * 6 = 128 x 192 wide tiles (128 weight rows x 192 activation rows), 7 = weight rows streamed on
+ * the VALU (M <= 4, no split-K; it needs K % 16 == 0 and 16-byte aligned x rows and weights, and
+ * runs the skinny kernel otherwise); splits = the
  * number of K splits (0 = the variant's own rule, at most 256; splits > 1 sum fp32 partials in
  * the workspace). Every variant computes the same product up to fp32 summation order.
  * Unavailable combinations return TS_ERR_UNSUPPORTED.

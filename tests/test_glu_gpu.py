@@ -74,9 +74,11 @@ def test_glu_intermediate_not_a_multiple_of_8(M, inter):
 
 @pytest.mark.parametrize("variant,splits", [(1, 0), (1, 1), (1, 3), (2, 0), (2, 1), (2, 4),
                                             (3, 0), (3, 2), (4, 0), (4, 2), (5, 0), (6, 0),
-                                            (6, 2)])
-@pytest.mark.parametrize("M", [9, 32, 200])
+                                            (6, 2), (7, 0)])
+@pytest.mark.parametrize("M", [3, 9, 32, 200])
 def test_glu_every_variant_and_split(variant, splits, M):
+    if variant == 7 and M > 4:
+        pytest.skip("the VALU path is built for M <= 4")
     if variant == 1 and M > 32:
         pytest.skip("weight streaming is built for M <= 32")
     if variant == 5 and M > 64:

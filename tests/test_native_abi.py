@@ -160,6 +160,15 @@ def test_glu_argument_checks_and_workspace():
     assert lib.ts_w8a16_workspace_bytes(64, 1536, 8960, 256) > 0     # wide 128 x 32, split K
     assert lib.ts_w8a16_glu(p, 1536, p, p, 0, None, p, 8960, 65, 8960, 1536, 5, 0, None, 0,
                             None) == N.TS_ERR_UNSUPPORTED                # skinny is M <= 64
+    # the VALU path (variant 7): M <= 4, one K split, no workspace
+    for M in (1, 4):
+        assert lib.ts_w8a16_workspace_bytes_v(M, 1536, 8960, 7, 0, 256) == 0
+        assert lib.ts_w8a16_glu_workspace_bytes(M, 8960, 1536, 7, 1, 256) == 0
+    assert lib.ts_w8a16_workspace_bytes_v(5, 1536, 8960, 7, 0, 256) == 0      # not available
+    assert lib.ts_w8a16_glu(p, 1536, p, p, 0, None, p, 8960, 5, 8960, 1536, 7, 0, None, 0,
+                            None) == N.TS_ERR_UNSUPPORTED                # VALU path is M <= 4
+    assert lib.ts_w8a16_glu(p, 1536, p, p, 0, None, p, 8960, 2, 8960, 1536, 7, 2, None, 0,
+                            None) == N.TS_ERR_UNSUPPORTED                # and never splits K
 
 
 def test_zero_size_calls_are_no_ops():

@@ -39,7 +39,9 @@ def _problem(M, N, Kd, seed, fp16_scale=False):
 
 
 @pytest.mark.parametrize("M,N,Kd", [(1, 2048, 1536), (20, 1000, 520), (64, 1536, 8960),
-                                    (300, 2048, 1536), (129, 260, 1032)])
+                                    (300, 2048, 1536), (129, 260, 1032),
+                                    (1, 1536, 8960), (3, 260, 1040),    # VALU path, ragged N
+                                    (2, 1000, 520)])                    # K % 16 != 0: skinny
 def test_every_variant_matches_the_oracle(M, N, Kd):
     (x, wq, sc, b), ref = _problem(M, N, Kd, seed=M + N, fp16_scale=M % 2 == 0)
     auto = K.w8a16_linear(x, wq, sc, b)

@@ -589,6 +589,142 @@ __global__ void __launch_bounds__(KW * 64) w8a16_skinny_kernel(
   }
 }
 
+// ------------------------------------------------------------------------------------------
+// M <= 4: weight rows streamed on the VALU.
+// ------------------------------------------------------------------------------------------
+// The MFMA kernels' 16-row weight tiles leave most CUs idle on the 1536-row products at M = 1
+// (96 workgroups for the down projection). Here a workgroup of 256 threads takes R = 256 / LPR
+// weight rows (GLU: R / 2 gate rows and the matching up rows), each row on LPR consecutive
+// threads (LPR = 128: two wavefronts): K is cut into 16-column pieces and thread j of the row's
+// group takes pieces j, j + LPR, ..., PP of them requested before any is used. A thread keeps
+// one fp32 sum per activation row, accumulated piece by piece with v_dot2_f32_f16 on the exactly
+// widened int8 weights; a row's threads are summed by a fixed butterfly (and, over two
+// wavefronts, a fixed-order sum through LDS), so the result does not depend on timing, and
+// every output is fp16(acc * scale + bias) as in the other kernels. Needs K % 16 == 0 and
+// 16-byte aligned weights and activation rows (the host falls back to the skinny kernel).
+constexpr int kGemvMaxM = 4;
+
+template <int MR, int LPR, int RPT, int PP>
+__global__ void __launch_bounds__(256) w8a16_gemv_kernel(
+    const half_t* __restrict__ x, int64_t ldx, const int8_t* __restrict__ wq,
+    const void* __restrict__ scale, int scale_is_fp16, const half_t* __restrict__ bias,
+    half_t* __restrict__ y, int64_t ldy, int M, int N, int K, GemmIo io) {
+  constexpr int G = 256 / LPR;                   // thread groups (each RPT weight rows)
+  constexpr int R = G * RPT;                     // weight rows per workgroup
+  constexpr int WPR = LPR > kWave ? LPR / kWave : 1;   // wavefronts per group
+  constexpr int LW = LPR < kWave ? LPR : kWave;        // lanes of a group within one wavefront
+  static_assert(MR >= 1 && MR <= kGemvMaxM && LPR >= 16 && LPR <= 256 && (LPR & (LPR - 1)) == 0 &&
+                    (RPT == 1 || RPT == 2 || RPT == 4) && (R % 2 == 0 || RPT == 1),
+                "gemv shape");
+  __shared__ float s_part[R][WPR][MR];
+  const int tid = threadIdx.x;
+  const int grp = tid / LPR;                     // rows grp * RPT .. + RPT - 1 of the workgroup
+  const int j = tid % LPR;
+  const int glu = io.glu;
+  // weight row of workgroup row r (clamped into the matrix; GLU: gate rows first, then up)
+  auto weight_row = [&](int r) {
+    if (glu) {
+      const int i = blockIdx.x * (R / 2) + r % (R / 2);
+      return (r >= R / 2 ? glu : 0) + (i < glu ? i : glu - 1);
+    }
+    const int n = blockIdx.x * R + r;
+    return n < N ? n : N - 1;
+  };
+  const int8_t* wrow[RPT];
+#pragma unroll
+  for (int q = 0; q < RPT; ++q) wrow[q] = wq + (int64_t)weight_row(grp * RPT + q) * K;
+  const half_t* xrow[MR];
+#pragma unroll
+  for (int m = 0; m < MR; ++m) xrow[m] = x + x_row(io, m < M ? m : M - 1) * ldx;
+  const int C = K / 16;                          // pieces per row
+  float acc[RPT][MR];
+#pragma unroll
+  for (int q = 0; q < RPT; ++q)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) acc[q][m] = 0.f;
+  for (int base = 0; base < C; base += PP * LPR) {
+    int4_t wv[PP][RPT];
+    half8_t xa[PP][MR], xb[PP][MR];
+#pragma unroll
+    for (int u = 0; u < PP; ++u) {
+      int pc = base + u * LPR + j;
+      pc = pc < C ? pc : C - 1;                  // past the row: its last piece, not summed
+#pragma unroll
+      for (int q = 0; q < RPT; ++q) wv[u][q] = ld<int4_t>(wrow[q] + 16 * pc);
+#pragma unroll
+      for (int m = 0; m < MR; ++m) {
+        xa[u][m] = ld<half8_t>(xrow[m] + 16 * pc);
+        xb[u][m] = ld<half8_t>(xrow[m] + 16 * pc + 8);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < PP; ++u) {
+      if (base + u * LPR + j >= C) continue;
+#pragma unroll
+      for (int q = 0; q < RPT; ++q) {
+        const half8_t fa = i8x8_to_half8(int2_t{wv[u][q][0], wv[u][q][1]});
+        const half8_t fb = i8x8_to_half8(int2_t{wv[u][q][2], wv[u][q][3]});
+#pragma unroll
+        for (int m = 0; m < MR; ++m) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            acc[q][m] = __builtin_amdgcn_fdot2(half2_t{fa[2 * e], fa[2 * e + 1]},
+                                               half2_t{xa[u][m][2 * e], xa[u][m][2 * e + 1]},
+                                               acc[q][m], false);
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            acc[q][m] = __builtin_amdgcn_fdot2(half2_t{fb[2 * e], fb[2 * e + 1]},
+                                               half2_t{xb[u][m][2 * e], xb[u][m][2 * e + 1]},
+                                               acc[q][m], false);
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < RPT; ++q)
+#pragma unroll
+    for (int m = 0; m < MR; ++m) {
+#pragma unroll
+      for (int off = LW / 2; off > 0; off >>= 1) acc[q][m] += __shfl_xor(acc[q][m], off, kWave);
+    }
+  if (j % LW == 0) {
+#pragma unroll
+    for (int q = 0; q < RPT; ++q)
+#pragma unroll
+      for (int m = 0; m < MR; ++m) s_part[grp * RPT + q][j / LW][m] = acc[q][m];
+  }
+  __syncthreads();
+  auto row_sum = [&](int r, int m) {
+    float a = s_part[r][0][m];
+#pragma unroll
+    for (int k = 1; k < WPR; ++k) a += s_part[r][k][m];
+    return a;
+  };
+  auto value = [&](float a, int nr) {
+    return (half_t)(a * load_scale(scale, scale_is_fp16, nr) + (bias ? (float)bias[nr] : 0.f));
+  };
+  if (glu) {
+    for (int t = tid; t < (R / 2) * MR; t += 256) {
+      const int r = t / MR, m = t % MR;
+      const int col = blockIdx.x * (R / 2) + r;
+      if (m >= M || col >= glu) continue;
+      y[(int64_t)m * ldy + col] =
+          silu_mul_h(value(row_sum(r, m), col), value(row_sum(R / 2 + r, m), glu + col));
+    }
+    return;
+  }
+  for (int t = tid; t < R * MR; t += 256) {
+    const int r = t / MR, m = t % MR;
+    const int n = blockIdx.x * R + r;
+    if (m >= M || n >= N) continue;
+    const half_t v = value(row_sum(r, m), n);
+    if (io.yf)
+      io.yf[(int64_t)m * io.ldyf + n] = (float)v;
+    else
+      y[(int64_t)m * ldy + n] = v;
+  }
+}
+
 constexpr int kTileBK = 64;
 constexpr int kTileChunks = kTileBK / 8;          // 16-byte fp16 chunks per tile row
 
@@ -1090,12 +1226,14 @@ struct GemmPlan {
   int k_per_split;
   int rt;          // skinny path: 16-row weight tiles per workgroup (0: not skinny)
   int kw;          // skinny path: wavefronts per workgroup (the K split inside it)
+  int gv;          // VALU path: threads per weight-row group (0: not this path)
+  int gvr;         // VALU path: weight rows per thread
 };
 
 // Variants a caller (a tuning table) may name instead of the planner's choice.
 enum GemmVariant : int {
   kVarAuto = 0, kVarStream = 1, kVarWide64 = 2, kVarWide128 = 3, kVarWide32 = 4, kVarSkinny = 5,
-  kVarWide192 = 6
+  kVarWide192 = 6, kVarGemv = 7
 };
 constexpr int kSkinnyMMax = 64;
 
@@ -1119,6 +1257,26 @@ static bool use_skinny(int M, int N, int K) {
 }
 
 constexpr int kMaxSplits = 256;
+
+// VALU path (w8a16_gemv_kernel) shape, measured on the 1.5B projections (cold weights, M = 1 /
+// 2): K >= 4096 (down, 560 pieces per row) takes a whole workgroup per group of two rows (768
+// workgroups for 1536 rows: 5.75 / 6.78 us; one row per 128 threads 6.17 / 7.70, per 64 threads
+// 6.81 / 9.46); shorter K takes 32 threads per row, one row each (qkv 3.57 / 3.95 us, o 3.51 /
+// 3.92, gate_up at M = 1 7.97), two rows each for a GLU product at M >= 2 (gate_up 9.06 against
+// 9.84), sharing its activation loads between them.
+static void gemv_shape(int M, int K, bool glu, GemmPlan* p) {
+  if (K / 16 >= 256) {
+    p->gv = 256;
+    p->gvr = 2;
+  } else {
+    p->gv = 32;
+    p->gvr = glu && M >= 2 ? 2 : 1;
+  }
+}
+// Auto plan: the VALU path for M <= 2, where it beat the skinny kernel on all four projections
+// (M = 1: 20.8 against 29.3 us for the four, M = 2: 23.7 against 30.2 us).
+constexpr int kGemvAutoM = 2;
+static bool use_gemv(int M, int N, int K) { return M <= kGemvAutoM && K % 16 == 0; }
 
 // Weight streaming: fill the device with wavefronts (about eight per CU) by splitting K,
 // keeping at least 256 K per split and the fp32 partials (splits * M * N * 4 bytes) within a
@@ -1164,6 +1322,11 @@ static int wide64_splits(int M, int N, int K, int cus) {
 // and GLU mode plans them as 128 x 64.
 static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int splits,
                             bool glu = false) {
+  if (variant == kVarGemv || (variant == kVarAuto && use_gemv(M, N, K))) {
+    GemmPlan p{false, 1, 0, 0, 1, K, 0, 0, 0, 0};
+    gemv_shape(M, K, glu, &p);
+    return p;
+  }
   if (variant == kVarSkinny || (variant == kVarAuto && use_skinny(M, N, K))) {
     GemmPlan p{false, M <= 16 ? 1 : (M <= 32 ? 2 : 4), 0, 0, 1, K, 0, 0};
     skinny_shape(N, cus, glu, &p);
@@ -1240,7 +1403,8 @@ extern "C" size_t ts_w8a16_workspace_bytes(int32_t M, int32_t N, int32_t K, int3
 }
 
 static bool variant_valid(int variant, int splits, int M) {
-  return variant >= kVarAuto && variant <= kVarWide192 && splits >= 0 && splits <= kMaxSplits &&
+  return variant >= kVarAuto && variant <= kVarGemv && splits >= 0 && splits <= kMaxSplits &&
+         (variant != kVarGemv || (M <= kGemvMaxM && splits <= 1)) &&
          (variant != kVarStream || M <= kSmallMMax) &&
          (variant != kVarSkinny || (M <= kSkinnyMMax && splits <= 1));
 }
@@ -1266,6 +1430,9 @@ static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const v
   if (st != TS_OK) return st;
   const bool glu = io.glu > 0;                    // N = 2 * io.glu, y is [M, io.glu]
   GemmPlan p = plan_gemm_v(M, N, K, cus, variant, splits, glu);
+  if (p.gv > 0 && !(M <= kGemvMaxM && K % 16 == 0 && aligned(wq, 16) && aligned(xp, 16) &&
+                    ldx % 8 == 0))
+    p = plan_gemm_v(M, N, K, cus, kVarSkinny, 0, glu);   // the VALU path's alignment not met
   if (glu && p.bm == 32) p.bm = 64;               // GLU tiles pair 32-row subtiles (same splits)
   const size_t need = gemm_workspace(p, M, N);
   TS_REQUIRE(need == 0 || (workspace && workspace_bytes >= need && aligned(workspace, 16)),
@@ -1284,7 +1451,34 @@ static int w8a16_launch(const half_t* xp, int64_t ldx, const int8_t* wq, const v
           part, p.splits, scale, scale_is_fp16, bp, yp, ldy, M, N, io);
     }
   };
-  if (p.rt > 0) {
+  if (p.gv > 0) {
+    const int rows = 256 / p.gv * p.gvr;
+    const dim3 grid(glu ? (io.glu + rows / 2 - 1) / (rows / 2) : (N + rows - 1) / rows);
+    const int per = (K / 16 + p.gv - 1) / p.gv;  // pieces per thread
+#define TS_GV_LAUNCH(MR, LPR, RPT, PP)                                                             \
+  w8a16_gemv_kernel<MR, LPR, RPT, PP><<<grid, 256, 0, s>>>(xp, ldx, wq, scale, scale_is_fp16, bp, \
+                                                           yp, ldy, M, N, K, io)
+    // pieces requested at once per thread: all of them where the registers allow
+#define TS_GV_M(LPR, RPT)                                                                          \
+  {                                                                                                \
+    if (M == 1) {                                                                                  \
+      if (per <= 3) TS_GV_LAUNCH(1, LPR, RPT, 3); else TS_GV_LAUNCH(1, LPR, RPT, 6);               \
+    } else if (M == 2) {                                                                           \
+      if (per <= 3) TS_GV_LAUNCH(2, LPR, RPT, 3); else TS_GV_LAUNCH(2, LPR, RPT, 6);               \
+    } else {                                                                                       \
+      if (per <= 3) TS_GV_LAUNCH(4, LPR, RPT, 3); else TS_GV_LAUNCH(4, LPR, RPT, 4);               \
+    }                                                                                              \
+  }
+    if (p.gv == 256) {
+      TS_GV_M(256, 2)
+    } else if (p.gvr == 2) {
+      TS_GV_M(32, 2)
+    } else {
+      TS_GV_M(32, 1)
+    }
+#undef TS_GV_M
+#undef TS_GV_LAUNCH
+  } else if (p.rt > 0) {
     // GLU: a workgroup covers 8 RT gate columns (its RT / 2 gate tiles and their up tiles)
     const int cols = glu ? io.glu : N;
     const int per_wg = glu ? 8 * p.rt : 16 * p.rt;

@@ -11,13 +11,13 @@ buckets below the engine's token budget and the budget itself.
 
     kernel "decode": key (S, L)    (decode rows, max_seq_len)       -> {"version": "v2" | "v3",
                                                                          "partition": 0 | 256 | ...}
-    kernel "w8a16":  key (N, K, M) (out features, in features, rows) -> {"variant": 0..6,
+    kernel "w8a16":  key (N, K, M) (out features, in features, rows) -> {"variant": 0..7,
                                                                          "splits": 0..}
 
 W8A16 variants (ts_w8a16_gemm_v): 0 the library's plan, 1 weight streaming (M <= 32),
 2 128 x 64 wide tiles, 3 128 x 128 wide tiles, 4 128 x 32 wide tiles (128 x 64 in the fused
 gated-MLP product), 5 skinny (M <= 64: whole K per workgroup, no split-K), 6 128 x 192 wide
-tiles; splits 0 = the variant's own rule. Decode:
+tiles, 7 weight rows streamed on the VALU (M <= 4); splits 0 = the variant's own rule. Decode:
 v2 (one workgroup per sequence and KV head group) or v3 with partition 0 (own-length split) or a
 fixed partition in tokens. Every variant computes the same result up to fp32 summation order.
 """
@@ -100,7 +100,7 @@ def w8a16_choice(N: int, K: int, M: int) -> tuple[int, int]:
         return 0, 0
     c = shape[i][1]
     variant, splits = int(c["variant"]), int(c["splits"])
-    if (variant == 1 and M > 32) or (variant == 5 and M > 64):
+    if (variant == 1 and M > 32) or (variant == 5 and M > 64) or (variant == 7 and M > 4):
         return 0, 0
     return variant, splits
 
@@ -181,6 +181,8 @@ def w8a16_candidates(M: int) -> list[tuple[int, int]]:
         cands += [(1, 0), (1, 1), (1, 2), (1, 4)]
     if M <= 64:
         cands += [(5, 0)]
+    if M <= 4:
+        cands += [(7, 0)]
     return cands
 
 
