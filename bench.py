@@ -794,12 +794,15 @@ def main() -> int:
     st, r = bench_decode(args, torch, K, synth)
     b = r["bytes"]
     value = b["step"] / r["step_s"] / 1e9
-    # The dominant kernel: the fused step's launch (decode_mfma_kernel with the write, then the
-    # merge) priced with the step's bytes, or with the two-launch step the attention call alone.
+    # The dominant kernel: the fused step's launch (decode_mfma_kernel with the write; with the
+    # step's split map it merges its splits in-launch, else decode_merge_kernel follows) priced
+    # with the step's bytes, or with the two-launch step the attention call alone.
     if r["fused"]:
-        kern = ("decode attention with kv_write fused (decode_mfma_kernel<128, 4, write> + "
-                "decode_merge_kernel" + (f", decode_split_map_kernel once per {args.layers} steps)"
-                                         if r["split_map"] else ")"))
+        kern = ("decode attention with kv_write fused (decode_mfma_kernel<128, 4, write> merging "
+                f"its splits in-launch, decode_split_map_kernel once per {args.layers} steps)"
+                if r["split_map"] else
+                "decode attention with kv_write fused (decode_mfma_kernel<128, 4, write> + "
+                "decode_merge_kernel)")
         kern_ms, kern_bytes = r["step_ev_ms"], b["step"]
     else:
         kern = "decode attention (paged_attention, decode rows)"

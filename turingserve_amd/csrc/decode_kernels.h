@@ -229,7 +229,8 @@ constexpr int kMapHeader = 8;
 constexpr int kMapEntry = 32;
 constexpr int kMapPairs = 8;                 // two pairs per wavefront of a 4-wavefront launch
 constexpr int kMapMaxSeqs = 4096;            // sequences per step the builder handles
-constexpr int kMapThreads = 1024;
+constexpr int kMapThreads = 256;
+constexpr int kMapMaxGroups = 64;            // workgroups of the builder (each kMapThreads slots)
 
 __device__ __forceinline__ int4 int4_of(int a, int b, int c, int d) { return int4{a, b, c, d}; }
 
@@ -278,14 +279,17 @@ __global__ void __launch_bounds__(NT) decode_split_map_kernel(
   // the arrival counters of the split kernel's in-launch merge start at zero (each merge resets
   // its counter, so the map stays valid for every layer of the step)
   int* counters = map + kMapHeader + (int64_t)nslots * kMapEntry;
-  for (int i = tid; i < n_counters; i += NT) counters[i] = 0;
-  if (tid == 0) {
-    int4* h = reinterpret_cast<int4*>(map);
-    h[0] = int4_of(kMapMagic, S, nslots, part_blocks);
-    h[1] = int4_of(0, max_splits, cap_blocks, 0);
+  if (blockIdx.x == 0) {
+    for (int i = tid; i < n_counters; i += NT) counters[i] = 0;
+    if (tid == 0) {
+      int4* h = reinterpret_cast<int4*>(map);
+      h[0] = int4_of(kMapMagic, S, nslots, part_blocks);
+      h[1] = int4_of(0, max_splits, cap_blocks, 0);
+    }
   }
+  // Every workgroup computed the prefix above; the slots are shared among them.
   constexpr int NWF = kMapPairs / 2;           // wavefronts of the consuming launch
-  for (int slot = tid; slot < nslots; slot += NT) {
+  for (int slot = blockIdx.x * NT + tid; slot < nslots; slot += gridDim.x * NT) {
     int lo = 0, hi = S - 1;                    // last sequence whose first split is <= slot
     while (lo < hi) {
       const int mid = (lo + hi + 1) >> 1;
@@ -979,7 +983,9 @@ static int launch_cap_blocks(const SplitPlan& p, int max_blocks) {
 static void launch_split_map(const SplitPlan& p, hipStream_t st, const int* sl, const int* bt,
                              int64_t bt_st, int64_t NB, int max_blocks, int S, int groups,
                              int* map) {
-  decode_split_map_kernel<kMapThreads><<<1, kMapThreads, 0, st>>>(
+  int groups_x = (p.nslots + kMapThreads - 1) / kMapThreads;
+  groups_x = groups_x < 1 ? 1 : (groups_x > kMapMaxGroups ? kMapMaxGroups : groups_x);
+  decode_split_map_kernel<kMapThreads><<<groups_x, kMapThreads, 0, st>>>(
       sl, bt, bt_st, NB, S, launch_cap_blocks(p, max_blocks), p.part_blocks, p.max_splits,
       p.nslots, S * groups, map);
 }
