@@ -7,7 +7,8 @@
 // in one launch: the workgroups of the prefill tile plan come first, the decode split slots take
 // the remaining resident slots (two workgroups per CU), and one merge launch then combines the
 // split partials of both. The decode part uses the own-length split schedule of
-// ts_decode_attention, the prefill part a split plan sized for half the device. Each workgroup
+// ts_decode_attention, the prefill part a split plan sized for 6/8 of the resident slots (the
+// decode splits fill what the prefill tiles leave and free as they finish). Each workgroup
 // runs exactly the code of its standalone kernel (decode_mfma_body / prefill_tile_body), so the
 // results equal the standalone launches with the same plans.
 //
@@ -51,9 +52,11 @@ struct RaggedArgs {
 };
 
 // Share of the resident workgroup slots, in eighths, that the prefill tiles' plan gets as one
-// round (half: measured best on the config 5 attention shape among 2-5 eighths); the decode
-// splits take the slots the prefill leaves.
-constexpr int kRaggedPfShare = 4;
+// round; the decode splits take the slots the prefill leaves. Measured on the config 5
+// attention shape with the own-length decode splits and fp32 partials (cold caches, µs per call
+// with the merge): 2/8 50.8, 3/8 35.9, 4/8 33.9-34.2, 5/8 31.4-32.2, 6/8 31.3-31.4, 7/8 31.9,
+// 8/8 37.7.
+constexpr int kRaggedPfShare = 6;
 
 constexpr int kRaggedLds = 2 * TileLayout<128>::STAGE > DecodeLds<128, kDecodeWaves>::BYTES
                                ? 2 * TileLayout<128>::STAGE
@@ -90,7 +93,7 @@ __global__ void __launch_bounds__(256) ragged_merge_kernel(const RaggedArgs a) {
   }
 }
 
-// The fused plan: the prefill tiles get one round of half the resident slots, the decode
+// The fused plan: the prefill tiles get one round of 6/8 of the resident slots, the decode
 // splits follow (the own-length schedule, as in ts_decode_attention, so a decode row's result
 // does not depend on the prefill beside it). ok = false when the batch does not qualify.
 struct RaggedPlan {
