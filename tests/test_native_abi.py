@@ -153,7 +153,13 @@ def test_glu_argument_checks_and_workspace():
     # workgroup: no split-K workspace
     for M in (1, 7, 16):
         assert lib.ts_w8a16_glu_workspace_bytes(M, 8960, 1536, 0, 0, 256) == 0
+    # ... except long-K products whose 16-row tiles would cover under half the CUs (the down
+    # projection: 96 of them), which take 128 x 32 tiles split 8 ways over K from M = 5 (the VALU
+    # kernel, no workspace, below)
+    for M in (1, 4):
         assert lib.ts_w8a16_workspace_bytes(M, 1536, 8960, 256) == 0
+    for M in (5, 7, 16):
+        assert lib.ts_w8a16_workspace_bytes(M, 1536, 8960, 256) == 8 * M * 1536 * 4
     for M in (1, 16, 33, 64):
         assert lib.ts_w8a16_glu_workspace_bytes(M, 8960, 1536, 5, 0, 256) == 0
         assert lib.ts_w8a16_workspace_bytes_v(M, 2048, 1536, 5, 0, 256) == 0
@@ -211,9 +217,9 @@ def test_workspace_sizes():
     # fit and K = 1536 (24 steps) never splits
     assert lib.ts_w8a16_workspace_bytes(560, 1536, 8960, 256) == 2 * 560 * 1536 * 4
     assert lib.ts_w8a16_workspace_bytes(560, 1536, 1536, 256) == 0
-    # M <= 16 takes the skinny kernel (whole K per workgroup): no workspace
+    # M <= 16 takes the VALU or the skinny kernel (whole K per workgroup): no workspace
     assert lib.ts_w8a16_workspace_bytes(1, 2048, 1536, 256) == 0
-    assert lib.ts_w8a16_workspace_bytes(16, 1536, 8960, 256) == 0
+    assert lib.ts_w8a16_workspace_bytes(16, 2048, 1536, 256) == 0
     # weight streaming (variant 1) at M = 1: 32 workgroups, split into 6 (K / 256) partial rows
     assert lib.ts_w8a16_workspace_bytes_v(1, 2048, 1536, 1, 0, 256) == 6 * 2048 * 4
     ws = lib.ts_w8a16_workspace_bytes_v(1, 1536, 8960, 1, 0, 256)

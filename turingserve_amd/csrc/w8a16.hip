@@ -1274,9 +1274,19 @@ static void gemv_shape(int M, int K, bool glu, GemmPlan* p) {
   }
 }
 // Auto plan: the VALU path for M <= 2, where it beat the skinny kernel on all four projections
-// (M = 1: 20.8 against 29.3 us for the four, M = 2: 23.7 against 30.2 us).
+// (M = 1: 20.8 against 29.3 us for the four, M = 2: 23.7 against 30.2 us), and up to M = 4 for
+// long K (down at M = 3 / 4: 8.9 / 9.7 against 10.1 / 10.6 us skinny; at K = 1536 the skinny
+// kernel is 0.1-0.2 us faster there).
 constexpr int kGemvAutoM = 2;
-static bool use_gemv(int M, int N, int K) { return M <= kGemvAutoM && K % 16 == 0; }
+static bool use_gemv(int M, int N, int K) {
+  return K % 16 == 0 && (M <= kGemvAutoM || (M <= kGemvMaxM && K >= 4096));
+}
+// Long-K products whose 16-row skinny tiles would cover under half the CUs (the down projection,
+// 1536 x 8960: 96 workgroups) take 128 x 32 wide tiles split over K instead, from M = 5 to 16
+// (down at M = 8 / 12 / 16: 11.7 / 11.8 / 11.9 us against 12.4 / 14.1 / 15.4 us skinny).
+static bool use_wide_long_k(int M, int N, int K, int cus) {
+  return M <= 16 && K >= 4096 && (int64_t)((N + 15) / 16) * 2 < cus;
+}
 
 // Weight streaming: fill the device with wavefronts (about eight per CU) by splitting K,
 // keeping at least 256 K per split and the fp32 partials (splits * M * N * 4 bytes) within a
@@ -1327,14 +1337,15 @@ static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int split
     gemv_shape(M, K, glu, &p);
     return p;
   }
-  if (variant == kVarSkinny || (variant == kVarAuto && use_skinny(M, N, K))) {
+  if (variant == kVarSkinny ||
+      (variant == kVarAuto && use_skinny(M, N, K) && !use_wide_long_k(M, N, K, cus))) {
     GemmPlan p{false, M <= 16 ? 1 : (M <= 32 ? 2 : 4), 0, 0, 1, K, 0, 0};
     skinny_shape(N, cus, glu, &p);
     return p;
   }
   if (variant == kVarAuto) {
     const int64_t n_tiles = (N + 127) / 128;
-    variant = use_small_path(M, N, K)                                       ? kVarStream
+    variant = use_small_path(M, N, K) && !use_wide_long_k(M, N, K, cus)     ? kVarStream
               : (M > 64 && n_tiles * ((M + 127) / 128) * 2 >= cus) ? kVarWide128
                                                                         : kVarWide64;
     splits = 0;
