@@ -89,3 +89,28 @@ def test_tuned_decode_table_is_followed():
                                               partition=part))
     want = R.paged_attention(q, kc, vc, meta, D ** -0.5)
     assert (got.float() - want.float()).abs().max() < 1e-2
+
+
+def test_tuned_decode_choice_is_for_pure_decode_batches_only():
+    """A tuned fixed decode partition applies to pure-decode batches; a mixed batch keeps the
+    library's own-length plan, the one that runs its decode rows and prefill tiles in one
+    launch, so its output equals the untuned call's bit for bit."""
+    from .test_kernels_gpu import make_paged, meta_of
+
+    H, KVH, D = 12, 2, 128
+    seq, ql = [900, 40, 1700, 300 + 256], [1, 1, 1, 256]
+    q, kc, vc, qsl, sl, bt = make_paged(seq, H, KVH, D, ql, seed=5)
+    meta = meta_of(qsl, sl, bt, 3, ql, q.shape[0])
+    q, kc, vc = q.to(DEV), kc.to(DEV), vc.to(DEV)
+    T.set_active(T.VariantTable())
+    untuned = K.paged_attention(q, kc, vc, meta, D ** -0.5)
+    table = T.VariantTable()
+    table.set("decode", (3, 2048), {"version": "v3", "partition": 256, "us": 1.0})
+    T.set_active(table)
+    assert T.decode_choice(3, int(meta.max_seq_len)) == ("v3", 256)
+    assert torch.equal(K.paged_attention(q, kc, vc, meta, D ** -0.5), untuned)
+    # the same decode rows alone follow the table
+    dmeta = meta_of(qsl[:4], sl[:3], bt[:3], 3, [1, 1, 1], 3)
+    assert torch.equal(K.paged_attention(q[:3], kc, vc, dmeta, D ** -0.5),
+                       K.paged_attention(q[:3], kc, vc, dmeta, D ** -0.5, decode_version="v3",
+                                         partition=256))
