@@ -374,7 +374,9 @@ def bench_calibration(torch, synth, layers: int = 28) -> dict:
     * gather floor: ts_probe_gather over config 2's chunk list -- every cached (block, KV head) K
       and V chunk of the step's 64 sequences once (4 KiB each, the decode step's KV bytes), no
       arithmetic, no dependent metadata loads -- with `layers` layer caches rotated as in the
-      headline, and the same number of bytes read contiguously;
+      headline, and the same number of bytes read contiguously; the same list with the K chunks
+      read in the decode kernel's K operand layout (ts_probe_gather_k_operand); and persistent
+      forms of the gather (ts_probe_gather_persistent);
     * MFMA: ts_probe_mfma, back-to-back independent v_mfma_f32_32x32x16_f16 on every SIMD."""
     import numpy as np
 
@@ -418,9 +420,19 @@ def bench_calibration(torch, synth, layers: int = 28) -> dict:
 
         ms = time_graph(torch, run, reps=10) / layers
         results[name] = {"us": round(ms * 1e3, 2), "GBps": round(n * chunk / ms / 1e6, 1)}
+    # the same chunk list with each K chunk read in the decode kernel's K operand layout (64 bytes
+    # of each of 16 token rows per load instruction), V chunks as whole KiBs
+    d_off = torch.from_numpy(offs).to(dev)
+
+    def run_kop():
+        for l in range(layers):
+            N.check(lib.ts_probe_gather_k_operand(kv[l].data_ptr(), d_off.data_ptr(), n, chunk,
+                                                  sink.data_ptr(), cur()), "probe_gather_k_operand")
+
+    ms = time_graph(torch, run_kop, reps=10) / layers
+    results["gather_k_operand"] = {"us": round(ms * 1e3, 2), "GBps": round(n * chunk / ms / 1e6, 1)}
     # the same chunk list, persistent: a few workgroups per CU, each wavefront streaming its own
     # contiguous range with `depth` whole 1 KiB loads in flight, into registers or by LDS DMA
-    d_off = torch.from_numpy(offs).to(dev)
     cus = N.cu_count(0)
     psink = torch.empty(4 * 4 * cus, dtype=torch.int32, device=dev)
     persistent = []

@@ -26,6 +26,15 @@ int ts_probe_gather(const void* base, const int64_t* chunk_offsets, int32_t n_ch
 int ts_probe_mfma(int32_t workgroups, int32_t iters, float* sink, void* stream);
 
 /*
+ * ts_probe_gather_k_operand: as ts_probe_gather, but the first of each wavefront's two chunks
+ * (the K chunk of a block in a decode step's chunk list, which alternates K and V) is read in the
+ * decode kernel's K operand layout: each load instruction takes 64 bytes of each of the chunk's
+ * 16 token rows instead of one contiguous KiB. The second chunk is read as in ts_probe_gather.
+ */
+int ts_probe_gather_k_operand(const void* base, const int64_t* chunk_offsets, int32_t n_chunks,
+                              int32_t chunk_bytes, uint32_t* sink, void* stream);
+
+/*
  * ts_probe_gather_persistent: the same chunk list read by `workgroups` workgroups of 4
  * wavefronts, each wavefront streaming an equal contiguous range of the list's 1 KiB pieces with
  * `depth` (4 or 8) whole-piece loads in flight; use_lds != 0 issues them as LDS DMA into a ring.

@@ -37,7 +37,8 @@ def test_probes_are_a_separate_measurement_library():
     """The measurement probes are not part of the product ABI: declared in their own header,
     exported by libturingserve_probes.so only."""
     names = declared_functions(PROBES_HEADER)
-    assert sorted(names) == ["ts_probe_gather", "ts_probe_gather_persistent", "ts_probe_mfma"]
+    assert sorted(names) == ["ts_probe_gather", "ts_probe_gather_k_operand",
+                             "ts_probe_gather_persistent", "ts_probe_mfma"]
     assert not set(names) & set(declared_functions())
     for name in names:
         assert not hasattr(N.lib(), name), f"{name} exported by the product library"

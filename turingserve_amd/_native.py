@@ -104,6 +104,7 @@ PROBE_SIGNATURES = {
     "ts_probe_gather": (ctypes.c_int, [_p, _p, _i32, _i32, _p, _p]),
     "ts_probe_mfma": (ctypes.c_int, [_i32, _i32, _p, _p]),
     "ts_probe_gather_persistent": (ctypes.c_int, [_p, _p, _i32, _i32, _i32, _i32, _i32, _p, _p]),
+    "ts_probe_gather_k_operand": (ctypes.c_int, [_p, _p, _i32, _i32, _p, _p]),
 }
 
 

@@ -4,6 +4,8 @@
 //    and no dependent metadata loads -- with the chunk list of a decode step (every cached
 //    (block, KV head) K and V chunk once, in block-table order), the fastest that step's bytes
 //    can be gathered;
+//  * k-operand gather: the same, with each K chunk read in the decode kernel's K operand layout
+//    (64 bytes of each of 16 token rows per load instruction) instead of whole KiBs;
 //  * persistent gather: the same chunk list read by a few resident workgroups per CU, each
 //    wavefront streaming its own contiguous range with 4 or 8 loads in flight;
 //  * mfma: back-to-back independent v_mfma_f32_32x32x16_f16 chains, the matrix-core rate.
@@ -17,19 +19,27 @@ constexpr int kChunksPerGroup = 8;        // two chunks per wavefront
 // Workgroup b reads chunks 8b .. 8b+7 (wavefront w: 8b + 2w, 8b + 2w + 1; past the list the
 // last chunk again); each chunk of PIECES KiB is read with 16-byte lane loads, all issued before
 // any is used. The XOR of the loaded words goes to sink[b] so no load is dead.
-template <int PIECES>
+// KOP = false: every load instruction reads one contiguous KiB. KOP = true: a wavefront's first
+// chunk (the K chunk in a decode step's list, whose chunks alternate K and V of one block) is
+// read as the decode kernel reads its K operand -- load i of lane (c, g) (c = lane % 16,
+// g = lane / 16) takes bytes 64 i + 16 g of the chunk's token row c, so one instruction reads
+// 64 bytes of each of 16 rows -- and the second chunk (V) as whole KiBs, as the decode kernel
+// reads V rows.
+template <int PIECES, bool KOP>
 __global__ void __launch_bounds__(kProbeThreads) gather_probe_kernel(
     const uint8_t* __restrict__ base, const int64_t* __restrict__ offsets, int n_chunks,
     uint32_t* __restrict__ sink) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  constexpr int kRowBytes = PIECES * 1024 / 16;   // one token row of the chunk
   int4_t v[2][PIECES];
 #pragma unroll
   for (int c = 0; c < 2; ++c) {
     int chunk = blockIdx.x * kChunksPerGroup + 2 * w + c;
     chunk = chunk < n_chunks ? chunk : n_chunks - 1;
-    const uint8_t* p = base + offsets[chunk] + lane * 16;
+    const uint8_t* p = base + offsets[chunk] +
+                       (KOP && c == 0 ? (lane & 15) * kRowBytes + (lane >> 4) * 16 : lane * 16);
 #pragma unroll
-    for (int i = 0; i < PIECES; ++i) v[c][i] = ld<int4_t>(p + i * 1024);
+    for (int i = 0; i < PIECES; ++i) v[c][i] = ld<int4_t>(p + i * (KOP && c == 0 ? 64 : 1024));
   }
   int4_t acc = {0, 0, 0, 0};
 #pragma unroll
@@ -145,10 +155,30 @@ extern "C" int ts_probe_gather(const void* base, const int64_t* chunk_offsets, i
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   const uint8_t* b = static_cast<const uint8_t*>(base);
   if (chunk_bytes == 4096)
-    gather_probe_kernel<4><<<groups, kProbeThreads, 0, s>>>(b, chunk_offsets, n_chunks, sink);
+    gather_probe_kernel<4, false><<<groups, kProbeThreads, 0, s>>>(b, chunk_offsets, n_chunks, sink);
   else
-    gather_probe_kernel<2><<<groups, kProbeThreads, 0, s>>>(b, chunk_offsets, n_chunks, sink);
+    gather_probe_kernel<2, false><<<groups, kProbeThreads, 0, s>>>(b, chunk_offsets, n_chunks, sink);
   return check_launch("probe_gather");
+}
+
+extern "C" int ts_probe_gather_k_operand(const void* base, const int64_t* chunk_offsets,
+                                         int32_t n_chunks, int32_t chunk_bytes, uint32_t* sink,
+                                         void* stream) {
+  ts::clear_error();
+  TS_REQUIRE(base && chunk_offsets && sink && n_chunks >= 0, TS_ERR_INVALID_ARG,
+             "probe_gather_k_operand: null pointer or negative count");
+  TS_REQUIRE((chunk_bytes == 2048 || chunk_bytes == 4096) && aligned(base, 16),
+             TS_ERR_INVALID_ARG, "probe_gather_k_operand: chunk_bytes %d must be 2048 or 4096, "
+             "base 16-byte aligned", chunk_bytes);
+  if (n_chunks == 0) return TS_OK;
+  const int groups = (n_chunks + kChunksPerGroup - 1) / kChunksPerGroup;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  const uint8_t* b = static_cast<const uint8_t*>(base);
+  if (chunk_bytes == 4096)
+    gather_probe_kernel<4, true><<<groups, kProbeThreads, 0, s>>>(b, chunk_offsets, n_chunks, sink);
+  else
+    gather_probe_kernel<2, true><<<groups, kProbeThreads, 0, s>>>(b, chunk_offsets, n_chunks, sink);
+  return check_launch("probe_gather_k_operand");
 }
 
 extern "C" int ts_probe_gather_persistent(const void* base, const int64_t* chunk_offsets,
