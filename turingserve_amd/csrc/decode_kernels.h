@@ -337,8 +337,9 @@ __global__ void __launch_bounds__(NT) decode_split_map_kernel(
 // KV head, head group) in v2 (ws_acc == nullptr). The blocks of the range are consumed in pairs,
 // pair p by wavefront p % NW: two S^T chains, one online-softmax step per 32 tokens and the P.V
 // product as v_mfma_f32_16x16x32_f16 over the pair. Each wavefront keeps the next pair's loads in
-// flight while it multiplies the current one; block-table entries are wave-uniform scalar loads
-// issued a pair further ahead, so they never wait behind the K/V vector loads. The wavefronts
+// flight while it multiplies the current one (with KDMA the next two pairs', K through a ring in
+// LDS); block-table entries are wave-uniform scalar loads issued a pair further ahead, so they
+// never wait behind the K/V vector loads. The wavefronts
 // merge their (m, l, acc) in LDS; a sequence with one split writes its output here, otherwise
 // the split's partial goes to the workspace for decode_merge_kernel.
 // LDS of one decode workgroup: per-wavefront O^T rows, m and l, and the split lookup's scratch.
@@ -369,7 +370,7 @@ struct NewRows {
   int64_t qkv_st;
 };
 
-template <int D, int NW, bool WRITE = false, bool ROPE = false>
+template <int D, int NW, bool WRITE = false, bool ROPE = false, bool KDMA = false>
 __device__ __forceinline__ void decode_mfma_body(
     const half_t* __restrict__ q, int64_t q_st, int64_t q_sh, half_t* __restrict__ out,
     int64_t o_st, const half_t* __restrict__ kc, const half_t* __restrict__ vc, int64_t NB,
@@ -378,7 +379,8 @@ __device__ __forceinline__ void decode_mfma_body(
     int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
     float* __restrict__ ws_l, int* __restrict__ ws_cnt,
     int bx, int bz, char* __restrict__ lds, const NewRows& nr = NewRows{},
-    int* __restrict__ smap = nullptr, int nslots = 0) {
+    int* __restrict__ smap = nullptr, int nslots = 0, half8_t* kr0 = nullptr,
+    half8_t* kr1 = nullptr) {
   constexpr int KK = KvRegs<D>::KK;
   constexpr int VW = KvRegs<D>::VW;
   constexpr int TILES = KvRegs<D>::TILES;
@@ -560,13 +562,16 @@ __device__ __forceinline__ void decode_mfma_body(
 
   const int64_t head_off = (int64_t)kvh * kBlockSize * D;
   const int64_t blk_stride = (int64_t)KVH * kBlockSize * D;
-  // Register budget per wavefront: K of one pair (refilled for the next pair as soon as the
-  // S^T MFMAs have consumed it) and V of two pairs (the next pair's V is requested a whole
-  // iteration before its P.V product). At D = 128 this keeps the kernel at two wavefronts per
-  // SIMD; the remaining latency is hidden by the other resident wavefronts. The refills are
-  // unconditional (past a wavefront's last pair they repeat its current pair, a cache hit) so
-  // every iteration has the same loads in flight and each wait covers exactly what it needs.
-  // Block-table entries are scalar loads issued two pairs ahead.
+  // Two pipelines. KDMA (decode_mfma_kernel at D = 128): K of two pairs in a per-wavefront LDS
+  // ring filled by LDS DMA, V of two pairs in registers, so each pair's K and V are requested two
+  // pairs ahead. Otherwise (the ragged launch, other head sizes): K of one pair in registers
+  // (refilled for the next pair as soon as the S^T MFMAs have consumed it) and V of two pairs
+  // (the next pair's V is requested a whole iteration before its P.V product). Either form keeps
+  // the kernel at two wavefronts per SIMD at D = 128; the remaining latency is hidden by the
+  // other resident wavefronts. The refills are unconditional (past a wavefront's last pair they
+  // repeat its current pair, a cache hit) so every iteration has the same loads in flight and
+  // each wait covers exactly what it needs. Block-table entries are scalar loads issued two
+  // pairs ahead.
   auto load_k = [&](const int (&id)[2], half8_t (&kf)[2][KK]) {
 #pragma unroll
     for (int j = 0; j < 2; ++j) load_k_block<D>(kc + id[j] * blk_stride + head_off, c, g, kf[j]);
@@ -579,90 +584,199 @@ __device__ __forceinline__ void decode_mfma_body(
     id[0] = blk_id(pp, 0);
     id[1] = blk_id(pp, 1);
   };
-  half8_t kf[2][KK];
-  VRow vA[2][4], vB[2][4];
-  int idk[2] = {0, 0}, idv[2] = {0, 0};        // next K refill / next V refill (two pairs on)
+
   auto last_or = [&](int pp, int fallback) { return pp < npairs ? pp : fallback; };
-  // Pair p: S^T from kf, refill kf with pair p + NW, softmax, P.V from vr, refill vr with pair
-  // p + 2 NW.
-  auto step = [&](int p, VRow (&vr)[2][4]) {
-    int idk_next[2], idv_next[2];
-    ids_of(last_or(p + 2 * NW, last_or(p + NW, p)), idk_next);
-    ids_of(last_or(p + 3 * NW, last_or(p + 2 * NW, last_or(p + NW, p))), idv_next);
-    const int ba = blk_lo + 2 * p;
-    const int ta = ba * kBlockSize + 4 * g, tb = ta + kBlockSize;
-    float4_t sa = zero4, sb = zero4;             // S^T = K . Q^T: two independent MFMA chains
-#pragma unroll
-    for (int kk = 0; kk < KK; ++kk) {
-      if constexpr (D >= 32) {
-        sa = mfma16x16x32(kf[0][kk], qf[kk], sa);
-        sb = mfma16x16x32(kf[1][kk], qf[kk], sb);
-      } else {
-        sa = mfma16x16x16(lo4(kf[0][kk]), lo4(qf[kk]), sa);
-        sb = mfma16x16x16(lo4(kf[1][kk]), lo4(qf[kk]), sb);
-      }
-    }
-    load_k(idk, kf);
-    // Only the last pair of a range can reach past tok_hi (token 0 of block a never does), so
-    // the masked form is a separate, rarely taken path and the common one carries no selects.
-    auto finish = [&](auto masked) {
-      constexpr bool kMasked = decltype(masked)::value;
-      const bool tail_a = kMasked && (ba + 1) * kBlockSize > tok_hi;
-      if constexpr (kMasked) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          sa[r] = ta + r < tok_hi ? sa[r] : -INFINITY;
-          sb[r] = tb + r < tok_hi ? sb[r] : -INFINITY;
-        }
-      }
-      const SoftmaxStep st = softmax_pair(sa, sb, sl2, m, l);
-      // lane (c, g) of tile t: dims VW (4g + r) + t of head c
-      pv_update<TILES>(o, st, [&](int t) {
-        return vt_operand<VW>(vr[0], vr[1], t, tail_a, kMasked, ta, tb, tok_hi);
-      });
-    };
-    if ((ba + 2) * kBlockSize > tok_hi)
-      finish(std::true_type());
-    else
-      finish(std::false_type());
-    load_v(idv, vr);
-    idk[0] = idk_next[0];
-    idk[1] = idk_next[1];
-    idv[0] = idv_next[0];
-    idv[1] = idv_next[1];
-  };
-  int p = w;
-  if (p < npairs) {
-    int id0[2], id1[2];
-    if (mapped) {
-      id0[0] = m_id[0];
-      id0[1] = m_id[1];
-      id1[0] = m_id[2];
-      id1[1] = m_id[3];
-    } else {
-      ids_of(p, id0);
-      ids_of(last_or(p + NW, p), id1);
-    }
-    load_k(id0, kf);
-    load_v(id0, vA);
-    load_v(id1, vB);
-    ids_of(last_or(p + NW, p), idk);
-    ids_of(last_or(p + 2 * NW, last_or(p + NW, p)), idv);
-  }
-  if (mapped) {
-    // A map built for another step (other lengths or block tables, same plan) poisons the rows
-    // it would attend wrongly: the entry's clamped length and last block must be this step's.
-    // These loads follow the first K/V requests, off their critical path.
+  // A map built for another step (other lengths or block tables, same plan) poisons the rows
+  // it would attend wrongly: the entry's clamped length and last block must be this step's.
+  // These loads follow the first K/V requests, off their critical path.
+  auto stale = [&]() {
     const int cap = cap_blocks * kBlockSize;
     int cur = seq_lens[s];
     cur = cur < 0 ? 0 : (cur > cap ? cap : cur);
     const int cur_last = clamp_block(btrow[(seq_len - 1) / kBlockSize], NB);
-    poison = poison || cur != seq_len || cur_last != m_last;
-  }
-  for (; p < npairs; p += 2 * NW) {
-    step(p, vA);
-    if (p + NW >= npairs) break;
-    step(p + NW, vB);
+    return cur != seq_len || cur_last != m_last;
+  };
+  if constexpr (KDMA) {
+    static_assert(D == 128, "LDS-staged K: 16 pieces of 16 bytes per token row");
+    // This wavefront's 8 KB of each ring slot (a pair of blocks, 4 KB each). Token row r of a
+    // block holds its 16-byte piece q at position q ^ r, so the 16 lanes of an operand read
+    // (rows 0..15 at one piece index) cover the 64 banks once.
+    half8_t* kslot0 = kr0 + w * 512;
+    half8_t* kslot1 = kr1 + w * 512;
+    const int lr = lane >> 4, lq = lane & 15;
+    // The DMAs are issued from inline assembly, outside the compiler's wait bookkeeping (it
+    // would drain every load in flight before any LDS read after an LDS DMA in a loop); their
+    // waits are written out: each K pair's eight DMAs are followed, before the pair is read, by
+    // at least 24 younger vector memory operations (its own V loads and the next pair's DMAs
+    // and V loads), so vmcnt(24) means the pair has landed. The compiler's own waits for the V
+    // registers count only its own loads and so also cover the DMAs issued before them.
+    auto dma_k = [&](const int (&id)[2], half8_t* slot) {
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // the slot's last reads are done
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const half_t* base = kc + id[j] * blk_stride + head_off;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 4 * i + lr;
+          const unsigned dst = (unsigned)(size_t)(__attribute__((address_space(3))) half8_t*)(
+              slot + 256 * j + 64 * i);
+          asm volatile("s_nop 0\n\tglobal_load_lds_dwordx4 %0, off"
+                       :: "v"(base + r * D + 8 * (lq ^ r)), "{m0}"(dst) : "memory");
+        }
+      }
+    };
+    int idn[2] = {0, 0};
+    auto stepk = [&](int p, VRow (&vr)[2][4], half8_t* slot) {
+      int idnn[2];
+      ids_of(last_or(p + 3 * NW, last_or(p + 2 * NW, last_or(p + NW, p))), idnn);
+      const int ba = blk_lo + 2 * p;
+      const int ta = ba * kBlockSize + 4 * g, tb = ta + kBlockSize;
+      half8_t kf[2][KK];
+      asm volatile("s_waitcnt vmcnt(24)" ::: "memory");    // this pair's K has landed
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int kk = 0; kk < KK; ++kk) kf[j][kk] = slot[256 * j + 16 * c + ((4 * kk + g) ^ c)];
+      float4_t sa = zero4, sb = zero4;
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        sa = mfma16x16x32(kf[0][kk], qf[kk], sa);
+        sb = mfma16x16x32(kf[1][kk], qf[kk], sb);
+      }
+      auto finish = [&](auto masked) {
+        constexpr bool kMasked = decltype(masked)::value;
+        const bool tail_a = kMasked && (ba + 1) * kBlockSize > tok_hi;
+        if constexpr (kMasked) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            sa[r] = ta + r < tok_hi ? sa[r] : -INFINITY;
+            sb[r] = tb + r < tok_hi ? sb[r] : -INFINITY;
+          }
+        }
+        const SoftmaxStep st = softmax_pair(sa, sb, sl2, m, l);
+        pv_update<TILES>(o, st, [&](int t) {
+          return vt_operand<VW>(vr[0], vr[1], t, tail_a, kMasked, ta, tb, tok_hi);
+        });
+      };
+      if ((ba + 2) * kBlockSize > tok_hi)
+        finish(std::true_type());
+      else
+        finish(std::false_type());
+      dma_k(idn, slot);
+      load_v(idn, vr);
+      idn[0] = idnn[0];
+      idn[1] = idnn[1];
+    };
+    VRow vA[2][4], vB[2][4];
+    int p = w;
+    if (p < npairs) {
+      int id0[2], id1[2];
+      if (mapped) {
+        id0[0] = m_id[0];
+        id0[1] = m_id[1];
+        id1[0] = m_id[2];
+        id1[1] = m_id[3];
+      } else {
+        ids_of(p, id0);
+        ids_of(last_or(p + NW, p), id1);
+      }
+      dma_k(id0, kslot0);
+      dma_k(id1, kslot1);
+      load_v(id0, vA);
+      load_v(id1, vB);
+      ids_of(last_or(p + 2 * NW, last_or(p + NW, p)), idn);
+    }
+    // The loop sits on the prologue's path only, so the compiler's wait state at its head is the
+    // prologue's (q and the prologue loads in flight), not that of a path with no loads.
+    if (p < npairs) {
+      if (mapped) poison = poison || stale();
+      for (; p < npairs; p += 2 * NW) {
+        stepk(p, vA, kslot0);
+        if (p + NW >= npairs) break;
+        stepk(p + NW, vB, kslot1);
+      }
+    } else if (mapped) {
+      poison = poison || stale();
+    }
+    // the ring's memory is reused by the merge below: every DMA of every wavefront has landed
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+  } else {
+    half8_t kf[2][KK];
+    VRow vA[2][4], vB[2][4];
+    int idk[2] = {0, 0}, idv[2] = {0, 0};        // next K refill / next V refill (two pairs on)
+    // Pair p: S^T from kf, refill kf with pair p + NW, softmax, P.V from vr, refill vr with pair
+    // p + 2 NW.
+    auto step = [&](int p, VRow (&vr)[2][4]) {
+      int idk_next[2], idv_next[2];
+      ids_of(last_or(p + 2 * NW, last_or(p + NW, p)), idk_next);
+      ids_of(last_or(p + 3 * NW, last_or(p + 2 * NW, last_or(p + NW, p))), idv_next);
+      const int ba = blk_lo + 2 * p;
+      const int ta = ba * kBlockSize + 4 * g, tb = ta + kBlockSize;
+      float4_t sa = zero4, sb = zero4;             // S^T = K . Q^T: two independent MFMA chains
+#pragma unroll
+      for (int kk = 0; kk < KK; ++kk) {
+        if constexpr (D >= 32) {
+          sa = mfma16x16x32(kf[0][kk], qf[kk], sa);
+          sb = mfma16x16x32(kf[1][kk], qf[kk], sb);
+        } else {
+          sa = mfma16x16x16(lo4(kf[0][kk]), lo4(qf[kk]), sa);
+          sb = mfma16x16x16(lo4(kf[1][kk]), lo4(qf[kk]), sb);
+        }
+      }
+      load_k(idk, kf);
+      // Only the last pair of a range can reach past tok_hi (token 0 of block a never does), so
+      // the masked form is a separate, rarely taken path and the common one carries no selects.
+      auto finish = [&](auto masked) {
+        constexpr bool kMasked = decltype(masked)::value;
+        const bool tail_a = kMasked && (ba + 1) * kBlockSize > tok_hi;
+        if constexpr (kMasked) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            sa[r] = ta + r < tok_hi ? sa[r] : -INFINITY;
+            sb[r] = tb + r < tok_hi ? sb[r] : -INFINITY;
+          }
+        }
+        const SoftmaxStep st = softmax_pair(sa, sb, sl2, m, l);
+        // lane (c, g) of tile t: dims VW (4g + r) + t of head c
+        pv_update<TILES>(o, st, [&](int t) {
+          return vt_operand<VW>(vr[0], vr[1], t, tail_a, kMasked, ta, tb, tok_hi);
+        });
+      };
+      if ((ba + 2) * kBlockSize > tok_hi)
+        finish(std::true_type());
+      else
+        finish(std::false_type());
+      load_v(idv, vr);
+      idk[0] = idk_next[0];
+      idk[1] = idk_next[1];
+      idv[0] = idv_next[0];
+      idv[1] = idv_next[1];
+    };
+    int p = w;
+    if (p < npairs) {
+      int id0[2], id1[2];
+      if (mapped) {
+        id0[0] = m_id[0];
+        id0[1] = m_id[1];
+        id1[0] = m_id[2];
+        id1[1] = m_id[3];
+      } else {
+        ids_of(p, id0);
+        ids_of(last_or(p + NW, p), id1);
+      }
+      load_k(id0, kf);
+      load_v(id0, vA);
+      load_v(id1, vB);
+      ids_of(last_or(p + NW, p), idk);
+      ids_of(last_or(p + 2 * NW, last_or(p + NW, p)), idv);
+    }
+    if (mapped) poison = poison || stale();
+    for (; p < npairs; p += 2 * NW) {
+      step(p, vA);
+      if (p + NW >= npairs) break;
+      step(p + NW, vB);
+    }
   }
   l = rows_sum(l);
 
@@ -756,17 +870,32 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
     int max_splits, float* __restrict__ ws_acc, float* __restrict__ ws_m,
     float* __restrict__ ws_l, int* __restrict__ ws_cnt, const NewRows nr,
     int* __restrict__ smap) {
-  __shared__ __attribute__((aligned(16))) char lds[DecodeLds<D, NW>::BYTES];
   // One-dimensional grid of slots x (KV head, head group), the latter fastest: the launch
   // bounds the slot count from max_seq_len (S times the longest sequence's split count), so
   // most slots past the batch's last split exit at once; numbered last, they no longer hold
   // resident slots ahead of the second KV head's splits.
   const int zh = KVH * HG;
   const int bx = (int)blockIdx.x / zh, bz = (int)blockIdx.x - bx * zh;
-  decode_mfma_body<D, NW, WRITE, ROPE>(q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks,
-                                 seq_lens, S, H, KVH, G, HG, sl2, cap_blocks, part_blocks,
-                                 max_splits, ws_acc, ws_m, ws_l, ws_cnt, bx, bz, lds, nr, smap,
-                                 (int)gridDim.x / zh);
+  if constexpr (D == 128) {
+    // The K ring: two slots of NW x 8 KB (a pair of 4 KB blocks per wavefront). The merge's LDS
+    // (O^T rows, m, l, the lookup scratch) reuses the first slot once every DMA has landed, so
+    // the workgroup holds 64 KB plus the part of the merge's LDS past 32 KB (two per CU).
+    constexpr int kMergeVecs = (DecodeLds<D, NW>::BYTES + 15) / 16;
+    constexpr int R0 = NW * 512 > kMergeVecs ? NW * 512 : kMergeVecs;
+    __shared__ __attribute__((aligned(16))) half8_t s_k0[R0];
+    __shared__ __attribute__((aligned(16))) half8_t s_k1[NW * 512];
+    decode_mfma_body<D, NW, WRITE, ROPE, true>(q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st,
+                                   max_blocks, seq_lens, S, H, KVH, G, HG, sl2, cap_blocks,
+                                   part_blocks, max_splits, ws_acc, ws_m, ws_l, ws_cnt, bx, bz,
+                                   reinterpret_cast<char*>(s_k0), nr, smap, (int)gridDim.x / zh,
+                                   s_k0, s_k1);
+  } else {
+    __shared__ __attribute__((aligned(16))) char lds[DecodeLds<D, NW>::BYTES];
+    decode_mfma_body<D, NW, WRITE, ROPE>(q, q_st, q_sh, out, o_st, kc, vc, NB, bt, bt_st, max_blocks,
+                                   seq_lens, S, H, KVH, G, HG, sl2, cap_blocks, part_blocks,
+                                   max_splits, ws_acc, ws_m, ws_l, ws_cnt, bx, bz, lds, nr, smap,
+                                   (int)gridDim.x / zh);
+  }
 }
 
 // Merge of the split partials (ops/triton_decode_attention.py:144-163): each split leaves its
