@@ -98,6 +98,15 @@ __device__ __forceinline__ int clamp_block(int blk, int64_t num_blocks) {
   return (blk >= 0 && (int64_t)blk < num_blocks) ? blk : 0;
 }
 
+// One entry of a table the kernel only reads (block tables), read through the constant address
+// space: at a wave-uniform address this is a scalar load even when the compiler cannot prove
+// that no store of the kernel aliases the table (pointers that come in a struct argument carry
+// no restrict), so the entry does not wait behind the wavefront's vector loads.
+__device__ __forceinline__ int table_entry(const int* p) {
+  return *reinterpret_cast<const __attribute__((address_space(4))) int*>(
+      reinterpret_cast<uintptr_t>(p));
+}
+
 // 16-byte vector load / store through the vector memory path.
 template <typename T>
 __device__ __forceinline__ T ld(const void* p) { return *reinterpret_cast<const T*>(p); }

@@ -477,7 +477,8 @@ __device__ __forceinline__ void decode_mfma_body(
       // slot would put the row in a block another workgroup may be reading; it is not written,
       // and the sequence's output becomes NaN so the caller sees the broken precondition.
       const int last_blk =
-          mapped ? m_last : clamp_block(bt[(int64_t)s * bt_st + (seq_len - 1) / kBlockSize], NB);
+          mapped ? m_last
+                 : clamp_block(table_entry(bt + (int64_t)s * bt_st + (seq_len - 1) / kBlockSize), NB);
       const int64_t want = (int64_t)last_blk * kBlockSize + (seq_len - 1) % kBlockSize;
       poison = slot >= 0 && slot < nr.num_slots && slot != want;
       if (slot >= 0 && slot < nr.num_slots && !poison) {
@@ -521,7 +522,7 @@ __device__ __forceinline__ void decode_mfma_body(
   auto blk_id = [&](int p, int j) {
     int bi = blk_lo + 2 * p + j;
     bi = bi < blk_hi ? bi : blk_hi - 1;
-    return clamp_block(btrow[bi], NB);
+    return clamp_block(table_entry(btrow + bi), NB);
   };
 
   half8_t qf[KK];
@@ -593,7 +594,7 @@ __device__ __forceinline__ void decode_mfma_body(
     const int cap = cap_blocks * kBlockSize;
     int cur = seq_lens[s];
     cur = cur < 0 ? 0 : (cur > cap ? cap : cur);
-    const int cur_last = clamp_block(btrow[(seq_len - 1) / kBlockSize], NB);
+    const int cur_last = clamp_block(table_entry(btrow + (seq_len - 1) / kBlockSize), NB);
     return cur != seq_len || cur_last != m_last;
   };
   if constexpr (KDMA) {

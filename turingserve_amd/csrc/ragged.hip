@@ -62,6 +62,14 @@ constexpr int kRaggedLds = 2 * TileLayout<128>::STAGE > DecodeLds<128, kDecodeWa
                                ? 2 * TileLayout<128>::STAGE
                                : DecodeLds<128, kDecodeWaves>::BYTES;
 
+// The decode splits' K ring: slot 0 at the start of the LDS (at least the merge's LDS long), slot
+// 1 after it, kDecodeWaves x 8 KB each.
+constexpr int kRaggedRing1 = (DecodeLds<128, kDecodeWaves>::BYTES + 15) / 16 > kDecodeWaves * 512
+                                 ? (DecodeLds<128, kDecodeWaves>::BYTES + 15) / 16
+                                 : kDecodeWaves * 512;
+static_assert((kRaggedRing1 + kDecodeWaves * 512) * 16 <= kRaggedLds,
+              "the decode K ring must fit in the ragged launch's LDS");
+
 __global__ void __launch_bounds__(256, 2) ragged_split_kernel(const RaggedArgs a) {
   __shared__ __attribute__((aligned(16))) char lds[kRaggedLds];
   const int bx = (int)blockIdx.x;
@@ -70,12 +78,15 @@ __global__ void __launch_bounds__(256, 2) ragged_split_kernel(const RaggedArgs a
                            a.bt, a.bt_st, a.max_blocks, a.seq_lens, a.qsl, a.num_decode, a.H,
                            a.KVH, a.sl2, a.smax, a.slots, a.P, a.pf_ws, bx, lds);
   } else {
+    // the decode splits run the LDS-ring form of decode_mfma_kernel: its two K slots fit in the
+    // prefill tiles' LDS, the first one shared with the merge's LDS as there
     const int d = bx - a.pf_launch;
-    decode_mfma_body<128, kDecodeWaves>(a.q, a.q_st, a.q_sh, a.out, a.o_st, a.kc, a.vc, a.NB,
-                                        a.bt, a.bt_st, a.max_blocks, a.seq_lens, a.num_decode,
-                                        a.H, a.KVH, a.G, a.HG, a.sl2, a.cap_blocks, 0,
-                                        a.max_splits, a.ws_acc, a.ws_m, a.ws_l, a.ws_cnt,
-                                        d / (a.KVH * a.HG), d % (a.KVH * a.HG), lds);
+    half8_t* ring = reinterpret_cast<half8_t*>(lds);
+    decode_mfma_body<128, kDecodeWaves, false, false, true>(
+        a.q, a.q_st, a.q_sh, a.out, a.o_st, a.kc, a.vc, a.NB, a.bt, a.bt_st, a.max_blocks,
+        a.seq_lens, a.num_decode, a.H, a.KVH, a.G, a.HG, a.sl2, a.cap_blocks, 0, a.max_splits,
+        a.ws_acc, a.ws_m, a.ws_l, a.ws_cnt, d / (a.KVH * a.HG), d % (a.KVH * a.HG), lds,
+        NewRows{}, nullptr, 0, ring, ring + kRaggedRing1);
   }
 }
 
