@@ -155,12 +155,18 @@ def test_glu_argument_checks_and_workspace():
     for M in (1, 7, 16):
         assert lib.ts_w8a16_glu_workspace_bytes(M, 8960, 1536, 0, 0, 256) == 0
     # ... except long-K products whose 16-row tiles would cover under half the CUs (the down
-    # projection: 96 of them), which take 128 x 32 tiles split 8 ways over K from M = 5 (the VALU
-    # kernel, no workspace, below)
+    # projection: 96 of them), which take 128 x 32 tiles split 16 ways over K from M = 5 (the
+    # VALU kernel, no workspace, below), and 8 ways at M = 64 (two 32-row tiles), about three
+    # workgroups per four CUs
     for M in (1, 4):
         assert lib.ts_w8a16_workspace_bytes(M, 1536, 8960, 256) == 0
-    for M in (5, 7, 16):
-        assert lib.ts_w8a16_workspace_bytes(M, 1536, 8960, 256) == 8 * M * 1536 * 4
+    for M in (5, 7, 16, 32):
+        assert lib.ts_w8a16_workspace_bytes(M, 1536, 8960, 256) == 16 * M * 1536 * 4
+    assert lib.ts_w8a16_workspace_bytes(64, 1536, 8960, 256) == 8 * 64 * 1536 * 4
+    # short-K products with many output channels (gate_up, 140 tiles of 128 rows) at M = 9 to
+    # 32: 128 x 32 tiles, no split, no workspace; the skinny kernel below that
+    for M in (9, 16, 32):
+        assert lib.ts_w8a16_workspace_bytes(M, 17920, 1536, 256) == 0
     for M in (1, 16, 33, 64):
         assert lib.ts_w8a16_glu_workspace_bytes(M, 8960, 1536, 5, 0, 256) == 0
         assert lib.ts_w8a16_workspace_bytes_v(M, 2048, 1536, 5, 0, 256) == 0

@@ -1283,9 +1283,19 @@ static bool use_gemv(int M, int N, int K) {
 }
 // Long-K products whose 16-row skinny tiles would cover under half the CUs (the down projection,
 // 1536 x 8960: 96 workgroups) take 128 x 32 wide tiles split over K instead, from M = 5 to 16
-// (down at M = 8 / 12 / 16: 11.7 / 11.8 / 11.9 us against 12.4 / 14.1 / 15.4 us skinny).
+// (down at M = 8 / 12 / 16: 11.7 / 11.8 / 11.9 us with 8 splits, 10.1 / 10.4 / 10.5 us with the
+// 16 of the rule below, against 12.4 / 14.1 / 15.4 us skinny).
 static bool use_wide_long_k(int M, int N, int K, int cus) {
   return M <= 16 && K >= 4096 && (int64_t)((N + 15) / 16) * 2 < cus;
+}
+// Short-K products with many output channels past the streaming path (M = 9 to 32) take 128 x 32
+// wide tiles with no K split when their grid covers at least half the CUs: each activation row
+// is then read by 140 tiles instead of 1120 skinny ones (the gate_up projection, 17920 x 1536,
+// cold weights: M = 12 / 16 / 24 / 32 11.5 / 11.6 / 11.8 / 12.0 us against 12.7 / 15.0 / 12.6 /
+// 12.8 us for the skinny and 128 x 64 plans). The fused gated form follows the same plan (14.1 ->
+// 14.3 us at M = 16, 13.6 -> 13.6 at M = 24), so its result stays equal to the unfused pair's.
+static bool use_wide32_wide_n(int M, int N, int K, int cus) {
+  return M > 8 && M <= kSmallMMax && K <= 2048 && (int64_t)((N + 127) / 128) * 2 >= cus;
 }
 
 // Weight streaming: fill the device with wavefronts (about eight per CU) by splitting K,
@@ -1328,7 +1338,8 @@ static int wide64_splits(int M, int N, int K, int cus) {
 // with no K split (short K): twice the workgroups for the same weights, which measured ~13 %
 // faster on the 1536 x 1536 and 2048 x 1536 products at M = 256 and the former at M = 560;
 // for M <= 64 (past the streaming path) 128 x 32 tiles split over K when 128 x 64 tiles would
-// cover under a quarter of the CUs. 128 x 32 tiles never split K by their own rule (splits 0),
+// cover under a quarter of the CUs, and unsplit for short-K products with many output channels
+// at M = 9 to 32 (use_wide32_wide_n). 128 x 32 tiles never split K by their own rule (splits 0),
 // and GLU mode plans them as 128 x 64.
 static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int splits,
                             bool glu = false) {
@@ -1338,7 +1349,8 @@ static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int split
     return p;
   }
   if (variant == kVarSkinny ||
-      (variant == kVarAuto && use_skinny(M, N, K) && !use_wide_long_k(M, N, K, cus))) {
+      (variant == kVarAuto && use_skinny(M, N, K) && !use_wide_long_k(M, N, K, cus) &&
+       !use_wide32_wide_n(M, N, K, cus))) {
     GemmPlan p{false, M <= 16 ? 1 : (M <= 32 ? 2 : 4), 0, 0, 1, K, 0, 0};
     skinny_shape(N, cus, glu, &p);
     return p;
@@ -1362,16 +1374,22 @@ static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int split
       variant = kVarWide192;
     if (variant == kVarWide64 && M <= 64 && n_tiles * ((M + 63) / 64) * 4 < cus) {
       // Few rows and few columns (a decode step's projections): 128 x 32 tiles split over K
-      // until about one workgroup per CU, at most 8 ways and at least 6 K steps each (the
-      // reduction of M x N x 4-byte partials is cheap at this M). Measured at M = 48 and 64:
-      // 2048 x 1536 11.1 -> 8.8 us, 1536 x 1536 11.0 -> 8.6 us, 1536 x 8960 18.6 -> 14.4 us.
+      // until about three workgroups per four CUs, at most 16 ways and at least 6 K steps each
+      // (the reduction of M x N x 4-byte partials is cheap at this M). Measured at M = 48 and
+      // 64: 2048 x 1536 11.1 -> 8.8 us, 1536 x 1536 11.0 -> 8.6 us, 1536 x 8960 18.6 -> 14.4 us
+      // (8 splits); the 1536 x 8960 product at M = 5 / 16 / 32 with 16 splits instead of 8:
+      // 11.7 / 12.0 / 12.5 -> 10.0 / 10.5 / 11.4 us (at M = 48 and 64, 8 splits stay fastest).
       const int64_t tiles32 = n_tiles * ((M + 31) / 32);
       const int nk = (K + kTileBK - 1) / kTileBK;
-      int64_t sp = (cus + tiles32 - 1) / tiles32;
-      sp = sp < 8 ? sp : 8;
+      int64_t sp = (3LL * cus / 4 + tiles32 - 1) / tiles32;
+      sp = sp < 16 ? sp : 16;
       sp = sp < nk / 6 ? sp : nk / 6;
       variant = kVarWide32;
       splits = sp > 1 ? (int)sp : 1;
+    }
+    if (use_wide32_wide_n(M, N, K, cus)) {
+      variant = kVarWide32;
+      splits = 1;
     }
   }
   GemmPlan p{variant == kVarStream, (M + 15) / 16, 128,
