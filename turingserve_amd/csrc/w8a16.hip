@@ -1315,15 +1315,17 @@ static int stream_splits(int M, int N, int K, int cus) {
 }
 
 // 128 x 64 wide tiles: split over K while the grid holds fewer than two workgroups per CU, each
-// split keeps at least 32 K steps (below that the reduction costs more than the split saves)
+// split keeps at least 20 K steps (below that the reduction costs more than the split saves)
 // and the fp32 partials (written and read once more by the reduction) stay within half the
-// weight bytes or 8 MB.
+// weight bytes or 8 MB. The 1536 x 8960 product at M = 96 / 128 / 192 (cold weights): 18.4 /
+// 19.3 / 19.8 us with the earlier floor of 32 K steps (4, 4 and 4 splits), 15.7 / 16.6 / 17.6
+// us at 6 splits.
 static int wide64_splits(int M, int N, int K, int cus) {
   const int nk = (K + kTileBK - 1) / kTileBK;
   const int64_t tiles = (int64_t)((N + 127) / 128) * ((M + 63) / 64);
   const int64_t part_budget = (int64_t)N * K / 2 > (8LL << 20) ? (int64_t)N * K / 2 : (8LL << 20);
   int splits = 1;
-  while (tiles * splits < 2LL * cus && nk / (splits + 1) >= 32 &&
+  while (tiles * splits < 2LL * cus && nk / (splits + 1) >= 20 &&
          (int64_t)(splits + 1) * M * N * 4 <= part_budget)
     ++splits;
   return splits;
@@ -1331,8 +1333,9 @@ static int wide64_splits(int M, int N, int K, int cus) {
 
 // The plan of a variant with `splits` K splits (0: the variant's own rule). kVarAuto: weight
 // streaming when use_small_path says so; else 128 x 128 tiles (two workgroups per CU; the most
-// work per CU of the shapes measured) once they cover half the CUs and M is past 64 (below
-// that most of their rows would be padding), or 128 x 192 tiles where those fit one resident
+// work per CU of the shapes measured) once they cover more than half the CUs and M is past 64
+// (below that most of their rows would be padding; at exactly half, 128 x 64 tiles give every
+// CU one: the 2048 x 1536 product at M = 1024 17.0 -> 13.2 us), or 128 x 192 tiles where those fit one resident
 // round and 128 x 128 tiles would not; else 128 x 64 tiles, or 128 x 32 tiles (four
 // workgroups per CU) when M is past 64 but 128 x 64 tiles would cover fewer than half the CUs
 // with no K split (short K): twice the workgroups for the same weights, which measured ~13 %
@@ -1358,12 +1361,15 @@ static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int split
   if (variant == kVarAuto) {
     const int64_t n_tiles = (N + 127) / 128;
     variant = use_small_path(M, N, K) && !use_wide_long_k(M, N, K, cus)     ? kVarStream
-              : (M > 64 && n_tiles * ((M + 127) / 128) * 2 >= cus) ? kVarWide128
+              : (M > 64 && n_tiles * ((M + 127) / 128) * 2 > cus) ? kVarWide128
                                                                         : kVarWide64;
     splits = 0;
-    if (variant == kVarWide64 && M > 64 && n_tiles * ((M + 63) / 64) * 2 < cus &&
-        wide64_splits(M, N, K, cus) == 1)
-      variant = kVarWide32;
+    // 128 x 64 tiles rather than 128 x 128 ones when they pad fewer rows and their grid still
+    // fits one round of resident workgroups (the gated gate_up product at M = 192: 30.4 -> 25.8
+    // us, plain 28.2 -> 25.6 us)
+    if (variant == kVarWide128 && (M + 63) / 64 * 64 < (M + 127) / 128 * 128 &&
+        n_tiles * ((M + 63) / 64) <= 2LL * cus)
+      variant = kVarWide64;
     // 128 x 192 tiles when their grid fits one round of resident workgroups (two per CU) and the
     // 128 x 128 grid does not: the leftover partial round of 128-row tiles costs more than the
     // larger tiles. Measured on the gate_up product (17920 x 1536, cold weights) at M = 560:
@@ -1372,13 +1378,15 @@ static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int split
     if (variant == kVarWide128 && n_tiles * ((M + 191) / 192) <= 2LL * cus &&
         n_tiles * ((M + 127) / 128) > 2LL * cus)
       variant = kVarWide192;
-    if (variant == kVarWide64 && M <= 64 && n_tiles * ((M + 63) / 64) * 4 < cus) {
+    if (variant == kVarWide64 && M <= 96 && n_tiles * ((M + 63) / 64) * 4 < cus) {
       // Few rows and few columns (a decode step's projections): 128 x 32 tiles split over K
       // until about three workgroups per four CUs, at most 16 ways and at least 6 K steps each
       // (the reduction of M x N x 4-byte partials is cheap at this M). Measured at M = 48 and
       // 64: 2048 x 1536 11.1 -> 8.8 us, 1536 x 1536 11.0 -> 8.6 us, 1536 x 8960 18.6 -> 14.4 us
       // (8 splits); the 1536 x 8960 product at M = 5 / 16 / 32 with 16 splits instead of 8:
-      // 11.7 / 12.0 / 12.5 -> 10.0 / 10.5 / 11.4 us (at M = 48 and 64, 8 splits stay fastest).
+      // 11.7 / 12.0 / 12.5 -> 10.0 / 10.5 / 11.4 us (at M = 48 and 64, 8 splits stay fastest);
+      // at M = 96 (three 32-row tiles): 1536 x 1536 10.0 -> 8.9 us, 2048 x 1536 10.3 -> 9.5 us,
+      // 1536 x 8960 15.0 -> 14.4 us.
       const int64_t tiles32 = n_tiles * ((M + 31) / 32);
       const int nk = (K + kTileBK - 1) / kTileBK;
       int64_t sp = (3LL * cus / 4 + tiles32 - 1) / tiles32;
@@ -1387,6 +1395,11 @@ static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int split
       variant = kVarWide32;
       splits = sp > 1 ? (int)sp : 1;
     }
+    // 128 x 32 tiles, unsplit, past M = 64 when 128 x 64 tiles would cover at most half the CUs
+    // and take no K split (the 2048 x 1536 product at M = 512: 12.3 -> 10.5 us)
+    if (variant == kVarWide64 && M > 64 && n_tiles * ((M + 63) / 64) * 2 <= cus &&
+        wide64_splits(M, N, K, cus) == 1)
+      variant = kVarWide32;
     if (use_wide32_wide_n(M, N, K, cus)) {
       variant = kVarWide32;
       splits = 1;
