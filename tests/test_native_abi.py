@@ -167,6 +167,14 @@ def test_glu_argument_checks_and_workspace():
     # 32: 128 x 32 tiles, no split, no workspace; the skinny kernel below that
     for M in (9, 16, 32):
         assert lib.ts_w8a16_workspace_bytes(M, 17920, 1536, 256) == 0
+    # the split 128 x 32 rule reaches M = 96 (three 32-row tiles, 4 splits of 6 K steps at
+    # K = 1536, 6 splits at K = 8960); past it 128 x 64 tiles split while each split keeps 20 K
+    # steps and the partials fit 8 MiB (7 splits of the down projection at M = 128 and 192)
+    assert lib.ts_w8a16_workspace_bytes(96, 1536, 1536, 256) == 4 * 96 * 1536 * 4
+    assert lib.ts_w8a16_workspace_bytes(96, 2048, 1536, 256) == 4 * 96 * 2048 * 4
+    assert lib.ts_w8a16_workspace_bytes(96, 1536, 8960, 256) == 6 * 96 * 1536 * 4
+    for M in (128, 192):
+        assert lib.ts_w8a16_workspace_bytes(M, 1536, 8960, 256) == 7 * M * 1536 * 4
     for M in (1, 16, 33, 64):
         assert lib.ts_w8a16_glu_workspace_bytes(M, 8960, 1536, 5, 0, 256) == 0
         assert lib.ts_w8a16_workspace_bytes_v(M, 2048, 1536, 5, 0, 256) == 0
