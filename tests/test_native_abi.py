@@ -175,6 +175,11 @@ def test_glu_argument_checks_and_workspace():
     assert lib.ts_w8a16_workspace_bytes(96, 1536, 8960, 256) == 6 * 96 * 1536 * 4
     for M in (128, 192):
         assert lib.ts_w8a16_workspace_bytes(M, 1536, 8960, 256) == 7 * M * 1536 * 4
+    # ... and where the partial budget leaves them unsplit on under 2/3 of the CUs (long K,
+    # M = 704 to 896 here), 128 x 128 tiles split 3 ways; past that, unsplit
+    for M in (768, 896):
+        assert lib.ts_w8a16_workspace_bytes(M, 1536, 8960, 256) == 3 * M * 1536 * 4
+    assert lib.ts_w8a16_workspace_bytes(1024, 1536, 8960, 256) == 0
     for M in (1, 16, 33, 64):
         assert lib.ts_w8a16_glu_workspace_bytes(M, 8960, 1536, 5, 0, 256) == 0
         assert lib.ts_w8a16_workspace_bytes_v(M, 2048, 1536, 5, 0, 256) == 0

@@ -1400,6 +1400,19 @@ static GemmPlan plan_gemm_v(int M, int N, int K, int cus, int variant, int split
     if (variant == kVarWide64 && M > 64 && n_tiles * ((M + 63) / 64) * 2 <= cus &&
         wide64_splits(M, N, K, cus) == 1)
       variant = kVarWide32;
+    // Long K where the partial budget leaves 128 x 64 tiles unsplit on under 2/3 of the CUs:
+    // 128 x 128 tiles split up to 3 ways instead (1536 x 8960, cold weights, at M = 768 / 896:
+    // 47.8 / 48.5 -> 40.6 / 42.1 us; at M = 960, past the bound, 128 x 64 unsplit stays fastest)
+    const int nk_all = (K + kTileBK - 1) / kTileBK;
+    if (variant == kVarWide64 && M > 96 && nk_all >= 64 &&
+        n_tiles * ((M + 63) / 64) * 3 < 2LL * cus && wide64_splits(M, N, K, cus) == 1) {
+      const int64_t t128 = n_tiles * ((M + 127) / 128);
+      const int64_t sp = cus / t128;
+      if (sp >= 2) {
+        variant = kVarWide128;
+        splits = sp < 3 ? (int)sp : 3;
+      }
+    }
     if (use_wide32_wide_n(M, N, K, cus)) {
       variant = kVarWide32;
       splits = 1;
