@@ -563,9 +563,9 @@ __device__ __forceinline__ void decode_mfma_body(
 
   const int64_t head_off = (int64_t)kvh * kBlockSize * D;
   const int64_t blk_stride = (int64_t)KVH * kBlockSize * D;
-  // Two pipelines. KDMA (decode_mfma_kernel at D = 128): K of two pairs in a per-wavefront LDS
-  // ring filled by LDS DMA, V of two pairs in registers, so each pair's K and V are requested two
-  // pairs ahead. Otherwise (the ragged launch, other head sizes): K of one pair in registers
+  // Two pipelines. KDMA (decode_mfma_kernel at D = 128 without RoPE, and the ragged launch): K
+  // of two pairs in a per-wavefront LDS ring filled by LDS DMA, V of two pairs in registers, so
+  // each pair's K and V are requested two pairs ahead. Otherwise: K of one pair in registers
   // (refilled for the next pair as soon as the S^T MFMAs have consumed it) and V of two pairs
   // (the next pair's V is requested a whole iteration before its P.V product). Either form keeps
   // the kernel at two wavefronts per SIMD at D = 128; the remaining latency is hidden by the
@@ -877,10 +877,13 @@ __global__ void __launch_bounds__(NW * 64) decode_mfma_kernel(
   // resident slots ahead of the second KV head's splits.
   const int zh = KVH * HG;
   const int bx = (int)blockIdx.x / zh, bz = (int)blockIdx.x - bx * zh;
-  if constexpr (D == 128) {
+  if constexpr (D == 128 && !ROPE) {
     // The K ring: two slots of NW x 8 KB (a pair of 4 KB blocks per wavefront). The merge's LDS
     // (O^T rows, m, l, the lookup scratch) reuses the first slot once every DMA has landed, so
-    // the workgroup holds 64 KB plus the part of the merge's LDS past 32 KB (two per CU).
+    // the workgroup holds 64 KB plus the part of the merge's LDS past 32 KB (two per CU). Not
+    // with RoPE: the compiler's waits for q and the RoPE tables, which count only the loads it
+    // sees, then also wait for the ring's first DMAs before the rotation, and the model step
+    // measured 2.230 against 2.246-2.251 ms with the register form.
     constexpr int kMergeVecs = (DecodeLds<D, NW>::BYTES + 15) / 16;
     constexpr int R0 = NW * 512 > kMergeVecs ? NW * 512 : kMergeVecs;
     __shared__ __attribute__((aligned(16))) half8_t s_k0[R0];
